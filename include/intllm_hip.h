@@ -1,0 +1,153 @@
+/*
+ * intllm_hip.h — C ABI of libintllm_hip: the Q16.48 (int64 fixed-point)
+ * Llama forward pass of nmicic/int-llm's llama_int, on one AMD MI355X.
+ *
+ * The reference has no FFI for this path: its hot path is `static` C
+ * functions in llama_int.c.  Each entry point below replaces one of them
+ * (cited as reference file:line) with the same argument meaning and the
+ * same bits: every output equals the reference's CPU result exactly.
+ *
+ * Conventions
+ *   - Every int64_t* / int* argument of an op is a DEVICE pointer owned
+ *     by the caller (allocate with q48_malloc or any HIP allocator).
+ *   - Values are Q16.48 fixed point (`fixed_t`, fp_math.h:175).
+ *   - Ops are enqueued on the context's stream, in call order; q48_sync
+ *     waits for them.  Results are visible after q48_sync or a
+ *     q48_memcpy_d2h (which is synchronous).
+ *   - Return 0 (Q48_OK) or a negative Q48_E* code; nothing aborts.
+ *     q48_strerror turns a code into text.
+ *   - One context per host thread.  The reference is single-threaded
+ *     (llama_int.c has no threads); contexts are independent.
+ */
+#ifndef INTLLM_HIP_H
+#define INTLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q48_OK          0
+#define Q48_EINVAL     (-1)   /* bad argument (null pointer, size <= 0, shape) */
+#define Q48_ENOMEM     (-2)   /* device allocation failed                     */
+#define Q48_EHIP       (-3)   /* HIP runtime / launch error                    */
+#define Q48_ERANGE     (-4)   /* token or position out of range               */
+#define Q48_ESTATE     (-5)   /* op needs state not yet set up (rope tables)  */
+
+typedef struct q48_ctx q48_ctx;
+
+/* ---- context, memory, stream -------------------------------------------- */
+
+/* Create a context on HIP device `device`: a stream of default priority and
+ * the fp_math constants (FP_PI, CORDIC angles and gain) computed on the
+ * device exactly as fp_math_init does (fp_math.h:833-858). */
+int q48_ctx_create(q48_ctx **out, int device);
+int q48_ctx_destroy(q48_ctx *ctx);
+
+int q48_malloc(q48_ctx *ctx, void **dptr, size_t bytes);
+int q48_free(q48_ctx *ctx, void *dptr);
+/* Synchronous copies (the stream is drained first). */
+int q48_memcpy_h2d(q48_ctx *ctx, void *dst, const void *src, size_t bytes);
+int q48_memcpy_d2h(q48_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Stream-ordered device-to-device copy. */
+int q48_memcpy_d2d(q48_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Stream-ordered zero fill (a kernel, so it may be graph-captured).
+ * Replaces kv_cache_reset's memset (llama_int.c:1170-1183). */
+int q48_zero(q48_ctx *ctx, void *dptr, size_t bytes);
+int q48_sync(q48_ctx *ctx);
+const char *q48_strerror(int code);
+
+/* ---- the six hot-path ops ------------------------------------------------ */
+
+/* y[i] = (int64)((sum_j (int128)W[i*K + j] * x[j]) >> 48), i < M.
+ * Replaces matmul_vec(out, weight, in, M, N=K)  (llama_int.c:1014-1046). */
+int q48_gemv(q48_ctx *ctx, int64_t *y, const int64_t *W, const int64_t *x,
+             int M, int K);
+
+/* Batched prefill: Y[t][i] = matmul_vec row i of token t, for t < T.
+ * W [N][K], X [T][K], Y [T][N].  Each element is exactly what
+ * matmul_vec gives for that token (llama_int.c:1014-1046 per token; the
+ * reference prefills one token at a time, llama_int.c:3081-3092). */
+int q48_gemm(q48_ctx *ctx, int64_t *Y, const int64_t *W, const int64_t *X,
+             int T, int N, int K);
+
+/* out = rmsnorm(x) * w.  Replaces rmsnorm (llama_int.c:1048-1058). */
+int q48_rmsnorm(q48_ctx *ctx, int64_t *out, const int64_t *x,
+                const int64_t *w, int dim);
+
+/* Build the RoPE cos/sin tables [max_seq][head_dim/2] on the device.
+ * Replaces rope_init (llama_int.c:960-986); same bits. */
+int q48_rope_init(q48_ctx *ctx, int head_dim, int max_seq, int theta);
+
+/* Rotate n_heads consecutive head vectors of vec in place at `pos`.
+ * Replaces the rope_apply loops (llama_int.c:997-1008, 1392-1395). */
+int q48_rope(q48_ctx *ctx, int64_t *vec, int n_heads, int head_dim, int pos);
+
+/* Store k_new / v_new ([n_kv][head_dim]) at cache[layer][pos] and compute
+ * exact GQA attention for all n_heads query heads over positions 0..pos.
+ * Cache layout [layers][max_seq][n_kv][head_dim] (kv_key_at,
+ * llama_int.c:1185-1195).  Replaces the KV store, scale, exact attention
+ * and softmax of transformer_layer_forward (llama_int.c:1414-1416, 1433,
+ * 1502-1529, 1060-1072).  q and k_new must already be rotated. */
+int q48_attn_decode(q48_ctx *ctx, int64_t *out, const int64_t *q,
+                    int64_t *kcache, int64_t *vcache, const int64_t *k_new,
+                    const int64_t *v_new, int layer, int pos, int n_heads,
+                    int n_kv, int head_dim, int max_seq);
+
+/* out[i] = fp_mul(fp_silu(gate[i]), up[i]).  Replaces the SwiGLU loops
+ * (llama_int.c:1549-1552, fp_math.h:911-921). */
+int q48_silu_mul(q48_ctx *ctx, int64_t *out, const int64_t *gate,
+                 const int64_t *up, int n);
+
+/* ---- small ops of llama_forward ----------------------------------------- */
+
+/* acc[i] += d[i] (int64, wrapping): the residual adds (llama_int.c:1535,
+ * 1556). */
+int q48_add(q48_ctx *ctx, int64_t *acc, const int64_t *d, int n);
+
+/* out = table[token] ([dim] row): the embedding lookup
+ * (llama_int.c:2822-2824).  The caller range-checks token as
+ * llama_forward does (llama_int.c:2813-2820). */
+int q48_embed(q48_ctx *ctx, int64_t *out, const int64_t *table, int token,
+              int dim);
+
+/* Greedy token: index of the first maximum of v[0..n) (argmax,
+ * llama_int.c:2888-2893).  Writes *host_out; synchronises. */
+int q48_argmax(q48_ctx *ctx, const int64_t *v, int n, int *host_out);
+
+/* ---- introspection / parity hooks ---------------------------------------- */
+
+/* Device pointers of the current RoPE tables (after q48_rope_init). */
+int q48_rope_tables(q48_ctx *ctx, const int64_t **cos_t, const int64_t **sin_t);
+
+/* Evaluate one fp_math function element-wise on the device (no reference
+ * FFI counterpart: this is fp_determinism.c's evaluation step,
+ * fp_determinism.c:175-195, exposed so the gate can run on the GPU).
+ * func: 0 mul(x,y) 1 div(x,y) [0 where y==0] 2 sqrt 3 sqrt_fast
+ * 4 inv_sqrt 5 exp 6 log 7 sincos (out0=cos, out1=sin) 8 sigmoid 9 silu
+ * 10 safe_exp 11 exp_dyadic(x, k=y).  out1 may be NULL unless func 7. */
+int q48_fp_eval(q48_ctx *ctx, int func, const int64_t *x, const int64_t *y,
+                int64_t *out0, int64_t *out1, int n);
+
+/* ---- kernel timing (diagnostic) -------------------------------------------- */
+
+/* HIP-event timing of every q48_gemv launch on the context's stream while
+ * enabled (no reference counterpart: llama_int's profiler, llama_int.c:65-108,
+ * times whole forwards with clock_gettime).  `bytes` is the algorithmic
+ * traffic 8*(M*K + K + M) per launch. */
+typedef struct {
+    int launches;
+    double ms;       /* sum of launch durations */
+    double bytes;    /* sum of algorithmic bytes */
+} q48_prof;
+
+int q48_prof_enable(q48_ctx *ctx, int on);
+/* Synchronise, then report (and with reset != 0 clear) the GEMV timings. */
+int q48_prof_read(q48_ctx *ctx, q48_prof *gemv, int reset);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INTLLM_HIP_H */

@@ -1,0 +1,386 @@
+// q48_abi.hip — extern "C" entry points of libintllm_hip (include/intllm_hip.h).
+//
+// Validates every argument on the host before anything is launched (a
+// kernel never sees a shape it does not support), then enqueues the
+// kernels on the context's stream.
+#include "../../include/intllm_hip.h"
+#include "q48_internal.h"
+
+#include <new>
+#include <stdlib.h>
+
+namespace {
+
+int hip_rc(hipError_t e) { return e == hipSuccess ? Q48_OK : Q48_EHIP; }
+int launch_rc(int e) { return e == (int)hipSuccess ? Q48_OK : Q48_EHIP; }
+
+// Largest sizes the kernels are written for.
+constexpr int kMaxDim = 1 << 28;
+constexpr int kMaxHeadDim = 256;
+
+} // namespace
+
+int q48_ws_reserve(q48_ctx *c, size_t bytes)
+{
+    if (bytes <= c->ws_bytes)
+        return Q48_OK;
+    if (c->ws) {
+        // earlier kernels may still read the old workspace
+        if (hipStreamSynchronize(c->stream) != hipSuccess)
+            return Q48_EHIP;
+        (void)hipFree(c->ws);
+        c->ws = nullptr;
+        c->ws_bytes = 0;
+    }
+    size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    if (hipMalloc(&c->ws, sz) != hipSuccess) {
+        c->ws = nullptr;
+        return Q48_ENOMEM;
+    }
+    c->ws_bytes = sz;
+    return Q48_OK;
+}
+
+extern "C" {
+
+const char *q48_strerror(int code)
+{
+    switch (code) {
+    case Q48_OK: return "ok";
+    case Q48_EINVAL: return "invalid argument";
+    case Q48_ENOMEM: return "device out of memory";
+    case Q48_EHIP: return "HIP runtime error";
+    case Q48_ERANGE: return "token or position out of range";
+    case Q48_ESTATE: return "context state not initialised (call q48_rope_init)";
+    default: return "unknown error";
+    }
+}
+
+int q48_ctx_create(q48_ctx **out, int device)
+{
+    if (!out)
+        return Q48_EINVAL;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
+        return Q48_EINVAL;
+    if (hipSetDevice(device) != hipSuccess)
+        return Q48_EHIP;
+    q48_ctx *c = new (std::nothrow) q48_ctx();
+    if (!c)
+        return Q48_ENOMEM;
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return Q48_EHIP;
+    }
+    if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
+        hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess) {
+        q48_ctx_destroy(c);
+        return Q48_ENOMEM;
+    }
+    int rc = launch_rc(q48_launch_math_init(c));
+    if (rc == Q48_OK)
+        rc = hip_rc(hipStreamSynchronize(c->stream));
+    if (rc != Q48_OK) {
+        q48_ctx_destroy(c);
+        return rc;
+    }
+    *out = c;
+    return Q48_OK;
+}
+
+int q48_ctx_destroy(q48_ctx *c)
+{
+    if (!c)
+        return Q48_EINVAL;
+    if (c->stream)
+        (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(c->consts);
+    (void)hipFree(c->rope_cos);
+    (void)hipFree(c->rope_sin);
+    (void)hipFree(c->ws);
+    (void)hipFree(c->d_scalar);
+    for (int i = 0; i < c->prof_cap; ++i) {
+        if (c->prof[i].a)
+            (void)hipEventDestroy(c->prof[i].a);
+        if (c->prof[i].b)
+            (void)hipEventDestroy(c->prof[i].b);
+    }
+    free(c->prof);
+    if (c->stream)
+        (void)hipStreamDestroy(c->stream);
+    delete c;
+    return Q48_OK;
+}
+
+int q48_malloc(q48_ctx *c, void **dptr, size_t bytes)
+{
+    if (!c || !dptr || bytes == 0)
+        return Q48_EINVAL;
+    if (hipMalloc(dptr, bytes) != hipSuccess) {
+        *dptr = nullptr;
+        return Q48_ENOMEM;
+    }
+    return Q48_OK;
+}
+
+int q48_free(q48_ctx *c, void *dptr)
+{
+    if (!c)
+        return Q48_EINVAL;
+    if (!dptr)
+        return Q48_OK;
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q48_EHIP;
+    return hip_rc(hipFree(dptr));
+}
+
+int q48_memcpy_h2d(q48_ctx *c, void *dst, const void *src, size_t bytes)
+{
+    if (!c || (bytes && (!dst || !src)))
+        return Q48_EINVAL;
+    if (!bytes)
+        return Q48_OK;
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q48_EHIP;
+    return hip_rc(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+}
+
+int q48_memcpy_d2h(q48_ctx *c, void *dst, const void *src, size_t bytes)
+{
+    if (!c || (bytes && (!dst || !src)))
+        return Q48_EINVAL;
+    if (!bytes)
+        return Q48_OK;
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q48_EHIP;
+    return hip_rc(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+}
+
+int q48_memcpy_d2d(q48_ctx *c, void *dst, const void *src, size_t bytes)
+{
+    if (!c || (bytes && (!dst || !src)))
+        return Q48_EINVAL;
+    if (!bytes)
+        return Q48_OK;
+    return hip_rc(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream));
+}
+
+int q48_zero(q48_ctx *c, void *dptr, size_t bytes)
+{
+    if (!c || (bytes && !dptr))
+        return Q48_EINVAL;
+    if (!bytes)
+        return Q48_OK;
+    if (((uintptr_t)dptr & 7) != 0)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_zero(c, dptr, bytes));
+}
+
+int q48_sync(q48_ctx *c)
+{
+    if (!c)
+        return Q48_EINVAL;
+    return hip_rc(hipStreamSynchronize(c->stream));
+}
+
+int q48_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x, int M, int K)
+{
+    if (!c || !y || !W || !x || M <= 0 || K <= 0 || M > kMaxDim || K > kMaxDim)
+        return Q48_EINVAL;
+    if ((((uintptr_t)W | (uintptr_t)x | (uintptr_t)y) & 7) != 0)
+        return Q48_EINVAL;
+    q48_ctx::ProfRec *r = nullptr;
+    if (c->prof_on) {
+        if (c->prof_n == c->prof_cap) {
+            int cap = c->prof_cap ? 2 * c->prof_cap : 1024;
+            auto *p = (q48_ctx::ProfRec *)realloc(c->prof, sizeof(q48_ctx::ProfRec) * cap);
+            if (!p)
+                return Q48_ENOMEM;
+            for (int i = c->prof_cap; i < cap; ++i)
+                p[i].a = p[i].b = nullptr;
+            c->prof = p;
+            c->prof_cap = cap;
+        }
+        r = &c->prof[c->prof_n];
+        if ((!r->a && hipEventCreate(&r->a) != hipSuccess) ||
+            (!r->b && hipEventCreate(&r->b) != hipSuccess))
+            return Q48_EHIP;
+        r->bytes = 8.0 * ((double)M * K + K + M);
+        if (hipEventRecord(r->a, c->stream) != hipSuccess)
+            return Q48_EHIP;
+    }
+    int rc = launch_rc(q48_launch_gemv(c, y, W, x, M, K));
+    if (r && rc == Q48_OK) {
+        if (hipEventRecord(r->b, c->stream) != hipSuccess)
+            return Q48_EHIP;
+        c->prof_n++;
+    }
+    return rc;
+}
+
+int q48_prof_enable(q48_ctx *c, int on)
+{
+    if (!c)
+        return Q48_EINVAL;
+    c->prof_on = on != 0;
+    return Q48_OK;
+}
+
+int q48_prof_read(q48_ctx *c, q48_prof *out, int reset)
+{
+    if (!c || !out)
+        return Q48_EINVAL;
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q48_EHIP;
+    out->launches = c->prof_n;
+    out->ms = 0;
+    out->bytes = 0;
+    for (int i = 0; i < c->prof_n; ++i) {
+        float ms = 0;
+        if (hipEventElapsedTime(&ms, c->prof[i].a, c->prof[i].b) != hipSuccess)
+            return Q48_EHIP;
+        out->ms += ms;
+        out->bytes += c->prof[i].bytes;
+    }
+    if (reset)
+        c->prof_n = 0;
+    return Q48_OK;
+}
+
+int q48_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int T, int N, int K)
+{
+    if (!c || !Y || !W || !X || T <= 0 || N <= 0 || K <= 0 || T > 65535 * 64 ||
+        N > kMaxDim || K > kMaxDim)
+        return Q48_EINVAL;
+    if ((((uintptr_t)W | (uintptr_t)X | (uintptr_t)Y) & 7) != 0)
+        return Q48_EINVAL;
+    int rc = q48_launch_gemm(c, Y, W, X, T, N, K);
+    if (rc == Q48_ENOMEM)
+        return rc;
+    return launch_rc(rc);
+}
+
+int q48_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *x, const int64_t *w, int dim)
+{
+    if (!c || !out || !x || !w || dim <= 0 || dim > kMaxDim)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_rmsnorm(c, out, x, w, dim));
+}
+
+int q48_rope_init(q48_ctx *c, int head_dim, int max_seq, int theta)
+{
+    if (!c || head_dim <= 0 || head_dim % 2 || head_dim > kMaxHeadDim || max_seq <= 0 ||
+        max_seq > 32767 || theta <= 0 || theta > 32767)
+        return Q48_EINVAL;
+    if (c->rope_cos && c->rope_head_dim == head_dim && c->rope_max_seq == max_seq &&
+        c->rope_theta == theta)
+        return Q48_OK;
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q48_EHIP;
+    (void)hipFree(c->rope_cos);
+    (void)hipFree(c->rope_sin);
+    c->rope_cos = c->rope_sin = nullptr;
+    c->rope_head_dim = c->rope_max_seq = c->rope_theta = 0;
+    size_t n = (size_t)max_seq * (head_dim / 2) * sizeof(int64_t);
+    if (hipMalloc(&c->rope_cos, n) != hipSuccess || hipMalloc(&c->rope_sin, n) != hipSuccess) {
+        (void)hipFree(c->rope_cos);
+        c->rope_cos = c->rope_sin = nullptr;
+        return Q48_ENOMEM;
+    }
+    c->rope_head_dim = head_dim;
+    c->rope_max_seq = max_seq;
+    c->rope_theta = theta;
+    return launch_rc(q48_launch_rope_init(c));
+}
+
+int q48_rope(q48_ctx *c, int64_t *vec, int n_heads, int head_dim, int pos)
+{
+    if (!c || !vec || n_heads <= 0 || head_dim <= 0)
+        return Q48_EINVAL;
+    if (!c->rope_cos || head_dim != c->rope_head_dim)
+        return Q48_ESTATE;
+    if (pos < 0 || pos >= c->rope_max_seq)
+        return Q48_ERANGE;
+    return launch_rc(q48_launch_rope(c, vec, n_heads, head_dim, nullptr, pos));
+}
+
+int q48_attn_decode(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
+                    int64_t *vcache, const int64_t *k_new, const int64_t *v_new, int layer,
+                    int pos, int n_heads, int n_kv, int head_dim, int max_seq)
+{
+    if (!c || !out || !q || !kcache || !vcache || !k_new || !v_new)
+        return Q48_EINVAL;
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || head_dim <= 0 ||
+        head_dim > kMaxHeadDim || 256 % head_dim || layer < 0 || max_seq <= 0)
+        return Q48_EINVAL;
+    if (pos < 0 || pos >= max_seq)
+        return Q48_ERANGE;
+    int rc = q48_launch_attn(c, out, q, kcache, vcache, k_new, v_new, layer, nullptr, pos,
+                             n_heads, n_kv, head_dim, max_seq);
+    if (rc == Q48_ENOMEM)
+        return rc;
+    return launch_rc(rc);
+}
+
+int q48_silu_mul(q48_ctx *c, int64_t *out, const int64_t *gate, const int64_t *up, int n)
+{
+    if (!c || !out || !gate || !up || n <= 0 || n > kMaxDim)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_silu_mul(c, out, gate, up, n));
+}
+
+int q48_add(q48_ctx *c, int64_t *acc, const int64_t *d, int n)
+{
+    if (!c || !acc || !d || n <= 0 || n > kMaxDim)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_add(c, acc, d, n));
+}
+
+int q48_embed(q48_ctx *c, int64_t *out, const int64_t *table, int token, int dim)
+{
+    if (!c || !out || !table || dim <= 0 || dim > kMaxDim)
+        return Q48_EINVAL;
+    if (token < 0)
+        return Q48_ERANGE;
+    return launch_rc(q48_launch_embed(c, out, table, nullptr, token, dim));
+}
+
+int q48_argmax(q48_ctx *c, const int64_t *v, int n, int *host_out)
+{
+    if (!c || !v || !host_out || n <= 0)
+        return Q48_EINVAL;
+    int rc = launch_rc(q48_launch_argmax(c, c->d_scalar, v, n));
+    if (rc)
+        return rc;
+    if (hipMemcpyAsync(host_out, c->d_scalar, sizeof(int), hipMemcpyDeviceToHost,
+                       c->stream) != hipSuccess)
+        return Q48_EHIP;
+    return hip_rc(hipStreamSynchronize(c->stream));
+}
+
+int q48_rope_tables(q48_ctx *c, const int64_t **cos_t, const int64_t **sin_t)
+{
+    if (!c || !cos_t || !sin_t)
+        return Q48_EINVAL;
+    if (!c->rope_cos)
+        return Q48_ESTATE;
+    *cos_t = c->rope_cos;
+    *sin_t = c->rope_sin;
+    return Q48_OK;
+}
+
+int q48_fp_eval(q48_ctx *c, int func, const int64_t *x, const int64_t *y, int64_t *out0,
+                int64_t *out1, int n)
+{
+    if (!c || !x || !out0 || n <= 0 || func < 0 || func > 11)
+        return Q48_EINVAL;
+    if ((func == 0 || func == 1 || func == 11) && !y)
+        return Q48_EINVAL;
+    if (func == 7 && !out1)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_fp_eval(c, func, x, y, out0, out1, n));
+}
+
+} // extern "C"

@@ -1,0 +1,372 @@
+// q48_device.hpp — Q16.48 integer math as gfx950 device functions.
+//
+// Bit-identical to the reference's fp_math.h (native __int128 backend,
+// fp_math.h:184-290) and to llama_int.c's use of it.  Every function
+// below cites the reference lines it reproduces.  All int64 adds wrap
+// (two's complement), as the reference's -fwrapv build does.
+//
+// 128-bit values: clang's __int128 on amdgcn lowers multiplies to
+// v_mad_u64_u32 chains; division goes through q48_udiv128_64 below
+// (128 / 64 -> 128 quotient, exact).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __int128 q48_i128;
+typedef unsigned __int128 q48_u128;
+
+#define Q48_ONE ((int64_t)1 << 48)
+#define Q48_HALF ((int64_t)1 << 47)
+
+// Constants computed by fp_math_init (fp_math.h:833-858) on the device at
+// context creation: FP_PI, fp_cordic_gain, fp_cordic_angles[48].
+struct q48_consts {
+    int64_t pi;
+    int64_t gain;
+    int64_t angles[48];
+    int ready;
+};
+
+// ---------------------------------------------------------------------------
+// Exact unsigned 128 / 64 division (quotient up to 128 bits).
+//
+// Two base-2^64 long-division digits, each an exact 128/64 step done by
+// normalised restoring division on 64-bit words (shift-subtract over the
+// significant quotient bits).  Used by fp_div / fp_sqrt, never in the GEMV.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t q48_udiv128_step(uint64_t hi, uint64_t lo,
+                                                     uint64_t d, uint64_t *rem)
+{
+    // Precondition hi < d: the quotient fits in 64 bits.
+    uint64_t q = 0;
+    if (hi == 0) {
+        q = lo / d;
+        *rem = lo - q * d;
+        return q;
+    }
+    // restoring division: 64 iterations of (hi:lo) << 1, compare, subtract
+    for (int i = 0; i < 64; ++i) {
+        uint64_t top = hi >> 63;
+        hi = (hi << 1) | (lo >> 63);
+        lo <<= 1;
+        q <<= 1;
+        if (top || hi >= d) {
+            hi -= d;
+            q |= 1;
+        }
+    }
+    *rem = hi;
+    return q;
+}
+
+__device__ __forceinline__ q48_u128 q48_udiv128_64(q48_u128 n, uint64_t d)
+{
+    uint64_t nh = (uint64_t)(n >> 64), nl = (uint64_t)n;
+    uint64_t qh = nh / d;
+    uint64_t r1 = nh - qh * d;
+    uint64_t r;
+    uint64_t ql = q48_udiv128_step(r1, nl, d, &r);
+    return ((q48_u128)qh << 64) | ql;
+}
+
+// fp_w_divs (fp_math.h:249-256) for a divisor that fits int64: truncating
+// signed division; b == -1 wraps like negation.
+__device__ __forceinline__ q48_i128 q48_divs_128_64(q48_i128 a, int64_t b)
+{
+    if (b == -1)
+        return (q48_i128)(0 - (q48_u128)a);
+    bool na = a < 0, nb = b < 0;
+    q48_u128 ua = na ? (0 - (q48_u128)a) : (q48_u128)a;
+    uint64_t ub = nb ? (uint64_t)0 - (uint64_t)b : (uint64_t)b;
+    q48_u128 q = q48_udiv128_64(ua, ub);
+    return (na != nb) ? (q48_i128)(0 - q) : (q48_i128)q;
+}
+
+// ---------------------------------------------------------------------------
+// fp_math.h primitives
+// ---------------------------------------------------------------------------
+
+// fp_mul, fp_math.h:491-506
+__device__ __forceinline__ int64_t q48_mul(int64_t a, int64_t b)
+{
+    return (int64_t)(((q48_i128)a * b) >> 48);
+}
+
+// fp_div, fp_math.h:508-524
+__device__ __forceinline__ int64_t q48_div(int64_t a, int64_t b)
+{
+    uint64_t mag = a < 0 ? (uint64_t)0 - (uint64_t)a : (uint64_t)a;
+    q48_i128 num = (q48_i128)((q48_u128)mag << 48);
+    if (a < 0)
+        num = (q48_i128)(0 - (q48_u128)num);
+    return (int64_t)q48_divs_128_64(num, b);
+}
+
+// fp_from_int, fp_math.h:530-538
+__device__ __forceinline__ int64_t q48_from_int(int x)
+{
+    uint64_t mag = x < 0 ? (uint64_t)0 - (uint64_t)(int64_t)x : (uint64_t)x;
+    q48_u128 r = (q48_u128)mag << 48;
+    if (x < 0)
+        r = 0 - r;
+    return (int64_t)r;
+}
+
+__device__ __forceinline__ int64_t q48_abs(int64_t a) { return a >= 0 ? a : (int64_t)(0 - (uint64_t)a); }
+
+// fp_sqrt_fast, fp_math.h:605-622
+__device__ __forceinline__ int64_t q48_sqrt_fast(int64_t x)
+{
+    if (x <= 0)
+        return 0;
+    uint64_t ux = (uint64_t)x;
+    int bw = 64 - __builtin_clzll(ux);
+    uint64_t r = (uint64_t)1 << ((bw + 1) / 2);
+    for (int i = 0; i < 5; ++i) {
+        uint64_t nr = (r + ux / r) >> 1;
+        if (nr >= r)
+            break;
+        r = nr;
+    }
+    return (int64_t)(r << 24);
+}
+
+// fp_sqrt, fp_math.h:626-652
+__device__ __forceinline__ int64_t q48_sqrt(int64_t x)
+{
+    if (x <= 0)
+        return 0;
+    q48_u128 n = (q48_u128)(uint64_t)x << 48;
+    uint64_t hi = (uint64_t)(n >> 64), lo = (uint64_t)n;
+    int bw = hi ? 128 - __builtin_clzll(hi) : (lo ? 64 - __builtin_clzll(lo) : 0);
+    uint64_t r = (uint64_t)1 << ((bw + 1) / 2);
+    for (int i = 0; i < 7; ++i) {
+        if (r == 0)
+            return 0;
+        uint64_t q = (uint64_t)q48_udiv128_64(n, r);
+        uint64_t nr = (r + q) >> 1;
+        if (nr >= r)
+            break;
+        r = nr;
+    }
+    while ((q48_i128)(int64_t)r * (int64_t)r > (q48_i128)n)
+        r--;
+    return (int64_t)r;
+}
+
+// fp_inv_sqrt, fp_math.h:658-707
+__device__ __forceinline__ int64_t q48_inv_sqrt(int64_t x)
+{
+    if (x <= 0)
+        return 0;
+    int msb = 63 - __builtin_clzll((uint64_t)x);
+    int k = (msb - 48) >> 1;
+    int64_t xn = k >= 0 ? (x >> (2 * k)) : (int64_t)((uint64_t)x << (-2 * k));
+    int msb_n = 63 - __builtin_clzll((uint64_t)xn);
+    int64_t y = msb_n == 48 ? Q48_ONE : Q48_HALF;
+    const int64_t three = (int64_t)3 << 48;
+    for (int i = 0; i < 8; ++i) {
+        int64_t y2 = (int64_t)(((q48_i128)y * y) >> 48);
+        int64_t xy2 = (int64_t)(((q48_i128)xn * y2) >> 48);
+        int64_t factor = three - xy2;
+        y = (int64_t)(((q48_i128)y * factor) >> 49);
+        if (y <= 0) {
+            y = 1;
+            break;
+        }
+    }
+    if (k >= 0) {
+        int64_t r = y >> k;
+        return r < 0 ? 0 : r;
+    }
+    q48_i128 r = (q48_i128)((q48_u128)(q48_i128)y << (-k));
+    if (r > (q48_i128)INT64_MAX)
+        return INT64_MAX;
+    if (r < 0)
+        return 0;
+    return (int64_t)r;
+}
+
+// fp_exp_dyadic, fp_math.h:714-720
+__device__ __forceinline__ int64_t q48_exp_dyadic(int64_t x, int k)
+{
+    int64_t r = (int64_t)((uint64_t)Q48_ONE + (uint64_t)(x >> k));
+    for (int i = 0; i < k; ++i)
+        r = q48_mul(r, r);
+    return r;
+}
+
+// fp_exp, fp_math.h:724-732
+__device__ __forceinline__ int64_t q48_exp(int64_t x)
+{
+    if (x >= 0)
+        return q48_exp_dyadic(x, 14);
+    int64_t pos = q48_exp_dyadic((int64_t)(0 - (uint64_t)x), 14);
+    if (pos == 0)
+        return 0;
+    return q48_div(Q48_ONE, pos);
+}
+
+// fp_safe_exp, fp_math.h:739-744
+__device__ __forceinline__ int64_t q48_safe_exp(int64_t x)
+{
+    const int64_t max_x = (int64_t)10 << 48;
+    if (x > max_x)
+        x = max_x;
+    if (x < -max_x)
+        return 0;
+    return q48_exp(x);
+}
+
+// fp_log, fp_math.h:752-773
+__device__ __forceinline__ int64_t q48_log(int64_t x)
+{
+    if (x <= 0)
+        return -((int64_t)50 << 48);
+    const int64_t ln2 = 195103586505167LL;
+    int lz = __builtin_clzll((uint64_t)x);
+    int log2_approx = 63 - lz - 48;
+    int64_t y = (int64_t)((uint64_t)(int64_t)log2_approx * (uint64_t)ln2);
+    for (int i = 0; i < 10; ++i) {
+        int64_t ey = q48_exp(y);
+        if (ey == 0)
+            break;
+        int64_t y_new = (int64_t)((uint64_t)y - (uint64_t)Q48_ONE + (uint64_t)q48_div(x, ey));
+        int64_t diff = q48_abs((int64_t)((uint64_t)y_new - (uint64_t)y));
+        if (diff < 2)
+            break;
+        y = y_new;
+    }
+    return y;
+}
+
+// fp_atan_taylor, fp_math.h:789-800
+__device__ __forceinline__ int64_t q48_atan_taylor(int64_t x, int max_terms)
+{
+    int64_t x_sq = q48_mul(x, x);
+    int64_t term = x, sum = x;
+    for (int n = 1; n <= max_terms; ++n) {
+        term = (int64_t)(0 - (uint64_t)q48_mul(term, x_sq));
+        int64_t c = term / (2 * n + 1);
+        if (c == 0)
+            break;
+        sum = (int64_t)((uint64_t)sum + (uint64_t)c);
+    }
+    return sum;
+}
+
+// fp_compute_pi (fp_math.h:804-812), fp_atan_pow2 (:823-827),
+// fp_math_init (:833-858).  Run by one thread at context creation.
+__device__ inline void q48_math_init(q48_consts *k)
+{
+    int64_t atan5 = q48_atan_taylor(Q48_ONE / 5, 40);
+    int64_t atan239 = q48_atan_taylor(Q48_ONE / 239, 15);
+    k->pi = (int64_t)(((uint64_t)atan5 << 4) - ((uint64_t)atan239 << 2));
+    k->angles[0] = k->pi >> 2;
+    for (int i = 1; i < 48; ++i)
+        k->angles[i] = i >= 25 ? (Q48_ONE >> i) : q48_atan_taylor(Q48_ONE >> i, 40);
+    int64_t k_sq = Q48_ONE;
+    for (int i = 0; i < 48; ++i) {
+        int64_t sv = (2 * i < 63) ? (Q48_ONE >> (2 * i)) : 0;
+        k_sq = q48_mul(k_sq, Q48_ONE + sv);
+    }
+    k->gain = q48_div(Q48_ONE, q48_sqrt(k_sq));
+    k->ready = 1;
+}
+
+// fp_sincos, fp_math.h:861-902
+__device__ __forceinline__ void q48_sincos(const q48_consts *__restrict__ k,
+                                           int64_t angle, int64_t *c, int64_t *s)
+{
+    const int64_t pi = k->pi;
+    const int64_t two_pi = (int64_t)((uint64_t)pi << 1);
+    while (angle > pi)
+        angle = (int64_t)((uint64_t)angle - (uint64_t)two_pi);
+    while (angle < -pi)
+        angle = (int64_t)((uint64_t)angle + (uint64_t)two_pi);
+    const int64_t pi_half = pi >> 1;
+    bool neg_cos = false;
+    if (angle > pi_half) {
+        angle = pi - angle;
+        neg_cos = true;
+    } else if (angle < -pi_half) {
+        angle = -pi - angle;
+        neg_cos = true;
+    }
+    int64_t x = k->gain, y = 0, z = angle;
+    for (int i = 0; i < 48; ++i) {
+        int64_t xs = x >> i, ys = y >> i;
+        int64_t a = k->angles[i];
+        if (z >= 0) {
+            int64_t xn = (int64_t)((uint64_t)x - (uint64_t)ys);
+            int64_t yn = (int64_t)((uint64_t)y + (uint64_t)xs);
+            z = (int64_t)((uint64_t)z - (uint64_t)a);
+            x = xn;
+            y = yn;
+        } else {
+            int64_t xn = (int64_t)((uint64_t)x + (uint64_t)ys);
+            int64_t yn = (int64_t)((uint64_t)y - (uint64_t)xs);
+            z = (int64_t)((uint64_t)z + (uint64_t)a);
+            x = xn;
+            y = yn;
+        }
+    }
+    *c = neg_cos ? (int64_t)(0 - (uint64_t)x) : x;
+    *s = y;
+}
+
+// fp_sigmoid, fp_math.h:911-916
+__device__ __forceinline__ int64_t q48_sigmoid(int64_t x)
+{
+    const int64_t ten = (int64_t)10 << 48;
+    if (x > ten)
+        return Q48_ONE;
+    if (x < -ten)
+        return 0;
+    int64_t en = q48_safe_exp((int64_t)(0 - (uint64_t)x));
+    return q48_div(Q48_ONE, (int64_t)((uint64_t)Q48_ONE + (uint64_t)en));
+}
+
+// fp_silu, fp_math.h:919-921
+__device__ __forceinline__ int64_t q48_silu(int64_t x)
+{
+    return q48_mul(x, q48_sigmoid(x));
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level reductions (wave64)
+// ---------------------------------------------------------------------------
+
+// 128-bit two's-complement sum across the 64 lanes of a wave; every lane
+// returns the total.  Integer addition mod 2^128 is associative, so the
+// butterfly order gives the same bits as the reference's serial loop.
+__device__ __forceinline__ q48_u128 q48_wave_sum128(q48_u128 v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        uint64_t lo = (uint64_t)v, hi = (uint64_t)(v >> 64);
+        uint64_t olo = __shfl_xor(lo, off, 64);
+        uint64_t ohi = __shfl_xor(hi, off, 64);
+        v += ((q48_u128)ohi << 64) | olo;
+    }
+    return v;
+}
+
+__device__ __forceinline__ int64_t q48_wave_sum64(int64_t v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+        v = (int64_t)((uint64_t)v + (uint64_t)__shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ int64_t q48_wave_max64(int64_t v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        int64_t o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}

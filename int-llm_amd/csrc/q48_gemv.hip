@@ -1,0 +1,305 @@
+// q48_gemv.hip — exact Q16.48 GEMV / GEMM for gfx950 (VALU limb arithmetic).
+//
+// Contract (matmul_vec, llama_int.c:1014-1046):
+//     y[i] = (int64)( (sum_j (int128) W[i][j] * x[j]) >> 48 )
+// with W row-major [M][K].  Only bits [48, 112) of the two's-complement
+// sum reach y, so any summation order mod 2^128 is bit-exact.
+//
+// Limb scheme (offset binary).  Flip the sign bit of both operands:
+//     X' = x ^ 2^63 = x + 2^63,   W' = w ^ 2^63 = w + 2^63   (unsigned)
+//     x*w = X'W' - 2^63 (X' + W') + 2^126
+// X'W' is a product of unsigned 64-bit numbers, i.e. four unsigned 32x32
+// partials, each one v_mad_u64_u32 with a 64-bit accumulate.  Summed over
+// j, the 2^126 terms only touch bits 126-127, and 2^63 (X' + W') mod 2^112
+// only depends on (sum x + sum w) mod 2^49 — one 64-bit running sum per
+// lane, plus a per-row sum of x shared by every row.  Per MAC per lane:
+//     a0 += xl*wl  (carry count c0)     bits   0..  (64 + log2 K)
+//     a1 += xh*wl + xl*wh  (carry c1)   bits  32..
+//     a2 += xh*wh  (mod 2^64)           bits  64..127
+//     ws += w      (mod 2^64)
+// then S = a0 + 2^64 c0 + 2^32 a1 + 2^96 c1 + 2^64 a2 - 2^63 (ws + xs).
+//
+// GEMV layout: one wavefront per output row (64 lanes x 16 B = 1 KiB per
+// load instruction, fully coalesced), x staged once per block in LDS in
+// flipped form, rows-per-block waves sharing it; 128-bit cross-lane sum.
+#include "q48_internal.h"
+
+namespace {
+
+struct LimbAcc {
+    uint64_t a0, a1, a2, ws;
+    uint32_t c0, c1;
+};
+
+__device__ __forceinline__ void mac_flip(LimbAcc &A, uint32_t xl, uint32_t xh,
+                                         uint64_t w)
+{
+    const uint32_t wl = (uint32_t)w;
+    const uint32_t wh = (uint32_t)(w >> 32) ^ 0x80000000u;
+    uint64_t s;
+    s = (uint64_t)xl * wl + A.a0;
+    A.c0 += s < A.a0;
+    A.a0 = s;
+    s = (uint64_t)xh * wl + A.a1;
+    A.c1 += s < A.a1;
+    A.a1 = s;
+    s = (uint64_t)xl * wh + A.a1;
+    A.c1 += s < A.a1;
+    A.a1 = s;
+    A.a2 += (uint64_t)xh * wh;
+    A.ws += w;
+}
+
+__device__ __forceinline__ q48_u128 acc_value(const LimbAcc &A)
+{
+    q48_u128 S = (q48_u128)A.a0;
+    S += (q48_u128)A.c0 << 64;
+    S += (q48_u128)A.a1 << 32;
+    S += (q48_u128)A.c1 << 96;
+    S += (q48_u128)A.a2 << 64;
+    S -= (q48_u128)A.ws << 63;
+    return S;
+}
+
+constexpr int KCHUNK = 4096;   // x elements staged per pass (32 KiB LDS)
+
+// RPB waves per block, one row per wave.  VEC = 2: 16-byte loads (K even,
+// W 16-byte aligned); VEC = 1: 8-byte loads (any K).
+template <int RPB, int VEC>
+__global__ __launch_bounds__(64 * RPB) void k_gemv(int64_t *__restrict__ y,
+                                                   const int64_t *__restrict__ W,
+                                                   const int64_t *__restrict__ x,
+                                                   int M, int K)
+{
+    __shared__ __align__(16) uint64_t xs[KCHUNK];
+    __shared__ uint64_t xsum_w[RPB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int row = blockIdx.x * RPB + wave;
+    const bool active = row < M;
+    const int64_t *wr = W + (size_t)(active ? row : 0) * (size_t)K;
+
+    LimbAcc A = {0, 0, 0, 0, 0, 0};
+    uint64_t xsum = 0;
+
+    for (int k0 = 0; k0 < K; k0 += KCHUNK) {
+        const int kc = min(KCHUNK, K - k0);
+        __syncthreads();
+        for (int j = tid; j < kc; j += 64 * RPB) {
+            uint64_t v = (uint64_t)x[k0 + j];
+            xs[j] = v ^ 0x8000000000000000ull;
+            xsum += v;
+        }
+        __syncthreads();
+        if (active) {
+            if (VEC == 2) {
+                const ulonglong2 *w2 = reinterpret_cast<const ulonglong2 *>(wr + k0);
+                const uint4 *x4 = reinterpret_cast<const uint4 *>(xs);
+                const int np = kc >> 1;
+                int p = lane;
+                for (; p + 192 < np; p += 256) {
+                    ulonglong2 wa = w2[p], wb = w2[p + 64], wc = w2[p + 128], wd = w2[p + 192];
+                    uint4 xa = x4[p], xb = x4[p + 64], xc = x4[p + 128], xd = x4[p + 192];
+                    mac_flip(A, xa.x, xa.y, wa.x);
+                    mac_flip(A, xa.z, xa.w, wa.y);
+                    mac_flip(A, xb.x, xb.y, wb.x);
+                    mac_flip(A, xb.z, xb.w, wb.y);
+                    mac_flip(A, xc.x, xc.y, wc.x);
+                    mac_flip(A, xc.z, xc.w, wc.y);
+                    mac_flip(A, xd.x, xd.y, wd.x);
+                    mac_flip(A, xd.z, xd.w, wd.y);
+                }
+                for (; p < np; p += 64) {
+                    ulonglong2 wa = w2[p];
+                    uint4 xa = x4[p];
+                    mac_flip(A, xa.x, xa.y, wa.x);
+                    mac_flip(A, xa.z, xa.w, wa.y);
+                }
+            } else {
+                const uint2 *x2 = reinterpret_cast<const uint2 *>(xs);
+                for (int j = lane; j < kc; j += 64) {
+                    uint64_t wv = (uint64_t)wr[k0 + j];
+                    uint2 xa = x2[j];
+                    mac_flip(A, xa.x, xa.y, wv);
+                }
+            }
+        }
+    }
+
+    // sum of x over the whole row (shared by every row of the block)
+    xsum = (uint64_t)q48_wave_sum64((int64_t)xsum);
+    if (lane == 0)
+        xsum_w[wave] = xsum;
+    __syncthreads();
+    if (!active)
+        return;
+    uint64_t xtot = 0;
+#pragma unroll
+    for (int w = 0; w < RPB; ++w)
+        xtot += xsum_w[w];
+
+    q48_u128 S = q48_wave_sum128(acc_value(A));
+    S -= (q48_u128)xtot << 63;
+    if (lane == 0)
+        y[row] = (int64_t)((q48_i128)S >> 48);
+}
+
+// Per-row sums mod 2^64 (one wave per row): the 2^63 correction terms of
+// the flipped-limb GEMM.
+__global__ __launch_bounds__(256) void k_rowsum(uint64_t *__restrict__ out,
+                                               const int64_t *__restrict__ A,
+                                               int rows, int K)
+{
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows)
+        return;
+    const int64_t *r = A + (size_t)row * K;
+    uint64_t s = 0;
+    for (int j = lane; j < K; j += 64)
+        s += (uint64_t)r[j];
+    s = (uint64_t)q48_wave_sum64((int64_t)s);
+    if (lane == 0)
+        out[row] = s;
+}
+
+// GEMM Y[T][N] = X[T][K] . W[N][K]^T >> 48, per element exactly the GEMV.
+// Block 256 threads = 16 x 16, tile 64 tokens x 64 rows, 4x4 outputs per
+// thread, K staged 16 at a time in LDS in flipped form (zero padding
+// flips to 2^63 and contributes 2^126 per product: bits >= 126 only).
+constexpr int GT = 64, GN = 64, GK = 16;
+
+__global__ __launch_bounds__(256) void k_gemm(int64_t *__restrict__ Y,
+                                             const int64_t *__restrict__ W,
+                                             const int64_t *__restrict__ X,
+                                             const uint64_t *__restrict__ wsum,
+                                             const uint64_t *__restrict__ xsum,
+                                             int T, int N, int K)
+{
+    __shared__ __align__(16) uint64_t Xs[GK][GT];
+    __shared__ __align__(16) uint64_t Ws[GK][GN];
+
+    const int tid = threadIdx.x;
+    const int tx = tid & 15;       // row group
+    const int ty = tid >> 4;       // token group
+    const int t0 = blockIdx.y * GT;
+    const int n0 = blockIdx.x * GN;
+
+    uint64_t a0[4][4], a1[4][4], a2[4][4];
+    uint32_t c0[4][4], c1[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            a0[i][j] = a1[i][j] = a2[i][j] = 0;
+            c0[i][j] = c1[i][j] = 0;
+        }
+
+    for (int k0 = 0; k0 < K; k0 += GK) {
+        __syncthreads();
+        // stage 64 x 16 of X and of W: 1024 elements each, 4 per thread
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            int idx = tid + 256 * e;
+            int r = idx >> 4, k = idx & 15;
+            int kk = k0 + k;
+            uint64_t xv = 0, wv = 0;
+            if (t0 + r < T && kk < K)
+                xv = (uint64_t)X[(size_t)(t0 + r) * K + kk];
+            if (n0 + r < N && kk < K)
+                wv = (uint64_t)W[(size_t)(n0 + r) * K + kk];
+            Xs[k][r] = xv ^ 0x8000000000000000ull;
+            Ws[k][r] = wv ^ 0x8000000000000000ull;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int k = 0; k < GK; ++k) {
+            uint32_t xl[4], xh[4], wl[4], wh[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint64_t xv = Xs[k][ty * 4 + i];
+                uint64_t wv = Ws[k][tx * 4 + i];
+                xl[i] = (uint32_t)xv;
+                xh[i] = (uint32_t)(xv >> 32);
+                wl[i] = (uint32_t)wv;
+                wh[i] = (uint32_t)(wv >> 32);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint64_t s;
+                    s = (uint64_t)xl[i] * wl[j] + a0[i][j];
+                    c0[i][j] += s < a0[i][j];
+                    a0[i][j] = s;
+                    s = (uint64_t)xh[i] * wl[j] + a1[i][j];
+                    c1[i][j] += s < a1[i][j];
+                    a1[i][j] = s;
+                    s = (uint64_t)xl[i] * wh[j] + a1[i][j];
+                    c1[i][j] += s < a1[i][j];
+                    a1[i][j] = s;
+                    a2[i][j] += (uint64_t)xh[i] * wh[j];
+                }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int t = t0 + ty * 4 + i;
+        if (t >= T)
+            continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int n = n0 + tx * 4 + j;
+            if (n >= N)
+                continue;
+            q48_u128 S = (q48_u128)a0[i][j];
+            S += (q48_u128)c0[i][j] << 64;
+            S += (q48_u128)a1[i][j] << 32;
+            S += (q48_u128)c1[i][j] << 96;
+            S += (q48_u128)a2[i][j] << 64;
+            S -= (q48_u128)(xsum[t] + wsum[n]) << 63;
+            Y[(size_t)t * N + n] = (int64_t)((q48_i128)S >> 48);
+        }
+    }
+}
+
+} // namespace
+
+int q48_launch_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                    int M, int K)
+{
+    const bool vec = (K % 2 == 0) && (((uintptr_t)W & 15) == 0);
+    if (M >= 1024) {
+        dim3 grid((M + 7) / 8);
+        if (vec)
+            hipLaunchKernelGGL((k_gemv<8, 2>), grid, dim3(512), 0, c->stream, y, W, x, M, K);
+        else
+            hipLaunchKernelGGL((k_gemv<8, 1>), grid, dim3(512), 0, c->stream, y, W, x, M, K);
+    } else {
+        dim3 grid((M + 3) / 4);
+        if (vec)
+            hipLaunchKernelGGL((k_gemv<4, 2>), grid, dim3(256), 0, c->stream, y, W, x, M, K);
+        else
+            hipLaunchKernelGGL((k_gemv<4, 1>), grid, dim3(256), 0, c->stream, y, W, x, M, K);
+    }
+    return (int)hipGetLastError();
+}
+
+int q48_launch_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X,
+                    int T, int N, int K)
+{
+    size_t need = ((size_t)T + (size_t)N) * sizeof(uint64_t);
+    int rc = q48_ws_reserve(c, need);
+    if (rc)
+        return rc;
+    uint64_t *wsum = (uint64_t *)c->ws;
+    uint64_t *xsum = wsum + N;
+    hipLaunchKernelGGL(k_rowsum, dim3((N + 3) / 4), dim3(256), 0, c->stream, wsum, W, N, K);
+    hipLaunchKernelGGL(k_rowsum, dim3((T + 3) / 4), dim3(256), 0, c->stream, xsum, X, T, K);
+    dim3 grid((N + GN - 1) / GN, (T + GT - 1) / GT);
+    hipLaunchKernelGGL(k_gemm, grid, dim3(256), 0, c->stream, Y, W, X, wsum, xsum, T, N, K);
+    return (int)hipGetLastError();
+}

@@ -1,0 +1,53 @@
+// q48_internal.h — context and kernel launchers shared by the HIP sources
+// of libintllm_hip (not installed; the public ABI is include/intllm_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "q48_device.hpp"
+
+struct q48_ctx {
+    int device;
+    hipStream_t stream;
+    q48_consts *consts;          // device: fp_math_init constants
+    int64_t *rope_cos, *rope_sin; // device: [max_seq][head_dim/2]
+    int rope_head_dim, rope_max_seq, rope_theta;
+    void *ws;                    // device workspace (scores, row sums, partials)
+    size_t ws_bytes;
+    int *d_scalar;               // device: small int outputs (argmax)
+    // GEMV launch timing (q48_prof_*): event pairs in use, then a free pool
+    int prof_on;
+    struct ProfRec { hipEvent_t a, b; double bytes; };
+    ProfRec *prof;
+    int prof_n, prof_cap;
+};
+
+// Grow the context workspace to at least `bytes` (stream-synchronising).
+int q48_ws_reserve(q48_ctx *c, size_t bytes);
+
+// ---- launchers (return hipError_t as int; shapes already validated) ----
+int q48_launch_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                    int M, int K);
+int q48_launch_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X,
+                    int T, int N, int K);
+int q48_launch_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *x,
+                       const int64_t *w, int dim);
+int q48_launch_rope_init(q48_ctx *c);
+int q48_launch_rope(q48_ctx *c, int64_t *vec, int n_heads, int head_dim,
+                    const int *d_pos, int pos);
+int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
+                    int64_t *kcache, int64_t *vcache, const int64_t *k_new,
+                    const int64_t *v_new, int layer, const int *d_pos, int pos,
+                    int n_heads, int n_kv, int head_dim, int max_seq);
+int q48_launch_silu_mul(q48_ctx *c, int64_t *out, const int64_t *g,
+                        const int64_t *u, int n);
+int q48_launch_add(q48_ctx *c, int64_t *acc, const int64_t *d, int n);
+int q48_launch_embed(q48_ctx *c, int64_t *out, const int64_t *table,
+                     const int *d_token, int token, int dim);
+int q48_launch_argmax(q48_ctx *c, int *d_out, const int64_t *v, int n);
+int q48_launch_zero(q48_ctx *c, void *p, size_t bytes);
+int q48_launch_math_init(q48_ctx *c);
+int q48_launch_fp_eval(q48_ctx *c, int func, const int64_t *x,
+                       const int64_t *y, int64_t *out0, int64_t *out1, int n);

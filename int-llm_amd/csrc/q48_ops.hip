@@ -1,0 +1,442 @@
+// q48_ops.hip — the non-GEMV ops of the Q16.48 layer on gfx950:
+// RMSNorm, RoPE (tables + rotation), exact GQA decode attention with its
+// fixed-point softmax, SwiGLU, residual add, embedding row, argmax, the
+// fp_math constant init and an element-wise fp_math evaluator.
+//
+// Every output is bit-identical to llama_int.c (cited per kernel): all
+// arithmetic is integer, and every reduction is an integer sum (mod 2^64
+// or 2^128) or a max, so the parallel order cannot change a bit.
+#include "q48_internal.h"
+
+namespace {
+
+// Sum an int64 (wrapping) across a block of NT threads; every thread gets it.
+template <int NT>
+__device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t *red)
+{
+    v = q48_wave_sum64(v);
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0)
+        red[w] = v;
+    __syncthreads();
+    uint64_t t = 0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i)
+        t += (uint64_t)red[i];
+    return (int64_t)t;
+}
+
+template <int NT>
+__device__ __forceinline__ int64_t block_max64(int64_t v, int64_t *red)
+{
+    v = q48_wave_max64(v);
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0)
+        red[w] = v;
+    __syncthreads();
+    int64_t t = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i)
+        t = red[i] > t ? red[i] : t;
+    return t;
+}
+
+// ---------------------------------------------------------------------------
+// fp_math_init on the device (fp_math.h:833-858)
+// ---------------------------------------------------------------------------
+__global__ void k_math_init(q48_consts *k)
+{
+    if (threadIdx.x == 0 && blockIdx.x == 0)
+        q48_math_init(k);
+}
+
+// ---------------------------------------------------------------------------
+// rmsnorm, llama_int.c:1048-1058.  One block of 256 threads.
+//   ss = sum (int128) x^2;  ms = (int64)((ss >> 48) / dim) + 2814749767
+//   r = fp_inv_sqrt(ms);    out[i] = fp_mul(fp_mul(x[i], r), w[i])
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rmsnorm(int64_t *__restrict__ out,
+                                                const int64_t *__restrict__ x,
+                                                const int64_t *__restrict__ w,
+                                                int dim)
+{
+    __shared__ uint64_t red_lo[4], red_hi[4];
+    __shared__ int64_t r_sh;
+    const int tid = threadIdx.x;
+    q48_u128 ss = 0;
+    for (int i = tid; i < dim; i += 256) {
+        int64_t v = x[i];
+        ss += (q48_u128)((q48_i128)v * v);
+    }
+    ss = q48_wave_sum128(ss);
+    if ((tid & 63) == 0) {
+        red_lo[tid >> 6] = (uint64_t)ss;
+        red_hi[tid >> 6] = (uint64_t)(ss >> 64);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        q48_u128 t = 0;
+        for (int i = 0; i < 4; ++i)
+            t += ((q48_u128)red_hi[i] << 64) | red_lo[i];
+        int64_t ms = (int64_t)q48_divs_128_64((q48_i128)t >> 48, (int64_t)dim);
+        ms = (int64_t)((uint64_t)ms + 2814749767ull);
+        r_sh = q48_inv_sqrt(ms);
+    }
+    __syncthreads();
+    const int64_t r = r_sh;
+    for (int i = tid; i < dim; i += 256)
+        out[i] = q48_mul(q48_mul(x[i], r), w[i]);
+}
+
+// ---------------------------------------------------------------------------
+// rope_init, llama_int.c:960-986.  One thread per (pos, i < half).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rope_init(int64_t *__restrict__ cos_t,
+                                                  int64_t *__restrict__ sin_t,
+                                                  const q48_consts *__restrict__ k,
+                                                  int head_dim, int max_seq, int theta)
+{
+    const int half = head_dim / 2;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)half * max_seq)
+        return;
+    const int pos = (int)(idx / half), i = (int)(idx % half);
+    const int64_t lt = q48_log(q48_from_int(theta));
+    const int64_t nf = (int64_t)(0 - (uint64_t)q48_div(q48_from_int(2 * i), q48_from_int(head_dim)));
+    const int64_t th = q48_exp(q48_mul(nf, lt));
+    int64_t c, s;
+    q48_sincos(k, q48_mul(q48_from_int(pos), th), &c, &s);
+    cos_t[idx] = c;
+    sin_t[idx] = s;
+}
+
+// ---------------------------------------------------------------------------
+// rope_apply, llama_int.c:997-1008, over n_heads heads of one vector.
+// pos comes from device memory when d_pos != nullptr (graph replay).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rope(int64_t *__restrict__ vec,
+                                             const int64_t *__restrict__ cos_t,
+                                             const int64_t *__restrict__ sin_t,
+                                             int n_heads, int head_dim,
+                                             const int *__restrict__ d_pos, int pos)
+{
+    const int half = head_dim / 2;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_heads * half)
+        return;
+    if (d_pos)
+        pos = *d_pos;
+    const int h = idx / half, i = idx % half;
+    int64_t *v = vec + (size_t)h * head_dim;
+    const int64_t c = cos_t[(size_t)pos * half + i];
+    const int64_t s = sin_t[(size_t)pos * half + i];
+    const int64_t x0 = v[i], x1 = v[i + half];
+    v[i] = (int64_t)((uint64_t)q48_mul(x0, c) - (uint64_t)q48_mul(x1, s));
+    v[i + half] = (int64_t)((uint64_t)q48_mul(x1, c) + (uint64_t)q48_mul(x0, s));
+}
+
+// ---------------------------------------------------------------------------
+// Exact GQA decode attention: KV store (llama_int.c:1414-1416), scale
+// (:1433) and the exact branch (:1502-1529) with softmax (:1060-1072).
+// One block (256 threads) per query head; sc = per-head score row in the
+// workspace.  Position pos reads k_new / v_new directly, so the cache write
+// done by the first head of each KV group cannot race with the reads.
+// ---------------------------------------------------------------------------
+constexpr int ATT_NT = 256;
+
+__global__ __launch_bounds__(ATT_NT) void k_attn_decode(
+    int64_t *__restrict__ out, const int64_t *__restrict__ q,
+    int64_t *__restrict__ kcache, int64_t *__restrict__ vcache,
+    const int64_t *__restrict__ k_new, const int64_t *__restrict__ v_new,
+    int64_t *__restrict__ scores, int layer, const int *__restrict__ d_pos, int pos,
+    int n_heads, int n_kv, int hd, int max_seq)
+{
+    __shared__ int64_t qs[256];
+    __shared__ int64_t red[ATT_NT / 64];
+    __shared__ int64_t part[ATT_NT];
+    if (d_pos)
+        pos = *d_pos;
+    const int h = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int group = n_heads / n_kv;
+    const int kh = h / group;
+    const size_t kvd = (size_t)n_kv * hd;
+    const size_t base = (size_t)layer * max_seq;
+    const int64_t *kn = k_new + (size_t)kh * hd;
+    const int64_t *vn = v_new + (size_t)kh * hd;
+
+    if (h % group == 0)
+        for (int d = tid; d < hd; d += ATT_NT) {
+            kcache[(base + pos) * kvd + (size_t)kh * hd + d] = kn[d];
+            vcache[(base + pos) * kvd + (size_t)kh * hd + d] = vn[d];
+        }
+    for (int d = tid; d < hd; d += ATT_NT)
+        qs[d] = q[(size_t)h * hd + d];
+    __syncthreads();
+
+    const int64_t scale = q48_inv_sqrt(q48_from_int(hd));
+    const int S = pos + 1;
+    int64_t *sc = scores + (size_t)h * max_seq;
+
+    // scores s_t = fp_mul((int64)(q . k_t >> 48), scale)
+    int64_t mx = INT64_MIN;
+    for (int t = tid; t < S; t += ATT_NT) {
+        const int64_t *kt = t == pos ? kn : kcache + (base + t) * kvd + (size_t)kh * hd;
+        q48_u128 dot = 0;
+        for (int d = 0; d < hd; ++d)
+            dot += (q48_u128)((q48_i128)qs[d] * kt[d]);
+        const int64_t s = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
+        sc[t] = s;
+        mx = s > mx ? s : mx;
+    }
+    mx = block_max64<ATT_NT>(mx, red);
+
+    // e_t = fp_safe_exp(s_t - max); sum (int64, wrapping)
+    int64_t sum = 0;
+    for (int t = tid; t < S; t += ATT_NT) {
+        const int64_t e = q48_safe_exp((int64_t)((uint64_t)sc[t] - (uint64_t)mx));
+        sc[t] = e;
+        sum = (int64_t)((uint64_t)sum + (uint64_t)e);
+    }
+    sum = block_sum64<ATT_NT>(sum, red);
+    if (sum > 0)
+        for (int t = tid; t < S; t += ATT_NT)
+            sc[t] = q48_div(sc[t], sum);
+    __syncthreads();
+
+    // o[d] = sum_t fp_mul(p_t, v_t[d])  (int64, wrapping)
+    const int slices = ATT_NT / hd;   // hd divides ATT_NT (checked on host)
+    const int d = tid % hd, sl = tid / hd;
+    int64_t acc = 0;
+    for (int t = sl; t < S; t += slices) {
+        const int64_t *vt = t == pos ? vn : vcache + (base + t) * kvd + (size_t)kh * hd;
+        acc = (int64_t)((uint64_t)acc + (uint64_t)q48_mul(sc[t], vt[d]));
+    }
+    part[tid] = acc;
+    __syncthreads();
+    if (sl == 0) {
+        uint64_t o = 0;
+        for (int s2 = 0; s2 < slices; ++s2)
+            o += (uint64_t)part[s2 * hd + d];
+        out[(size_t)h * hd + d] = (int64_t)o;
+    }
+}
+
+// SwiGLU, llama_int.c:1549-1552: out = fp_mul(fp_silu(g), u)
+__global__ __launch_bounds__(256) void k_silu_mul(int64_t *__restrict__ out,
+                                                 const int64_t *__restrict__ g,
+                                                 const int64_t *__restrict__ u, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        out[i] = q48_mul(q48_silu(g[i]), u[i]);
+}
+
+// Residual add, llama_int.c:1535 and :1556 (int64, wrapping)
+__global__ __launch_bounds__(256) void k_add(int64_t *__restrict__ acc,
+                                            const int64_t *__restrict__ d, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        acc[i] = (int64_t)((uint64_t)acc[i] + (uint64_t)d[i]);
+}
+
+// hidden = embed_tokens[token] (llama_int.c:2822-2824)
+__global__ __launch_bounds__(256) void k_embed(int64_t *__restrict__ out,
+                                              const int64_t *__restrict__ table,
+                                              const int *__restrict__ d_token,
+                                              int token, int dim)
+{
+    if (d_token)
+        token = *d_token;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < dim)
+        out[i] = table[(size_t)token * dim + i];
+}
+
+// argmax, llama_int.c:2888-2893: first index of the maximum.
+__global__ __launch_bounds__(1024) void k_argmax(int *__restrict__ out,
+                                                const int64_t *__restrict__ v, int n)
+{
+    __shared__ int64_t bv[16];
+    __shared__ int bi[16];
+    const int tid = threadIdx.x;
+    int64_t best = INT64_MIN;
+    int idx = n;   // sentinel larger than any index
+    for (int i = tid; i < n; i += 1024) {
+        const int64_t x = v[i];
+        if (x > best) {   // strided ascending scan: keeps the first max
+            best = x;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const int64_t ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        bv[tid >> 6] = best;
+        bi[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
+                best = bv[w];
+                idx = bi[w];
+            }
+        *out = idx < n ? idx : 0;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_zero(uint64_t *__restrict__ p, size_t n8)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+__global__ void k_zero_bytes(uint8_t *__restrict__ p, size_t n)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        p[i] = 0;
+}
+
+// Element-wise fp_math evaluation (determinism gate and unit parity).
+__global__ __launch_bounds__(256) void k_fp_eval(int func, const int64_t *__restrict__ x,
+                                                const int64_t *__restrict__ y,
+                                                int64_t *__restrict__ o0,
+                                                int64_t *__restrict__ o1,
+                                                const q48_consts *__restrict__ k, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    const int64_t a = x[i];
+    int64_t r = 0, r1 = 0;
+    switch (func) {
+    case 0: r = q48_mul(a, y[i]); break;
+    case 1: r = y[i] != 0 ? q48_div(a, y[i]) : 0; break;
+    case 2: r = q48_sqrt(a); break;
+    case 3: r = q48_sqrt_fast(a); break;
+    case 4: r = q48_inv_sqrt(a); break;
+    case 5: r = q48_exp(a); break;
+    case 6: r = q48_log(a); break;
+    case 7: q48_sincos(k, a, &r, &r1); break;
+    case 8: r = q48_sigmoid(a); break;
+    case 9: r = q48_silu(a); break;
+    case 10: r = q48_safe_exp(a); break;
+    case 11: r = q48_exp_dyadic(a, (int)y[i]); break;
+    default: break;
+    }
+    o0[i] = r;
+    if (o1)
+        o1[i] = r1;
+}
+
+} // namespace
+
+int q48_launch_math_init(q48_ctx *c)
+{
+    hipLaunchKernelGGL(k_math_init, dim3(1), dim3(64), 0, c->stream, c->consts);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *x,
+                       const int64_t *w, int dim)
+{
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(256), 0, c->stream, out, x, w, dim);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_rope_init(q48_ctx *c)
+{
+    const long n = (long)(c->rope_head_dim / 2) * c->rope_max_seq;
+    hipLaunchKernelGGL(k_rope_init, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       c->stream, c->rope_cos, c->rope_sin, c->consts,
+                       c->rope_head_dim, c->rope_max_seq, c->rope_theta);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_rope(q48_ctx *c, int64_t *vec, int n_heads, int head_dim,
+                    const int *d_pos, int pos)
+{
+    const int n = n_heads * (head_dim / 2);
+    hipLaunchKernelGGL(k_rope, dim3((n + 255) / 256), dim3(256), 0, c->stream, vec,
+                       c->rope_cos, c->rope_sin, n_heads, head_dim, d_pos, pos);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
+                    int64_t *kcache, int64_t *vcache, const int64_t *k_new,
+                    const int64_t *v_new, int layer, const int *d_pos, int pos,
+                    int n_heads, int n_kv, int head_dim, int max_seq)
+{
+    int rc = q48_ws_reserve(c, (size_t)n_heads * max_seq * sizeof(int64_t));
+    if (rc)
+        return rc;
+    hipLaunchKernelGGL(k_attn_decode, dim3(n_heads), dim3(ATT_NT), 0, c->stream, out, q,
+                       kcache, vcache, k_new, v_new, (int64_t *)c->ws, layer, d_pos,
+                       pos, n_heads, n_kv, head_dim, max_seq);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_silu_mul(q48_ctx *c, int64_t *out, const int64_t *g,
+                        const int64_t *u, int n)
+{
+    hipLaunchKernelGGL(k_silu_mul, dim3((n + 255) / 256), dim3(256), 0, c->stream, out, g, u, n);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_add(q48_ctx *c, int64_t *acc, const int64_t *d, int n)
+{
+    hipLaunchKernelGGL(k_add, dim3((n + 255) / 256), dim3(256), 0, c->stream, acc, d, n);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_embed(q48_ctx *c, int64_t *out, const int64_t *table,
+                     const int *d_token, int token, int dim)
+{
+    hipLaunchKernelGGL(k_embed, dim3((dim + 255) / 256), dim3(256), 0, c->stream, out,
+                       table, d_token, token, dim);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_argmax(q48_ctx *c, int *d_out, const int64_t *v, int n)
+{
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, c->stream, d_out, v, n);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_zero(q48_ctx *c, void *p, size_t bytes)
+{
+    const size_t n8 = bytes / 8;
+    if (n8) {
+        size_t blocks = (n8 + 255) / 256;
+        if (blocks > 65536)
+            blocks = 65536;
+        hipLaunchKernelGGL(k_zero, dim3((unsigned)blocks), dim3(256), 0, c->stream,
+                           (uint64_t *)p, n8);
+    }
+    const size_t tail = bytes - n8 * 8;
+    if (tail)
+        hipLaunchKernelGGL(k_zero_bytes, dim3(1), dim3(64), 0, c->stream,
+                           (uint8_t *)p + n8 * 8, tail);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_fp_eval(q48_ctx *c, int func, const int64_t *x,
+                       const int64_t *y, int64_t *out0, int64_t *out1, int n)
+{
+    hipLaunchKernelGGL(k_fp_eval, dim3((n + 255) / 256), dim3(256), 0, c->stream, func, x, y,
+                       out0, out1, c->consts, n);
+    return (int)hipGetLastError();
+}

@@ -1,0 +1,717 @@
+/*
+ * q48_host.c — C host of the Q16.48 forward pass over libintllm_hip.
+ *
+ * Device memory layout (one weight slab, one activation slab):
+ *   weights   embed [vocab][dim] | final_norm [dim] | lm_head [vocab][dim]
+ *             then per layer: attn_norm | ffn_norm | Wqkv | Wo | Wgu | Wd
+ *             where Wqkv = q_proj;k_proj;v_proj stacked ([dim+2kvd][dim])
+ *             and Wgu = gate_proj;up_proj stacked ([2 ffn][dim]), so one
+ *             GEMV produces q|k|v and one produces gate|up.  Stacking rows
+ *             does not change any row's dot product, so the bits are the
+ *             reference's (matmul_vec is row-independent).
+ *   KV cache  [L][max_seq][n_kv][hd] int64, keys and values separately
+ *             (kv_cache_t, llama_int.c:1078-1095).
+ * Every region starts on a 256-byte boundary (16-byte vector loads).
+ */
+#include "q48_host.h"
+#include "q48_synth.h"
+
+#include <fcntl.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <time.h>
+#include <unistd.h>
+
+#define LLAMA_EOS 2
+#define FNV_OFF 1469598103934665603ULL
+
+#define ALIGN_ELEMS 32   /* 256 bytes */
+
+static size_t align_up(size_t n) { return (n + ALIGN_ELEMS - 1) / ALIGN_ELEMS * ALIGN_ELEMS; }
+
+struct q48h_model {
+    q48h_config c;
+    q48_ctx *ctx;
+    int tied;
+    int64_t *w;                 /* device weight slab */
+    size_t off_embed, off_norm, off_lm, off_layers, layer_elems;
+    size_t lo_an, lo_fn, lo_qkv, lo_wo, lo_gu, lo_wd;
+    int64_t *kc, *vc;           /* device KV cache */
+    int64_t *act;               /* device activations */
+    int64_t *hidden, *normed, *qkv, *attn, *o, *gu, *h_ffn, *mlp, *logits;
+};
+
+/* ---------------------------------------------------------------------- */
+/* config.json (load_config_json, llama_int.c:819-903)                     */
+/* ---------------------------------------------------------------------- */
+
+static int json_int(const char *json, const char *key, int dflt)
+{
+    char pat[256];
+    snprintf(pat, sizeof pat, "\"%s\"", key);
+    const char *p = strstr(json, pat);
+    if (!p)
+        return dflt;
+    p += strlen(pat);
+    while (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r' || *p == ':')
+        p++;
+    if (*p == 'n')
+        return dflt;   /* null */
+    return (int)strtol(p, NULL, 10);
+}
+
+int q48h_config_from_json_text(const char *json, q48h_config *c)
+{
+    if (!json || !c)
+        return -2;
+    c->dim = json_int(json, "hidden_size", -1);
+    c->n_heads = json_int(json, "num_attention_heads", -1);
+    c->n_kv_heads = json_int(json, "num_key_value_heads", c->n_heads);
+    c->n_layers = json_int(json, "num_hidden_layers", -1);
+    c->ffn = json_int(json, "intermediate_size", -1);
+    c->vocab = json_int(json, "vocab_size", -1);
+    c->max_seq = json_int(json, "max_position_embeddings", 2048);
+    c->rope_theta = json_int(json, "rope_theta", 10000);
+    if (c->dim <= 0 || c->n_heads <= 0 || c->n_layers <= 0 || c->ffn <= 0 || c->vocab <= 0)
+        return -2;
+    if (c->dim % c->n_heads != 0)
+        return -2;
+    c->head_dim = c->dim / c->n_heads;
+    if (c->n_kv_heads <= 0 || c->n_heads % c->n_kv_heads != 0)
+        return -2;
+    return 0;
+}
+
+int q48h_config_from_json(const char *model_dir, q48h_config *c)
+{
+    char path[512];
+    snprintf(path, sizeof path, "%s/config.json", model_dir);
+    FILE *f = fopen(path, "r");
+    if (!f)
+        return -1;
+    fseek(f, 0, SEEK_END);
+    long len = ftell(f);
+    if (len <= 0 || len > 1024 * 1024) {
+        fclose(f);
+        return -1;
+    }
+    fseek(f, 0, SEEK_SET);
+    char *buf = (char *)malloc((size_t)len + 1);
+    if (!buf) {
+        fclose(f);
+        return -1;
+    }
+    size_t n = fread(buf, 1, (size_t)len, f);
+    fclose(f);
+    buf[n] = 0;
+    int rc = q48h_config_from_json_text(buf, c);
+    free(buf);
+    return rc;
+}
+
+int q48h_config_check(const q48h_config *c)
+{
+    if (!c || c->dim <= 0 || c->n_heads <= 0 || c->n_kv_heads <= 0 || c->n_layers <= 0 ||
+        c->ffn <= 0 || c->vocab <= 0 || c->max_seq <= 0 || c->rope_theta <= 0)
+        return Q48_EINVAL;
+    if (c->n_heads % c->n_kv_heads || c->head_dim * c->n_heads != c->dim)
+        return Q48_EINVAL;
+    if (c->head_dim % 2 || c->head_dim > 256 || 256 % c->head_dim)
+        return Q48_EINVAL;
+    if (c->max_seq > 32767 || c->rope_theta > 32767)
+        return Q48_EINVAL;
+    return Q48_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* model                                                                   */
+/* ---------------------------------------------------------------------- */
+
+static void layout(q48h_model *m)
+{
+    const q48h_config *c = &m->c;
+    size_t dim = (size_t)c->dim, kvd = (size_t)c->n_kv_heads * c->head_dim, ffn = (size_t)c->ffn;
+    size_t o = 0;
+    m->off_embed = o;
+    o += align_up((size_t)c->vocab * dim);
+    m->off_norm = o;
+    o += align_up(dim);
+    m->off_lm = m->tied ? m->off_embed : o;
+    if (!m->tied)
+        o += align_up((size_t)c->vocab * dim);
+    m->off_layers = o;
+    size_t l = 0;
+    m->lo_an = l; l += align_up(dim);
+    m->lo_fn = l; l += align_up(dim);
+    m->lo_qkv = l; l += align_up((dim + 2 * kvd) * dim);
+    m->lo_wo = l; l += align_up(dim * dim);
+    m->lo_gu = l; l += align_up(2 * ffn * dim);
+    m->lo_wd = l; l += align_up(dim * ffn);
+    m->layer_elems = l;
+}
+
+static size_t weight_elems(const q48h_model *m)
+{
+    return m->off_layers + (size_t)m->c.n_layers * m->layer_elems;
+}
+
+static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, int tied)
+{
+    int rc = q48h_config_check(cfg);
+    if (rc)
+        return rc;
+    q48h_model *m = (q48h_model *)calloc(1, sizeof *m);
+    if (!m)
+        return Q48_ENOMEM;
+    m->c = *cfg;
+    m->ctx = ctx;
+    m->tied = tied;
+    layout(m);
+    const q48h_config *c = &m->c;
+    size_t dim = (size_t)c->dim, kvd = (size_t)c->n_kv_heads * c->head_dim, ffn = (size_t)c->ffn;
+    size_t kvn = (size_t)c->n_layers * c->max_seq * kvd;
+    size_t an = 0;
+    size_t a_hidden = an; an += align_up(dim);
+    size_t a_normed = an; an += align_up(dim);
+    size_t a_qkv = an; an += align_up(dim + 2 * kvd);
+    size_t a_attn = an; an += align_up(dim);
+    size_t a_o = an; an += align_up(dim);
+    size_t a_gu = an; an += align_up(2 * ffn);
+    size_t a_ffn = an; an += align_up(ffn);
+    size_t a_mlp = an; an += align_up(dim);
+    size_t a_log = an; an += align_up((size_t)c->vocab);
+
+    if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
+        (rc = q48_malloc(ctx, (void **)&m->kc, kvn * 8)) ||
+        (rc = q48_malloc(ctx, (void **)&m->vc, kvn * 8)) ||
+        (rc = q48_malloc(ctx, (void **)&m->act, an * 8))) {
+        q48h_model_free(m);
+        return rc;
+    }
+    m->hidden = m->act + a_hidden;
+    m->normed = m->act + a_normed;
+    m->qkv = m->act + a_qkv;
+    m->attn = m->act + a_attn;
+    m->o = m->act + a_o;
+    m->gu = m->act + a_gu;
+    m->h_ffn = m->act + a_ffn;
+    m->mlp = m->act + a_mlp;
+    m->logits = m->act + a_log;
+    if ((rc = q48_zero(ctx, m->w, weight_elems(m) * 8)) ||
+        (rc = q48_zero(ctx, m->kc, kvn * 8)) || (rc = q48_zero(ctx, m->vc, kvn * 8)) ||
+        (rc = q48_zero(ctx, m->act, an * 8)) ||
+        (rc = q48_rope_init(ctx, c->head_dim, c->max_seq, c->rope_theta)) ||
+        (rc = q48_sync(ctx))) {
+        q48h_model_free(m);
+        return rc;
+    }
+    *out = m;
+    return Q48_OK;
+}
+
+int q48h_model_create(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg)
+{
+    if (!out || !ctx || !cfg)
+        return Q48_EINVAL;
+    *out = NULL;
+    return model_alloc(out, ctx, cfg, 0);
+}
+
+void q48h_model_free(q48h_model *m)
+{
+    if (!m)
+        return;
+    q48_free(m->ctx, m->w);
+    q48_free(m->ctx, m->kc);
+    q48_free(m->ctx, m->vc);
+    q48_free(m->ctx, m->act);
+    free(m);
+}
+
+const q48h_config *q48h_model_config(const q48h_model *m) { return &m->c; }
+q48_ctx *q48h_model_ctx(q48h_model *m) { return m->ctx; }
+int64_t *q48h_kv_keys(q48h_model *m) { return m->kc; }
+int64_t *q48h_kv_values(q48h_model *m) { return m->vc; }
+
+/* Device address and element count of the tensor `name`. */
+static int tensor_slot(q48h_model *m, const char *name, int64_t **dst, int64_t *n)
+{
+    const q48h_config *c = &m->c;
+    int64_t dim = c->dim, kvd = (int64_t)c->n_kv_heads * c->head_dim, ffn = c->ffn;
+    if (!strcmp(name, "model.embed_tokens.weight")) {
+        *dst = m->w + m->off_embed;
+        *n = (int64_t)c->vocab * dim;
+        return 0;
+    }
+    if (!strcmp(name, "model.norm.weight")) {
+        *dst = m->w + m->off_norm;
+        *n = dim;
+        return 0;
+    }
+    if (!strcmp(name, "lm_head.weight")) {
+        if (m->tied)
+            return -1;
+        *dst = m->w + m->off_lm;
+        *n = (int64_t)c->vocab * dim;
+        return 0;
+    }
+    int l = -1;
+    char rest[128];
+    if (sscanf(name, "model.layers.%d.%127s", &l, rest) != 2 || l < 0 || l >= c->n_layers)
+        return -1;
+    int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
+    struct { const char *s; size_t off; int64_t n; } t[] = {
+        {"input_layernorm.weight", m->lo_an, dim},
+        {"post_attention_layernorm.weight", m->lo_fn, dim},
+        {"self_attn.q_proj.weight", m->lo_qkv, dim * dim},
+        {"self_attn.k_proj.weight", m->lo_qkv + (size_t)(dim * dim), kvd * dim},
+        {"self_attn.v_proj.weight", m->lo_qkv + (size_t)(dim * dim + kvd * dim), kvd * dim},
+        {"self_attn.o_proj.weight", m->lo_wo, dim * dim},
+        {"mlp.gate_proj.weight", m->lo_gu, ffn * dim},
+        {"mlp.up_proj.weight", m->lo_gu + (size_t)(ffn * dim), ffn * dim},
+        {"mlp.down_proj.weight", m->lo_wd, dim * ffn},
+    };
+    for (size_t i = 0; i < sizeof t / sizeof t[0]; ++i)
+        if (!strcmp(rest, t[i].s)) {
+            *dst = b + t[i].off;
+            *n = t[i].n;
+            return 0;
+        }
+    return -1;
+}
+
+int q48h_upload(q48h_model *m, const char *name, const int64_t *host, int64_t n)
+{
+    if (!m || !name || !host)
+        return Q48_EINVAL;
+    int64_t *dst;
+    int64_t want;
+    if (tensor_slot(m, name, &dst, &want) || n != want)
+        return Q48_EINVAL;
+    return q48_memcpy_h2d(m->ctx, dst, host, (size_t)n * 8);
+}
+
+/* Names and shapes of every tensor, in mgw_export's order
+ * (llama_int.c:1736-1760). */
+typedef struct {
+    char name[64];
+    int ndims;
+    int64_t rows, cols;
+} tdesc;
+
+static int tensor_list(const q48h_config *c, int tied, tdesc *t)
+{
+    int n = 0, kvd = c->n_kv_heads * c->head_dim;
+#define ADD(nm, nd, r, k) do { snprintf(t[n].name, 64, "%s", nm); t[n].ndims = nd; \
+        t[n].rows = r; t[n].cols = k; n++; } while (0)
+    ADD("model.embed_tokens.weight", 2, c->vocab, c->dim);
+    ADD("model.norm.weight", 1, 1, c->dim);
+    if (!tied)
+        ADD("lm_head.weight", 2, c->vocab, c->dim);
+    for (int l = 0; l < c->n_layers; ++l) {
+        char b[64];
+#define ADDL(sfx, nd, r, k) do { snprintf(b, sizeof b, "model.layers.%d." sfx, l); ADD(b, nd, r, k); } while (0)
+        ADDL("input_layernorm.weight", 1, 1, c->dim);
+        ADDL("self_attn.q_proj.weight", 2, c->dim, c->dim);
+        ADDL("self_attn.k_proj.weight", 2, kvd, c->dim);
+        ADDL("self_attn.v_proj.weight", 2, kvd, c->dim);
+        ADDL("self_attn.o_proj.weight", 2, c->dim, c->dim);
+        ADDL("post_attention_layernorm.weight", 1, 1, c->dim);
+        ADDL("mlp.gate_proj.weight", 2, c->ffn, c->dim);
+        ADDL("mlp.up_proj.weight", 2, c->ffn, c->dim);
+        ADDL("mlp.down_proj.weight", 2, c->dim, c->ffn);
+#undef ADDL
+    }
+#undef ADD
+    return n;
+}
+
+int q48h_model_synth(q48h_model *m, uint64_t seed, int threads)
+{
+    if (!m)
+        return Q48_EINVAL;
+    const q48h_config *c = &m->c;
+    int nt = 3 + 9 * c->n_layers;
+    tdesc *t = (tdesc *)malloc(sizeof(tdesc) * (size_t)nt);
+    if (!t)
+        return Q48_ENOMEM;
+    nt = tensor_list(c, m->tied, t);
+    int64_t maxn = 0;
+    for (int i = 0; i < nt; ++i)
+        if (t[i].rows * t[i].cols > maxn)
+            maxn = t[i].rows * t[i].cols;
+    int64_t *buf = (int64_t *)malloc((size_t)maxn * 8);
+    int rc = buf ? Q48_OK : Q48_ENOMEM;
+    for (int i = 0; i < nt && rc == Q48_OK; ++i) {
+        q48s_fill_named(buf, t[i].rows, t[i].cols, seed, t[i].name, Q48_SIGMA_W, 1, threads);
+        rc = q48h_upload(m, t[i].name, buf, t[i].rows * t[i].cols);
+    }
+    free(buf);
+    free(t);
+    return rc;
+}
+
+/* ---------------------------------------------------------------------- */
+/* .mgw (llama_int.c:385-454, 1718-1904, 2344-2560)                        */
+/* ---------------------------------------------------------------------- */
+
+#define MGW_HEADER_SIZE 64
+#define MGW_CONFIG_SIZE 64
+#define MGW_ENTRY_SIZE 96
+#define MGW_VERSION 1
+#define MGW_ENDIAN 0x01020304u
+
+static void put32(uint8_t *p, uint32_t v) { memcpy(p, &v, 4); }
+static void put64(uint8_t *p, uint64_t v) { memcpy(p, &v, 8); }
+static uint32_t get32(const uint8_t *p) { uint32_t v; memcpy(&v, p, 4); return v; }
+static uint64_t get64(const uint8_t *p) { uint64_t v; memcpy(&v, p, 8); return v; }
+
+int q48h_mgw_write_synth(const char *path, const q48h_config *c, uint64_t seed, int threads)
+{
+    if (!path || !c)
+        return Q48_EINVAL;
+    int nt = 3 + 9 * c->n_layers;
+    tdesc *t = (tdesc *)malloc(sizeof(tdesc) * (size_t)nt);
+    if (!t)
+        return Q48_ENOMEM;
+    nt = tensor_list(c, 0, t);
+    uint64_t index_off = MGW_HEADER_SIZE + MGW_CONFIG_SIZE;
+    uint64_t data_off = (index_off + (uint64_t)nt * MGW_ENTRY_SIZE + 7) & ~7ull;
+    size_t head_n = (size_t)data_off;
+    uint8_t *head = (uint8_t *)calloc(1, head_n);
+    if (!head) {
+        free(t);
+        return Q48_ENOMEM;
+    }
+    memcpy(head, "MGW\0", 4);
+    put32(head + 4, MGW_VERSION);
+    put32(head + 8, MGW_ENDIAN);
+    put32(head + 12, (uint32_t)nt);
+    put64(head + 16, index_off);
+    put64(head + 24, data_off);
+    int32_t cfgv[10] = {c->dim, c->n_heads, c->n_kv_heads, c->head_dim, c->n_layers,
+                        c->ffn, c->vocab, c->max_seq, c->rope_theta, 0};
+    memcpy(head + MGW_HEADER_SIZE, cfgv, sizeof cfgv);
+    uint64_t cur = data_off;
+    for (int i = 0; i < nt; ++i) {
+        uint8_t *e = head + index_off + (size_t)i * MGW_ENTRY_SIZE;
+        uint64_t ne = (uint64_t)(t[i].rows * t[i].cols);
+        strncpy((char *)e, t[i].name, 63);
+        put64(e + 64, ne);
+        put64(e + 72, cur);
+        put32(e + 80, (uint32_t)t[i].ndims);
+        put32(e + 84, (uint32_t)(t[i].ndims == 2 ? t[i].rows : t[i].cols));
+        put32(e + 88, (uint32_t)(t[i].ndims == 2 ? t[i].cols : 0));
+        cur += ne * 8;
+    }
+    FILE *f = fopen(path, "wb");
+    int rc = f ? Q48_OK : Q48_EINVAL;
+    if (f && fwrite(head, 1, head_n, f) != head_n)
+        rc = Q48_EINVAL;
+    int64_t maxn = 0;
+    for (int i = 0; i < nt; ++i)
+        if (t[i].rows * t[i].cols > maxn)
+            maxn = t[i].rows * t[i].cols;
+    int64_t *buf = rc == Q48_OK ? (int64_t *)malloc((size_t)maxn * 8) : NULL;
+    if (rc == Q48_OK && !buf)
+        rc = Q48_ENOMEM;
+    for (int i = 0; i < nt && rc == Q48_OK; ++i) {
+        size_t ne = (size_t)(t[i].rows * t[i].cols);
+        q48s_fill_named(buf, t[i].rows, t[i].cols, seed, t[i].name, Q48_SIGMA_W, 1, threads);
+        if (fwrite(buf, 8, ne, f) != ne)
+            rc = Q48_EINVAL;
+    }
+    free(buf);
+    if (f && fclose(f) != 0)
+        rc = Q48_EINVAL;
+    free(head);
+    free(t);
+    return rc;
+}
+
+int q48h_model_load_mgw(q48h_model **out, q48_ctx *ctx, const char *path, int max_seq)
+{
+    if (!out || !ctx || !path)
+        return Q48_EINVAL;
+    *out = NULL;
+    int fd = open(path, O_RDONLY);
+    if (fd < 0)
+        return Q48_EINVAL;
+    struct stat sb;
+    if (fstat(fd, &sb) != 0 || sb.st_size < MGW_HEADER_SIZE + MGW_CONFIG_SIZE) {
+        close(fd);
+        return Q48_EINVAL;
+    }
+    size_t fsz = (size_t)sb.st_size;
+    const uint8_t *base = (const uint8_t *)mmap(NULL, fsz, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (base == (const uint8_t *)MAP_FAILED)
+        return Q48_EINVAL;
+    int rc = Q48_EINVAL;
+    q48h_model *m = NULL;
+    if (memcmp(base, "MGW\0", 4) || get32(base + 4) != MGW_VERSION || get32(base + 8) != MGW_ENDIAN)
+        goto done;
+    uint32_t nt = get32(base + 12);
+    uint64_t ioff = get64(base + 16);
+    if (ioff > fsz || (uint64_t)nt * MGW_ENTRY_SIZE > fsz - ioff)
+        goto done;
+    int32_t cv[10];
+    memcpy(cv, base + MGW_HEADER_SIZE, sizeof cv);
+    q48h_config c = {cv[0], cv[1], cv[2], cv[3], cv[4], cv[5], cv[6], cv[7], cv[8]};
+    int tied = cv[9] != 0;
+    if (c.dim <= 0 || c.n_heads <= 0 || c.n_layers <= 0 || c.vocab <= 0)
+        goto done;
+    if (max_seq > 0)
+        c.max_seq = max_seq;
+    if ((rc = model_alloc(&m, ctx, &c, tied)) != Q48_OK)
+        goto done;
+    rc = Q48_EINVAL;
+    int got_embed = 0, got_norm = 0, got_lm = 0;
+    int *got_layer = (int *)calloc((size_t)c.n_layers, sizeof(int));
+    if (!got_layer) {
+        rc = Q48_ENOMEM;
+        goto done;
+    }
+    for (uint32_t i = 0; i < nt; ++i) {
+        const uint8_t *e = base + ioff + (uint64_t)i * MGW_ENTRY_SIZE;
+        char name[64];
+        memcpy(name, e, 63);
+        name[63] = 0;
+        uint64_t ne = get64(e + 64), doff = get64(e + 72);
+        if (ne > UINT64_MAX / 8 || doff > fsz || ne * 8 > fsz - doff || doff % 8) {
+            free(got_layer);
+            goto done;
+        }
+        int64_t *dst;
+        int64_t want;
+        if (tensor_slot(m, name, &dst, &want) != 0)
+            continue;   /* the reference warns and skips unknown tensors */
+        if ((int64_t)ne != want) {
+            free(got_layer);
+            goto done;
+        }
+        if (q48_memcpy_h2d(ctx, dst, base + doff, ne * 8) != Q48_OK) {
+            rc = Q48_EHIP;
+            free(got_layer);
+            goto done;
+        }
+        int l;
+        char rest[128];
+        if (!strcmp(name, "model.embed_tokens.weight"))
+            got_embed = 1;
+        else if (!strcmp(name, "model.norm.weight"))
+            got_norm = 1;
+        else if (!strcmp(name, "lm_head.weight"))
+            got_lm = 1;
+        else if (sscanf(name, "model.layers.%d.%127s", &l, rest) == 2)
+            got_layer[l]++;
+    }
+    int complete = got_embed && got_norm && (tied || got_lm);
+    for (int l = 0; l < c.n_layers; ++l)
+        complete = complete && got_layer[l] == 9;
+    free(got_layer);
+    if (!complete)
+        goto done;
+    rc = Q48_OK;
+done:
+    munmap((void *)base, fsz);
+    if (rc != Q48_OK) {
+        q48h_model_free(m);
+        return rc;
+    }
+    *out = m;
+    return Q48_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* KV cache                                                                */
+/* ---------------------------------------------------------------------- */
+
+int q48h_kv_reset(q48h_model *m)
+{
+    if (!m)
+        return Q48_EINVAL;
+    size_t n = (size_t)m->c.n_layers * m->c.max_seq * m->c.n_kv_heads * m->c.head_dim * 8;
+    int rc = q48_zero(m->ctx, m->kc, n);
+    return rc ? rc : q48_zero(m->ctx, m->vc, n);
+}
+
+int q48h_kv_fill_synth(q48h_model *m, uint64_t seed, int npos, int threads)
+{
+    if (!m || npos < 0 || npos > m->c.max_seq)
+        return Q48_EINVAL;
+    if (npos == 0)
+        return Q48_OK;
+    int kvd = m->c.n_kv_heads * m->c.head_dim;
+    int64_t *buf = (int64_t *)malloc((size_t)npos * kvd * 8);
+    if (!buf)
+        return Q48_ENOMEM;
+    int rc = Q48_OK;
+    char nm[64];
+    for (int l = 0; l < m->c.n_layers && rc == Q48_OK; ++l) {
+        size_t off = (size_t)l * m->c.max_seq * kvd;
+        snprintf(nm, sizeof nm, "kv.key.%d", l);
+        q48s_fill_named(buf, npos, kvd, seed, nm, Q48_SIGMA_ACT, 1, threads);
+        rc = q48_memcpy_h2d(m->ctx, m->kc + off, buf, (size_t)npos * kvd * 8);
+        if (rc)
+            break;
+        snprintf(nm, sizeof nm, "kv.value.%d", l);
+        q48s_fill_named(buf, npos, kvd, seed, nm, Q48_SIGMA_ACT, 1, threads);
+        rc = q48_memcpy_h2d(m->ctx, m->vc + off, buf, (size_t)npos * kvd * 8);
+    }
+    free(buf);
+    return rc;
+}
+
+/* ---------------------------------------------------------------------- */
+/* forward / generate                                                      */
+/* ---------------------------------------------------------------------- */
+
+#define TRY(x) do { int rc_ = (x); if (rc_) return rc_; } while (0)
+
+/* transformer_layer_forward, llama_int.c:1326-1569 (exact-cache path). */
+static int layer_forward(q48h_model *m, int l, int pos)
+{
+    const q48h_config *c = &m->c;
+    q48_ctx *x = m->ctx;
+    int dim = c->dim, hd = c->head_dim, kvd = c->n_kv_heads * hd, ffn = c->ffn;
+    const int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
+    int64_t *q = m->qkv, *k = m->qkv + dim, *v = m->qkv + dim + kvd;
+
+    TRY(q48_rmsnorm(x, m->normed, m->hidden, b + m->lo_an, dim));
+    TRY(q48_gemv(x, m->qkv, b + m->lo_qkv, m->normed, dim + 2 * kvd, dim));
+    TRY(q48_rope(x, q, c->n_heads, hd, pos));
+    TRY(q48_rope(x, k, c->n_kv_heads, hd, pos));
+    TRY(q48_attn_decode(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
+                        c->n_kv_heads, hd, c->max_seq));
+    TRY(q48_gemv(x, m->o, b + m->lo_wo, m->attn, dim, dim));
+    TRY(q48_add(x, m->hidden, m->o, dim));
+    TRY(q48_rmsnorm(x, m->normed, m->hidden, b + m->lo_fn, dim));
+    TRY(q48_gemv(x, m->gu, b + m->lo_gu, m->normed, 2 * ffn, dim));
+    TRY(q48_silu_mul(x, m->h_ffn, m->gu, m->gu + ffn, ffn));
+    TRY(q48_gemv(x, m->mlp, b + m->lo_wd, m->h_ffn, dim, ffn));
+    TRY(q48_add(x, m->hidden, m->mlp, dim));
+    return Q48_OK;
+}
+
+int q48h_forward(q48h_model *m, int token, int pos, int64_t *logits, int *next)
+{
+    if (!m)
+        return Q48_EINVAL;
+    const q48h_config *c = &m->c;
+    if (token < 0 || token >= c->vocab || pos < 0 || pos >= c->max_seq)
+        return Q48_ERANGE;
+    TRY(q48_embed(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim));
+    for (int l = 0; l < c->n_layers; ++l)
+        TRY(layer_forward(m, l, pos));
+    TRY(q48_rmsnorm(m->ctx, m->normed, m->hidden, m->w + m->off_norm, c->dim));
+    TRY(q48_gemv(m->ctx, m->logits, m->w + m->off_lm, m->normed, c->vocab, c->dim));
+    if (next)
+        TRY(q48_argmax(m->ctx, m->logits, c->vocab, next));
+    if (logits)
+        TRY(q48_memcpy_d2h(m->ctx, logits, m->logits, (size_t)c->vocab * 8));
+    if (!next && !logits)
+        TRY(q48_sync(m->ctx));
+    return Q48_OK;
+}
+
+static double now_s(void)
+{
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+int q48h_generate(q48h_model *m, const int *prompt, int prompt_len, int max_new,
+                  int *out_tokens, uint64_t *step_hash, int *n_steps, q48h_stats *st)
+{
+    if (!m || !prompt || !out_tokens || prompt_len <= 0)
+        return Q48_EINVAL;
+    int vocab = m->c.vocab, steps = 0;
+    int64_t *logits = step_hash ? (int64_t *)malloc((size_t)vocab * 8) : NULL;
+    if (step_hash && !logits)
+        return Q48_ENOMEM;
+    int rc = q48h_kv_reset(m);
+    memcpy(out_tokens, prompt, (size_t)prompt_len * sizeof(int));
+    int total = prompt_len;
+    double t0 = now_s();
+    for (int pos = 0; pos < prompt_len && rc == Q48_OK; ++pos) {
+        int next;
+        rc = q48h_forward(m, out_tokens[pos], pos, logits, &next);
+        if (rc)
+            break;
+        if (step_hash)
+            step_hash[steps] = q48s_fnv_i64(FNV_OFF, logits, (size_t)vocab);
+        steps++;
+        if (pos == prompt_len - 1)
+            out_tokens[total++] = next;
+    }
+    double t1 = now_s();
+    int dec0 = total;
+    for (int i = 1; i < max_new && rc == Q48_OK; ++i) {
+        int pos = prompt_len + i - 1, next;
+        int frc = q48h_forward(m, out_tokens[pos], pos, logits, &next);
+        if (frc == Q48_ERANGE)
+            break;   /* llama_forward's NULL: generate stops (llama_int.c:3106) */
+        if (frc) {
+            rc = frc;
+            break;
+        }
+        if (step_hash)
+            step_hash[steps] = q48s_fnv_i64(FNV_OFF, logits, (size_t)vocab);
+        steps++;
+        if (next == LLAMA_EOS)
+            break;
+        out_tokens[total++] = next;
+    }
+    double t2 = now_s();
+    free(logits);
+    if (st) {
+        st->prefill_s += t1 - t0;
+        st->prefill_tokens += prompt_len;
+        st->decode_s += t2 - t1;
+        st->decode_tokens += total - dec0;
+    }
+    if (n_steps)
+        *n_steps = steps;
+    return rc ? rc : total;
+}
+
+int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
+                     uint64_t *step_hash, q48h_stats *st)
+{
+    if (!m || n < 0)
+        return Q48_EINVAL;
+    int vocab = m->c.vocab, steps = 0, tok = token, rc = Q48_OK;
+    int64_t *logits = step_hash ? (int64_t *)malloc((size_t)vocab * 8) : NULL;
+    if (step_hash && !logits)
+        return Q48_ENOMEM;
+    double t0 = now_s();
+    for (int i = 0; i < n; ++i) {
+        int next;
+        rc = q48h_forward(m, tok, start_pos + i, logits, &next);
+        if (rc == Q48_ERANGE) {
+            rc = Q48_OK;
+            break;
+        }
+        if (rc)
+            break;
+        if (step_hash)
+            step_hash[i] = q48s_fnv_i64(FNV_OFF, logits, (size_t)vocab);
+        steps++;
+        tok = next;
+        if (out_tokens)
+            out_tokens[i] = tok;
+        if (tok == LLAMA_EOS)
+            break;
+    }
+    if (st) {
+        st->decode_s += now_s() - t0;
+        st->decode_tokens += steps;
+    }
+    free(logits);
+    return rc ? rc : steps;
+}

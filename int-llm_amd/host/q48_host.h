@@ -1,0 +1,112 @@
+/*
+ * q48_host.h — the C host of the Q16.48 Llama forward pass.
+ *
+ * Keeps llama_int.c's host-side behaviour (config.json parsing, .mgw
+ * loading, llama_forward and the greedy generate loop) and runs every
+ * tensor op through libintllm_hip (include/intllm_hip.h) on device-resident
+ * int64 weights and an int64 KV cache.  Token ids in, token ids (and,
+ * on request, the logits) out: the host <-> device boundary is crossed
+ * once per token.
+ */
+#ifndef Q48_HOST_H
+#define Q48_HOST_H
+
+#include <stdint.h>
+#include "../../include/intllm_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* llama_config_t (llama_int.c:788-798). */
+typedef struct {
+    int dim;          /* hidden_size               */
+    int n_heads;      /* num_attention_heads       */
+    int n_kv_heads;   /* num_key_value_heads (GQA) */
+    int head_dim;     /* dim / n_heads (derived)   */
+    int n_layers;     /* num_hidden_layers         */
+    int ffn;          /* intermediate_size         */
+    int vocab;        /* vocab_size                */
+    int max_seq;      /* max_position_embeddings   */
+    int rope_theta;   /* rope_theta                */
+} q48h_config;
+
+/* Timing counters, named like llama_int's KPI lines (llama_int.c:248-297). */
+typedef struct {
+    double prefill_s, decode_s;
+    int prefill_tokens, decode_tokens;
+} q48h_stats;
+
+/* load_config_json (llama_int.c:834-903): same keys, defaults
+ * (num_key_value_heads = num_attention_heads, max_position_embeddings =
+ * 2048, rope_theta = 10000) and checks.  0, -1 (no file) or -2 (invalid). */
+int q48h_config_from_json(const char *model_dir, q48h_config *cfg);
+/* The same integer extraction on a JSON text already in memory. */
+int q48h_config_from_json_text(const char *json, q48h_config *cfg);
+
+/* Shapes the device path supports (head_dim even, <= 256, divides 256). */
+int q48h_config_check(const q48h_config *cfg);
+
+typedef struct q48h_model q48h_model;
+
+/* Allocate device weights, KV cache and activations for cfg and build the
+ * RoPE tables; weights are zero until uploaded. */
+int q48h_model_create(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg);
+void q48h_model_free(q48h_model *m);
+const q48h_config *q48h_model_config(const q48h_model *m);
+q48_ctx *q48h_model_ctx(q48h_model *m);
+
+/* Upload one tensor by its HF name (the names of load_layer_weights,
+ * llama_int.c:1290-1298, and llama_load_global_weights, :1640-1677);
+ * n must equal the tensor's element count. */
+int q48h_upload(q48h_model *m, const char *name, const int64_t *host, int64_t n);
+
+/* Fill every weight with the synthetic random-init values of q48_synth.h
+ * (sigma 0.02, bf16-rounded), generated on the host with `threads`
+ * threads and uploaded tensor by tensor. */
+int q48h_model_synth(q48h_model *m, uint64_t seed, int threads);
+
+/* mgw_load (llama_int.c:2344-2560): validate and upload a native .mgw
+ * file.  max_seq > 0 overrides the file's max_seq_len.  Also checks each
+ * tensor's element count against the config (the device must never read
+ * past a tensor). */
+int q48h_model_load_mgw(q48h_model **out, q48_ctx *ctx, const char *path, int max_seq);
+
+/* mgw_export layout (llama_int.c:1718-1904) for the synthetic model of
+ * cfg (no GPU needed): 64 B header, 64 B config, 96 B index entries,
+ * 8-aligned int64 data, host byte order. */
+int q48h_mgw_write_synth(const char *path, const q48h_config *cfg, uint64_t seed,
+                         int threads);
+
+/* KV cache (device) pointers, layout [L][max_seq][n_kv][head_dim]. */
+int64_t *q48h_kv_keys(q48h_model *m);
+int64_t *q48h_kv_values(q48h_model *m);
+/* kv_cache_reset (llama_int.c:1170-1183). */
+int q48h_kv_reset(q48h_model *m);
+/* Positions [0, npos) of every layer <- N(0,1) bf16 samples (q48_synth.h,
+ * tensors "kv.key.<l>" / "kv.value.<l>"); long-context configuration. */
+int q48h_kv_fill_synth(q48h_model *m, uint64_t seed, int npos, int threads);
+
+/* llama_forward (llama_int.c:2807-2886).  logits (host, may be NULL)
+ * receives logits[vocab]; next (may be NULL) the greedy token.
+ * Q48_ERANGE for a token or position out of range, like the
+ * reference's NULL return. */
+int q48h_forward(q48h_model *m, int token, int pos, int64_t *logits, int *next);
+
+/* generate (llama_int.c:3067-3135), greedy.  step_hash (may be NULL) gets
+ * FNV-1a-64 of every forward call's logits (prompt positions included);
+ * n_steps the number of forward calls.  Returns the total token count or
+ * a negative Q48_E* code. */
+int q48h_generate(q48h_model *m, const int *prompt, int prompt_len, int max_new,
+                  int *out_tokens, uint64_t *step_hash, int *n_steps,
+                  q48h_stats *stats);
+
+/* Greedy decode from an already filled cache: forward(token, start_pos),
+ * then n - 1 more steps, stopping after EOS (long-context configuration). */
+int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
+                     uint64_t *step_hash, q48h_stats *stats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

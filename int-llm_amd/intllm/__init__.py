@@ -1,0 +1,365 @@
+"""intllm — Python bindings (ctypes) of the Q16.48 forward-pass libraries.
+
+The product is native: ``lib/libintllm_hip.so`` (HIP kernels behind the C ABI
+of ``include/intllm_hip.h``) and ``lib/libq48host.so`` (the C host:
+config.json / .mgw loading, llama_forward and generate over that ABI).  This
+module only loads them and moves numpy int64 arrays across the boundary, for
+tests and benchmarks.  It never computes a result itself: if the libraries
+are missing it raises instead of falling back to anything.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG_ROOT = Path(__file__).resolve().parent.parent
+LIB_DIR = PKG_ROOT / "lib"
+HIP_LIB = LIB_DIR / "libintllm_hip.so"
+HOST_LIB = LIB_DIR / "libq48host.so"
+
+Q48_OK, Q48_EINVAL, Q48_ENOMEM, Q48_EHIP, Q48_ERANGE, Q48_ESTATE = 0, -1, -2, -3, -4, -5
+
+# fp_eval function ids (include/intllm_hip.h, q48_fp_eval)
+FP_MUL, FP_DIV, FP_SQRT, FP_SQRT_FAST, FP_INV_SQRT, FP_EXP, FP_LOG, FP_SINCOS, \
+    FP_SIGMOID, FP_SILU, FP_SAFE_EXP, FP_EXP_DYADIC = range(12)
+
+# ABI entry points and their argument types (include/intllm_hip.h)
+_P, _I, _SZ = C.c_void_p, C.c_int, C.c_size_t
+ABI_SIGNATURES = {
+    "q48_ctx_create": [C.POINTER(C.c_void_p), _I],
+    "q48_ctx_destroy": [_P],
+    "q48_malloc": [_P, C.POINTER(C.c_void_p), _SZ],
+    "q48_free": [_P, _P],
+    "q48_memcpy_h2d": [_P, _P, _P, _SZ],
+    "q48_memcpy_d2h": [_P, _P, _P, _SZ],
+    "q48_memcpy_d2d": [_P, _P, _P, _SZ],
+    "q48_zero": [_P, _P, _SZ],
+    "q48_sync": [_P],
+    "q48_gemv": [_P, _P, _P, _P, _I, _I],
+    "q48_gemm": [_P, _P, _P, _P, _I, _I, _I],
+    "q48_rmsnorm": [_P, _P, _P, _P, _I],
+    "q48_rope_init": [_P, _I, _I, _I],
+    "q48_rope": [_P, _P, _I, _I, _I],
+    "q48_attn_decode": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
+    "q48_silu_mul": [_P, _P, _P, _P, _I],
+    "q48_add": [_P, _P, _P, _I],
+    "q48_embed": [_P, _P, _P, _I, _I],
+    "q48_argmax": [_P, _P, _I, C.POINTER(C.c_int)],
+    "q48_rope_tables": [_P, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)],
+    "q48_fp_eval": [_P, _I, _P, _P, _P, _P, _I],
+    "q48_prof_enable": [_P, _I],
+    "q48_prof_read": [_P, _P, _I],
+}
+
+
+class Prof(C.Structure):
+    """q48_prof: HIP-event timing of q48_gemv launches."""
+    _fields_ = [("launches", C.c_int), ("ms", C.c_double), ("bytes", C.c_double)]
+
+
+class Q48Error(RuntimeError):
+    def __init__(self, fn: str, code: int):
+        self.code = code
+        super().__init__(f"{fn} failed: {code} ({strerror(code)})")
+
+
+_hip = None
+_host = None
+
+
+def _require(path: Path) -> None:
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is not built: run `make -C {PKG_ROOT}` (or __graft_entry__.build())"
+        )
+
+
+def hip_lib() -> C.CDLL:
+    """libintllm_hip.so with typed entry points (raises if not built)."""
+    global _hip
+    if _hip is None:
+        _require(HIP_LIB)
+        lib = C.CDLL(str(HIP_LIB), mode=C.RTLD_GLOBAL)
+        for name, args in ABI_SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = C.c_int
+        lib.q48_strerror.argtypes = [C.c_int]
+        lib.q48_strerror.restype = C.c_char_p
+        _hip = lib
+    return _hip
+
+
+def strerror(code: int) -> str:
+    try:
+        return hip_lib().q48_strerror(code).decode()
+    except Exception:  # library not loadable: message only
+        return "unknown"
+
+
+def check(fn: str, rc: int) -> int:
+    if rc < 0:
+        raise Q48Error(fn, rc)
+    return rc
+
+
+def i64(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int64)
+
+
+class Buffer:
+    """A device allocation of int64 elements owned by a Context."""
+
+    def __init__(self, ctx: "Context", n: int, itemsize: int = 8):
+        self.ctx, self.n, self.itemsize = ctx, int(n), itemsize
+        p = C.c_void_p()
+        check("q48_malloc", hip_lib().q48_malloc(ctx.h, C.byref(p), max(1, self.n) * itemsize))
+        self.ptr = p.value
+
+    @property
+    def nbytes(self) -> int:
+        return self.n * self.itemsize
+
+    def upload(self, arr) -> "Buffer":
+        a = i64(arr) if self.itemsize == 8 else np.ascontiguousarray(arr)
+        assert a.nbytes <= self.nbytes, (a.nbytes, self.nbytes)
+        check("q48_memcpy_h2d", hip_lib().q48_memcpy_h2d(self.ctx.h, self.ptr, a.ctypes.data, a.nbytes))
+        return self
+
+    def download(self, n: int | None = None) -> np.ndarray:
+        n = self.n if n is None else n
+        out = np.empty(n, dtype=np.int64)
+        check("q48_memcpy_d2h", hip_lib().q48_memcpy_d2h(self.ctx.h, out.ctypes.data, self.ptr, n * 8))
+        return out
+
+    def at(self, elem_offset: int) -> int:
+        return self.ptr + 8 * int(elem_offset)
+
+    def free(self) -> None:
+        if self.ptr:
+            hip_lib().q48_free(self.ctx.h, self.ptr)
+            self.ptr = None
+
+
+class Context:
+    """q48_ctx: one HIP stream plus the device fp_math constants."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check("q48_ctx_create", hip_lib().q48_ctx_create(C.byref(h), device))
+        self.h = h.value
+        self._bufs: list[Buffer] = []
+
+    def close(self) -> None:
+        if self.h:
+            for b in self._bufs:
+                b.free()
+            hip_lib().q48_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def buffer(self, n: int) -> Buffer:
+        b = Buffer(self, n)
+        self._bufs.append(b)
+        return b
+
+    def to_device(self, arr) -> Buffer:
+        a = i64(arr).ravel()
+        return self.buffer(a.size).upload(a)
+
+    def sync(self) -> None:
+        check("q48_sync", hip_lib().q48_sync(self.h))
+
+    # ---- ops (device pointers are ints) ----
+    def gemv(self, y, W, x, M, K):
+        return check("q48_gemv", hip_lib().q48_gemv(self.h, y, W, x, M, K))
+
+    def gemm(self, Y, W, X, T, N, K):
+        return check("q48_gemm", hip_lib().q48_gemm(self.h, Y, W, X, T, N, K))
+
+    def rmsnorm(self, out, x, w, dim):
+        return check("q48_rmsnorm", hip_lib().q48_rmsnorm(self.h, out, x, w, dim))
+
+    def rope_init(self, head_dim, max_seq, theta):
+        return check("q48_rope_init", hip_lib().q48_rope_init(self.h, head_dim, max_seq, theta))
+
+    def rope(self, vec, n_heads, head_dim, pos):
+        return check("q48_rope", hip_lib().q48_rope(self.h, vec, n_heads, head_dim, pos))
+
+    def attn_decode(self, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq):
+        return check("q48_attn_decode", hip_lib().q48_attn_decode(
+            self.h, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq))
+
+    def silu_mul(self, out, g, u, n):
+        return check("q48_silu_mul", hip_lib().q48_silu_mul(self.h, out, g, u, n))
+
+    def add(self, acc, d, n):
+        return check("q48_add", hip_lib().q48_add(self.h, acc, d, n))
+
+    def embed(self, out, table, token, dim):
+        return check("q48_embed", hip_lib().q48_embed(self.h, out, table, token, dim))
+
+    def argmax(self, v, n) -> int:
+        r = C.c_int()
+        check("q48_argmax", hip_lib().q48_argmax(self.h, v, n, C.byref(r)))
+        return r.value
+
+    def zero(self, p, nbytes):
+        return check("q48_zero", hip_lib().q48_zero(self.h, p, nbytes))
+
+    def rope_tables(self):
+        c, s = C.c_void_p(), C.c_void_p()
+        check("q48_rope_tables", hip_lib().q48_rope_tables(self.h, C.byref(c), C.byref(s)))
+        return c.value, s.value
+
+    def prof_enable(self, on: bool = True):
+        check("q48_prof_enable", hip_lib().q48_prof_enable(self.h, int(on)))
+
+    def prof_read(self, reset: bool = True) -> "Prof":
+        p = Prof()
+        check("q48_prof_read", hip_lib().q48_prof_read(self.h, C.byref(p), int(reset)))
+        return p
+
+    def fp_eval(self, func, x, y, out0, out1, n):
+        return check("q48_fp_eval", hip_lib().q48_fp_eval(self.h, func, x, y or None, out0, out1 or None, n))
+
+
+# ---------------------------------------------------------------------------
+# C host (libq48host.so)
+# ---------------------------------------------------------------------------
+
+class Config(C.Structure):
+    """q48h_config == llama_config_t field for field (llama_int.c:788-798)."""
+    _fields_ = [(n, C.c_int) for n in
+                ("dim", "n_heads", "n_kv_heads", "head_dim", "n_layers", "ffn",
+                 "vocab", "max_seq", "rope_theta")]
+
+    def as_tuple(self):
+        return tuple(getattr(self, n) for n, _ in self._fields_)
+
+
+class Stats(C.Structure):
+    _fields_ = [("prefill_s", C.c_double), ("decode_s", C.c_double),
+                ("prefill_tokens", C.c_int), ("decode_tokens", C.c_int)]
+
+
+TINY = Config(256, 8, 2, 32, 2, 688, 512, 2048, 10000)
+TINYLLAMA = Config(2048, 32, 4, 64, 22, 5632, 32000, 2048, 10000)
+
+
+def config(base: Config, **kw) -> Config:
+    c = Config(*base.as_tuple())
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+HOST_SIGNATURES = {
+    "q48h_config_from_json": ([C.c_char_p, C.POINTER(Config)], C.c_int),
+    "q48h_config_from_json_text": ([C.c_char_p, C.POINTER(Config)], C.c_int),
+    "q48h_config_check": ([C.POINTER(Config)], C.c_int),
+    "q48h_model_create": ([C.POINTER(C.c_void_p), _P, C.POINTER(Config)], C.c_int),
+    "q48h_model_free": ([_P], None),
+    "q48h_upload": ([_P, C.c_char_p, _P, C.c_int64], C.c_int),
+    "q48h_model_synth": ([_P, C.c_uint64, _I], C.c_int),
+    "q48h_model_load_mgw": ([C.POINTER(C.c_void_p), _P, C.c_char_p, _I], C.c_int),
+    "q48h_mgw_write_synth": ([C.c_char_p, C.POINTER(Config), C.c_uint64, _I], C.c_int),
+    "q48h_kv_keys": ([_P], C.c_void_p),
+    "q48h_kv_values": ([_P], C.c_void_p),
+    "q48h_kv_reset": ([_P], C.c_int),
+    "q48h_kv_fill_synth": ([_P, C.c_uint64, _I, _I], C.c_int),
+    "q48h_forward": ([_P, _I, _I, _P, C.POINTER(C.c_int)], C.c_int),
+    "q48h_generate": ([_P, C.POINTER(C.c_int), _I, _I, C.POINTER(C.c_int),
+                       C.POINTER(C.c_uint64), C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
+    "q48h_decode_from": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(C.c_uint64),
+                          C.POINTER(Stats)], C.c_int),
+}
+
+
+def host_lib() -> C.CDLL:
+    """libq48host.so (loads libintllm_hip.so first; raises if not built)."""
+    global _host
+    if _host is None:
+        hip_lib()
+        _require(HOST_LIB)
+        lib = C.CDLL(str(HOST_LIB))
+        for name, (args, res) in HOST_SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _host = lib
+    return _host
+
+
+class HostModel:
+    """q48h_model: device-resident weights + KV cache driven by the C host."""
+
+    def __init__(self, ctx: Context, cfg: Config | None = None, *, mgw: str | None = None,
+                 max_seq: int = 0):
+        h = C.c_void_p()
+        if mgw is not None:
+            check("q48h_model_load_mgw",
+                  host_lib().q48h_model_load_mgw(C.byref(h), ctx.h, mgw.encode(), max_seq))
+        else:
+            check("q48h_model_create", host_lib().q48h_model_create(C.byref(h), ctx.h, C.byref(cfg)))
+        self.h, self.ctx = h.value, ctx
+        self.cfg = cfg
+
+    def free(self):
+        if self.h:
+            host_lib().q48h_model_free(self.h)
+            self.h = None
+
+    def synth(self, seed: int, threads: int = 8):
+        check("q48h_model_synth", host_lib().q48h_model_synth(self.h, seed, threads))
+
+    def upload(self, name: str, arr):
+        a = i64(arr).ravel()
+        check("q48h_upload", host_lib().q48h_upload(self.h, name.encode(), a.ctypes.data, a.size))
+
+    def kv_fill_synth(self, seed: int, npos: int, threads: int = 8):
+        check("q48h_kv_fill_synth", host_lib().q48h_kv_fill_synth(self.h, seed, npos, threads))
+
+    def kv_pointers(self):
+        return host_lib().q48h_kv_keys(self.h), host_lib().q48h_kv_values(self.h)
+
+    def forward(self, token: int, pos: int, vocab: int, logits: bool = True):
+        out = np.empty(vocab, dtype=np.int64) if logits else None
+        nxt = C.c_int()
+        check("q48h_forward", host_lib().q48h_forward(
+            self.h, token, pos, out.ctypes.data if logits else None, C.byref(nxt)))
+        return nxt.value, out
+
+    def generate(self, prompt, max_new: int, hashes: bool = True):
+        p = (C.c_int * len(prompt))(*prompt)
+        cap = len(prompt) + max_new + 1
+        out = (C.c_int * cap)()
+        hs = (C.c_uint64 * cap)() if hashes else None
+        n = C.c_int()
+        st = Stats()
+        total = check("q48h_generate", host_lib().q48h_generate(
+            self.h, p, len(prompt), max_new, out, hs, C.byref(n), C.byref(st)))
+        return list(out[:total]), (list(hs[:n.value]) if hashes else None), st
+
+    def decode_from(self, token: int, start_pos: int, n: int, hashes: bool = True):
+        out = (C.c_int * max(1, n))()
+        hs = (C.c_uint64 * max(1, n))() if hashes else None
+        st = Stats()
+        steps = check("q48h_decode_from", host_lib().q48h_decode_from(
+            self.h, token, start_pos, n, out, hs, C.byref(st)))
+        return list(out[:steps]), (list(hs[:steps]) if hashes else None), st
+
+
+def gpu_available() -> bool:
+    """True when a HIP device is visible (does not initialise HIP)."""
+    if os.environ.get("HIP_VISIBLE_DEVICES", None) == "":
+        return False
+    return os.path.exists("/dev/kfd")

@@ -726,6 +726,11 @@ static void layer_forward(q48o_model *m, int l, int pos, int64_t *hidden)
         hidden[i] += mlp[i];
 }
 
+void q48o_layer_forward(q48o_model *m, int layer, int pos, int64_t *hidden)
+{
+    layer_forward(m, layer, pos, hidden);
+}
+
 /* llama_forward, llama_int.c:2807-2886. */
 int q48o_forward(q48o_model *m, int token, int pos, int64_t *logits)
 {

@@ -82,6 +82,8 @@ void q48o_kv_fill_synth(q48o_model *m, uint64_t seed, int npos, int threads);
 /* KV cache base pointers ([L][max_seq][n_kv][hd]). */
 int64_t *q48o_kv_keys(q48o_model *m);
 int64_t *q48o_kv_values(q48o_model *m);
+/* transformer_layer_forward (llama_int.c:1326-1569) on hidden in place. */
+void q48o_layer_forward(q48o_model *m, int layer, int pos, int64_t *hidden);
 /* llama_forward (llama_int.c:2807-2886): 0 and logits[vocab], or -1. */
 int q48o_forward(q48o_model *m, int token, int pos, int64_t *logits);
 /* generate (llama_int.c:3067-3135), greedy.  step_hash[i] is the FNV-1a-64

@@ -245,3 +245,30 @@ int q48r_decode_from(void *mm, int token, int start_pos, int n, int *out,
     }
     return steps;
 }
+
+/* The reference's own .mgw loader (mgw_load, llama_int.c:2344-2560) on a
+ * file written by the C host, then the rest of model setup as main does. */
+void *q48r_model_load_mgw(const char *path)
+{
+    llama_model_t *m = (llama_model_t *)calloc(1, sizeof *m);
+    m->native_stream_fd = -1;
+    if (mgw_load(m, path) != 0) {
+        free(m);
+        return NULL;
+    }
+    rope_init(&m->rope, &m->cfg);
+    if (kv_cache_init(&m->kv, &m->cfg) != 0 || llama_init_scratch(m) != 0)
+        return NULL;
+    return m;
+}
+
+void q48r_model_free_mgw(void *mm)
+{
+    llama_model_t *m = (llama_model_t *)mm;
+    munmap(m->native_mmap, m->native_mmap_size);
+    free(m->cached_layers);
+    rope_free(&m->rope);
+    kv_cache_free(&m->kv);
+    free(m->scratch_buf);
+    free(m);
+}

@@ -1,0 +1,144 @@
+"""End-to-end GPU parity: the C host's generate loop over libintllm_hip
+against the token streams and per-step logits hashes recorded from the
+reference's own llama_forward / generate (tests/golden/*_generate.json,
+longctx_decode.json)."""
+import ctypes as C
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import intllm
+import oracle_lib as O
+import spec
+from conftest import golden
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def test_tiny_generate_bit_exact(ctx):
+    g = golden("tiny_generate.json")
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    try:
+        say("tiny synth")
+        m.synth(g["seed"], threads())
+        say("tiny generate")
+        toks, hs, _ = m.generate(g["prompt"], g["max_new"])
+        assert toks == g["tokens"]
+        assert ["%016x" % h for h in hs] == g["step_fnv"]
+        # determinism: a second run (kv reset inside generate) is identical
+        toks2, hs2, _ = m.generate(g["prompt"], g["max_new"])
+        assert toks2 == toks and hs2 == hs
+    finally:
+        m.free()
+
+
+def test_tiny_forward_logits_equal_oracle(ctx):
+    g = golden("tiny_generate.json")
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    om = O.Model(spec.TINY, g["seed"])
+    try:
+        m.synth(g["seed"], threads())
+        for pos, tok in enumerate(g["prompt"][:6]):
+            say("tiny forward pos", pos)
+            nxt, lg = m.forward(tok, pos, spec.TINY[6])
+            rc, want = om.forward(tok, pos)
+            assert rc == 0 and np.array_equal(lg, want), pos
+            assert nxt == int(np.argmax(want))
+    finally:
+        m.free()
+        om.free()
+
+
+def test_forward_range_errors(ctx):
+    m = intllm.HostModel(ctx, intllm.Config(*spec.TINY))
+    try:
+        for tok, pos in ((spec.TINY[6], 0), (-1, 0), (3, spec.TINY[7])):
+            with pytest.raises(intllm.Q48Error) as e:
+                m.forward(tok, pos, spec.TINY[6])
+            assert e.value.code == intllm.Q48_ERANGE
+    finally:
+        m.free()
+
+
+def test_mgw_roundtrip_bit_exact(ctx):
+    """A .mgw written in mgw_export's layout loads through mgw_load's checks
+    and generates the reference token stream."""
+    g = golden("tiny_generate.json")
+    cfg = intllm.Config(*g["config"])
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "tiny.mgw")
+        say("mgw write")
+        intllm.check("q48h_mgw_write_synth", intllm.host_lib().q48h_mgw_write_synth(
+            path.encode(), C.byref(cfg), g["seed"], threads()))
+        say("mgw load")
+        m = intllm.HostModel(ctx, mgw=path)
+        try:
+            toks, hs, _ = m.generate(g["prompt"], g["max_new"])
+            assert toks == g["tokens"]
+            assert ["%016x" % h for h in hs] == g["step_fnv"]
+        finally:
+            m.free()
+        # a truncated file is rejected, not read past its end
+        with open(path, "rb") as f:
+            data = f.read()
+        bad = os.path.join(d, "bad.mgw")
+        with open(bad, "wb") as f:
+            f.write(data[: len(data) // 2])
+        with pytest.raises(intllm.Q48Error):
+            intllm.HostModel(ctx, mgw=bad)
+
+
+def test_tinyllama_generate_bit_exact(ctx):
+    """Config 3: TinyLlama-1.1B shape, 32-token prompt, 128 greedy tokens."""
+    g = golden("tinyllama_generate.json")
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    try:
+        say("tinyllama synth (8.8 GB)")
+        m.synth(g["seed"], threads())
+        say("tinyllama generate")
+        toks, hs, st = m.generate(g["prompt"], g["max_new"])
+        assert toks == g["tokens"]
+        assert ["%016x" % h for h in hs] == g["step_fnv"]
+        print(f"decode {1e3 * st.decode_s / max(1, st.decode_tokens):.3f} ms/tok", flush=True)
+    finally:
+        m.free()
+
+
+def test_long_context_decode_bit_exact(ctx):
+    """Config 5: KV pre-filled to 2048 positions, 256 greedy decode steps."""
+    g = golden("longctx_decode.json")
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    try:
+        say("longctx synth + kv fill")
+        m.synth(g["seed"], threads())
+        m.kv_fill_synth(g["kv_seed"], g["prefill"], threads())
+        say("longctx decode")
+        toks, hs, st = m.decode_from(g["start_token"], g["prefill"], spec.LONG_STEPS)
+        assert toks == g["tokens"]
+        assert ["%016x" % h for h in hs] == g["step_fnv"]
+    finally:
+        m.free()
+
+
+@pytest.mark.parametrize("T", spec.GEMM_TOKENS)
+def test_gemm_config4_vs_reference(ctx, T):
+    g = golden("gemm.json")["shapes"]
+    for (N, K) in spec.GEMV_SHAPES:
+        W = O.synth(spec.gemv_w_name(N, K), N, K, spec.SEED_GEMV, spec.SIGMA_W, 1)
+        X = O.synth(spec.gemm_x_name(T, K), T, K, spec.SEED_GEMV, spec.SIGMA_ACT, 0)
+        dW, dX, dY = ctx.to_device(W), ctx.to_device(X), ctx.buffer(T * N)
+        say("gemm config4", T, N, K)
+        ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K)
+        assert O.fnv(dY.download()) == g[f"{T}x{N}x{K}"]["fnv"], (T, N, K)
+        for b in (dW, dX, dY):
+            b.free()

@@ -1,0 +1,306 @@
+"""GPU parity of every op of libintllm_hip against the oracle and the
+golden vectors recorded from the reference — bit-exact (integer work).
+
+Each test prints the case it is about to run (flushed) before the device
+call, so a failure names its case even from a truncated log.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import intllm
+import oracle_lib as O
+import spec
+from conftest import golden
+
+pytestmark = pytest.mark.gpu
+ONE = spec.ONE
+SUB_ORDER = ["fp_mul", "fp_div", "fp_sqrt", "fp_sqrt_fast", "fp_inv_sqrt", "fp_exp", "fp_log",
+             "fp_sincos_cos", "fp_sincos_sin", "fp_sigmoid", "fp_silu", "fp_rng"]
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def dev_eval(ctx, func, x, y=None, two=False):
+    n = len(x)
+    dx = ctx.to_device(x)
+    dy = ctx.to_device(y) if y is not None else None
+    o0 = ctx.buffer(n)
+    o1 = ctx.buffer(n) if two else None
+    ctx.fp_eval(func, dx.ptr, dy.ptr if dy else None, o0.ptr, o1.ptr if o1 else None, n)
+    r0 = o0.download()
+    r1 = o1.download() if two else None
+    for b in (dx, dy, o0, o1):
+        if b is not None:
+            b.free()
+    return (r0, r1) if two else r0
+
+
+def test_device_determinism_gate(ctx):
+    """The gate of fp_determinism.c evaluated by the device fp_math: all 11
+    function sub-hashes and the combined hash (the RNG sub-hash is host
+    state, not device math) equal the reference golden."""
+    g = golden("fp.json")
+    grid = spec.det_grid()
+    n = len(grid)
+    x = np.array(grid, dtype=np.int64)
+    y = np.array([grid[(i * 7 + 3) % n] for i in range(n)], dtype=np.int64)
+    pos = np.array([spec.pos_of(int(v)) for v in grid], dtype=np.int64)
+    ex = np.array([spec.exp_arg(int(v)) for v in grid], dtype=np.int64)
+    say("determinism grid", n)
+    got = {}
+    got["fp_mul"] = O.fnv(dev_eval(ctx, intllm.FP_MUL, x, y))
+    d = dev_eval(ctx, intllm.FP_DIV, x, y)
+    got["fp_div"] = O.fnv(d[y != 0])
+    got["fp_sqrt"] = O.fnv(dev_eval(ctx, intllm.FP_SQRT, pos))
+    got["fp_sqrt_fast"] = O.fnv(dev_eval(ctx, intllm.FP_SQRT_FAST, pos))
+    got["fp_inv_sqrt"] = O.fnv(dev_eval(ctx, intllm.FP_INV_SQRT, pos))
+    got["fp_exp"] = O.fnv(dev_eval(ctx, intllm.FP_EXP, ex))
+    got["fp_log"] = O.fnv(dev_eval(ctx, intllm.FP_LOG, pos))
+    c, s = dev_eval(ctx, intllm.FP_SINCOS, x, two=True)
+    got["fp_sincos_cos"], got["fp_sincos_sin"] = O.fnv(c), O.fnv(s)
+    got["fp_sigmoid"] = O.fnv(dev_eval(ctx, intllm.FP_SIGMOID, x))
+    got["fp_silu"] = O.fnv(dev_eval(ctx, intllm.FP_SILU, x))
+    got["fp_rng"] = g["sub_hashes"]["fp_rng"]
+    for k in SUB_ORDER:
+        assert got[k] == g["sub_hashes"][k], k
+    comb = np.array([int(got[k], 16) for k in SUB_ORDER], dtype=np.uint64).view(np.int64)
+    assert O.fnv(comb) == g["determinism_golden"]
+
+
+def test_device_fp_vectors_with_extremes(ctx):
+    g = golden("fp.json")["vectors"]["fnv"]
+    x, y = spec.fp_inputs()
+    pos = np.array([spec.pos_of(int(v)) for v in x], dtype=np.int64)
+    ex = np.array([spec.exp_arg(int(v)) for v in x], dtype=np.int64)
+    say("fp vectors", len(x))
+    assert O.fnv(dev_eval(ctx, intllm.FP_MUL, x, y)) == g["mul"]
+    assert O.fnv(np.where(y != 0, dev_eval(ctx, intllm.FP_DIV, x, y), 0)) == g["div"]
+    assert O.fnv(dev_eval(ctx, intllm.FP_INV_SQRT, pos)) == g["inv_sqrt"]
+    assert O.fnv(dev_eval(ctx, intllm.FP_SQRT, pos)) == g["sqrt"]
+    assert O.fnv(dev_eval(ctx, intllm.FP_LOG, pos)) == g["log"]
+    assert O.fnv(dev_eval(ctx, intllm.FP_EXP, ex)) == g["exp"]
+    assert O.fnv(dev_eval(ctx, intllm.FP_SAFE_EXP, ex)) == g["safe_exp"]
+    c, s = dev_eval(ctx, intllm.FP_SINCOS, x, two=True)
+    assert O.fnv(c) == g["cos"] and O.fnv(s) == g["sin"]
+    assert O.fnv(dev_eval(ctx, intllm.FP_SIGMOID, x)) == g["sigmoid"]
+    assert O.fnv(dev_eval(ctx, intllm.FP_SILU, x)) == g["silu"]
+
+
+def test_device_div_random_vs_oracle(ctx, oracle):
+    rng = np.random.default_rng(21)
+    a = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=4096, dtype=np.int64)
+    b = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=4096, dtype=np.int64)
+    b[:64] = rng.integers(-1000, 1000, size=64)      # tiny divisors: quotient overflows
+    b[64] = -1
+    a[65] = spec.INT64_MIN
+    b[65] = -1
+    b[b == 0] = 7
+    say("div random", a.size)
+    d = dev_eval(ctx, intllm.FP_DIV, a, b)
+    want = np.array([oracle.q48o_fp_div(int(p), int(q)) for p, q in zip(a, b)], dtype=np.int64)
+    assert np.array_equal(d, want)
+
+
+def gemv_dev(ctx, W, x, M, K, w_offset=0):
+    dW = ctx.buffer(M * K + w_offset)
+    if w_offset:
+        pad = np.zeros(w_offset, dtype=np.int64)
+        dW.upload(np.concatenate([pad, np.asarray(W, dtype=np.int64)]))
+    else:
+        dW.upload(W)
+    dx = ctx.to_device(x)
+    dy = ctx.buffer(M)
+    ctx.gemv(dy.ptr, dW.at(w_offset), dx.ptr, M, K)
+    y = dy.download()
+    for b in (dW, dx, dy):
+        b.free()
+    return y
+
+
+def test_gemv_edges(ctx):
+    g = golden("gemv.json")["edges"]
+    for (M, K, W, x), e in zip(spec.gemv_edge_cases(), g):
+        for off in (0, 1):
+            say("gemv edge", M, K, "offset", off)
+            y = gemv_dev(ctx, W, x, M, K, off)
+            assert [int(v) for v in y] == e["y"], (M, K, off)
+
+
+@pytest.mark.parametrize("M,K", spec.GEMV_SHAPES)
+def test_gemv_tinyllama_shapes(ctx, M, K):
+    W, x = spec.gemv_inputs_ref(O.synth, M, K)
+    g = golden("gemv.json")["shapes"][f"{M}x{K}"]
+    say("gemv shape", M, K)
+    y = gemv_dev(ctx, W, x, M, K)
+    assert O.fnv(y) == g["fnv"]
+
+
+@pytest.mark.parametrize("M,K", [(1, 2), (1, 3), (63, 130), (64, 4096), (33, 4098),
+                                 (17, 8200), (1000, 688), (2500, 256), (5, 12289)])
+def test_gemv_random_vs_oracle(ctx, M, K):
+    rng = np.random.default_rng(M * 7919 + K)
+    W = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=M * K, dtype=np.int64)
+    x = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=K, dtype=np.int64)
+    want = O.gemv(W, x, M, K)
+    for off in (0, 1):
+        say("gemv random", M, K, "offset", off)
+        assert np.array_equal(gemv_dev(ctx, W, x, M, K, off), want), (M, K, off)
+
+
+@pytest.mark.parametrize("T,N,K", [(1, 1, 1), (3, 5, 7), (64, 64, 16), (65, 70, 33),
+                                   (130, 129, 688), (128, 256, 2048)])
+def test_gemm_random_vs_oracle(ctx, oracle, T, N, K):
+    rng = np.random.default_rng(T * 31 + N * 7 + K)
+    W = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=N * K, dtype=np.int64)
+    X = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=T * K, dtype=np.int64)
+    want = np.empty(T * N, dtype=np.int64)
+    oracle.q48o_gemm(want.ctypes.data, W.ctypes.data, X.ctypes.data, T, N, K)
+    dW, dX, dY = ctx.to_device(W), ctx.to_device(X), ctx.buffer(T * N)
+    say("gemm", T, N, K)
+    ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K)
+    assert np.array_equal(dY.download(), want)
+    for b in (dW, dX, dY):
+        b.free()
+
+
+def test_rmsnorm(ctx, oracle):
+    g = golden("ops.json")["rmsnorm"]
+    for dim, want in g.items():
+        dim = int(dim)
+        x, w = spec.rmsnorm_inputs(O.synth, dim)
+        dx, dw, do = ctx.to_device(x), ctx.to_device(w), ctx.buffer(dim)
+        say("rmsnorm", dim)
+        ctx.rmsnorm(do.ptr, dx.ptr, dw.ptr, dim)
+        assert O.fnv(do.download()) == want, dim
+    # extremes: sum of squares wraps int128, mean < 0 -> inv_sqrt 0
+    rng = np.random.default_rng(2)
+    for dim in (1, 3, 4096, 5000):
+        x = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=dim, dtype=np.int64)
+        w = rng.integers(-ONE, ONE, size=dim, dtype=np.int64)
+        want = np.empty(dim, dtype=np.int64)
+        oracle.q48o_rmsnorm(want.ctypes.data, x.ctypes.data, w.ctypes.data, dim)
+        dx, dw, do = ctx.to_device(x), ctx.to_device(w), ctx.buffer(dim)
+        say("rmsnorm extreme", dim)
+        ctx.rmsnorm(do.ptr, dx.ptr, dw.ptr, dim)
+        assert np.array_equal(do.download(), want), dim
+
+
+def test_rope_tables_and_apply(ctx):
+    g = golden("ops.json")["rope"]
+    for (hd, ms, th) in spec.ROPE_TABLES:
+        say("rope tables", hd, ms, th)
+        ctx.rope_init(hd, ms, th)
+        cp, sp = ctx.rope_tables()
+        n = ms * hd // 2
+        c = np.empty(n, dtype=np.int64)
+        s = np.empty(n, dtype=np.int64)
+        intllm.check("d2h", intllm.hip_lib().q48_memcpy_d2h(ctx.h, c.ctypes.data, cp, n * 8))
+        intllm.check("d2h", intllm.hip_lib().q48_memcpy_d2h(ctx.h, s.ctypes.data, sp, n * 8))
+        e = g[f"{hd}x{ms}x{th}"]
+        assert O.fnv(c) == e["cos"] and O.fnv(s) == e["sin"], (hd, ms)
+        if "apply" in e:
+            v0 = O.synth("rope.vec", 1, hd, spec.SEED_OPS, spec.SIGMA_ACT, 0)
+            dv = ctx.buffer(hd)
+            for pos, want in enumerate(e["apply"]):
+                dv.upload(v0)
+                ctx.rope(dv.ptr, 1, hd, pos)
+                assert O.fnv(dv.download()) == want, pos
+
+
+def test_rope_errors(ctx):
+    ctx.rope_init(32, 64, 10000)
+    d = ctx.buffer(64)
+    with pytest.raises(intllm.Q48Error) as e:
+        ctx.rope(d.ptr, 2, 32, 64)
+    assert e.value.code == intllm.Q48_ERANGE
+    with pytest.raises(intllm.Q48Error) as e:
+        ctx.rope(d.ptr, 1, 64, 0)
+    assert e.value.code == intllm.Q48_ESTATE
+
+
+@pytest.mark.parametrize("nh,nkv,hd,max_seq,positions", [
+    (8, 2, 32, 64, [0, 1, 5, 63]),
+    (32, 4, 64, 600, [0, 300, 599]),
+    (4, 4, 64, 40, [0, 39]),
+    (6, 1, 128, 300, [257]),
+])
+def test_attention_vs_oracle(ctx, oracle, nh, nkv, hd, max_seq, positions):
+    rng = np.random.default_rng(nh * 100 + hd)
+    L = 2
+    kvd = nkv * hd
+    kc = (rng.standard_normal(L * max_seq * kvd) * ONE).astype(np.int64)
+    vc = (rng.standard_normal(L * max_seq * kvd) * ONE).astype(np.int64)
+    dk, dv = ctx.to_device(kc), ctx.to_device(vc)
+    for pos in positions:
+        for layer in range(L):
+            q = (rng.standard_normal(nh * hd) * 3 * ONE).astype(np.int64)
+            kn = (rng.standard_normal(kvd) * ONE).astype(np.int64)
+            vn = (rng.standard_normal(kvd) * ONE).astype(np.int64)
+            out = np.empty(nh * hd, dtype=np.int64)
+            oracle.q48o_attn_decode(out.ctypes.data, q.ctypes.data, kc.ctypes.data, vc.ctypes.data,
+                                    kn.ctypes.data, vn.ctypes.data, layer, pos, nh, nkv, hd, max_seq)
+            dq, dkn, dvn, do = ctx.to_device(q), ctx.to_device(kn), ctx.to_device(vn), ctx.buffer(nh * hd)
+            say("attention", nh, nkv, hd, max_seq, "pos", pos, "layer", layer)
+            ctx.attn_decode(do.ptr, dq.ptr, dk.ptr, dv.ptr, dkn.ptr, dvn.ptr, layer, pos, nh, nkv, hd, max_seq)
+            assert np.array_equal(do.download(), out), (pos, layer)
+            # the cache write at [layer][pos] happened exactly like the oracle's
+            assert np.array_equal(dk.download(), kc) and np.array_equal(dv.download(), vc)
+            for b in (dq, dkn, dvn, do):
+                b.free()
+    dk.free()
+    dv.free()
+
+
+def test_silu_mul_vs_oracle(ctx, oracle):
+    x, y = spec.fp_inputs()
+    rng = np.random.default_rng(4)
+    g = np.concatenate([x, (rng.standard_normal(5632) * 4 * ONE).astype(np.int64)])
+    u = np.concatenate([y, (rng.standard_normal(5632) * ONE).astype(np.int64)])
+    n = g.size
+    want = np.empty(n, dtype=np.int64)
+    oracle.q48o_silu_mul(want.ctypes.data, g.ctypes.data, u.ctypes.data, n)
+    dg, du, do = ctx.to_device(g), ctx.to_device(u), ctx.buffer(n)
+    say("silu_mul", n)
+    ctx.silu_mul(do.ptr, dg.ptr, du.ptr, n)
+    assert np.array_equal(do.download(), want)
+
+
+def test_add_embed_argmax(ctx):
+    rng = np.random.default_rng(8)
+    a = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=3001, dtype=np.int64)
+    b = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=3001, dtype=np.int64)
+    da, db = ctx.to_device(a), ctx.to_device(b)
+    say("add")
+    ctx.add(da.ptr, db.ptr, a.size)
+    assert np.array_equal(da.download(), (a.view(np.uint64) + b.view(np.uint64)).view(np.int64))
+    table = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=7 * 300, dtype=np.int64)
+    dt, do = ctx.to_device(table), ctx.buffer(300)
+    say("embed")
+    ctx.embed(do.ptr, dt.ptr, 5, 300)
+    assert np.array_equal(do.download(), table[1500:1800])
+    # argmax: first index of the maximum, ties included
+    for n in (1, 2, 1023, 1025, 32000):
+        v = rng.integers(-1000, 1000, size=n, dtype=np.int64)
+        if n > 10:
+            v[n // 3] = v[n - 2] = v.max() + 5
+        dvv = ctx.to_device(v)
+        say("argmax", n)
+        assert ctx.argmax(dvv.ptr, n) == int(np.argmax(v))
+        dvv.free()
+
+
+def test_abi_rejects_bad_arguments(ctx):
+    lib = intllm.hip_lib()
+    assert lib.q48_gemv(ctx.h, None, None, None, 4, 4) == intllm.Q48_EINVAL
+    d = ctx.buffer(16)
+    assert lib.q48_gemv(ctx.h, d.ptr, d.ptr, d.ptr, 0, 4) == intllm.Q48_EINVAL
+    assert lib.q48_gemv(ctx.h, d.ptr, d.ptr + 4, d.ptr, 1, 1) == intllm.Q48_EINVAL
+    assert lib.q48_attn_decode(ctx.h, d.ptr, d.ptr, d.ptr, d.ptr, d.ptr, d.ptr, 0, 5, 2, 1, 8,
+                               4) == intllm.Q48_ERANGE
+    assert lib.q48_attn_decode(ctx.h, d.ptr, d.ptr, d.ptr, d.ptr, d.ptr, d.ptr, 0, 0, 3, 2, 8,
+                               4) == intllm.Q48_EINVAL
+    assert lib.q48_embed(ctx.h, d.ptr, d.ptr, -1, 4) == intllm.Q48_ERANGE
