@@ -180,18 +180,18 @@ def main():
         nxt, _ = m.forward(tok, pos, cfg.vocab, logits=False)
     toks = [nxt]
     pos = len(prompt)
-    for _ in range(args.warmup):
-        nxt, _ = m.forward(toks[-1], pos, cfg.vocab, logits=False)
-        toks.append(nxt)
-        pos += 1
+    # warm-up decode steps (also captures the decode-step graph)
+    _, steps, _ = m.decode_graph(toks[-1], pos, args.warmup)
+    toks += steps
+    pos += args.warmup
     ctx.sync()
+    # timed: K greedy decode steps replayed from the graph, argmax on device
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        nxt, _ = m.forward(toks[-1], pos, cfg.vocab, logits=False)
-        toks.append(nxt)
-        pos += 1
+    _, steps, _ = m.decode_graph(toks[-1], pos, args.steps)
     ctx.sync()
     dt = time.perf_counter() - t0
+    toks += steps
+    pos += args.steps
     ms = 1e3 * dt / args.steps
     log(f"decode {ms:.3f} ms/tok")
 
@@ -205,7 +205,7 @@ def main():
     ctx.prof_enable(True)
     ctx.prof_read(reset=True)
     p0 = len(prompt) + args.warmup
-    for i in range(min(args.steps, 16)):
+    for i in range(min(args.steps, 16)):   # eager, same fused ops as the graph
         m.forward(toks[args.warmup + i], p0 + i, cfg.vocab, logits=False)
     prof = ctx.prof_read(reset=True)
     ctx.prof_enable(False)

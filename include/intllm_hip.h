@@ -131,12 +131,64 @@ int q48_rope_tables(q48_ctx *ctx, const int64_t **cos_t, const int64_t **sin_t);
 int q48_fp_eval(q48_ctx *ctx, int func, const int64_t *x, const int64_t *y,
                 int64_t *out0, int64_t *out1, int n);
 
+/* ---- fused decode ops ------------------------------------------------------- */
+/* Each is exactly the composition it names (same bits as the separate ops);
+ * fusing removes launches and a round trip of the activation through HBM. */
+
+/* y = W . rmsnorm(x, norm_w): rmsnorm (llama_int.c:1048-1058) followed by
+ * matmul_vec (llama_int.c:1014-1046), K = dim of x.  Used for q|k|v
+ * (llama_int.c:1384-1389) and the lm_head (llama_int.c:2876-2880). */
+int q48_rmsnorm_gemv(q48_ctx *ctx, int64_t *y, const int64_t *W, const int64_t *x,
+                     const int64_t *norm_w, int M, int K);
+
+/* acc += W . x: matmul_vec then the residual add (llama_int.c:1532-1535,
+ * 1553-1556). */
+int q48_gemv_residual(q48_ctx *ctx, int64_t *acc, const int64_t *W, const int64_t *x,
+                      int M, int K);
+
+/* out[i] = fp_mul(fp_silu(g_i), u_i) with g = rows 0..ffn-1 and u = rows
+ * ffn..2ffn-1 of Wgu . rmsnorm(x, norm_w): the post-attention norm, the
+ * gate/up projections and SwiGLU (llama_int.c:1544-1552).  Wgu [2*ffn][K]
+ * is gate_proj stacked on up_proj. */
+int q48_rmsnorm_gemv_swiglu(q48_ctx *ctx, int64_t *out, const int64_t *Wgu,
+                            const int64_t *x, const int64_t *norm_w, int ffn, int K);
+
+/* q48_attn_decode with the RoPE of q and k_new fused in (rope_apply,
+ * llama_int.c:997-1008, 1392-1395): q and k_new are given unrotated, the
+ * cache receives rotated k.  Needs q48_rope_init(head_dim, >= max_seq) and
+ * head_dim % 8 == 0. */
+int q48_attn_decode_rope(q48_ctx *ctx, int64_t *out, const int64_t *q,
+                         int64_t *kcache, int64_t *vcache, const int64_t *k_new,
+                         const int64_t *v_new, int layer, int pos, int n_heads,
+                         int n_kv, int head_dim, int max_seq);
+
+/* ---- device-resident decode steps (graph replay) ---------------------------- */
+/* No reference counterpart: llama_int's generate (llama_int.c:3067-3135)
+ * passes token and pos as C arguments each call.  In step mode q48_embed
+ * reads the token, and q48_rope / q48_attn_decode(_rope) read pos, from a
+ * device-side state {token, pos, count} instead of their arguments, and
+ * q48_argmax_step writes the greedy token back into that state (pos += 1),
+ * so one captured forward can be replayed for consecutive tokens with no
+ * host round trip.  Kernels ignore a state position outside the cache. */
+int q48_step_mode(q48_ctx *ctx, int on);
+int q48_step_set(q48_ctx *ctx, int token, int pos);      /* stream-ordered */
+int q48_step_get(q48_ctx *ctx, int *token, int *pos, int *count);  /* syncs */
+/* argmax (llama_int.c:2888-2893) of v[0..n) into the state; the token is
+ * also stored at d_tokens[count] while count < cap. */
+int q48_argmax_step(q48_ctx *ctx, const int64_t *v, int n, int *d_tokens, int cap);
+/* Capture the ops enqueued between begin and end into the context's graph. */
+int q48_graph_begin(q48_ctx *ctx);
+int q48_graph_end(q48_ctx *ctx);
+int q48_graph_launch(q48_ctx *ctx, int times);
+int q48_graph_drop(q48_ctx *ctx);
+
 /* ---- kernel timing (diagnostic) -------------------------------------------- */
 
-/* HIP-event timing of every q48_gemv launch on the context's stream while
- * enabled (no reference counterpart: llama_int's profiler, llama_int.c:65-108,
- * times whole forwards with clock_gettime).  `bytes` is the algorithmic
- * traffic 8*(M*K + K + M) per launch. */
+/* HIP-event timing of every GEMV launch (q48_gemv and the fused GEMV entry
+ * points) on the context's stream while enabled (no reference counterpart:
+ * llama_int's profiler, llama_int.c:65-108, times whole forwards with
+ * clock_gettime).  `bytes` is the algorithmic traffic 8*(M*K + K + outputs)
+ * per launch.  Not recorded while a graph is being captured. */
 typedef struct {
     int launches;
     double ms;       /* sum of launch durations */

@@ -75,11 +75,14 @@ int q48_ctx_create(q48_ctx **out, int device)
         return Q48_EHIP;
     }
     if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
-        hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess) {
+        hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess ||
+        hipMalloc(&c->d_step, 4 * sizeof(int)) != hipSuccess) {
         q48_ctx_destroy(c);
         return Q48_ENOMEM;
     }
     int rc = launch_rc(q48_launch_math_init(c));
+    if (rc == Q48_OK)
+        rc = launch_rc(q48_launch_step_set(c, 0, 0));
     if (rc == Q48_OK)
         rc = hip_rc(hipStreamSynchronize(c->stream));
     if (rc != Q48_OK) {
@@ -101,6 +104,12 @@ int q48_ctx_destroy(q48_ctx *c)
     (void)hipFree(c->rope_sin);
     (void)hipFree(c->ws);
     (void)hipFree(c->d_scalar);
+    (void)hipFree(c->d_step);
+    (void)hipFree(c->tmp);
+    if (c->graph_exec)
+        (void)hipGraphExecDestroy(c->graph_exec);
+    if (c->graph)
+        (void)hipGraphDestroy(c->graph);
     for (int i = 0; i < c->prof_cap; ++i) {
         if (c->prof[i].a)
             (void)hipEventDestroy(c->prof[i].a);
@@ -127,6 +136,8 @@ int q48_malloc(q48_ctx *c, void **dptr, size_t bytes)
 
 int q48_free(q48_ctx *c, void *dptr)
 {
+    if (c && c->capturing)
+        return Q48_ESTATE;
     if (!c)
         return Q48_EINVAL;
     if (!dptr)
@@ -138,6 +149,8 @@ int q48_free(q48_ctx *c, void *dptr)
 
 int q48_memcpy_h2d(q48_ctx *c, void *dst, const void *src, size_t bytes)
 {
+    if (c && c->capturing)
+        return Q48_ESTATE;
     if (!c || (bytes && (!dst || !src)))
         return Q48_EINVAL;
     if (!bytes)
@@ -149,6 +162,8 @@ int q48_memcpy_h2d(q48_ctx *c, void *dst, const void *src, size_t bytes)
 
 int q48_memcpy_d2h(q48_ctx *c, void *dst, const void *src, size_t bytes)
 {
+    if (c && c->capturing)
+        return Q48_ESTATE;
     if (!c || (bytes && (!dst || !src)))
         return Q48_EINVAL;
     if (!bytes)
@@ -182,8 +197,53 @@ int q48_sync(q48_ctx *c)
 {
     if (!c)
         return Q48_EINVAL;
+    if (c->capturing)
+        return Q48_ESTATE;
     return hip_rc(hipStreamSynchronize(c->stream));
 }
+
+namespace {
+// HIP-event bracket of one GEMV launch while timing is enabled.
+q48_ctx::ProfRec *prof_begin(q48_ctx *c, double bytes, int *rc)
+{
+    *rc = Q48_OK;
+    if (!c->prof_on || c->capturing)
+        return nullptr;
+    if (c->prof_n == c->prof_cap) {
+        int cap = c->prof_cap ? 2 * c->prof_cap : 1024;
+        auto *p = (q48_ctx::ProfRec *)realloc(c->prof, sizeof(q48_ctx::ProfRec) * cap);
+        if (!p) {
+            *rc = Q48_ENOMEM;
+            return nullptr;
+        }
+        for (int i = c->prof_cap; i < cap; ++i)
+            p[i].a = p[i].b = nullptr;
+        c->prof = p;
+        c->prof_cap = cap;
+    }
+    q48_ctx::ProfRec *r = &c->prof[c->prof_n];
+    if ((!r->a && hipEventCreate(&r->a) != hipSuccess) ||
+        (!r->b && hipEventCreate(&r->b) != hipSuccess) ||
+        hipEventRecord(r->a, c->stream) != hipSuccess) {
+        *rc = Q48_EHIP;
+        return nullptr;
+    }
+    r->bytes = bytes;
+    return r;
+}
+
+int prof_end(q48_ctx *c, q48_ctx::ProfRec *r, int rc)
+{
+    if (r && rc == Q48_OK) {
+        if (hipEventRecord(r->b, c->stream) != hipSuccess)
+            return Q48_EHIP;
+        c->prof_n++;
+    }
+    return rc;
+}
+
+double gemv_bytes(int M, int K, int out) { return 8.0 * ((double)M * K + K + out); }
+} // namespace
 
 int q48_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x, int M, int K)
 {
@@ -191,33 +251,11 @@ int q48_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x, int M, 
         return Q48_EINVAL;
     if ((((uintptr_t)W | (uintptr_t)x | (uintptr_t)y) & 7) != 0)
         return Q48_EINVAL;
-    q48_ctx::ProfRec *r = nullptr;
-    if (c->prof_on) {
-        if (c->prof_n == c->prof_cap) {
-            int cap = c->prof_cap ? 2 * c->prof_cap : 1024;
-            auto *p = (q48_ctx::ProfRec *)realloc(c->prof, sizeof(q48_ctx::ProfRec) * cap);
-            if (!p)
-                return Q48_ENOMEM;
-            for (int i = c->prof_cap; i < cap; ++i)
-                p[i].a = p[i].b = nullptr;
-            c->prof = p;
-            c->prof_cap = cap;
-        }
-        r = &c->prof[c->prof_n];
-        if ((!r->a && hipEventCreate(&r->a) != hipSuccess) ||
-            (!r->b && hipEventCreate(&r->b) != hipSuccess))
-            return Q48_EHIP;
-        r->bytes = 8.0 * ((double)M * K + K + M);
-        if (hipEventRecord(r->a, c->stream) != hipSuccess)
-            return Q48_EHIP;
-    }
-    int rc = launch_rc(q48_launch_gemv(c, y, W, x, M, K));
-    if (r && rc == Q48_OK) {
-        if (hipEventRecord(r->b, c->stream) != hipSuccess)
-            return Q48_EHIP;
-        c->prof_n++;
-    }
-    return rc;
+    int rc;
+    q48_ctx::ProfRec *r = prof_begin(c, gemv_bytes(M, K, M), &rc);
+    if (rc)
+        return rc;
+    return prof_end(c, r, launch_rc(q48_launch_gemv(c, y, W, x, M, K)));
 }
 
 int q48_prof_enable(q48_ctx *c, int on)
@@ -303,7 +341,8 @@ int q48_rope(q48_ctx *c, int64_t *vec, int n_heads, int head_dim, int pos)
         return Q48_ESTATE;
     if (pos < 0 || pos >= c->rope_max_seq)
         return Q48_ERANGE;
-    return launch_rc(q48_launch_rope(c, vec, n_heads, head_dim, nullptr, pos));
+    return launch_rc(q48_launch_rope(c, vec, n_heads, head_dim,
+                                     c->step_mode ? c->d_step + 1 : nullptr, pos));
 }
 
 int q48_attn_decode(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
@@ -317,8 +356,12 @@ int q48_attn_decode(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
         return Q48_EINVAL;
     if (pos < 0 || pos >= max_seq)
         return Q48_ERANGE;
-    int rc = q48_launch_attn(c, out, q, kcache, vcache, k_new, v_new, layer, nullptr, pos,
-                             n_heads, n_kv, head_dim, max_seq);
+    const int *dp = c->step_mode ? c->d_step + 1 : nullptr;
+    int rc = head_dim % 8 == 0
+                 ? q48_launch_attn_v2(c, out, q, kcache, vcache, k_new, v_new, layer, dp, pos,
+                                      n_heads, n_kv, head_dim, max_seq, 0)
+                 : q48_launch_attn(c, out, q, kcache, vcache, k_new, v_new, layer, dp, pos,
+                                   n_heads, n_kv, head_dim, max_seq);
     if (rc == Q48_ENOMEM)
         return rc;
     return launch_rc(rc);
@@ -344,7 +387,8 @@ int q48_embed(q48_ctx *c, int64_t *out, const int64_t *table, int token, int dim
         return Q48_EINVAL;
     if (token < 0)
         return Q48_ERANGE;
-    return launch_rc(q48_launch_embed(c, out, table, nullptr, token, dim));
+    return launch_rc(q48_launch_embed(c, out, table, c->step_mode ? c->d_step : nullptr,
+                                      token, dim));
 }
 
 int q48_argmax(q48_ctx *c, const int64_t *v, int n, int *host_out)
@@ -381,6 +425,223 @@ int q48_fp_eval(q48_ctx *c, int func, const int64_t *x, const int64_t *y, int64_
     if (func == 7 && !out1)
         return Q48_EINVAL;
     return launch_rc(q48_launch_fp_eval(c, func, x, y, out0, out1, n));
+}
+
+
+// ---- fused decode ops ------------------------------------------------------
+
+namespace {
+int tmp_reserve(q48_ctx *c, size_t bytes)
+{
+    if (bytes <= c->tmp_bytes)
+        return Q48_OK;
+    if (c->capturing)
+        return Q48_ESTATE;
+    if (c->tmp) {
+        if (hipStreamSynchronize(c->stream) != hipSuccess)
+            return Q48_EHIP;
+        (void)hipFree(c->tmp);
+        c->tmp = nullptr;
+        c->tmp_bytes = 0;
+    }
+    if (hipMalloc(&c->tmp, bytes) != hipSuccess)
+        return Q48_ENOMEM;
+    c->tmp_bytes = bytes;
+    return Q48_OK;
+}
+
+bool bad_ptrs(const void *a, const void *b, const void *d)
+{
+    return !a || !b || !d || ((((uintptr_t)a) | ((uintptr_t)b) | ((uintptr_t)d)) & 7);
+}
+} // namespace
+
+int q48_rmsnorm_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                     const int64_t *norm_w, int M, int K)
+{
+    if (!c || bad_ptrs(y, W, x) || !norm_w || M <= 0 || K <= 0 || M > kMaxDim || K > kMaxDim)
+        return Q48_EINVAL;
+    if (q48_gemv_v2_ok(W, K)) {
+        int prc;
+        q48_ctx::ProfRec *r = prof_begin(c, gemv_bytes(M, K, M), &prc);
+        if (prc)
+            return prc;
+        return prof_end(c, r, launch_rc(q48_launch_gemv_fused(c, y, W, x, norm_w, M, K, 1, 0)));
+    }
+    int rc = tmp_reserve(c, (size_t)K * 8);
+    if (rc)
+        return rc;
+    int64_t *t = (int64_t *)c->tmp;
+    rc = launch_rc(q48_launch_rmsnorm(c, t, x, norm_w, K));
+    return rc ? rc : launch_rc(q48_launch_gemv(c, y, W, t, M, K));
+}
+
+int q48_gemv_residual(q48_ctx *c, int64_t *acc, const int64_t *W, const int64_t *x, int M,
+                      int K)
+{
+    if (!c || bad_ptrs(acc, W, x) || M <= 0 || K <= 0 || M > kMaxDim || K > kMaxDim)
+        return Q48_EINVAL;
+    if (q48_gemv_v2_ok(W, K)) {
+        int prc;
+        q48_ctx::ProfRec *r = prof_begin(c, gemv_bytes(M, K, M), &prc);
+        if (prc)
+            return prc;
+        return prof_end(c, r, launch_rc(q48_launch_gemv_fused(c, acc, W, x, nullptr, M, K, 0, 1)));
+    }
+    int rc = tmp_reserve(c, (size_t)M * 8);
+    if (rc)
+        return rc;
+    int64_t *t = (int64_t *)c->tmp;
+    rc = launch_rc(q48_launch_gemv(c, t, W, x, M, K));
+    return rc ? rc : launch_rc(q48_launch_add(c, acc, t, M));
+}
+
+int q48_rmsnorm_gemv_swiglu(q48_ctx *c, int64_t *out, const int64_t *Wgu, const int64_t *x,
+                            const int64_t *norm_w, int ffn, int K)
+{
+    if (!c || bad_ptrs(out, Wgu, x) || !norm_w || ffn <= 0 || K <= 0 || ffn > kMaxDim / 2 ||
+        K > kMaxDim)
+        return Q48_EINVAL;
+    if (q48_gemv_v2_ok(Wgu, K)) {
+        int prc;
+        q48_ctx::ProfRec *r = prof_begin(c, gemv_bytes(2 * ffn, K, ffn), &prc);
+        if (prc)
+            return prc;
+        return prof_end(c, r,
+                        launch_rc(q48_launch_gemv_fused(c, out, Wgu, x, norm_w, 2 * ffn, K, 1, 2)));
+    }
+    int rc = tmp_reserve(c, ((size_t)K + 2 * (size_t)ffn) * 8);
+    if (rc)
+        return rc;
+    int64_t *xn = (int64_t *)c->tmp, *t = xn + K;
+    if ((rc = launch_rc(q48_launch_rmsnorm(c, xn, x, norm_w, K))) ||
+        (rc = launch_rc(q48_launch_gemv(c, t, Wgu, xn, 2 * ffn, K))))
+        return rc;
+    return launch_rc(q48_launch_silu_mul(c, out, t, t + ffn, ffn));
+}
+
+int q48_attn_decode_rope(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
+                         int64_t *vcache, const int64_t *k_new, const int64_t *v_new, int layer,
+                         int pos, int n_heads, int n_kv, int head_dim, int max_seq)
+{
+    if (!c || !out || !q || !kcache || !vcache || !k_new || !v_new)
+        return Q48_EINVAL;
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || head_dim <= 0 ||
+        head_dim > kMaxHeadDim || 256 % head_dim || head_dim % 8 || layer < 0 || max_seq <= 0)
+        return Q48_EINVAL;
+    if (!c->rope_cos || head_dim != c->rope_head_dim || max_seq > c->rope_max_seq)
+        return Q48_ESTATE;
+    if (pos < 0 || pos >= max_seq)
+        return Q48_ERANGE;
+    const int *dp = c->step_mode ? c->d_step + 1 : nullptr;
+    int rc = q48_launch_attn_v2(c, out, q, kcache, vcache, k_new, v_new, layer, dp, pos, n_heads,
+                                n_kv, head_dim, max_seq, 1);
+    if (rc == Q48_ENOMEM)
+        return rc;
+    return launch_rc(rc);
+}
+
+// ---- decode-step state and graphs --------------------------------------------
+
+int q48_step_mode(q48_ctx *c, int on)
+{
+    if (!c)
+        return Q48_EINVAL;
+    c->step_mode = on != 0;
+    return Q48_OK;
+}
+
+int q48_step_set(q48_ctx *c, int token, int pos)
+{
+    if (!c || token < 0 || pos < 0)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_step_set(c, token, pos));
+}
+
+int q48_step_get(q48_ctx *c, int *token, int *pos, int *count)
+{
+    if (!c)
+        return Q48_EINVAL;
+    if (c->capturing)
+        return Q48_ESTATE;
+    int st[4];
+    if (hipMemcpyAsync(st, c->d_step, 4 * sizeof(int), hipMemcpyDeviceToHost, c->stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q48_EHIP;
+    if (token)
+        *token = st[0];
+    if (pos)
+        *pos = st[1];
+    if (count)
+        *count = st[2];
+    return Q48_OK;
+}
+
+int q48_argmax_step(q48_ctx *c, const int64_t *v, int n, int *d_tokens, int cap)
+{
+    if (!c || !v || n <= 0 || cap < 0 || (cap > 0 && !d_tokens))
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_step_argmax(c, d_tokens, cap, v, n));
+}
+
+int q48_graph_begin(q48_ctx *c)
+{
+    if (!c || c->capturing)
+        return Q48_EINVAL;
+    if (c->graph_exec) {
+        (void)hipGraphExecDestroy(c->graph_exec);
+        c->graph_exec = nullptr;
+    }
+    if (c->graph) {
+        (void)hipGraphDestroy(c->graph);
+        c->graph = nullptr;
+    }
+    if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+        return Q48_EHIP;
+    c->capturing = 1;
+    return Q48_OK;
+}
+
+int q48_graph_end(q48_ctx *c)
+{
+    if (!c || !c->capturing)
+        return Q48_EINVAL;
+    c->capturing = 0;
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture(c->stream, &g) != hipSuccess || !g)
+        return Q48_EHIP;
+    c->graph = g;
+    if (hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0) != hipSuccess) {
+        c->graph_exec = nullptr;
+        return Q48_EHIP;
+    }
+    return Q48_OK;
+}
+
+int q48_graph_launch(q48_ctx *c, int times)
+{
+    if (!c || times < 0 || c->capturing)
+        return Q48_EINVAL;
+    if (!c->graph_exec)
+        return Q48_ESTATE;
+    for (int i = 0; i < times; ++i)
+        if (hipGraphLaunch(c->graph_exec, c->stream) != hipSuccess)
+            return Q48_EHIP;
+    return Q48_OK;
+}
+
+int q48_graph_drop(q48_ctx *c)
+{
+    if (!c || c->capturing)
+        return Q48_EINVAL;
+    if (c->graph_exec)
+        (void)hipGraphExecDestroy(c->graph_exec);
+    if (c->graph)
+        (void)hipGraphDestroy(c->graph);
+    c->graph_exec = nullptr;
+    c->graph = nullptr;
+    return Q48_OK;
 }
 
 } // extern "C"

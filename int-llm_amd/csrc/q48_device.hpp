@@ -60,7 +60,7 @@ __device__ __forceinline__ uint64_t q48_udiv128_step(uint64_t hi, uint64_t lo,
     return q;
 }
 
-__device__ __forceinline__ q48_u128 q48_udiv128_64(q48_u128 n, uint64_t d)
+__device__ __forceinline__ q48_u128 q48_udiv128_64_slow(q48_u128 n, uint64_t d)
 {
     uint64_t nh = (uint64_t)(n >> 64), nl = (uint64_t)n;
     uint64_t qh = nh / d;
@@ -68,6 +68,32 @@ __device__ __forceinline__ q48_u128 q48_udiv128_64(q48_u128 n, uint64_t d)
     uint64_t r;
     uint64_t ql = q48_udiv128_step(r1, nl, d, &r);
     return ((q48_u128)qh << 64) | ql;
+}
+
+// floor(n / d), exact.  Fast path when the quotient is below 2^52 (every
+// division of the forward pass: fp_div(ONE, e^x), the softmax and the
+// sigmoid all have quotients <= 2^48): an FP64 estimate, within a few
+// units of the true quotient, fixed up by exact 128-bit remainder steps
+// until 0 <= n - q d < d.  Otherwise the long division above.
+__device__ __forceinline__ q48_u128 q48_udiv128_64(q48_u128 n, uint64_t d)
+{
+    const q48_u128 hi52 = n >> 52;
+    if ((uint64_t)(hi52 >> 64) == 0 && (uint64_t)hi52 < d) {
+        const double nd = (double)(uint64_t)(n >> 64) * 18446744073709551616.0 +
+                          (double)(uint64_t)n;
+        uint64_t q = (uint64_t)(nd / (double)d);
+        q48_i128 r = (q48_i128)(n - (q48_u128)q * d);
+        while (r < 0) {
+            --q;
+            r += d;
+        }
+        while (r >= (q48_i128)d) {
+            ++q;
+            r -= d;
+        }
+        return q;
+    }
+    return q48_udiv128_64_slow(n, d);
 }
 
 // fp_w_divs (fp_math.h:249-256) for a divisor that fits int64: truncating

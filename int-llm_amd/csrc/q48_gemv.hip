@@ -146,6 +146,172 @@ __global__ __launch_bounds__(64 * RPB) void k_gemv(int64_t *__restrict__ y,
         y[row] = (int64_t)((q48_i128)S >> 48);
 }
 
+// ---------------------------------------------------------------------------
+// GEMV v2: 8 rows per block, one 8-lane group per row (each load
+// instruction of a group reads one full 128-byte line of its row), NW
+// waves per block each taking one K-segment of all 8 rows.  Every lane
+// issues UNR 16-byte loads before it computes, so a wave keeps
+// UNR * 1 KiB of weights in flight.  Per-segment partials meet in LDS.
+//
+// PRO = 1 fuses rmsnorm (llama_int.c:1048-1058) into the x staging: every
+// block recomputes the (integer, order-free) statistics of the whole x and
+// stages fp_mul(fp_mul(x, r), norm_w) — the values rmsnorm would write.
+// EPI = 0 stores y; EPI = 1 adds y into `out` (the residual adds,
+// llama_int.c:1535, 1556); EPI = 2 reads W as [gate; up] (M = 2 ffn rows):
+// block b takes gate rows 4b..4b+3 (groups 0-3) and the matching up rows
+// ffn+4b.. (groups 4-7) and stores fp_mul(fp_silu(gate_i), up_i) to y[i]
+// (llama_int.c:1549-1552).
+// ---------------------------------------------------------------------------
+constexpr int V2_RB = 8;
+
+template <int NW>
+__device__ __forceinline__ int64_t block_rms_inv(const int64_t *__restrict__ x, int K,
+                                                  uint64_t *red_lo, uint64_t *red_hi)
+{
+    const int tid = threadIdx.x;
+    q48_u128 ss = 0;
+    for (int j = tid; j < K; j += 64 * NW) {
+        const int64_t v = x[j];
+        ss += (q48_u128)((q48_i128)v * v);
+    }
+    ss = q48_wave_sum128(ss);
+    if ((tid & 63) == 0) {
+        red_lo[tid >> 6] = (uint64_t)ss;
+        red_hi[tid >> 6] = (uint64_t)(ss >> 64);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        q48_u128 t = 0;
+        for (int w = 0; w < NW; ++w)
+            t += ((q48_u128)red_hi[w] << 64) | red_lo[w];
+        int64_t ms = (int64_t)q48_divs_128_64((q48_i128)t >> 48, (int64_t)K);
+        ms = (int64_t)((uint64_t)ms + 2814749767ull);
+        red_lo[NW] = (uint64_t)q48_inv_sqrt(ms);
+    }
+    __syncthreads();
+    return (int64_t)red_lo[NW];
+}
+
+template <int NW, int UNR, int PRO, int EPI>
+__global__ __launch_bounds__(64 * NW) void k_gemv_v2(int64_t *__restrict__ y,
+                                                    const int64_t *__restrict__ W,
+                                                    const int64_t *__restrict__ x,
+                                                    const int64_t *__restrict__ norm_w,
+                                                    int M, int K, int seg)
+{
+    extern __shared__ __align__(16) uint64_t xs[];   // K flipped x values (segments)
+    __shared__ uint64_t red_lo[NW + 1], red_hi[NW];
+    __shared__ uint64_t part[NW][V2_RB][2];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 3, l8 = lane & 7;
+    const int row0 = blockIdx.x * V2_RB;
+    const int ffn = M >> 1;
+    const int k0 = wave * seg;
+    const int kn = max(0, min(seg, K - k0));
+
+    int64_t r = 0;
+    if (PRO == 1)
+        r = block_rms_inv<NW>(x, K, red_lo, red_hi);
+
+    // stage this wave's segment of x, flipped; sum x over the segment
+    uint64_t xsum = 0;
+    uint64_t *xw = xs + (size_t)wave * seg;
+    for (int j = lane; j < kn; j += 64) {
+        int64_t v = x[k0 + j];
+        if (PRO == 1)
+            v = q48_mul(q48_mul(v, r), norm_w[k0 + j]);
+        xw[j] = (uint64_t)v ^ 0x8000000000000000ull;
+        xsum += (uint64_t)v;
+    }
+    xsum = (uint64_t)q48_wave_sum64((int64_t)xsum);
+    __syncthreads();
+
+    // row of group g (EPI 2: gate rows 4b+g, then up rows ffn+4b+g-4)
+    const int pr = blockIdx.x * 4 + (g & 3);
+    const int row = EPI == 2 ? (g < 4 ? pr : ffn + pr) : row0 + g;
+    const bool live = EPI == 2 ? pr < ffn : row < M;
+    LimbAcc A = {0, 0, 0, 0, 0, 0};
+    if (live) {
+        const ulonglong2 *w2 = reinterpret_cast<const ulonglong2 *>(W + (size_t)row * K + k0) + l8;
+        const uint4 *x4 = reinterpret_cast<const uint4 *>(xw) + l8;
+        const int nt = kn >> 4;
+        int t = 0;
+        for (; t + UNR <= nt; t += UNR) {
+            ulonglong2 wv[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; ++u)
+                wv[u] = w2[(t + u) * 8];
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+                const uint4 xv = x4[(t + u) * 8];
+                mac_flip(A, xv.x, xv.y, wv[u].x);
+                mac_flip(A, xv.z, xv.w, wv[u].y);
+            }
+        }
+        for (; t < nt; ++t) {
+            const ulonglong2 wv = w2[t * 8];
+            const uint4 xv = x4[t * 8];
+            mac_flip(A, xv.x, xv.y, wv.x);
+            mac_flip(A, xv.z, xv.w, wv.y);
+        }
+        // segment tail: kn % 16 elements (even), one pair per lane
+        if (2 * l8 < (kn & 15)) {
+            const ulonglong2 wv = w2[nt * 8];
+            const uint4 xv = x4[nt * 8];
+            mac_flip(A, xv.x, xv.y, wv.x);
+            mac_flip(A, xv.z, xv.w, wv.y);
+        }
+    }
+    q48_u128 S = acc_value(A);
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        const uint64_t lo = (uint64_t)S, hi = (uint64_t)(S >> 64);
+        S += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
+    }
+    if (l8 == 0) {
+        S -= (q48_u128)xsum << 63;
+        part[wave][g][0] = (uint64_t)S;
+        part[wave][g][1] = (uint64_t)(S >> 64);
+    }
+    __syncthreads();
+    if (tid < V2_RB) {
+        q48_u128 T = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+            T += ((q48_u128)part[w][tid][1] << 64) | part[w][tid][0];
+        const int64_t v = (int64_t)((q48_i128)T >> 48);
+        const int rr = row0 + tid;
+        if (EPI == 0) {
+            if (rr < M)
+                y[rr] = v;
+        } else if (EPI == 1) {
+            if (rr < M)
+                y[rr] = (int64_t)((uint64_t)y[rr] + (uint64_t)v);
+        } else {
+            // threads 0-3 hold gate rows, 4-7 the matching up rows
+            const int64_t up = __shfl_down(v, 4, 64);
+            const int i = blockIdx.x * 4 + tid;
+            if (tid < 4 && i < ffn)
+                y[i] = q48_mul(q48_silu(v), up);
+        }
+    }
+}
+
+template <int PRO, int EPI>
+static int launch_v2(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                     const int64_t *norm_w, int M, int K)
+{
+    constexpr int NW = 8;
+    // segment: K / NW rounded up to a multiple of 16 elements
+    const int seg = ((K + NW - 1) / NW + 15) / 16 * 16;
+    const size_t lds = (size_t)seg * NW * sizeof(uint64_t);
+    dim3 grid(EPI == 2 ? (M / 2 + 3) / 4 : (M + V2_RB - 1) / V2_RB);
+    hipLaunchKernelGGL((k_gemv_v2<NW, 16, PRO, EPI>), grid, dim3(64 * NW), lds, c->stream,
+                       y, W, x, norm_w, M, K, seg);
+    return (int)hipGetLastError();
+}
+
 // Per-row sums mod 2^64 (one wave per row): the 2^63 correction terms of
 // the flipped-limb GEMM.
 __global__ __launch_bounds__(256) void k_rowsum(uint64_t *__restrict__ out,
@@ -268,9 +434,29 @@ __global__ __launch_bounds__(256) void k_gemm(int64_t *__restrict__ Y,
 
 } // namespace
 
+// Largest K the v2 kernel stages in LDS (64 KiB of x).
+constexpr int V2_MAX_K = 7680;   // staged x (seg * 8 waves * 8 B) stays under 62 KiB
+
+bool q48_gemv_v2_ok(const int64_t *W, int K)
+{
+    return K % 2 == 0 && K <= V2_MAX_K && (((uintptr_t)W & 15) == 0);
+}
+
+int q48_launch_gemv_fused(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                          const int64_t *norm_w, int M, int K, int pro, int epi)
+{
+    if (pro)
+        return epi == 2 ? launch_v2<1, 2>(c, y, W, x, norm_w, M, K)
+                        : launch_v2<1, 0>(c, y, W, x, norm_w, M, K);
+    return epi == 1 ? launch_v2<0, 1>(c, y, W, x, norm_w, M, K)
+                    : launch_v2<0, 0>(c, y, W, x, norm_w, M, K);
+}
+
 int q48_launch_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
                     int M, int K)
 {
+    if (q48_gemv_v2_ok(W, K))
+        return launch_v2<0, 0>(c, y, W, x, nullptr, M, K);
     const bool vec = (K % 2 == 0) && (((uintptr_t)W & 15) == 0);
     if (M >= 1024) {
         dim3 grid((M + 7) / 8);

@@ -17,6 +17,13 @@ struct q48_ctx {
     void *ws;                    // device workspace (scores, row sums, partials)
     size_t ws_bytes;
     int *d_scalar;               // device: small int outputs (argmax)
+    int *d_step;                 // device: decode-step state {token, pos, count}
+    int step_mode;               // ops read token / pos from d_step
+    void *tmp;                   // device temporaries of the unfused fallbacks
+    size_t tmp_bytes;
+    hipGraph_t graph;            // captured decode step
+    hipGraphExec_t graph_exec;
+    int capturing;
     // GEMV launch timing (q48_prof_*): event pairs in use, then a free pool
     int prof_on;
     struct ProfRec { hipEvent_t a, b; double bytes; };
@@ -30,6 +37,10 @@ int q48_ws_reserve(q48_ctx *c, size_t bytes);
 // ---- launchers (return hipError_t as int; shapes already validated) ----
 int q48_launch_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
                     int M, int K);
+bool q48_gemv_v2_ok(const int64_t *W, int K);
+// pro: 1 = rmsnorm(x, norm_w) prologue; epi: 0 store, 1 add into y, 2 SwiGLU pairs
+int q48_launch_gemv_fused(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                          const int64_t *norm_w, int M, int K, int pro, int epi);
 int q48_launch_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X,
                     int T, int N, int K);
 int q48_launch_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *x,
@@ -41,6 +52,13 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
                     int64_t *kcache, int64_t *vcache, const int64_t *k_new,
                     const int64_t *v_new, int layer, const int *d_pos, int pos,
                     int n_heads, int n_kv, int head_dim, int max_seq);
+int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
+                       int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
+                       int layer, const int *d_pos, int pos, int n_heads, int n_kv,
+                       int head_dim, int max_seq, int rope);
+int q48_launch_step_set(q48_ctx *c, int token, int pos);
+int q48_launch_step_argmax(q48_ctx *c, int *tokens, int cap, const int64_t *v, int n);
+int q48_launch_silu_mul_pairs(q48_ctx *c, int64_t *out, const int64_t *t, int n);
 int q48_launch_silu_mul(q48_ctx *c, int64_t *out, const int64_t *g,
                         const int64_t *u, int n);
 int q48_launch_add(q48_ctx *c, int64_t *acc, const int64_t *d, int n);

@@ -120,7 +120,8 @@ __global__ __launch_bounds__(256) void k_rope(int64_t *__restrict__ vec,
                                              const int64_t *__restrict__ cos_t,
                                              const int64_t *__restrict__ sin_t,
                                              int n_heads, int head_dim,
-                                             const int *__restrict__ d_pos, int pos)
+                                             const int *__restrict__ d_pos, int pos,
+                                             int max_seq)
 {
     const int half = head_dim / 2;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
@@ -128,6 +129,8 @@ __global__ __launch_bounds__(256) void k_rope(int64_t *__restrict__ vec,
         return;
     if (d_pos)
         pos = *d_pos;
+    if (pos < 0 || pos >= max_seq)
+        return;
     const int h = idx / half, i = idx % half;
     int64_t *v = vec + (size_t)h * head_dim;
     const int64_t c = cos_t[(size_t)pos * half + i];
@@ -158,6 +161,8 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_decode(
     __shared__ int64_t part[ATT_NT];
     if (d_pos)
         pos = *d_pos;
+    if (pos < 0 || pos >= max_seq)
+        return;   // uniform over the block
     const int h = blockIdx.x;
     const int tid = threadIdx.x;
     const int group = n_heads / n_kv;
@@ -222,6 +227,192 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_decode(
             o += (uint64_t)part[s2 * hd + d];
         out[(size_t)h * hd + d] = (int64_t)o;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Attention v2: the same exact computation as k_attn_decode with
+//  - RoPE fused (ROPE = 1): q_h and k_new are rotated in the block
+//    (rope_apply, llama_int.c:997-1008, 1392-1395); the first head of each
+//    KV group writes the rotated k and v_new into the cache;
+//  - 8 lanes per score: each lane multiplies hd/8 dimensions, a 3-step
+//    128-bit butterfly sums them, so a score costs hd/8 MACs of latency.
+// pos is read from *d_pos when given (graph replay of a decode step).
+// hd must be a multiple of 8 and divide 256 (checked on the host).
+// ---------------------------------------------------------------------------
+template <int ROPE>
+__global__ __launch_bounds__(ATT_NT) void k_attn_v2(
+    int64_t *__restrict__ out, const int64_t *__restrict__ q,
+    int64_t *__restrict__ kcache, int64_t *__restrict__ vcache,
+    const int64_t *__restrict__ k_new, const int64_t *__restrict__ v_new,
+    int64_t *__restrict__ scores, const int64_t *__restrict__ cos_t,
+    const int64_t *__restrict__ sin_t, int layer, const int *__restrict__ d_pos, int pos,
+    int n_heads, int n_kv, int hd, int max_seq)
+{
+    __shared__ int64_t qs[256], ks[256];
+    __shared__ int64_t red[ATT_NT / 64];
+    __shared__ int64_t part[ATT_NT];
+    if (d_pos)
+        pos = *d_pos;
+    if (pos < 0 || pos >= max_seq)
+        return;   // uniform over the block: no barrier is skipped by part of it
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int group = n_heads / n_kv, kh = h / group;
+    const size_t kvd = (size_t)n_kv * hd;
+    const size_t base = (size_t)layer * max_seq;
+    const int64_t *qh = q + (size_t)h * hd;
+    const int64_t *kn = k_new + (size_t)kh * hd;
+    const int64_t *vn = v_new + (size_t)kh * hd;
+    const int half = hd / 2;
+
+    if (ROPE) {
+        if (tid < half) {
+            const int64_t c = cos_t[(size_t)pos * half + tid];
+            const int64_t sn = sin_t[(size_t)pos * half + tid];
+            const int64_t q0 = qh[tid], q1 = qh[tid + half];
+            qs[tid] = (int64_t)((uint64_t)q48_mul(q0, c) - (uint64_t)q48_mul(q1, sn));
+            qs[tid + half] = (int64_t)((uint64_t)q48_mul(q1, c) + (uint64_t)q48_mul(q0, sn));
+            const int64_t k0 = kn[tid], k1 = kn[tid + half];
+            ks[tid] = (int64_t)((uint64_t)q48_mul(k0, c) - (uint64_t)q48_mul(k1, sn));
+            ks[tid + half] = (int64_t)((uint64_t)q48_mul(k1, c) + (uint64_t)q48_mul(k0, sn));
+        }
+    } else {
+        for (int d = tid; d < hd; d += ATT_NT) {
+            qs[d] = qh[d];
+            ks[d] = kn[d];
+        }
+    }
+    __syncthreads();
+    if (h % group == 0)
+        for (int d = tid; d < hd; d += ATT_NT) {
+            kcache[(base + pos) * kvd + (size_t)kh * hd + d] = ks[d];
+            vcache[(base + pos) * kvd + (size_t)kh * hd + d] = vn[d];
+        }
+
+    const int64_t scale = q48_inv_sqrt(q48_from_int(hd));
+    const int S = pos + 1;
+    int64_t *sc = scores + (size_t)h * max_seq;
+
+    // scores: group g of 8 lanes takes position t; lane l8 dims [l8*dpl, +dpl)
+    const int g = tid >> 3, l8 = tid & 7, dpl = hd >> 3;
+    int64_t mx = INT64_MIN;
+    for (int t0 = 0; t0 < S; t0 += ATT_NT / 8) {
+        const int t = t0 + g;
+        q48_u128 dot = 0;
+        if (t < S) {
+            const int64_t *kt = t == pos ? ks : kcache + (base + t) * kvd + (size_t)kh * hd;
+            for (int d = l8 * dpl; d < (l8 + 1) * dpl; ++d)
+                dot += (q48_u128)((q48_i128)qs[d] * kt[d]);
+        }
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            const uint64_t lo = (uint64_t)dot, hi = (uint64_t)(dot >> 64);
+            dot += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
+        }
+        if (t < S && l8 == 0) {
+            const int64_t s = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
+            sc[t] = s;
+            mx = s > mx ? s : mx;
+        }
+    }
+    mx = block_max64<ATT_NT>(mx, red);
+
+    int64_t sum = 0;
+    for (int t = tid; t < S; t += ATT_NT) {
+        const int64_t e = q48_safe_exp((int64_t)((uint64_t)sc[t] - (uint64_t)mx));
+        sc[t] = e;
+        sum = (int64_t)((uint64_t)sum + (uint64_t)e);
+    }
+    sum = block_sum64<ATT_NT>(sum, red);
+    if (sum > 0)
+        for (int t = tid; t < S; t += ATT_NT)
+            sc[t] = q48_div(sc[t], sum);
+    __syncthreads();
+
+    const int slices = ATT_NT / hd;
+    const int d = tid % hd, sl = tid / hd;
+    int64_t acc = 0;
+    for (int t = sl; t < S; t += slices) {
+        const int64_t *vt = t == pos ? vn : vcache + (base + t) * kvd + (size_t)kh * hd;
+        acc = (int64_t)((uint64_t)acc + (uint64_t)q48_mul(sc[t], vt[d]));
+    }
+    part[tid] = acc;
+    __syncthreads();
+    if (sl == 0) {
+        uint64_t o = 0;
+        for (int s2 = 0; s2 < slices; ++s2)
+            o += (uint64_t)part[s2 * hd + d];
+        out[(size_t)h * hd + d] = (int64_t)o;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode-step state (graph replay): st[0] = token, st[1] = pos, st[2] =
+// number of tokens recorded.  k_step_argmax is argmax (llama_int.c:
+// 2888-2893) feeding the next step: token <- argmax, pos += 1, and the
+// token is appended to tokens[] while st[2] < cap.
+// ---------------------------------------------------------------------------
+__global__ void k_step_set(int *__restrict__ st, int token, int pos)
+{
+    if (threadIdx.x == 0) {
+        st[0] = token;
+        st[1] = pos;
+        st[2] = 0;
+    }
+}
+
+__global__ __launch_bounds__(1024) void k_step_argmax(int *__restrict__ st,
+                                                     int *__restrict__ tokens, int cap,
+                                                     const int64_t *__restrict__ v, int n)
+{
+    __shared__ int64_t bv[16];
+    __shared__ int bi[16];
+    const int tid = threadIdx.x;
+    int64_t best = INT64_MIN;
+    int idx = n;
+    for (int i = tid; i < n; i += 1024) {
+        const int64_t x = v[i];
+        if (x > best) {
+            best = x;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const int64_t ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        bv[tid >> 6] = best;
+        bi[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
+                best = bv[w];
+                idx = bi[w];
+            }
+        const int tok = idx < n ? idx : 0;
+        st[0] = tok;
+        st[1] = st[1] + 1;
+        const int k = st[2];
+        if (k < cap)
+            tokens[k] = tok;
+        st[2] = k + 1;
+    }
+}
+
+// SwiGLU over interleaved (gate, up) pairs: out[i] = fp_mul(silu(t[2i]), t[2i+1])
+__global__ __launch_bounds__(256) void k_silu_mul_pairs(int64_t *__restrict__ out,
+                                                       const int64_t *__restrict__ t, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n)
+        out[i] = q48_mul(q48_silu(t[2 * i]), t[2 * i + 1]);
 }
 
 // SwiGLU, llama_int.c:1549-1552: out = fp_mul(fp_silu(g), u)
@@ -371,7 +562,8 @@ int q48_launch_rope(q48_ctx *c, int64_t *vec, int n_heads, int head_dim,
 {
     const int n = n_heads * (head_dim / 2);
     hipLaunchKernelGGL(k_rope, dim3((n + 255) / 256), dim3(256), 0, c->stream, vec,
-                       c->rope_cos, c->rope_sin, n_heads, head_dim, d_pos, pos);
+                       c->rope_cos, c->rope_sin, n_heads, head_dim, d_pos, pos,
+                       c->rope_max_seq);
     return (int)hipGetLastError();
 }
 
@@ -386,6 +578,44 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
     hipLaunchKernelGGL(k_attn_decode, dim3(n_heads), dim3(ATT_NT), 0, c->stream, out, q,
                        kcache, vcache, k_new, v_new, (int64_t *)c->ws, layer, d_pos,
                        pos, n_heads, n_kv, head_dim, max_seq);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
+                       int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
+                       int layer, const int *d_pos, int pos, int n_heads, int n_kv,
+                       int head_dim, int max_seq, int rope)
+{
+    int rc = q48_ws_reserve(c, (size_t)n_heads * max_seq * sizeof(int64_t));
+    if (rc)
+        return rc;
+    if (rope)
+        hipLaunchKernelGGL(k_attn_v2<1>, dim3(n_heads), dim3(ATT_NT), 0, c->stream, out, q,
+                           kcache, vcache, k_new, v_new, (int64_t *)c->ws, c->rope_cos,
+                           c->rope_sin, layer, d_pos, pos, n_heads, n_kv, head_dim, max_seq);
+    else
+        hipLaunchKernelGGL(k_attn_v2<0>, dim3(n_heads), dim3(ATT_NT), 0, c->stream, out, q,
+                           kcache, vcache, k_new, v_new, (int64_t *)c->ws, c->rope_cos,
+                           c->rope_sin, layer, d_pos, pos, n_heads, n_kv, head_dim, max_seq);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_step_set(q48_ctx *c, int token, int pos)
+{
+    hipLaunchKernelGGL(k_step_set, dim3(1), dim3(64), 0, c->stream, c->d_step, token, pos);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_step_argmax(q48_ctx *c, int *tokens, int cap, const int64_t *v, int n)
+{
+    hipLaunchKernelGGL(k_step_argmax, dim3(1), dim3(1024), 0, c->stream, c->d_step, tokens,
+                       cap, v, n);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_silu_mul_pairs(q48_ctx *c, int64_t *out, const int64_t *t, int n)
+{
+    hipLaunchKernelGGL(k_silu_mul_pairs, dim3((n + 255) / 256), dim3(256), 0, c->stream, out, t, n);
     return (int)hipGetLastError();
 }
 

@@ -42,6 +42,9 @@ struct q48h_model {
     int64_t *kc, *vc;           /* device KV cache */
     int64_t *act;               /* device activations */
     int64_t *hidden, *normed, *qkv, *attn, *o, *gu, *h_ffn, *mlp, *logits;
+    int *d_tokens;              /* device: tokens of graph-replayed decode steps */
+    int fused;                  /* 1: fused decode ops (default), 0: one op per kernel */
+    int graph_ready;            /* the context graph holds this model's decode step */
 };
 
 /* ---------------------------------------------------------------------- */
@@ -184,10 +187,12 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
     size_t a_mlp = an; an += align_up(dim);
     size_t a_log = an; an += align_up((size_t)c->vocab);
 
+    m->fused = 1;
     if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->kc, kvn * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->vc, kvn * 8)) ||
-        (rc = q48_malloc(ctx, (void **)&m->act, an * 8))) {
+        (rc = q48_malloc(ctx, (void **)&m->act, an * 8)) ||
+        (rc = q48_malloc(ctx, (void **)&m->d_tokens, (size_t)c->max_seq * sizeof(int)))) {
         q48h_model_free(m);
         return rc;
     }
@@ -228,7 +233,21 @@ void q48h_model_free(q48h_model *m)
     q48_free(m->ctx, m->kc);
     q48_free(m->ctx, m->vc);
     q48_free(m->ctx, m->act);
+    q48_free(m->ctx, m->d_tokens);
+    if (m->graph_ready)
+        q48_graph_drop(m->ctx);
     free(m);
+}
+
+void q48h_model_set_fused(q48h_model *m, int fused)
+{
+    if (m && (m->fused != (fused != 0))) {
+        m->fused = fused != 0;
+        if (m->graph_ready) {
+            q48_graph_drop(m->ctx);
+            m->graph_ready = 0;
+        }
+    }
 }
 
 const q48h_config *q48h_model_config(const q48h_model *m) { return &m->c; }
@@ -572,7 +591,27 @@ int q48h_kv_fill_synth(q48h_model *m, uint64_t seed, int npos, int threads)
 
 #define TRY(x) do { int rc_ = (x); if (rc_) return rc_; } while (0)
 
-/* transformer_layer_forward, llama_int.c:1326-1569 (exact-cache path). */
+/* transformer_layer_forward, llama_int.c:1326-1569 (exact-cache path),
+ * fused: 5 launches.  rmsnorm+q|k|v, RoPE+KV store+attention, o+residual,
+ * rmsnorm+gate|up+SwiGLU, down+residual. */
+static int layer_forward_fused(q48h_model *m, int l, int pos)
+{
+    const q48h_config *c = &m->c;
+    q48_ctx *x = m->ctx;
+    int dim = c->dim, hd = c->head_dim, kvd = c->n_kv_heads * hd, ffn = c->ffn;
+    const int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
+    int64_t *q = m->qkv, *k = m->qkv + dim, *v = m->qkv + dim + kvd;
+
+    TRY(q48_rmsnorm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an, dim + 2 * kvd, dim));
+    TRY(q48_attn_decode_rope(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
+                             c->n_kv_heads, hd, c->max_seq));
+    TRY(q48_gemv_residual(x, m->hidden, b + m->lo_wo, m->attn, dim, dim));
+    TRY(q48_rmsnorm_gemv_swiglu(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn, ffn, dim));
+    TRY(q48_gemv_residual(x, m->hidden, b + m->lo_wd, m->h_ffn, dim, ffn));
+    return Q48_OK;
+}
+
+/* The same layer as one library op per reference step (testing path). */
 static int layer_forward(q48h_model *m, int l, int pos)
 {
     const q48h_config *c = &m->c;
@@ -597,6 +636,25 @@ static int layer_forward(q48h_model *m, int l, int pos)
     return Q48_OK;
 }
 
+/* Enqueue one llama_forward (llama_int.c:2807-2886) up to the logits. */
+static int enqueue_forward(q48h_model *m, int token, int pos)
+{
+    const q48h_config *c = &m->c;
+    TRY(q48_embed(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim));
+    if (m->fused) {
+        for (int l = 0; l < c->n_layers; ++l)
+            TRY(layer_forward_fused(m, l, pos));
+        TRY(q48_rmsnorm_gemv(m->ctx, m->logits, m->w + m->off_lm, m->hidden,
+                             m->w + m->off_norm, c->vocab, c->dim));
+    } else {
+        for (int l = 0; l < c->n_layers; ++l)
+            TRY(layer_forward(m, l, pos));
+        TRY(q48_rmsnorm(m->ctx, m->normed, m->hidden, m->w + m->off_norm, c->dim));
+        TRY(q48_gemv(m->ctx, m->logits, m->w + m->off_lm, m->normed, c->vocab, c->dim));
+    }
+    return Q48_OK;
+}
+
 int q48h_forward(q48h_model *m, int token, int pos, int64_t *logits, int *next)
 {
     if (!m)
@@ -604,11 +662,7 @@ int q48h_forward(q48h_model *m, int token, int pos, int64_t *logits, int *next)
     const q48h_config *c = &m->c;
     if (token < 0 || token >= c->vocab || pos < 0 || pos >= c->max_seq)
         return Q48_ERANGE;
-    TRY(q48_embed(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim));
-    for (int l = 0; l < c->n_layers; ++l)
-        TRY(layer_forward(m, l, pos));
-    TRY(q48_rmsnorm(m->ctx, m->normed, m->hidden, m->w + m->off_norm, c->dim));
-    TRY(q48_gemv(m->ctx, m->logits, m->w + m->off_lm, m->normed, c->vocab, c->dim));
+    TRY(enqueue_forward(m, token, pos));
     if (next)
         TRY(q48_argmax(m->ctx, m->logits, c->vocab, next));
     if (logits)
@@ -714,4 +768,69 @@ int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_to
     }
     free(logits);
     return rc ? rc : steps;
+}
+
+/* ---------------------------------------------------------------------- */
+/* graph-replayed greedy decode                                            */
+/* ---------------------------------------------------------------------- */
+
+/* Run decode step 0 eagerly in step mode (forward(token, pos), device
+ * argmax recorded as tokens[0]) -- workspaces reach their size outside any
+ * capture -- then capture the same step into the context graph.  Kernels
+ * read token / pos from the device step state, so the graph serves every
+ * later position. */
+static int first_step_and_capture(q48h_model *m, int token, int pos)
+{
+    q48_ctx *x = m->ctx;
+    const q48h_config *c = &m->c;
+    TRY(q48_step_mode(x, 1));
+    int rc = q48_step_set(x, token, pos);
+    if (rc == Q48_OK)
+        rc = enqueue_forward(m, token, pos);
+    if (rc == Q48_OK)
+        rc = q48_argmax_step(x, m->logits, c->vocab, m->d_tokens, c->max_seq);
+    if (rc == Q48_OK)
+        rc = q48_sync(x);
+    if (rc == Q48_OK && !m->graph_ready) {
+        rc = q48_graph_begin(x);
+        if (rc == Q48_OK) {
+            int rc1 = enqueue_forward(m, token, pos);
+            if (rc1 == Q48_OK)
+                rc1 = q48_argmax_step(x, m->logits, c->vocab, m->d_tokens, c->max_seq);
+            rc = q48_graph_end(x);
+            if (rc1)
+                rc = rc1;
+            if (rc == Q48_OK)
+                m->graph_ready = 1;
+        }
+    }
+    q48_step_mode(x, 0);
+    return rc;
+}
+
+int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
+                      q48h_stats *st)
+{
+    if (!m || !out_tokens || n < 0)
+        return Q48_EINVAL;
+    const q48h_config *c = &m->c;
+    if (token < 0 || token >= c->vocab || start_pos < 0)
+        return Q48_ERANGE;
+    if (start_pos + n > c->max_seq)
+        n = c->max_seq - start_pos;   /* llama_forward's NULL past max_seq */
+    if (n <= 0)
+        return 0;
+    double t0 = now_s();
+    TRY(first_step_and_capture(m, token, start_pos));
+    TRY(q48_graph_launch(m->ctx, n - 1));
+    TRY(q48_memcpy_d2h(m->ctx, out_tokens, m->d_tokens, (size_t)n * sizeof(int)));
+    if (st) {
+        st->decode_s += now_s() - t0;
+        st->decode_tokens += n;
+    }
+    /* generate stops at EOS (llama_int.c:3111): report the steps up to it */
+    for (int i = 0; i < n; ++i)
+        if (out_tokens[i] == LLAMA_EOS)
+            return i + 1;
+    return n;
 }

@@ -106,6 +106,18 @@ int q48h_generate(q48h_model *m, const int *prompt, int prompt_len, int max_new,
 int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
                      uint64_t *step_hash, q48h_stats *stats);
 
+/* Choose the fused decode ops (1, default: 5 launches per layer) or one
+ * library op per reference step (0).  Same bits either way. */
+void q48h_model_set_fused(q48h_model *m, int fused);
+
+/* Greedy decode of n steps replayed from a captured graph: step i runs
+ * forward(token_i, start_pos + i) and its argmax becomes token_{i+1} on the
+ * device, with no host round trip between steps.  out_tokens[i] receives
+ * the argmax of step i.  Returns the number of steps up to and including
+ * the first EOS (generate stops there, llama_int.c:3111), or n. */
+int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
+                      q48h_stats *stats);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,18 @@ ABI_SIGNATURES = {
     "q48_argmax": [_P, _P, _I, C.POINTER(C.c_int)],
     "q48_rope_tables": [_P, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)],
     "q48_fp_eval": [_P, _I, _P, _P, _P, _P, _I],
+    "q48_rmsnorm_gemv": [_P, _P, _P, _P, _P, _I, _I],
+    "q48_gemv_residual": [_P, _P, _P, _P, _I, _I],
+    "q48_rmsnorm_gemv_swiglu": [_P, _P, _P, _P, _P, _I, _I],
+    "q48_attn_decode_rope": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
+    "q48_step_mode": [_P, _I],
+    "q48_step_set": [_P, _I, _I],
+    "q48_step_get": [_P, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)],
+    "q48_argmax_step": [_P, _P, _I, _P, _I],
+    "q48_graph_begin": [_P],
+    "q48_graph_end": [_P],
+    "q48_graph_launch": [_P, _I],
+    "q48_graph_drop": [_P],
     "q48_prof_enable": [_P, _I],
     "q48_prof_read": [_P, _P, _I],
 }
@@ -220,6 +232,20 @@ class Context:
         check("q48_rope_tables", hip_lib().q48_rope_tables(self.h, C.byref(c), C.byref(s)))
         return c.value, s.value
 
+    def rmsnorm_gemv(self, y, W, x, norm_w, M, K):
+        return check("q48_rmsnorm_gemv", hip_lib().q48_rmsnorm_gemv(self.h, y, W, x, norm_w, M, K))
+
+    def gemv_residual(self, acc, W, x, M, K):
+        return check("q48_gemv_residual", hip_lib().q48_gemv_residual(self.h, acc, W, x, M, K))
+
+    def rmsnorm_gemv_swiglu(self, out, Wgu, x, norm_w, ffn, K):
+        return check("q48_rmsnorm_gemv_swiglu",
+                     hip_lib().q48_rmsnorm_gemv_swiglu(self.h, out, Wgu, x, norm_w, ffn, K))
+
+    def attn_decode_rope(self, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq):
+        return check("q48_attn_decode_rope", hip_lib().q48_attn_decode_rope(
+            self.h, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq))
+
     def prof_enable(self, on: bool = True):
         check("q48_prof_enable", hip_lib().q48_prof_enable(self.h, int(on)))
 
@@ -281,6 +307,8 @@ HOST_SIGNATURES = {
                        C.POINTER(C.c_uint64), C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
     "q48h_decode_from": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(C.c_uint64),
                           C.POINTER(Stats)], C.c_int),
+    "q48h_model_set_fused": ([_P, _I], None),
+    "q48h_decode_graph": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
 }
 
 
@@ -348,6 +376,18 @@ class HostModel:
         total = check("q48h_generate", host_lib().q48h_generate(
             self.h, p, len(prompt), max_new, out, hs, C.byref(n), C.byref(st)))
         return list(out[:total]), (list(hs[:n.value]) if hashes else None), st
+
+    def set_fused(self, fused: bool):
+        host_lib().q48h_model_set_fused(self.h, int(fused))
+
+    def decode_graph(self, token: int, start_pos: int, n: int):
+        """n greedy steps replayed from a captured graph; returns (tokens up
+        to and including the first EOS, all n step tokens, stats)."""
+        out = (C.c_int * max(1, n))()
+        st = Stats()
+        k = check("q48h_decode_graph", host_lib().q48h_decode_graph(
+            self.h, token, start_pos, n, out, C.byref(st)))
+        return list(out[:k]), list(out[:n]), st
 
     def decode_from(self, token: int, start_pos: int, n: int, hashes: bool = True):
         out = (C.c_int * max(1, n))()

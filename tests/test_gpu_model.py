@@ -142,3 +142,65 @@ def test_gemm_config4_vs_reference(ctx, T):
         assert O.fnv(dY.download()) == g[f"{T}x{N}x{K}"]["fnv"], (T, N, K)
         for b in (dW, dX, dY):
             b.free()
+
+
+def test_tiny_generate_unfused_path_bit_exact(ctx):
+    """One library op per reference step gives the same stream as the fused path."""
+    g = golden("tiny_generate.json")
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    try:
+        m.synth(g["seed"], threads())
+        m.set_fused(False)
+        say("tiny generate unfused")
+        toks, hs, _ = m.generate(g["prompt"], g["max_new"])
+        assert toks == g["tokens"]
+        assert ["%016x" % h for h in hs] == g["step_fnv"]
+    finally:
+        m.free()
+
+
+def test_tiny_graph_decode_replays(ctx):
+    """Graph-replayed decode: several launches of the captured step, with
+    eager work and host synchronisation between the calls, each continuing
+    the token stream exactly where the eager generate has it."""
+    g = golden("tiny_generate.json")
+    prompt, ref = g["prompt"], g["tokens"]
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    try:
+        m.synth(g["seed"], threads())
+        for pos, tok in enumerate(prompt):          # eager prefill
+            nxt, _ = m.forward(tok, pos, spec.TINY[6], logits=False)
+        assert nxt == ref[len(prompt)]
+        tok, pos, got = nxt, len(prompt), [nxt]
+        for chunk in (5, 9, 10):
+            say("graph decode chunk", chunk, "from pos", pos)
+            _, steps, _ = m.decode_graph(tok, pos, chunk)
+            got += steps
+            tok, pos = steps[-1], pos + chunk
+            ctx.sync()
+            # eager work between replays: a forward whose result must also agree
+            _, lg = m.forward(tok, pos, spec.TINY[6])
+            got_next = int(np.argmax(lg))
+            _, steps1, _ = m.decode_graph(tok, pos, 1)
+            assert steps1[0] == got_next
+        n = min(len(got), len(ref) - len(prompt))
+        assert got[:n] == ref[len(prompt):len(prompt) + n]
+    finally:
+        m.free()
+
+
+def test_tinyllama_graph_decode_bit_exact(ctx):
+    g = golden("tinyllama_generate.json")
+    prompt, ref = g["prompt"], g["tokens"]
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    try:
+        say("tinyllama synth")
+        m.synth(g["seed"], threads())
+        for pos, tok in enumerate(prompt):
+            nxt, _ = m.forward(tok, pos, spec.TINYLLAMA[6], logits=False)
+        say("tinyllama graph decode")
+        toks, steps, st = m.decode_graph(nxt, len(prompt), g["max_new"] - 1)
+        assert [nxt] + toks[:len(ref) - len(prompt) - 1] == ref[len(prompt):]
+        print(f"graph decode {1e3 * st.decode_s / max(1, st.decode_tokens):.3f} ms/tok", flush=True)
+    finally:
+        m.free()

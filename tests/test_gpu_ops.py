@@ -304,3 +304,100 @@ def test_abi_rejects_bad_arguments(ctx):
     assert lib.q48_attn_decode(ctx.h, d.ptr, d.ptr, d.ptr, d.ptr, d.ptr, d.ptr, 0, 0, 3, 2, 8,
                                4) == intllm.Q48_EINVAL
     assert lib.q48_embed(ctx.h, d.ptr, d.ptr, -1, 4) == intllm.Q48_ERANGE
+
+
+# ---------------------------------------------------------------------------
+# fused decode ops: each equals the composition of the separate reference ops
+# ---------------------------------------------------------------------------
+
+def _rms(oracle, x, w):
+    out = np.empty(x.size, dtype=np.int64)
+    oracle.q48o_rmsnorm(out.ctypes.data, x.ctypes.data, w.ctypes.data, x.size)
+    return out
+
+
+@pytest.mark.parametrize("M,K", [(2560, 2048), (32000, 2048), (64, 256), (17, 688), (9, 7681),
+                                 (5, 129)])
+def test_rmsnorm_gemv_fused(ctx, oracle, M, K):
+    rng = np.random.default_rng(M + K)
+    W = (rng.standard_normal(M * K) * spec.SIGMA_W).astype(np.int64)
+    x = (rng.standard_normal(K) * 3 * ONE).astype(np.int64)
+    w = (rng.standard_normal(K) * ONE).astype(np.int64)
+    want = O.gemv(W, _rms(oracle, x, w), M, K)
+    dW, dx, dw, dy = ctx.to_device(W), ctx.to_device(x), ctx.to_device(w), ctx.buffer(M)
+    say("rmsnorm_gemv", M, K)
+    ctx.rmsnorm_gemv(dy.ptr, dW.ptr, dx.ptr, dw.ptr, M, K)
+    assert np.array_equal(dy.download(), want)
+    for b in (dW, dx, dw, dy):
+        b.free()
+
+
+@pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 5632), (256, 688), (3, 7681), (7, 33)])
+def test_gemv_residual_fused(ctx, M, K):
+    rng = np.random.default_rng(M * 3 + K)
+    W = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=M * K, dtype=np.int64)
+    x = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=K, dtype=np.int64)
+    h = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=M, dtype=np.int64)
+    want = (h.view(np.uint64) + O.gemv(W, x, M, K).view(np.uint64)).view(np.int64)
+    dW, dx, dh = ctx.to_device(W), ctx.to_device(x), ctx.to_device(h)
+    say("gemv_residual", M, K)
+    ctx.gemv_residual(dh.ptr, dW.ptr, dx.ptr, M, K)
+    assert np.array_equal(dh.download(), want)
+    for b in (dW, dx, dh):
+        b.free()
+
+
+@pytest.mark.parametrize("ffn,K", [(5632, 2048), (688, 256), (13, 64), (6, 7681)])
+def test_rmsnorm_gemv_swiglu_fused(ctx, oracle, ffn, K):
+    rng = np.random.default_rng(ffn + 7 * K)
+    W = (rng.standard_normal(2 * ffn * K) * spec.SIGMA_W * 20).astype(np.int64)
+    x = (rng.standard_normal(K) * ONE).astype(np.int64)
+    w = (rng.standard_normal(K) * ONE).astype(np.int64)
+    t = O.gemv(W, _rms(oracle, x, w), 2 * ffn, K)
+    want = np.empty(ffn, dtype=np.int64)
+    g, u = t[:ffn].copy(), t[ffn:].copy()
+    oracle.q48o_silu_mul(want.ctypes.data, g.ctypes.data, u.ctypes.data, ffn)
+    dW, dx, dw, do = ctx.to_device(W), ctx.to_device(x), ctx.to_device(w), ctx.buffer(ffn)
+    say("swiglu", ffn, K)
+    ctx.rmsnorm_gemv_swiglu(do.ptr, dW.ptr, dx.ptr, dw.ptr, ffn, K)
+    assert np.array_equal(do.download(), want)
+    for b in (dW, dx, dw, do):
+        b.free()
+
+
+@pytest.mark.parametrize("nh,nkv,hd,max_seq,positions", [
+    (8, 2, 32, 64, [0, 1, 63]),
+    (32, 4, 64, 300, [0, 7, 299]),
+])
+def test_attention_rope_fused(ctx, oracle, nh, nkv, hd, max_seq, positions):
+    rng = np.random.default_rng(nh + hd + max_seq)
+    kvd = nkv * hd
+    kc = (rng.standard_normal(2 * max_seq * kvd) * ONE).astype(np.int64)
+    vc = (rng.standard_normal(2 * max_seq * kvd) * ONE).astype(np.int64)
+    cos_t = np.empty(max_seq * hd // 2, dtype=np.int64)
+    sin_t = np.empty(max_seq * hd // 2, dtype=np.int64)
+    oracle.q48o_rope_tables(cos_t.ctypes.data, sin_t.ctypes.data, hd, max_seq, 10000)
+    ctx.rope_init(hd, max_seq, 10000)
+    dk, dv = ctx.to_device(kc), ctx.to_device(vc)
+    for pos in positions:
+        q = (rng.standard_normal(nh * hd) * 3 * ONE).astype(np.int64)
+        kn = (rng.standard_normal(kvd) * ONE).astype(np.int64)
+        vn = (rng.standard_normal(kvd) * ONE).astype(np.int64)
+        qr, kr = q.copy(), kn.copy()
+        for h in range(nh):
+            oracle.q48o_rope_apply(cos_t.ctypes.data, sin_t.ctypes.data, hd // 2,
+                                   qr[h * hd:].ctypes.data, pos)
+        for h in range(nkv):
+            oracle.q48o_rope_apply(cos_t.ctypes.data, sin_t.ctypes.data, hd // 2,
+                                   kr[h * hd:].ctypes.data, pos)
+        out = np.empty(nh * hd, dtype=np.int64)
+        oracle.q48o_attn_decode(out.ctypes.data, qr.ctypes.data, kc.ctypes.data, vc.ctypes.data,
+                                kr.ctypes.data, vn.ctypes.data, 1, pos, nh, nkv, hd, max_seq)
+        dq, dkn, dvn, do = ctx.to_device(q), ctx.to_device(kn), ctx.to_device(vn), ctx.buffer(nh * hd)
+        say("attention+rope", nh, nkv, hd, "pos", pos)
+        ctx.attn_decode_rope(do.ptr, dq.ptr, dk.ptr, dv.ptr, dkn.ptr, dvn.ptr, 1, pos, nh, nkv, hd,
+                             max_seq)
+        assert np.array_equal(do.download(), out), pos
+        assert np.array_equal(dk.download(), kc) and np.array_equal(dv.download(), vc)
+        for b in (dq, dkn, dvn, do):
+            b.free()
