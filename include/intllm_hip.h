@@ -162,10 +162,29 @@ int q48_attn_decode_rope(q48_ctx *ctx, int64_t *out, const int64_t *q,
                          const int64_t *v_new, int layer, int pos, int n_heads,
                          int n_kv, int head_dim, int max_seq);
 
+/* The same fusions with the rmsnorm statistics computed once per vector:
+ * r = fp_inv_sqrt((int64)((sum x^2 >> 48) / dim) + 2814749767), the scalar
+ * of rmsnorm (llama_int.c:1049-1055), lives in device memory (*r) and the
+ * consumers apply fp_mul(fp_mul(x, r), norm_w) (llama_int.c:1056-1057). */
+int q48_rms_inv(q48_ctx *ctx, int64_t *r_out, const int64_t *x, int dim);
+/* out = table[token] (llama_int.c:2822-2824) and *r_out = its statistics. */
+int q48_embed_rms(q48_ctx *ctx, int64_t *out, const int64_t *table, int token, int dim,
+                  int64_t *r_out);
+/* y = W . (x * r * norm_w): q48_rmsnorm_gemv with r given. */
+int q48_norm_gemv(q48_ctx *ctx, int64_t *y, const int64_t *W, const int64_t *x,
+                  const int64_t *norm_w, const int64_t *r, int M, int K);
+/* q48_rmsnorm_gemv_swiglu with r given. */
+int q48_norm_gemv_swiglu(q48_ctx *ctx, int64_t *out, const int64_t *Wgu, const int64_t *x,
+                         const int64_t *norm_w, const int64_t *r, int ffn, int K);
+/* acc += W . x (residual add), then *r_out = the rmsnorm statistics of the
+ * updated acc (dim M): the producer of the next norm's r. */
+int q48_gemv_residual_rms(q48_ctx *ctx, int64_t *acc, const int64_t *W, const int64_t *x,
+                          int M, int K, int64_t *r_out);
+
 /* ---- device-resident decode steps (graph replay) ---------------------------- */
 /* No reference counterpart: llama_int's generate (llama_int.c:3067-3135)
  * passes token and pos as C arguments each call.  In step mode q48_embed
- * reads the token, and q48_rope / q48_attn_decode(_rope) read pos, from a
+ * and q48_embed_rms read the token, and q48_rope / q48_attn_decode(_rope) read pos, from a
  * device-side state {token, pos, count} instead of their arguments, and
  * q48_argmax_step writes the greedy token back into that state (pos += 1),
  * so one captured forward can be replayed for consecutive tokens with no

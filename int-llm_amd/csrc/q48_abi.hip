@@ -41,6 +41,26 @@ int q48_ws_reserve(q48_ctx *c, size_t bytes)
     return Q48_OK;
 }
 
+int q48_rms_reserve(q48_ctx *c, int blocks)
+{
+    if (blocks <= c->rms_blocks)
+        return Q48_OK;
+    if (c->capturing)
+        return Q48_ESTATE;
+    if (c->rms_part) {
+        if (hipStreamSynchronize(c->stream) != hipSuccess)
+            return Q48_EHIP;
+        (void)hipFree(c->rms_part);
+        c->rms_part = nullptr;
+        c->rms_blocks = 0;
+    }
+    int n = blocks < 1024 ? 1024 : blocks;
+    if (hipMalloc(&c->rms_part, (size_t)n * 2 * sizeof(uint64_t)) != hipSuccess)
+        return Q48_ENOMEM;
+    c->rms_blocks = n;
+    return Q48_OK;
+}
+
 extern "C" {
 
 const char *q48_strerror(int code)
@@ -76,13 +96,16 @@ int q48_ctx_create(q48_ctx **out, int device)
     }
     if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
         hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess ||
-        hipMalloc(&c->d_step, 4 * sizeof(int)) != hipSuccess) {
+        hipMalloc(&c->d_step, 4 * sizeof(int)) != hipSuccess ||
+        hipMalloc(&c->rms_count, 64 * sizeof(int)) != hipSuccess) {
         q48_ctx_destroy(c);
         return Q48_ENOMEM;
     }
     int rc = launch_rc(q48_launch_math_init(c));
     if (rc == Q48_OK)
         rc = launch_rc(q48_launch_step_set(c, 0, 0));
+    if (rc == Q48_OK)
+        rc = launch_rc(q48_launch_zero(c, c->rms_count, 64 * sizeof(int)));
     if (rc == Q48_OK)
         rc = hip_rc(hipStreamSynchronize(c->stream));
     if (rc != Q48_OK) {
@@ -105,6 +128,8 @@ int q48_ctx_destroy(q48_ctx *c)
     (void)hipFree(c->ws);
     (void)hipFree(c->d_scalar);
     (void)hipFree(c->d_step);
+    (void)hipFree(c->rms_count);
+    (void)hipFree(c->rms_part);
     (void)hipFree(c->tmp);
     if (c->graph_exec)
         (void)hipGraphExecDestroy(c->graph_exec);
@@ -466,7 +491,7 @@ int q48_rmsnorm_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
         q48_ctx::ProfRec *r = prof_begin(c, gemv_bytes(M, K, M), &prc);
         if (prc)
             return prc;
-        return prof_end(c, r, launch_rc(q48_launch_gemv_fused(c, y, W, x, norm_w, M, K, 1, 0)));
+        return prof_end(c, r, launch_rc(q48_launch_gemv_fused(c, y, W, x, norm_w, nullptr, nullptr, M, K, 1, 0)));
     }
     int rc = tmp_reserve(c, (size_t)K * 8);
     if (rc)
@@ -486,7 +511,7 @@ int q48_gemv_residual(q48_ctx *c, int64_t *acc, const int64_t *W, const int64_t 
         q48_ctx::ProfRec *r = prof_begin(c, gemv_bytes(M, K, M), &prc);
         if (prc)
             return prc;
-        return prof_end(c, r, launch_rc(q48_launch_gemv_fused(c, acc, W, x, nullptr, M, K, 0, 1)));
+        return prof_end(c, r, launch_rc(q48_launch_gemv_fused(c, acc, W, x, nullptr, nullptr, nullptr, M, K, 0, 1)));
     }
     int rc = tmp_reserve(c, (size_t)M * 8);
     if (rc)
@@ -508,7 +533,7 @@ int q48_rmsnorm_gemv_swiglu(q48_ctx *c, int64_t *out, const int64_t *Wgu, const 
         if (prc)
             return prc;
         return prof_end(c, r,
-                        launch_rc(q48_launch_gemv_fused(c, out, Wgu, x, norm_w, 2 * ffn, K, 1, 2)));
+                        launch_rc(q48_launch_gemv_fused(c, out, Wgu, x, norm_w, nullptr, nullptr, 2 * ffn, K, 1, 2)));
     }
     int rc = tmp_reserve(c, ((size_t)K + 2 * (size_t)ffn) * 8);
     if (rc)
@@ -539,6 +564,99 @@ int q48_attn_decode_rope(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kc
     if (rc == Q48_ENOMEM)
         return rc;
     return launch_rc(rc);
+}
+
+
+// ---- norm statistics computed once per vector ---------------------------------
+
+int q48_rms_inv(q48_ctx *c, int64_t *r_out, const int64_t *x, int dim)
+{
+    if (!c || !r_out || !x || dim <= 0 || dim > kMaxDim)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_rms_inv(c, r_out, nullptr, x, nullptr, nullptr, 0, dim));
+}
+
+int q48_embed_rms(q48_ctx *c, int64_t *out, const int64_t *table, int token, int dim,
+                  int64_t *r_out)
+{
+    if (!c || !out || !table || !r_out || dim <= 0 || dim > kMaxDim)
+        return Q48_EINVAL;
+    if (token < 0)
+        return Q48_ERANGE;
+    return launch_rc(q48_launch_rms_inv(c, r_out, out, nullptr, table,
+                                        c->step_mode ? c->d_step : nullptr, token, dim));
+}
+
+int q48_norm_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                  const int64_t *norm_w, const int64_t *r, int M, int K)
+{
+    if (!c || bad_ptrs(y, W, x) || !norm_w || !r || M <= 0 || K <= 0 || M > kMaxDim ||
+        K > kMaxDim)
+        return Q48_EINVAL;
+    if (q48_gemv_v2_ok(W, K)) {
+        int prc;
+        q48_ctx::ProfRec *pr = prof_begin(c, gemv_bytes(M, K, M), &prc);
+        if (prc)
+            return prc;
+        return prof_end(c, pr, launch_rc(q48_launch_gemv_fused(c, y, W, x, norm_w, r, nullptr,
+                                                               M, K, 2, 0)));
+    }
+    int rc = tmp_reserve(c, (size_t)K * 8);
+    if (rc)
+        return rc;
+    int64_t *t = (int64_t *)c->tmp;
+    rc = launch_rc(q48_launch_rms_apply(c, t, x, norm_w, r, K));
+    return rc ? rc : launch_rc(q48_launch_gemv(c, y, W, t, M, K));
+}
+
+int q48_norm_gemv_swiglu(q48_ctx *c, int64_t *out, const int64_t *Wgu, const int64_t *x,
+                         const int64_t *norm_w, const int64_t *r, int ffn, int K)
+{
+    if (!c || bad_ptrs(out, Wgu, x) || !norm_w || !r || ffn <= 0 || K <= 0 ||
+        ffn > kMaxDim / 2 || K > kMaxDim)
+        return Q48_EINVAL;
+    if (q48_gemv_v2_ok(Wgu, K)) {
+        int prc;
+        q48_ctx::ProfRec *pr = prof_begin(c, gemv_bytes(2 * ffn, K, ffn), &prc);
+        if (prc)
+            return prc;
+        return prof_end(c, pr, launch_rc(q48_launch_gemv_fused(c, out, Wgu, x, norm_w, r,
+                                                               nullptr, 2 * ffn, K, 2, 2)));
+    }
+    int rc = tmp_reserve(c, ((size_t)K + 2 * (size_t)ffn) * 8);
+    if (rc)
+        return rc;
+    int64_t *xn = (int64_t *)c->tmp, *t = xn + K;
+    if ((rc = launch_rc(q48_launch_rms_apply(c, xn, x, norm_w, r, K))) ||
+        (rc = launch_rc(q48_launch_gemv(c, t, Wgu, xn, 2 * ffn, K))))
+        return rc;
+    return launch_rc(q48_launch_silu_mul(c, out, t, t + ffn, ffn));
+}
+
+int q48_gemv_residual_rms(q48_ctx *c, int64_t *acc, const int64_t *W, const int64_t *x, int M,
+                          int K, int64_t *r_out)
+{
+    if (!c || bad_ptrs(acc, W, x) || !r_out || M <= 0 || K <= 0 || M > kMaxDim ||
+        K > kMaxDim)
+        return Q48_EINVAL;
+    if (q48_gemv_v2_ok(W, K)) {
+        int prc;
+        q48_ctx::ProfRec *pr = prof_begin(c, gemv_bytes(M, K, M), &prc);
+        if (prc)
+            return prc;
+        int rc = q48_launch_gemv_fused(c, acc, W, x, nullptr, nullptr, r_out, M, K, 0, 3);
+        if (rc == Q48_ENOMEM || rc == Q48_ESTATE || rc == Q48_EHIP)
+            return rc;
+        return prof_end(c, pr, launch_rc(rc));
+    }
+    int rc = tmp_reserve(c, (size_t)M * 8);
+    if (rc)
+        return rc;
+    int64_t *t = (int64_t *)c->tmp;
+    if ((rc = launch_rc(q48_launch_gemv(c, t, W, x, M, K))) ||
+        (rc = launch_rc(q48_launch_add(c, acc, t, M))))
+        return rc;
+    return launch_rc(q48_launch_rms_inv(c, r_out, nullptr, acc, nullptr, nullptr, 0, M));
 }
 
 // ---- decode-step state and graphs --------------------------------------------

@@ -147,22 +147,35 @@ __global__ __launch_bounds__(64 * RPB) void k_gemv(int64_t *__restrict__ y,
 }
 
 // ---------------------------------------------------------------------------
-// GEMV v2: 8 rows per block, one 8-lane group per row (each load
+// GEMV v3: 8 rows per block, one 8-lane group per row (each load
 // instruction of a group reads one full 128-byte line of its row), NW
-// waves per block each taking one K-segment of all 8 rows.  Every lane
-// issues UNR 16-byte loads before it computes, so a wave keeps
-// UNR * 1 KiB of weights in flight.  Per-segment partials meet in LDS.
+// waves per block each taking one K-segment of all 8 rows.  Every lane has
+// UNR 16-byte weight loads in flight; the first batch is issued before the
+// prologue (x staging, norm statistics), so HBM latency overlaps it.
+// Per-segment partials meet in LDS.
 //
-// PRO = 1 fuses rmsnorm (llama_int.c:1048-1058) into the x staging: every
-// block recomputes the (integer, order-free) statistics of the whole x and
-// stages fp_mul(fp_mul(x, r), norm_w) — the values rmsnorm would write.
-// EPI = 0 stores y; EPI = 1 adds y into `out` (the residual adds,
-// llama_int.c:1535, 1556); EPI = 2 reads W as [gate; up] (M = 2 ffn rows):
+// Prologues (the staged x is exactly what rmsnorm, llama_int.c:1048-1058,
+// would write):  PRO 0: x as given;  PRO 1: every block computes the
+// rmsnorm statistics of x itself and stages fp_mul(fp_mul(x, r), norm_w);
+// PRO 2: the same with r = *r_in, computed once by the producer of x.
+// Epilogues:  EPI 0 stores y;  EPI 1 adds y into `y` (the residual adds,
+// llama_int.c:1535, 1556);  EPI 2 reads W as [gate; up] (M = 2 ffn):
 // block b takes gate rows 4b..4b+3 (groups 0-3) and the matching up rows
-// ffn+4b.. (groups 4-7) and stores fp_mul(fp_silu(gate_i), up_i) to y[i]
-// (llama_int.c:1549-1552).
+// ffn+4b.. (groups 4-7) and stores fp_mul(fp_silu(gate), up)
+// (llama_int.c:1549-1552);  EPI 3 is EPI 1 followed by the statistics of
+// the next rmsnorm of the updated vector: each block writes its partial sum
+// of squares, the last block to finish adds them in block order and writes
+// r = fp_inv_sqrt((int64)((ss >> 48) / M) + 2814749767) to *r_out.
 // ---------------------------------------------------------------------------
-constexpr int V2_RB = 8;
+constexpr int V3_RB = 8;
+
+// (ss >> 48) / dim + eps, then fp_inv_sqrt: the scalar part of rmsnorm.
+__device__ __forceinline__ int64_t rms_inv_of(q48_u128 ss, int dim)
+{
+    int64_t ms = (int64_t)q48_divs_128_64((q48_i128)ss >> 48, (int64_t)dim);
+    ms = (int64_t)((uint64_t)ms + 2814749767ull);
+    return q48_inv_sqrt(ms);
+}
 
 template <int NW>
 __device__ __forceinline__ int64_t block_rms_inv(const int64_t *__restrict__ x, int K,
@@ -184,42 +197,62 @@ __device__ __forceinline__ int64_t block_rms_inv(const int64_t *__restrict__ x, 
         q48_u128 t = 0;
         for (int w = 0; w < NW; ++w)
             t += ((q48_u128)red_hi[w] << 64) | red_lo[w];
-        int64_t ms = (int64_t)q48_divs_128_64((q48_i128)t >> 48, (int64_t)K);
-        ms = (int64_t)((uint64_t)ms + 2814749767ull);
-        red_lo[NW] = (uint64_t)q48_inv_sqrt(ms);
+        red_lo[NW] = (uint64_t)rms_inv_of(t, K);
     }
     __syncthreads();
     return (int64_t)red_lo[NW];
 }
 
 template <int NW, int UNR, int PRO, int EPI>
-__global__ __launch_bounds__(64 * NW) void k_gemv_v2(int64_t *__restrict__ y,
+__global__ __launch_bounds__(64 * NW) void k_gemv_v3(int64_t *__restrict__ y,
                                                     const int64_t *__restrict__ W,
                                                     const int64_t *__restrict__ x,
                                                     const int64_t *__restrict__ norm_w,
+                                                    const int64_t *__restrict__ r_in,
+                                                    int64_t *__restrict__ r_out,
+                                                    uint64_t *__restrict__ rms_part,
+                                                    int *__restrict__ rms_count,
                                                     int M, int K, int seg)
 {
     extern __shared__ __align__(16) uint64_t xs[];   // K flipped x values (segments)
     __shared__ uint64_t red_lo[NW + 1], red_hi[NW];
-    __shared__ uint64_t part[NW][V2_RB][2];
+    __shared__ uint64_t part[NW][V3_RB][2];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 3, l8 = lane & 7;
-    const int row0 = blockIdx.x * V2_RB;
+    const int row0 = blockIdx.x * V3_RB;
     const int ffn = M >> 1;
     const int k0 = wave * seg;
     const int kn = max(0, min(seg, K - k0));
 
+    // row of group g (EPI 2: gate rows 4b+g, then up rows ffn+4b+g-4)
+    const int pr = blockIdx.x * 4 + (g & 3);
+    const int row = EPI == 2 ? (g < 4 ? pr : ffn + pr) : row0 + g;
+    const bool live = EPI == 2 ? pr < ffn : row < M;
+    const ulonglong2 *w2 =
+        reinterpret_cast<const ulonglong2 *>(W + (size_t)(live ? row : 0) * K + k0) + l8;
+    const int nt = kn >> 4;
+
+    // first batch of weight loads, before anything waits
+    ulonglong2 wv[UNR];
+    const int nb0 = live ? min(UNR, nt) : 0;
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+        if (u < nb0)
+            wv[u] = w2[u * 8];
+
     int64_t r = 0;
     if (PRO == 1)
         r = block_rms_inv<NW>(x, K, red_lo, red_hi);
+    else if (PRO == 2)
+        r = *r_in;
 
     // stage this wave's segment of x, flipped; sum x over the segment
     uint64_t xsum = 0;
     uint64_t *xw = xs + (size_t)wave * seg;
     for (int j = lane; j < kn; j += 64) {
         int64_t v = x[k0 + j];
-        if (PRO == 1)
+        if (PRO != 0)
             v = q48_mul(q48_mul(v, r), norm_w[k0 + j]);
         xw[j] = (uint64_t)v ^ 0x8000000000000000ull;
         xsum += (uint64_t)v;
@@ -227,18 +260,18 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v2(int64_t *__restrict__ y,
     xsum = (uint64_t)q48_wave_sum64((int64_t)xsum);
     __syncthreads();
 
-    // row of group g (EPI 2: gate rows 4b+g, then up rows ffn+4b+g-4)
-    const int pr = blockIdx.x * 4 + (g & 3);
-    const int row = EPI == 2 ? (g < 4 ? pr : ffn + pr) : row0 + g;
-    const bool live = EPI == 2 ? pr < ffn : row < M;
     LimbAcc A = {0, 0, 0, 0, 0, 0};
     if (live) {
-        const ulonglong2 *w2 = reinterpret_cast<const ulonglong2 *>(W + (size_t)row * K + k0) + l8;
         const uint4 *x4 = reinterpret_cast<const uint4 *>(xw) + l8;
-        const int nt = kn >> 4;
-        int t = 0;
+#pragma unroll
+        for (int u = 0; u < UNR; ++u)
+            if (u < nb0) {
+                const uint4 xv = x4[u * 8];
+                mac_flip(A, xv.x, xv.y, wv[u].x);
+                mac_flip(A, xv.z, xv.w, wv[u].y);
+            }
+        int t = nb0;
         for (; t + UNR <= nt; t += UNR) {
-            ulonglong2 wv[UNR];
 #pragma unroll
             for (int u = 0; u < UNR; ++u)
                 wv[u] = w2[(t + u) * 8];
@@ -250,17 +283,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v2(int64_t *__restrict__ y,
             }
         }
         for (; t < nt; ++t) {
-            const ulonglong2 wv = w2[t * 8];
+            const ulonglong2 w1 = w2[t * 8];
             const uint4 xv = x4[t * 8];
-            mac_flip(A, xv.x, xv.y, wv.x);
-            mac_flip(A, xv.z, xv.w, wv.y);
+            mac_flip(A, xv.x, xv.y, w1.x);
+            mac_flip(A, xv.z, xv.w, w1.y);
         }
         // segment tail: kn % 16 elements (even), one pair per lane
         if (2 * l8 < (kn & 15)) {
-            const ulonglong2 wv = w2[nt * 8];
+            const ulonglong2 w1 = w2[nt * 8];
             const uint4 xv = x4[nt * 8];
-            mac_flip(A, xv.x, xv.y, wv.x);
-            mac_flip(A, xv.z, xv.w, wv.y);
+            mac_flip(A, xv.x, xv.y, w1.x);
+            mac_flip(A, xv.z, xv.w, w1.y);
         }
     }
     q48_u128 S = acc_value(A);
@@ -275,40 +308,129 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v2(int64_t *__restrict__ y,
         part[wave][g][1] = (uint64_t)(S >> 64);
     }
     __syncthreads();
-    if (tid < V2_RB) {
-        q48_u128 T = 0;
+    if (tid >= V3_RB)
+        return;
+    q48_u128 T = 0;
 #pragma unroll
-        for (int w = 0; w < NW; ++w)
-            T += ((q48_u128)part[w][tid][1] << 64) | part[w][tid][0];
-        const int64_t v = (int64_t)((q48_i128)T >> 48);
-        const int rr = row0 + tid;
-        if (EPI == 0) {
-            if (rr < M)
-                y[rr] = v;
-        } else if (EPI == 1) {
-            if (rr < M)
-                y[rr] = (int64_t)((uint64_t)y[rr] + (uint64_t)v);
-        } else {
-            // threads 0-3 hold gate rows, 4-7 the matching up rows
-            const int64_t up = __shfl_down(v, 4, 64);
-            const int i = blockIdx.x * 4 + tid;
-            if (tid < 4 && i < ffn)
-                y[i] = q48_mul(q48_silu(v), up);
+    for (int w = 0; w < NW; ++w)
+        T += ((q48_u128)part[w][tid][1] << 64) | part[w][tid][0];
+    const int64_t v = (int64_t)((q48_i128)T >> 48);
+    const int rr = row0 + tid;
+    if (EPI == 0) {
+        if (rr < M)
+            y[rr] = v;
+    } else if (EPI == 1 || EPI == 3) {
+        int64_t h = 0;
+        if (rr < M) {
+            h = (int64_t)((uint64_t)y[rr] + (uint64_t)v);
+            y[rr] = h;
         }
+        if (EPI == 3) {
+            q48_u128 sq = (q48_u128)((q48_i128)h * h);
+#pragma unroll
+            for (int off = 1; off < 8; off <<= 1) {
+                const uint64_t lo = (uint64_t)sq, hi = (uint64_t)(sq >> 64);
+                sq += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
+            }
+            if (tid == 0) {
+                __hip_atomic_store(&rms_part[2 * blockIdx.x], (uint64_t)sq, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&rms_part[2 * blockIdx.x + 1], (uint64_t)(sq >> 64),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int ticket = __hip_atomic_fetch_add(rms_count, 1, __ATOMIC_ACQ_REL,
+                                                          __HIP_MEMORY_SCOPE_AGENT);
+                if (ticket == (int)gridDim.x - 1) {
+                    // last block: every partial is visible (acquire above)
+                    q48_u128 ss = 0;
+                    for (unsigned b = 0; b < gridDim.x; ++b) {
+                        const uint64_t lo = __hip_atomic_load(&rms_part[2 * b], __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+                        const uint64_t hi = __hip_atomic_load(&rms_part[2 * b + 1],
+                                                              __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+                        ss += ((q48_u128)hi << 64) | lo;
+                    }
+                    *r_out = rms_inv_of(ss, M);
+                    __hip_atomic_store(rms_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+    } else {
+        // threads 0-3 hold gate rows, 4-7 the matching up rows
+        const int64_t up = __shfl_down(v, 4, 64);
+        const int i = blockIdx.x * 4 + tid;
+        if (tid < 4 && i < ffn)
+            y[i] = q48_mul(q48_silu(v), up);
     }
 }
 
+// Standalone rmsnorm statistics r of x (one block): for the fallbacks and
+// for the first hidden vector of a token.  With table != nullptr it also
+// copies table[*d_token or token] to out first (the embedding row,
+// llama_int.c:2822-2824) and takes the statistics of that row.
+__global__ __launch_bounds__(256) void k_rms_inv(int64_t *__restrict__ r_out,
+                                                int64_t *__restrict__ out,
+                                                const int64_t *__restrict__ x,
+                                                const int64_t *__restrict__ table,
+                                                const int *__restrict__ d_token, int token,
+                                                int dim)
+{
+    __shared__ uint64_t red_lo[4], red_hi[4];
+    const int tid = threadIdx.x;
+    if (table) {
+        if (d_token)
+            token = *d_token;
+        x = table + (size_t)token * dim;
+    }
+    q48_u128 ss = 0;
+    for (int i = tid; i < dim; i += 256) {
+        const int64_t v = x[i];
+        if (table)
+            out[i] = v;
+        ss += (q48_u128)((q48_i128)v * v);
+    }
+    ss = q48_wave_sum128(ss);
+    if ((tid & 63) == 0) {
+        red_lo[tid >> 6] = (uint64_t)ss;
+        red_hi[tid >> 6] = (uint64_t)(ss >> 64);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        q48_u128 t = 0;
+        for (int w = 0; w < 4; ++w)
+            t += ((q48_u128)red_hi[w] << 64) | red_lo[w];
+        *r_out = rms_inv_of(t, dim);
+    }
+}
+
+// out = fp_mul(fp_mul(x, *r), w): the per-element part of rmsnorm.
+__global__ __launch_bounds__(256) void k_rms_apply(int64_t *__restrict__ out,
+                                                  const int64_t *__restrict__ x,
+                                                  const int64_t *__restrict__ w,
+                                                  const int64_t *__restrict__ r, int dim)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < dim)
+        out[i] = q48_mul(q48_mul(x[i], *r), w[i]);
+}
+
 template <int PRO, int EPI>
-static int launch_v2(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
-                     const int64_t *norm_w, int M, int K)
+static int launch_v3(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                     const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M, int K)
 {
     constexpr int NW = 8;
     // segment: K / NW rounded up to a multiple of 16 elements
     const int seg = ((K + NW - 1) / NW + 15) / 16 * 16;
     const size_t lds = (size_t)seg * NW * sizeof(uint64_t);
-    dim3 grid(EPI == 2 ? (M / 2 + 3) / 4 : (M + V2_RB - 1) / V2_RB);
-    hipLaunchKernelGGL((k_gemv_v2<NW, 16, PRO, EPI>), grid, dim3(64 * NW), lds, c->stream,
-                       y, W, x, norm_w, M, K, seg);
+    const int blocks = EPI == 2 ? (M / 2 + 3) / 4 : (M + V3_RB - 1) / V3_RB;
+    if (EPI == 3) {
+        int rc = q48_rms_reserve(c, blocks);
+        if (rc)
+            return rc;
+    }
+    hipLaunchKernelGGL((k_gemv_v3<NW, 16, PRO, EPI>), dim3(blocks), dim3(64 * NW), lds,
+                       c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count, M,
+                       K, seg);
     return (int)hipGetLastError();
 }
 
@@ -443,20 +565,42 @@ bool q48_gemv_v2_ok(const int64_t *W, int K)
 }
 
 int q48_launch_gemv_fused(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
-                          const int64_t *norm_w, int M, int K, int pro, int epi)
+                          const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
+                          int K, int pro, int epi)
 {
-    if (pro)
-        return epi == 2 ? launch_v2<1, 2>(c, y, W, x, norm_w, M, K)
-                        : launch_v2<1, 0>(c, y, W, x, norm_w, M, K);
-    return epi == 1 ? launch_v2<0, 1>(c, y, W, x, norm_w, M, K)
-                    : launch_v2<0, 0>(c, y, W, x, norm_w, M, K);
+    if (pro == 1)
+        return epi == 2 ? launch_v3<1, 2>(c, y, W, x, norm_w, nullptr, nullptr, M, K)
+                        : launch_v3<1, 0>(c, y, W, x, norm_w, nullptr, nullptr, M, K);
+    if (pro == 2)
+        return epi == 2 ? launch_v3<2, 2>(c, y, W, x, norm_w, r_in, nullptr, M, K)
+                        : launch_v3<2, 0>(c, y, W, x, norm_w, r_in, nullptr, M, K);
+    if (epi == 3)
+        return launch_v3<0, 3>(c, y, W, x, nullptr, nullptr, r_out, M, K);
+    return epi == 1 ? launch_v3<0, 1>(c, y, W, x, nullptr, nullptr, nullptr, M, K)
+                    : launch_v3<0, 0>(c, y, W, x, nullptr, nullptr, nullptr, M, K);
+}
+
+int q48_launch_rms_inv(q48_ctx *c, int64_t *r_out, int64_t *out, const int64_t *x,
+                       const int64_t *table, const int *d_token, int token, int dim)
+{
+    hipLaunchKernelGGL(k_rms_inv, dim3(1), dim3(256), 0, c->stream, r_out, out, x, table,
+                       d_token, token, dim);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_rms_apply(q48_ctx *c, int64_t *out, const int64_t *x, const int64_t *w,
+                         const int64_t *r, int dim)
+{
+    hipLaunchKernelGGL(k_rms_apply, dim3((dim + 255) / 256), dim3(256), 0, c->stream, out, x, w,
+                       r, dim);
+    return (int)hipGetLastError();
 }
 
 int q48_launch_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
                     int M, int K)
 {
     if (q48_gemv_v2_ok(W, K))
-        return launch_v2<0, 0>(c, y, W, x, nullptr, M, K);
+        return launch_v3<0, 0>(c, y, W, x, nullptr, nullptr, nullptr, M, K);
     const bool vec = (K % 2 == 0) && (((uintptr_t)W & 15) == 0);
     if (M >= 1024) {
         dim3 grid((M + 7) / 8);

@@ -21,6 +21,9 @@ struct q48_ctx {
     int step_mode;               // ops read token / pos from d_step
     void *tmp;                   // device temporaries of the unfused fallbacks
     size_t tmp_bytes;
+    uint64_t *rms_part;          // device: per-block partial sums of squares (EPI 3)
+    int *rms_count;              // device: blocks finished (EPI 3), back to 0 after use
+    int rms_blocks;
     hipGraph_t graph;            // captured decode step
     hipGraphExec_t graph_exec;
     int capturing;
@@ -39,8 +42,17 @@ int q48_launch_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
                     int M, int K);
 bool q48_gemv_v2_ok(const int64_t *W, int K);
 // pro: 1 = rmsnorm(x, norm_w) prologue; epi: 0 store, 1 add into y, 2 SwiGLU pairs
+// pro: 0 none, 1 rmsnorm(x, norm_w) computed in every block, 2 with r = *r_in;
+// epi: 0 store, 1 add into y, 2 SwiGLU pairs, 3 add into y + rms statistics -> *r_out
 int q48_launch_gemv_fused(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
-                          const int64_t *norm_w, int M, int K, int pro, int epi);
+                          const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
+                          int K, int pro, int epi);
+int q48_launch_rms_inv(q48_ctx *c, int64_t *r_out, int64_t *out, const int64_t *x,
+                       const int64_t *table, const int *d_token, int token, int dim);
+int q48_launch_rms_apply(q48_ctx *c, int64_t *out, const int64_t *x, const int64_t *w,
+                         const int64_t *r, int dim);
+// Grow the per-block partial sums of the rms epilogue to `blocks` entries.
+int q48_rms_reserve(q48_ctx *c, int blocks);
 int q48_launch_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X,
                     int T, int N, int K);
 int q48_launch_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *x,

@@ -235,11 +235,16 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_decode(
 //    (rope_apply, llama_int.c:997-1008, 1392-1395); the first head of each
 //    KV group writes the rotated k and v_new into the cache;
 //  - 8 lanes per score: each lane multiplies hd/8 dimensions, a 3-step
-//    128-bit butterfly sums them, so a score costs hd/8 MACs of latency.
+//    128-bit butterfly sums them, so a score costs hd/8 MACs of latency;
+//  - scores / probabilities in LDS when the cache fits (LDS = 1), else in
+//    the global workspace row of the head;
+//  - the V pass keeps 8 independent loads in flight per thread.
 // pos is read from *d_pos when given (graph replay of a decode step).
 // hd must be a multiple of 8 and divide 256 (checked on the host).
 // ---------------------------------------------------------------------------
-template <int ROPE>
+constexpr int ATT_LDS_MAX = 4096;   // positions whose scores fit in LDS (32 KiB)
+
+template <int ROPE, int LDS>
 __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
     int64_t *__restrict__ out, const int64_t *__restrict__ q,
     int64_t *__restrict__ kcache, int64_t *__restrict__ vcache,
@@ -248,9 +253,10 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
     const int64_t *__restrict__ sin_t, int layer, const int *__restrict__ d_pos, int pos,
     int n_heads, int n_kv, int hd, int max_seq)
 {
-    __shared__ int64_t qs[256], ks[256];
+    __shared__ int64_t qs[256], ks[256], vs[256];
     __shared__ int64_t red[ATT_NT / 64];
     __shared__ int64_t part[ATT_NT];
+    __shared__ int64_t sc_lds[LDS ? ATT_LDS_MAX : 1];
     if (d_pos)
         pos = *d_pos;
     if (pos < 0 || pos >= max_seq)
@@ -263,6 +269,7 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
     const int64_t *kn = k_new + (size_t)kh * hd;
     const int64_t *vn = v_new + (size_t)kh * hd;
     const int half = hd / 2;
+    int64_t *sc = LDS ? sc_lds : scores + (size_t)h * max_seq;
 
     if (ROPE) {
         if (tid < half) {
@@ -281,16 +288,17 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
             ks[d] = kn[d];
         }
     }
+    for (int d = tid; d < hd; d += ATT_NT)
+        vs[d] = vn[d];
     __syncthreads();
     if (h % group == 0)
         for (int d = tid; d < hd; d += ATT_NT) {
             kcache[(base + pos) * kvd + (size_t)kh * hd + d] = ks[d];
-            vcache[(base + pos) * kvd + (size_t)kh * hd + d] = vn[d];
+            vcache[(base + pos) * kvd + (size_t)kh * hd + d] = vs[d];
         }
 
     const int64_t scale = q48_inv_sqrt(q48_from_int(hd));
     const int S = pos + 1;
-    int64_t *sc = scores + (size_t)h * max_seq;
 
     // scores: group g of 8 lanes takes position t; lane l8 dims [l8*dpl, +dpl)
     const int g = tid >> 3, l8 = tid & 7, dpl = hd >> 3;
@@ -300,8 +308,13 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
         q48_u128 dot = 0;
         if (t < S) {
             const int64_t *kt = t == pos ? ks : kcache + (base + t) * kvd + (size_t)kh * hd;
-            for (int d = l8 * dpl; d < (l8 + 1) * dpl; ++d)
-                dot += (q48_u128)((q48_i128)qs[d] * kt[d]);
+            kt += l8 * dpl;
+            const int64_t *qd = qs + l8 * dpl;
+            for (int d = 0; d < dpl; d += 2) {
+                const int64_t a0 = kt[d], a1 = kt[d + 1];
+                dot += (q48_u128)((q48_i128)qd[d] * a0);
+                dot += (q48_u128)((q48_i128)qd[d + 1] * a1);
+            }
         }
 #pragma unroll
         for (int off = 1; off < 8; off <<= 1) {
@@ -328,14 +341,26 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
             sc[t] = q48_div(sc[t], sum);
     __syncthreads();
 
+    // o[d] = sum_t fp_mul(p_t, v_t[d]): 8 positions per batch, loads first
     const int slices = ATT_NT / hd;
     const int d = tid % hd, sl = tid / hd;
-    int64_t acc = 0;
-    for (int t = sl; t < S; t += slices) {
-        const int64_t *vt = t == pos ? vn : vcache + (base + t) * kvd + (size_t)kh * hd;
-        acc = (int64_t)((uint64_t)acc + (uint64_t)q48_mul(sc[t], vt[d]));
+    const int64_t *vcol = vcache + base * kvd + (size_t)kh * hd + d;
+    uint64_t acc = 0;
+    int t = sl;
+    for (; t + 7 * slices < S; t += 8 * slices) {
+        int64_t vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int tu = t + u * slices;
+            vv[u] = tu == pos ? vs[d] : vcol[(size_t)tu * kvd];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            acc += (uint64_t)q48_mul(sc[t + u * slices], vv[u]);
     }
-    part[tid] = acc;
+    for (; t < S; t += slices)
+        acc += (uint64_t)q48_mul(sc[t], t == pos ? vs[d] : vcol[(size_t)t * kvd]);
+    part[tid] = (int64_t)acc;
     __syncthreads();
     if (sl == 0) {
         uint64_t o = 0;
@@ -586,17 +611,26 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
                        int layer, const int *d_pos, int pos, int n_heads, int n_kv,
                        int head_dim, int max_seq, int rope)
 {
-    int rc = q48_ws_reserve(c, (size_t)n_heads * max_seq * sizeof(int64_t));
-    if (rc)
-        return rc;
-    if (rope)
-        hipLaunchKernelGGL(k_attn_v2<1>, dim3(n_heads), dim3(ATT_NT), 0, c->stream, out, q,
-                           kcache, vcache, k_new, v_new, (int64_t *)c->ws, c->rope_cos,
-                           c->rope_sin, layer, d_pos, pos, n_heads, n_kv, head_dim, max_seq);
+    const bool lds = max_seq <= ATT_LDS_MAX;
+    if (!lds) {
+        int rc = q48_ws_reserve(c, (size_t)n_heads * max_seq * sizeof(int64_t));
+        if (rc)
+            return rc;
+    }
+    int64_t *ws = (int64_t *)c->ws;
+#define ATT_LAUNCH(R, L)                                                                      \
+    hipLaunchKernelGGL((k_attn_v2<R, L>), dim3(n_heads), dim3(ATT_NT), 0, c->stream, out, q,   \
+                       kcache, vcache, k_new, v_new, ws, c->rope_cos, c->rope_sin, layer,     \
+                       d_pos, pos, n_heads, n_kv, head_dim, max_seq)
+    if (rope && lds)
+        ATT_LAUNCH(1, 1);
+    else if (rope)
+        ATT_LAUNCH(1, 0);
+    else if (lds)
+        ATT_LAUNCH(0, 1);
     else
-        hipLaunchKernelGGL(k_attn_v2<0>, dim3(n_heads), dim3(ATT_NT), 0, c->stream, out, q,
-                           kcache, vcache, k_new, v_new, (int64_t *)c->ws, c->rope_cos,
-                           c->rope_sin, layer, d_pos, pos, n_heads, n_kv, head_dim, max_seq);
+        ATT_LAUNCH(0, 0);
+#undef ATT_LAUNCH
     return (int)hipGetLastError();
 }
 

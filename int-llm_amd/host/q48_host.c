@@ -43,6 +43,7 @@ struct q48h_model {
     int64_t *act;               /* device activations */
     int64_t *hidden, *normed, *qkv, *attn, *o, *gu, *h_ffn, *mlp, *logits;
     int *d_tokens;              /* device: tokens of graph-replayed decode steps */
+    int64_t *r_attn, *r_ffn;    /* device: rmsnorm statistics of hidden for the next norm */
     int fused;                  /* 1: fused decode ops (default), 0: one op per kernel */
     int graph_ready;            /* the context graph holds this model's decode step */
 };
@@ -186,6 +187,7 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
     size_t a_ffn = an; an += align_up(ffn);
     size_t a_mlp = an; an += align_up(dim);
     size_t a_log = an; an += align_up((size_t)c->vocab);
+    size_t a_r = an; an += ALIGN_ELEMS;
 
     m->fused = 1;
     if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
@@ -205,6 +207,8 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
     m->h_ffn = m->act + a_ffn;
     m->mlp = m->act + a_mlp;
     m->logits = m->act + a_log;
+    m->r_attn = m->act + a_r;
+    m->r_ffn = m->act + a_r + 1;
     if ((rc = q48_zero(ctx, m->w, weight_elems(m) * 8)) ||
         (rc = q48_zero(ctx, m->kc, kvn * 8)) || (rc = q48_zero(ctx, m->vc, kvn * 8)) ||
         (rc = q48_zero(ctx, m->act, an * 8)) ||
@@ -602,12 +606,16 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
     const int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
     int64_t *q = m->qkv, *k = m->qkv + dim, *v = m->qkv + dim + kvd;
 
-    TRY(q48_rmsnorm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an, dim + 2 * kvd, dim));
+    /* r_attn holds the statistics of hidden (from the embedding or the
+     * previous layer's down projection) */
+    TRY(q48_norm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an, m->r_attn,
+                      dim + 2 * kvd, dim));
     TRY(q48_attn_decode_rope(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
                              c->n_kv_heads, hd, c->max_seq));
-    TRY(q48_gemv_residual(x, m->hidden, b + m->lo_wo, m->attn, dim, dim));
-    TRY(q48_rmsnorm_gemv_swiglu(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn, ffn, dim));
-    TRY(q48_gemv_residual(x, m->hidden, b + m->lo_wd, m->h_ffn, dim, ffn));
+    TRY(q48_gemv_residual_rms(x, m->hidden, b + m->lo_wo, m->attn, dim, dim, m->r_ffn));
+    TRY(q48_norm_gemv_swiglu(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn, m->r_ffn,
+                             ffn, dim));
+    TRY(q48_gemv_residual_rms(x, m->hidden, b + m->lo_wd, m->h_ffn, dim, ffn, m->r_attn));
     return Q48_OK;
 }
 
@@ -640,13 +648,14 @@ static int layer_forward(q48h_model *m, int l, int pos)
 static int enqueue_forward(q48h_model *m, int token, int pos)
 {
     const q48h_config *c = &m->c;
-    TRY(q48_embed(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim));
     if (m->fused) {
+        TRY(q48_embed_rms(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim, m->r_attn));
         for (int l = 0; l < c->n_layers; ++l)
             TRY(layer_forward_fused(m, l, pos));
-        TRY(q48_rmsnorm_gemv(m->ctx, m->logits, m->w + m->off_lm, m->hidden,
-                             m->w + m->off_norm, c->vocab, c->dim));
+        TRY(q48_norm_gemv(m->ctx, m->logits, m->w + m->off_lm, m->hidden, m->w + m->off_norm,
+                          m->r_attn, c->vocab, c->dim));
     } else {
+        TRY(q48_embed(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim));
         for (int l = 0; l < c->n_layers; ++l)
             TRY(layer_forward(m, l, pos));
         TRY(q48_rmsnorm(m->ctx, m->normed, m->hidden, m->w + m->off_norm, c->dim));

@@ -54,6 +54,11 @@ ABI_SIGNATURES = {
     "q48_gemv_residual": [_P, _P, _P, _P, _I, _I],
     "q48_rmsnorm_gemv_swiglu": [_P, _P, _P, _P, _P, _I, _I],
     "q48_attn_decode_rope": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
+    "q48_rms_inv": [_P, _P, _P, _I],
+    "q48_embed_rms": [_P, _P, _P, _I, _I, _P],
+    "q48_norm_gemv": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "q48_norm_gemv_swiglu": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "q48_gemv_residual_rms": [_P, _P, _P, _P, _I, _I, _P],
     "q48_step_mode": [_P, _I],
     "q48_step_set": [_P, _I, _I],
     "q48_step_get": [_P, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)],
@@ -245,6 +250,23 @@ class Context:
     def attn_decode_rope(self, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq):
         return check("q48_attn_decode_rope", hip_lib().q48_attn_decode_rope(
             self.h, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq))
+
+    def rms_inv(self, r_out, x, dim):
+        return check("q48_rms_inv", hip_lib().q48_rms_inv(self.h, r_out, x, dim))
+
+    def embed_rms(self, out, table, token, dim, r_out):
+        return check("q48_embed_rms", hip_lib().q48_embed_rms(self.h, out, table, token, dim, r_out))
+
+    def norm_gemv(self, y, W, x, norm_w, r, M, K):
+        return check("q48_norm_gemv", hip_lib().q48_norm_gemv(self.h, y, W, x, norm_w, r, M, K))
+
+    def norm_gemv_swiglu(self, out, Wgu, x, norm_w, r, ffn, K):
+        return check("q48_norm_gemv_swiglu",
+                     hip_lib().q48_norm_gemv_swiglu(self.h, out, Wgu, x, norm_w, r, ffn, K))
+
+    def gemv_residual_rms(self, acc, W, x, M, K, r_out):
+        return check("q48_gemv_residual_rms",
+                     hip_lib().q48_gemv_residual_rms(self.h, acc, W, x, M, K, r_out))
 
     def prof_enable(self, on: bool = True):
         check("q48_prof_enable", hip_lib().q48_prof_enable(self.h, int(on)))

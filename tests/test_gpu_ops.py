@@ -401,3 +401,83 @@ def test_attention_rope_fused(ctx, oracle, nh, nkv, hd, max_seq, positions):
         assert np.array_equal(dk.download(), kc) and np.array_equal(dv.download(), vc)
         for b in (dq, dkn, dvn, do):
             b.free()
+
+
+def rms_inv_exact(oracle, x):
+    """The scalar of rmsnorm (llama_int.c:1049-1055) with Python integers:
+    int128-wrapped sum of squares, floor shift, truncating division."""
+    ss = sum(int(v) * int(v) for v in x)
+    ss = ((ss + (1 << 127)) % (1 << 128)) - (1 << 127)
+    q = ss >> 48
+    ms = abs(q) // len(x) * (1 if q >= 0 else -1)
+    ms = spec.wrap64(spec.wrap64(ms) + 2814749767)
+    return oracle.q48o_fp_inv_sqrt(ms)
+
+
+@pytest.mark.parametrize("dim", [1, 7, 256, 2048, 5000])
+def test_rms_inv_and_embed_rms(ctx, oracle, dim):
+    rng = np.random.default_rng(dim)
+    table = (rng.standard_normal(3 * dim) * 2 * ONE).astype(np.int64)
+    dt, do, dr = ctx.to_device(table), ctx.buffer(dim), ctx.buffer(1)
+    say("embed_rms", dim)
+    ctx.embed_rms(do.ptr, dt.ptr, 2, dim, dr.ptr)
+    row = table[2 * dim:3 * dim]
+    assert np.array_equal(do.download(), row)
+    assert int(dr.download()[0]) == rms_inv_exact(oracle, row)
+    ctx.rms_inv(dr.ptr, dt.ptr, dim)
+    assert int(dr.download()[0]) == rms_inv_exact(oracle, table[:dim])
+
+
+@pytest.mark.parametrize("M,K", [(2560, 2048), (32000, 2048), (64, 256), (9, 7681)])
+def test_norm_gemv_with_r(ctx, oracle, M, K):
+    rng = np.random.default_rng(M * 5 + K)
+    W = (rng.standard_normal(M * K) * spec.SIGMA_W).astype(np.int64)
+    x = (rng.standard_normal(K) * 3 * ONE).astype(np.int64)
+    w = (rng.standard_normal(K) * ONE).astype(np.int64)
+    want = O.gemv(W, _rms(oracle, x, w), M, K)
+    dW, dx, dw, dy, dr = ctx.to_device(W), ctx.to_device(x), ctx.to_device(w), ctx.buffer(M), ctx.buffer(1)
+    say("norm_gemv", M, K)
+    ctx.rms_inv(dr.ptr, dx.ptr, K)
+    ctx.norm_gemv(dy.ptr, dW.ptr, dx.ptr, dw.ptr, dr.ptr, M, K)
+    assert np.array_equal(dy.download(), want)
+    for b in (dW, dx, dw, dy, dr):
+        b.free()
+
+
+@pytest.mark.parametrize("ffn,K", [(5632, 2048), (688, 256), (6, 7681)])
+def test_norm_gemv_swiglu_with_r(ctx, oracle, ffn, K):
+    rng = np.random.default_rng(ffn + 3 * K)
+    W = (rng.standard_normal(2 * ffn * K) * spec.SIGMA_W * 20).astype(np.int64)
+    x = (rng.standard_normal(K) * ONE).astype(np.int64)
+    w = (rng.standard_normal(K) * ONE).astype(np.int64)
+    t = O.gemv(W, _rms(oracle, x, w), 2 * ffn, K)
+    want = np.empty(ffn, dtype=np.int64)
+    g, u = t[:ffn].copy(), t[ffn:].copy()
+    oracle.q48o_silu_mul(want.ctypes.data, g.ctypes.data, u.ctypes.data, ffn)
+    dW, dx, dw, do, dr = ctx.to_device(W), ctx.to_device(x), ctx.to_device(w), ctx.buffer(ffn), ctx.buffer(1)
+    say("norm_gemv_swiglu", ffn, K)
+    ctx.rms_inv(dr.ptr, dx.ptr, K)
+    ctx.norm_gemv_swiglu(do.ptr, dW.ptr, dx.ptr, dw.ptr, dr.ptr, ffn, K)
+    assert np.array_equal(do.download(), want)
+    for b in (dW, dx, dw, do, dr):
+        b.free()
+
+
+@pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 5632), (256, 688), (13, 40), (3, 7681)])
+def test_gemv_residual_rms(ctx, oracle, M, K):
+    """acc += W x and r_out = statistics of the new acc; three calls in a row
+    (the last-block counter must reset itself)."""
+    rng = np.random.default_rng(M + 11 * K)
+    h = (rng.standard_normal(M) * ONE).astype(np.int64)
+    dh, dr = ctx.to_device(h), ctx.buffer(1)
+    for it in range(3):
+        W = (rng.standard_normal(M * K) * spec.SIGMA_W).astype(np.int64)
+        x = (rng.standard_normal(K) * ONE).astype(np.int64)
+        h = (h.view(np.uint64) + O.gemv(W, x, M, K).view(np.uint64)).view(np.int64)
+        dW, dx = ctx.to_device(W), ctx.to_device(x)
+        say("gemv_residual_rms", M, K, "call", it)
+        ctx.gemv_residual_rms(dh.ptr, dW.ptr, dx.ptr, M, K, dr.ptr)
+        assert np.array_equal(dh.download(), h), it
+        assert int(dr.download()[0]) == rms_inv_exact(oracle, h), it
+        dW.free()
+        dx.free()
