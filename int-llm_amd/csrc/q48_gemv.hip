@@ -147,12 +147,27 @@ __global__ __launch_bounds__(64 * RPB) void k_gemv(int64_t *__restrict__ y,
 }
 
 // ---------------------------------------------------------------------------
-// GEMV v3: 8 rows per block, one 8-lane group per row (each load
+// GEMV v4 (the decode kernel).
+//
+// Carry-free limbs.  x is shared by every row, so it is split once, when it
+// is staged, into three limbs of its flipped value X' = x ^ 2^63:
+//     X' = x0 + 2^22 x1 + 2^43 x2,   x0 < 2^22, x1, x2 < 2^21,
+// and each weight into two 32-bit limbs of W' = w ^ 2^63.  Every partial
+// product x_i * w_j is below 2^54, so a 64-bit accumulator holds the sum of
+// up to 1024 of them exactly: six v_mad_u64_u32 per MAC and no carry
+// handling.  A lane sums at most K / 8 / NW <= 1023 products per
+// accumulator (K <= V4_MAX_K).  At the end
+//     S = a00 + 2^32 a01 + 2^22 a10 + 2^54 a11 + 2^43 a20 + 2^75 a21
+//         - 2^63 (sum w + sum x)                                 (mod 2^128)
+// (the offset-binary identity above), and y = (int64)(S >> 48).
+//
+// Layout.  8 rows per block, one 8-lane group per row (each load
 // instruction of a group reads one full 128-byte line of its row), NW
 // waves per block each taking one K-segment of all 8 rows.  Every lane has
-// UNR 16-byte weight loads in flight; the first batch is issued before the
-// prologue (x staging, norm statistics), so HBM latency overlaps it.
-// Per-segment partials meet in LDS.
+// UNR 16-byte weight loads in flight and the first batch is issued before
+// the prologue.  Each wave stages only its own segment of x, so no
+// block-wide barrier sits between the prologue and the loads; the segment
+// partials meet in LDS at the end.
 //
 // Prologues (the staged x is exactly what rmsnorm, llama_int.c:1048-1058,
 // would write):  PRO 0: x as given;  PRO 1: every block computes the
@@ -164,10 +179,10 @@ __global__ __launch_bounds__(64 * RPB) void k_gemv(int64_t *__restrict__ y,
 // ffn+4b.. (groups 4-7) and stores fp_mul(fp_silu(gate), up)
 // (llama_int.c:1549-1552);  EPI 3 is EPI 1 followed by the statistics of
 // the next rmsnorm of the updated vector: each block writes its partial sum
-// of squares, the last block to finish adds them in block order and writes
+// of squares, the last block to finish adds them all and writes
 // r = fp_inv_sqrt((int64)((ss >> 48) / M) + 2814749767) to *r_out.
 // ---------------------------------------------------------------------------
-constexpr int V3_RB = 8;
+constexpr int V4_RB = 8;
 
 // (ss >> 48) / dim + eps, then fp_inv_sqrt: the scalar part of rmsnorm.
 __device__ __forceinline__ int64_t rms_inv_of(q48_u128 ss, int dim)
@@ -177,34 +192,50 @@ __device__ __forceinline__ int64_t rms_inv_of(q48_u128 ss, int dim)
     return q48_inv_sqrt(ms);
 }
 
-template <int NW>
-__device__ __forceinline__ int64_t block_rms_inv(const int64_t *__restrict__ x, int K,
-                                                  uint64_t *red_lo, uint64_t *red_hi)
+// 128-bit sum over the block (NT threads); result valid in thread 0.
+template <int NT>
+__device__ __forceinline__ q48_u128 block_sum128(q48_u128 v, uint64_t *red_lo, uint64_t *red_hi)
 {
+    v = q48_wave_sum128(v);
     const int tid = threadIdx.x;
-    q48_u128 ss = 0;
-    for (int j = tid; j < K; j += 64 * NW) {
-        const int64_t v = x[j];
-        ss += (q48_u128)((q48_i128)v * v);
-    }
-    ss = q48_wave_sum128(ss);
     if ((tid & 63) == 0) {
-        red_lo[tid >> 6] = (uint64_t)ss;
-        red_hi[tid >> 6] = (uint64_t)(ss >> 64);
+        red_lo[tid >> 6] = (uint64_t)v;
+        red_hi[tid >> 6] = (uint64_t)(v >> 64);
     }
     __syncthreads();
-    if (tid == 0) {
-        q48_u128 t = 0;
-        for (int w = 0; w < NW; ++w)
+    q48_u128 t = 0;
+    if (tid == 0)
+        for (int w = 0; w < NT / 64; ++w)
             t += ((q48_u128)red_hi[w] << 64) | red_lo[w];
-        red_lo[NW] = (uint64_t)rms_inv_of(t, K);
-    }
-    __syncthreads();
-    return (int64_t)red_lo[NW];
+    return t;
+}
+
+struct Acc6 {
+    uint64_t a00, a01, a10, a11, a20, a21, ws;
+};
+
+__device__ __forceinline__ void mac6(Acc6 &A, uint32_t x0, uint32_t x1, uint32_t x2,
+                                     uint64_t w)
+{
+    const uint32_t wl = (uint32_t)w, wh = (uint32_t)(w >> 32) ^ 0x80000000u;
+    A.a00 += (uint64_t)x0 * wl;
+    A.a01 += (uint64_t)x0 * wh;
+    A.a10 += (uint64_t)x1 * wl;
+    A.a11 += (uint64_t)x1 * wh;
+    A.a20 += (uint64_t)x2 * wl;
+    A.a21 += (uint64_t)x2 * wh;
+    A.ws += w;
+}
+
+__device__ __forceinline__ q48_u128 acc6_value(const Acc6 &A)
+{
+    return (q48_u128)A.a00 + ((q48_u128)A.a01 << 32) + ((q48_u128)A.a10 << 22) +
+           ((q48_u128)A.a11 << 54) + ((q48_u128)A.a20 << 43) + ((q48_u128)A.a21 << 75) -
+           ((q48_u128)A.ws << 63);
 }
 
 template <int NW, int UNR, int PRO, int EPI>
-__global__ __launch_bounds__(64 * NW) void k_gemv_v3(int64_t *__restrict__ y,
+__global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
                                                     const int64_t *__restrict__ W,
                                                     const int64_t *__restrict__ x,
                                                     const int64_t *__restrict__ norm_w,
@@ -214,13 +245,15 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v3(int64_t *__restrict__ y,
                                                     int *__restrict__ rms_count,
                                                     int M, int K, int seg)
 {
-    extern __shared__ __align__(16) uint64_t xs[];   // K flipped x values (segments)
-    __shared__ uint64_t red_lo[NW + 1], red_hi[NW];
-    __shared__ uint64_t part[NW][V3_RB][2];
+    extern __shared__ __align__(16) uint32_t xs[];   // 3 limbs per staged x
+    __shared__ uint64_t red_lo[NW], red_hi[NW];
+    __shared__ uint64_t part[NW][V4_RB][2];
+    __shared__ int64_t r_sh;
+    __shared__ int last_sh;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 3, l8 = lane & 7;
-    const int row0 = blockIdx.x * V3_RB;
+    const int row0 = blockIdx.x * V4_RB;
     const int ffn = M >> 1;
     const int k0 = wave * seg;
     const int kn = max(0, min(seg, K - k0));
@@ -242,33 +275,49 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v3(int64_t *__restrict__ y,
             wv[u] = w2[u * 8];
 
     int64_t r = 0;
-    if (PRO == 1)
-        r = block_rms_inv<NW>(x, K, red_lo, red_hi);
-    else if (PRO == 2)
+    if (PRO == 1) {
+        q48_u128 ss = 0;
+        for (int j = tid; j < K; j += 64 * NW) {
+            const int64_t v = x[j];
+            ss += (q48_u128)((q48_i128)v * v);
+        }
+        ss = block_sum128<64 * NW>(ss, red_lo, red_hi);
+        if (tid == 0)
+            r_sh = rms_inv_of(ss, K);
+        __syncthreads();
+        r = r_sh;
+    } else if (PRO == 2) {
         r = *r_in;
+    }
 
-    // stage this wave's segment of x, flipped; sum x over the segment
+    // stage this wave's segment of x as limbs; sum x over the segment
     uint64_t xsum = 0;
-    uint64_t *xw = xs + (size_t)wave * seg;
+    uint32_t *xw = xs + (size_t)wave * seg * 3;
     for (int j = lane; j < kn; j += 64) {
         int64_t v = x[k0 + j];
         if (PRO != 0)
             v = q48_mul(q48_mul(v, r), norm_w[k0 + j]);
-        xw[j] = (uint64_t)v ^ 0x8000000000000000ull;
+        const uint64_t X = (uint64_t)v ^ 0x8000000000000000ull;
+        xw[3 * j] = (uint32_t)X & 0x3FFFFFu;
+        xw[3 * j + 1] = (uint32_t)(X >> 22) & 0x1FFFFFu;
+        xw[3 * j + 2] = (uint32_t)(X >> 43);
         xsum += (uint64_t)v;
     }
     xsum = (uint64_t)q48_wave_sum64((int64_t)xsum);
-    __syncthreads();
+    // the segment is read only by the wave that wrote it
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    LimbAcc A = {0, 0, 0, 0, 0, 0};
+    Acc6 A = {0, 0, 0, 0, 0, 0, 0};
     if (live) {
-        const uint4 *x4 = reinterpret_cast<const uint4 *>(xw) + l8;
+        const uint32_t *xl = xw + 6 * l8;   // this lane's pair: 6 limbs per step of 16
 #pragma unroll
         for (int u = 0; u < UNR; ++u)
             if (u < nb0) {
-                const uint4 xv = x4[u * 8];
-                mac_flip(A, xv.x, xv.y, wv[u].x);
-                mac_flip(A, xv.z, xv.w, wv[u].y);
+                const uint32_t *p = xl + 48 * u;
+                mac6(A, p[0], p[1], p[2], wv[u].x);
+                mac6(A, p[3], p[4], p[5], wv[u].y);
             }
         int t = nb0;
         for (; t + UNR <= nt; t += UNR) {
@@ -277,26 +326,26 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v3(int64_t *__restrict__ y,
                 wv[u] = w2[(t + u) * 8];
 #pragma unroll
             for (int u = 0; u < UNR; ++u) {
-                const uint4 xv = x4[(t + u) * 8];
-                mac_flip(A, xv.x, xv.y, wv[u].x);
-                mac_flip(A, xv.z, xv.w, wv[u].y);
+                const uint32_t *p = xl + 48 * (t + u);
+                mac6(A, p[0], p[1], p[2], wv[u].x);
+                mac6(A, p[3], p[4], p[5], wv[u].y);
             }
         }
         for (; t < nt; ++t) {
             const ulonglong2 w1 = w2[t * 8];
-            const uint4 xv = x4[t * 8];
-            mac_flip(A, xv.x, xv.y, w1.x);
-            mac_flip(A, xv.z, xv.w, w1.y);
+            const uint32_t *p = xl + 48 * t;
+            mac6(A, p[0], p[1], p[2], w1.x);
+            mac6(A, p[3], p[4], p[5], w1.y);
         }
         // segment tail: kn % 16 elements (even), one pair per lane
         if (2 * l8 < (kn & 15)) {
             const ulonglong2 w1 = w2[nt * 8];
-            const uint4 xv = x4[nt * 8];
-            mac_flip(A, xv.x, xv.y, w1.x);
-            mac_flip(A, xv.z, xv.w, w1.y);
+            const uint32_t *p = xl + 48 * nt;
+            mac6(A, p[0], p[1], p[2], w1.x);
+            mac6(A, p[3], p[4], p[5], w1.y);
         }
     }
-    q48_u128 S = acc_value(A);
+    q48_u128 S = acc6_value(A);
 #pragma unroll
     for (int off = 1; off < 8; off <<= 1) {
         const uint64_t lo = (uint64_t)S, hi = (uint64_t)(S >> 64);
@@ -308,24 +357,21 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v3(int64_t *__restrict__ y,
         part[wave][g][1] = (uint64_t)(S >> 64);
     }
     __syncthreads();
-    if (tid >= V3_RB)
-        return;
-    q48_u128 T = 0;
+
+    if (EPI == 3) {
+        // residual add, then this block's sum of squares of the new rows
+        if (tid < V4_RB) {
+            q48_u128 T = 0;
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
-        T += ((q48_u128)part[w][tid][1] << 64) | part[w][tid][0];
-    const int64_t v = (int64_t)((q48_i128)T >> 48);
-    const int rr = row0 + tid;
-    if (EPI == 0) {
-        if (rr < M)
-            y[rr] = v;
-    } else if (EPI == 1 || EPI == 3) {
-        int64_t h = 0;
-        if (rr < M) {
-            h = (int64_t)((uint64_t)y[rr] + (uint64_t)v);
-            y[rr] = h;
-        }
-        if (EPI == 3) {
+            for (int w = 0; w < NW; ++w)
+                T += ((q48_u128)part[w][tid][1] << 64) | part[w][tid][0];
+            const int64_t v = (int64_t)((q48_i128)T >> 48);
+            const int rr = row0 + tid;
+            int64_t h = 0;
+            if (rr < M) {
+                h = (int64_t)((uint64_t)y[rr] + (uint64_t)v);
+                y[rr] = h;
+            }
             q48_u128 sq = (q48_u128)((q48_i128)h * h);
 #pragma unroll
             for (int off = 1; off < 8; off <<= 1) {
@@ -339,22 +385,45 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v3(int64_t *__restrict__ y,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const int ticket = __hip_atomic_fetch_add(rms_count, 1, __ATOMIC_ACQ_REL,
                                                           __HIP_MEMORY_SCOPE_AGENT);
-                if (ticket == (int)gridDim.x - 1) {
-                    // last block: every partial is visible (acquire above)
-                    q48_u128 ss = 0;
-                    for (unsigned b = 0; b < gridDim.x; ++b) {
-                        const uint64_t lo = __hip_atomic_load(&rms_part[2 * b], __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
-                        const uint64_t hi = __hip_atomic_load(&rms_part[2 * b + 1],
-                                                              __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
-                        ss += ((q48_u128)hi << 64) | lo;
-                    }
-                    *r_out = rms_inv_of(ss, M);
-                    __hip_atomic_store(rms_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
+                last_sh = ticket == (int)gridDim.x - 1;
             }
         }
+        __syncthreads();
+        if (!last_sh)
+            return;
+        // last block: every partial is visible (the acquire of its ticket);
+        // the whole block adds them (integer sum: any order gives the bits)
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        q48_u128 ss = 0;
+        for (unsigned b = tid; b < gridDim.x; b += 64 * NW) {
+            const uint64_t lo =
+                __hip_atomic_load(&rms_part[2 * b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t hi = __hip_atomic_load(&rms_part[2 * b + 1], __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+            ss += ((q48_u128)hi << 64) | lo;
+        }
+        ss = block_sum128<64 * NW>(ss, red_lo, red_hi);
+        if (tid == 0) {
+            *r_out = rms_inv_of(ss, M);
+            __hip_atomic_store(rms_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+
+    if (tid >= V4_RB)
+        return;
+    q48_u128 T = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+        T += ((q48_u128)part[w][tid][1] << 64) | part[w][tid][0];
+    const int64_t v = (int64_t)((q48_i128)T >> 48);
+    const int rr = row0 + tid;
+    if (EPI == 0) {
+        if (rr < M)
+            y[rr] = v;
+    } else if (EPI == 1) {
+        if (rr < M)
+            y[rr] = (int64_t)((uint64_t)y[rr] + (uint64_t)v);
     } else {
         // threads 0-3 hold gate rows, 4-7 the matching up rows
         const int64_t up = __shfl_down(v, 4, 64);
@@ -415,20 +484,20 @@ __global__ __launch_bounds__(256) void k_rms_apply(int64_t *__restrict__ out,
 }
 
 template <int PRO, int EPI>
-static int launch_v3(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
                      const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M, int K)
 {
     constexpr int NW = 8;
     // segment: K / NW rounded up to a multiple of 16 elements
     const int seg = ((K + NW - 1) / NW + 15) / 16 * 16;
-    const size_t lds = (size_t)seg * NW * sizeof(uint64_t);
-    const int blocks = EPI == 2 ? (M / 2 + 3) / 4 : (M + V3_RB - 1) / V3_RB;
+    const size_t lds = (size_t)seg * NW * 3 * sizeof(uint32_t);
+    const int blocks = EPI == 2 ? (M / 2 + 3) / 4 : (M + V4_RB - 1) / V4_RB;
     if (EPI == 3) {
         int rc = q48_rms_reserve(c, blocks);
         if (rc)
             return rc;
     }
-    hipLaunchKernelGGL((k_gemv_v3<NW, 16, PRO, EPI>), dim3(blocks), dim3(64 * NW), lds,
+    hipLaunchKernelGGL((k_gemv_v4<NW, 8, PRO, EPI>), dim3(blocks), dim3(64 * NW), lds,
                        c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count, M,
                        K, seg);
     return (int)hipGetLastError();
@@ -557,7 +626,9 @@ __global__ __launch_bounds__(256) void k_gemm(int64_t *__restrict__ Y,
 } // namespace
 
 // Largest K the v2 kernel stages in LDS (64 KiB of x).
-constexpr int V2_MAX_K = 7680;   // staged x (seg * 8 waves * 8 B) stays under 62 KiB
+// K the v4 kernel takes: staged limbs (12 B per x) stay under 144 KiB of LDS and a
+// lane sums at most K / 64 <= 1023 partial products per accumulator.
+constexpr int V2_MAX_K = 12288;
 
 bool q48_gemv_v2_ok(const int64_t *W, int K)
 {
@@ -569,15 +640,15 @@ int q48_launch_gemv_fused(q48_ctx *c, int64_t *y, const int64_t *W, const int64_
                           int K, int pro, int epi)
 {
     if (pro == 1)
-        return epi == 2 ? launch_v3<1, 2>(c, y, W, x, norm_w, nullptr, nullptr, M, K)
-                        : launch_v3<1, 0>(c, y, W, x, norm_w, nullptr, nullptr, M, K);
+        return epi == 2 ? launch_v4<1, 2>(c, y, W, x, norm_w, nullptr, nullptr, M, K)
+                        : launch_v4<1, 0>(c, y, W, x, norm_w, nullptr, nullptr, M, K);
     if (pro == 2)
-        return epi == 2 ? launch_v3<2, 2>(c, y, W, x, norm_w, r_in, nullptr, M, K)
-                        : launch_v3<2, 0>(c, y, W, x, norm_w, r_in, nullptr, M, K);
+        return epi == 2 ? launch_v4<2, 2>(c, y, W, x, norm_w, r_in, nullptr, M, K)
+                        : launch_v4<2, 0>(c, y, W, x, norm_w, r_in, nullptr, M, K);
     if (epi == 3)
-        return launch_v3<0, 3>(c, y, W, x, nullptr, nullptr, r_out, M, K);
-    return epi == 1 ? launch_v3<0, 1>(c, y, W, x, nullptr, nullptr, nullptr, M, K)
-                    : launch_v3<0, 0>(c, y, W, x, nullptr, nullptr, nullptr, M, K);
+        return launch_v4<0, 3>(c, y, W, x, nullptr, nullptr, r_out, M, K);
+    return epi == 1 ? launch_v4<0, 1>(c, y, W, x, nullptr, nullptr, nullptr, M, K)
+                    : launch_v4<0, 0>(c, y, W, x, nullptr, nullptr, nullptr, M, K);
 }
 
 int q48_launch_rms_inv(q48_ctx *c, int64_t *r_out, int64_t *out, const int64_t *x,
@@ -600,7 +671,7 @@ int q48_launch_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
                     int M, int K)
 {
     if (q48_gemv_v2_ok(W, K))
-        return launch_v3<0, 0>(c, y, W, x, nullptr, nullptr, nullptr, M, K);
+        return launch_v4<0, 0>(c, y, W, x, nullptr, nullptr, nullptr, M, K);
     const bool vec = (K % 2 == 0) && (((uintptr_t)W & 15) == 0);
     if (M >= 1024) {
         dim3 grid((M + 7) / 8);

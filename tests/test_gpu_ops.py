@@ -139,7 +139,7 @@ def test_gemv_tinyllama_shapes(ctx, M, K):
     assert O.fnv(y) == g["fnv"]
 
 
-@pytest.mark.parametrize("M,K", [(1, 2), (1, 3), (63, 130), (64, 4096), (33, 4098),
+@pytest.mark.parametrize("M,K", [(1, 2), (1, 3), (63, 130), (64, 4096), (33, 4098), (3, 12288),
                                  (17, 8200), (1000, 688), (2500, 256), (5, 12289)])
 def test_gemv_random_vs_oracle(ctx, M, K):
     rng = np.random.default_rng(M * 7919 + K)
