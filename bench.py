@@ -171,6 +171,8 @@ def main():
     t = time.time()
     m = intllm.HostModel(ctx, cfg)
     m.synth(spec.SEED_TL, threads())
+    if os.environ.get("INTLLM_FUSE"):
+        m.set_fused(int(os.environ["INTLLM_FUSE"]))
     log(f"model ready in {time.time() - t:.1f}s")
 
     prompt = gold["prompt"]

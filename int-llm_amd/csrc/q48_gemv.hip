@@ -274,12 +274,26 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
         if (u < nb0)
             wv[u] = w2[u * 8];
 
+    // this lane's x (and norm weight) values of the segment: every load is
+    // issued before any is used, so the staging costs one L2 round trip
+    constexpr int XB = PRO ? 8 : 16;   // x values per lane per staging batch
+    int64_t xv[XB], nw[XB];
+    uint64_t xsum = 0;
+    uint32_t *xw = xs + (size_t)wave * seg * 3;
+
     int64_t r = 0;
     if (PRO == 1) {
+        // whole-x statistics in every block (ssq over K, 512 threads)
         q48_u128 ss = 0;
-        for (int j = tid; j < K; j += 64 * NW) {
-            const int64_t v = x[j];
-            ss += (q48_u128)((q48_i128)v * v);
+        for (int j0 = 0; j0 < K; j0 += 64 * NW * XB) {
+#pragma unroll
+            for (int b = 0; b < XB; ++b) {
+                const int j = j0 + tid + b * 64 * NW;
+                xv[b] = j < K ? x[j] : 0;
+            }
+#pragma unroll
+            for (int b = 0; b < XB; ++b)
+                ss += (q48_u128)((q48_i128)xv[b] * xv[b]);
         }
         ss = block_sum128<64 * NW>(ss, red_lo, red_hi);
         if (tid == 0)
@@ -291,17 +305,28 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
     }
 
     // stage this wave's segment of x as limbs; sum x over the segment
-    uint64_t xsum = 0;
-    uint32_t *xw = xs + (size_t)wave * seg * 3;
-    for (int j = lane; j < kn; j += 64) {
-        int64_t v = x[k0 + j];
-        if (PRO != 0)
-            v = q48_mul(q48_mul(v, r), norm_w[k0 + j]);
-        const uint64_t X = (uint64_t)v ^ 0x8000000000000000ull;
-        xw[3 * j] = (uint32_t)X & 0x3FFFFFu;
-        xw[3 * j + 1] = (uint32_t)(X >> 22) & 0x1FFFFFu;
-        xw[3 * j + 2] = (uint32_t)(X >> 43);
-        xsum += (uint64_t)v;
+    for (int j0 = 0; j0 < kn; j0 += 64 * XB) {
+#pragma unroll
+        for (int b = 0; b < XB; ++b) {
+            const int j = j0 + lane + 64 * b;
+            xv[b] = j < kn ? x[k0 + j] : 0;
+            if (PRO != 0)
+                nw[b] = j < kn ? norm_w[k0 + j] : 0;
+        }
+#pragma unroll
+        for (int b = 0; b < XB; ++b) {
+            const int j = j0 + lane + 64 * b;
+            if (j < kn) {
+                int64_t v = xv[b];
+                if (PRO != 0)
+                    v = q48_mul(q48_mul(v, r), nw[b]);
+                const uint64_t X = (uint64_t)v ^ 0x8000000000000000ull;
+                xw[3 * j] = (uint32_t)X & 0x3FFFFFu;
+                xw[3 * j + 1] = (uint32_t)(X >> 22) & 0x1FFFFFu;
+                xw[3 * j + 2] = (uint32_t)(X >> 43);
+                xsum += (uint64_t)v;
+            }
+        }
     }
     xsum = (uint64_t)q48_wave_sum64((int64_t)xsum);
     // the segment is read only by the wave that wrote it
@@ -452,11 +477,21 @@ __global__ __launch_bounds__(256) void k_rms_inv(int64_t *__restrict__ r_out,
         x = table + (size_t)token * dim;
     }
     q48_u128 ss = 0;
-    for (int i = tid; i < dim; i += 256) {
-        const int64_t v = x[i];
-        if (table)
-            out[i] = v;
-        ss += (q48_u128)((q48_i128)v * v);
+    constexpr int B = 8;
+    for (int i0 = 0; i0 < dim; i0 += 256 * B) {
+        int64_t v[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int i = i0 + tid + 256 * b;
+            v[b] = i < dim ? x[i] : 0;
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int i = i0 + tid + 256 * b;
+            if (table && i < dim)
+                out[i] = v[b];
+            ss += (q48_u128)((q48_i128)v[b] * v[b]);
+        }
     }
     ss = q48_wave_sum128(ss);
     if ((tid & 63) == 0) {

@@ -44,7 +44,9 @@ struct q48h_model {
     int64_t *hidden, *normed, *qkv, *attn, *o, *gu, *h_ffn, *mlp, *logits;
     int *d_tokens;              /* device: tokens of graph-replayed decode steps */
     int64_t *r_attn, *r_ffn;    /* device: rmsnorm statistics of hidden for the next norm */
-    int fused;                  /* 1: fused decode ops (default), 0: one op per kernel */
+    int fused;                  /* 0: one op per kernel; 1: fused, norm statistics in
+                                   every consumer block; 2 (default): fused, statistics
+                                   once per vector by the producer */
     int graph_ready;            /* the context graph holds this model's decode step */
 };
 
@@ -189,7 +191,7 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
     size_t a_log = an; an += align_up((size_t)c->vocab);
     size_t a_r = an; an += ALIGN_ELEMS;
 
-    m->fused = 1;
+    m->fused = 2;
     if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->kc, kvn * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->vc, kvn * 8)) ||
@@ -245,8 +247,10 @@ void q48h_model_free(q48h_model *m)
 
 void q48h_model_set_fused(q48h_model *m, int fused)
 {
-    if (m && (m->fused != (fused != 0))) {
-        m->fused = fused != 0;
+    if (fused < 0 || fused > 2)
+        fused = 2;
+    if (m && m->fused != fused) {
+        m->fused = fused;
         if (m->graph_ready) {
             q48_graph_drop(m->ctx);
             m->graph_ready = 0;
@@ -606,16 +610,28 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
     const int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
     int64_t *q = m->qkv, *k = m->qkv + dim, *v = m->qkv + dim + kvd;
 
-    /* r_attn holds the statistics of hidden (from the embedding or the
-     * previous layer's down projection) */
-    TRY(q48_norm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an, m->r_attn,
-                      dim + 2 * kvd, dim));
+    if (m->fused == 2) {
+        /* r_attn holds the statistics of hidden (from the embedding or the
+         * previous layer's down projection) */
+        TRY(q48_norm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an, m->r_attn,
+                          dim + 2 * kvd, dim));
+    } else {
+        TRY(q48_rmsnorm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an,
+                             dim + 2 * kvd, dim));
+    }
     TRY(q48_attn_decode_rope(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
                              c->n_kv_heads, hd, c->max_seq));
-    TRY(q48_gemv_residual_rms(x, m->hidden, b + m->lo_wo, m->attn, dim, dim, m->r_ffn));
-    TRY(q48_norm_gemv_swiglu(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn, m->r_ffn,
-                             ffn, dim));
-    TRY(q48_gemv_residual_rms(x, m->hidden, b + m->lo_wd, m->h_ffn, dim, ffn, m->r_attn));
+    if (m->fused == 2) {
+        TRY(q48_gemv_residual_rms(x, m->hidden, b + m->lo_wo, m->attn, dim, dim, m->r_ffn));
+        TRY(q48_norm_gemv_swiglu(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn, m->r_ffn,
+                                 ffn, dim));
+        TRY(q48_gemv_residual_rms(x, m->hidden, b + m->lo_wd, m->h_ffn, dim, ffn, m->r_attn));
+    } else {
+        TRY(q48_gemv_residual(x, m->hidden, b + m->lo_wo, m->attn, dim, dim));
+        TRY(q48_rmsnorm_gemv_swiglu(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn, ffn,
+                                    dim));
+        TRY(q48_gemv_residual(x, m->hidden, b + m->lo_wd, m->h_ffn, dim, ffn));
+    }
     return Q48_OK;
 }
 
@@ -648,12 +664,18 @@ static int layer_forward(q48h_model *m, int l, int pos)
 static int enqueue_forward(q48h_model *m, int token, int pos)
 {
     const q48h_config *c = &m->c;
-    if (m->fused) {
+    if (m->fused == 2) {
         TRY(q48_embed_rms(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim, m->r_attn));
         for (int l = 0; l < c->n_layers; ++l)
             TRY(layer_forward_fused(m, l, pos));
         TRY(q48_norm_gemv(m->ctx, m->logits, m->w + m->off_lm, m->hidden, m->w + m->off_norm,
                           m->r_attn, c->vocab, c->dim));
+    } else if (m->fused == 1) {
+        TRY(q48_embed(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim));
+        for (int l = 0; l < c->n_layers; ++l)
+            TRY(layer_forward_fused(m, l, pos));
+        TRY(q48_rmsnorm_gemv(m->ctx, m->logits, m->w + m->off_lm, m->hidden,
+                             m->w + m->off_norm, c->vocab, c->dim));
     } else {
         TRY(q48_embed(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim));
         for (int l = 0; l < c->n_layers; ++l)

@@ -106,8 +106,10 @@ int q48h_generate(q48h_model *m, const int *prompt, int prompt_len, int max_new,
 int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
                      uint64_t *step_hash, q48h_stats *stats);
 
-/* Choose the fused decode ops (1, default: 5 launches per layer) or one
- * library op per reference step (0).  Same bits either way. */
+/* Choose how a layer maps onto library ops (same bits in every mode):
+ * 0 one op per reference step; 1 fused (5 launches per layer), every GEMV
+ * that starts with a norm recomputes its statistics; 2 (default) fused, the
+ * statistics computed once by the kernel that produced the vector. */
 void q48h_model_set_fused(q48h_model *m, int fused);
 
 /* Greedy decode of n steps replayed from a captured graph: step i runs

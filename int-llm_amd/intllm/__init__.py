@@ -399,8 +399,10 @@ class HostModel:
             self.h, p, len(prompt), max_new, out, hs, C.byref(n), C.byref(st)))
         return list(out[:total]), (list(hs[:n.value]) if hashes else None), st
 
-    def set_fused(self, fused: bool):
-        host_lib().q48h_model_set_fused(self.h, int(fused))
+    def set_fused(self, mode: int):
+        """0: one op per reference step; 1: fused with per-block norm
+        statistics; 2 (default): fused with producer-side statistics."""
+        host_lib().q48h_model_set_fused(self.h, int(mode))
 
     def decode_graph(self, token: int, start_pos: int, n: int):
         """n greedy steps replayed from a captured graph; returns (tokens up

@@ -144,14 +144,16 @@ def test_gemm_config4_vs_reference(ctx, T):
             b.free()
 
 
-def test_tiny_generate_unfused_path_bit_exact(ctx):
-    """One library op per reference step gives the same stream as the fused path."""
+@pytest.mark.parametrize("mode", [0, 1])
+def test_tiny_generate_other_paths_bit_exact(ctx, mode):
+    """One library op per reference step (0) and the per-block-statistics
+    fusion (1) give the same stream as the default path."""
     g = golden("tiny_generate.json")
     m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
     try:
         m.synth(g["seed"], threads())
-        m.set_fused(False)
-        say("tiny generate unfused")
+        m.set_fused(mode)
+        say("tiny generate mode", mode)
         toks, hs, _ = m.generate(g["prompt"], g["max_new"])
         assert toks == g["tokens"]
         assert ["%016x" % h for h in hs] == g["step_fnv"]
