@@ -33,6 +33,9 @@ sys.path.insert(0, str(ROOT / "int-llm_amd"))
 sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/);
+# None until measured for the current kernel
+TRAFFIC = None
 REF_CPU_MS_PER_TOK = 501.4   # reference decode, Zen 4, 1 thread
 
 
@@ -155,6 +158,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
+    ap.add_argument("--gemv-reps", type=int, default=8,
+                    help="decode-token GEMV sequences timed back to back for the roofline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the Q16.48 decode path is "
@@ -202,17 +207,16 @@ def main():
     n_cmp = min(len(ref_new), len(toks))
     parity = {"tokens_compared": n_cmp, "tokens_match_reference": toks[:n_cmp] == ref_new[:n_cmp]}
 
-    # roofline of the dominant kernel: a second pass over the same decode
-    # steps with HIP events around every q48_gemv on the library's stream
-    ctx.prof_enable(True)
-    ctx.prof_read(reset=True)
-    p0 = len(prompt) + args.warmup
-    for i in range(min(args.steps, 16)):   # eager, same fused ops as the graph
-        m.forward(toks[args.warmup + i], p0 + i, cfg.vocab, logits=False)
-    prof = ctx.prof_read(reset=True)
-    ctx.prof_enable(False)
-    avg_us = 1e3 * prof.ms / prof.launches
-    bytes_per_launch = prof.bytes / prof.launches
+    # roofline of the dominant kernel (q48_gemv): the GEMV launches of one
+    # decode token, in decode order on the model's own weights, timed back to
+    # back with two HIP events on the library's stream (no per-launch events,
+    # which would add their own gaps); average launch = elapsed / launches
+    m.gemv_sweep(1)                                   # warm
+    ctx.timer_start()
+    launches, gbytes = m.gemv_sweep(args.gemv_reps)
+    gemv_ms = ctx.timer_stop()
+    avg_us = 1e3 * gemv_ms / launches
+    bytes_per_launch = gbytes / launches
     achieved = bytes_per_launch / (avg_us * 1e-6) / 1e9
     m.free()
 
@@ -239,12 +243,14 @@ def main():
                                "int64 Q16.48 weights resident in HBM (8.28 GB read per token)",
                    "layers": 22, "dim": 2048, "heads": 32, "kv_heads": 4, "ffn": 5632,
                    "vocab": 32000, "prompt_tokens": len(prompt), "positions": [p0, p0 + args.steps]},
-        "roofline": {"bound": "hbm", "kernel": "q48_gemv (decode shapes, per launch)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "k_gemv_v4 (q48_gemv family: the 89 fused GEMV launches of a "
+                               "decode token, back to back)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC,
                      "avg_launch_us": round(avg_us, 3),
                      "algorithmic_bytes_per_launch": round(bytes_per_launch),
-                     "launches_timed": prof.launches},
+                     "launches_timed": launches},
         "cpu_baseline": cpu,
         "gemv_shapes": shapes,
         "parity": parity,

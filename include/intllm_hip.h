@@ -215,6 +215,10 @@ typedef struct {
 } q48_prof;
 
 int q48_prof_enable(q48_ctx *ctx, int on);
+/* Elapsed time of everything enqueued between start and stop, from two HIP
+ * events on the context's stream (stop synchronises). */
+int q48_timer_start(q48_ctx *ctx);
+int q48_timer_stop(q48_ctx *ctx, double *ms);
 /* Synchronise, then report (and with reset != 0 clear) the GEMV timings. */
 int q48_prof_read(q48_ctx *ctx, q48_prof *gemv, int reset);
 

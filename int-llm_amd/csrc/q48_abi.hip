@@ -142,6 +142,10 @@ int q48_ctx_destroy(q48_ctx *c)
             (void)hipEventDestroy(c->prof[i].b);
     }
     free(c->prof);
+    if (c->span_a)
+        (void)hipEventDestroy(c->span_a);
+    if (c->span_b)
+        (void)hipEventDestroy(c->span_b);
     if (c->stream)
         (void)hipStreamDestroy(c->stream);
     delete c;
@@ -281,6 +285,29 @@ int q48_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x, int M, 
     if (rc)
         return rc;
     return prof_end(c, r, launch_rc(q48_launch_gemv(c, y, W, x, M, K)));
+}
+
+int q48_timer_start(q48_ctx *c)
+{
+    if (!c || c->capturing)
+        return Q48_EINVAL;
+    if ((!c->span_a && hipEventCreate(&c->span_a) != hipSuccess) ||
+        (!c->span_b && hipEventCreate(&c->span_b) != hipSuccess))
+        return Q48_EHIP;
+    return hip_rc(hipEventRecord(c->span_a, c->stream));
+}
+
+int q48_timer_stop(q48_ctx *c, double *ms)
+{
+    if (!c || !ms || !c->span_a || c->capturing)
+        return Q48_EINVAL;
+    float f = 0;
+    if (hipEventRecord(c->span_b, c->stream) != hipSuccess ||
+        hipEventSynchronize(c->span_b) != hipSuccess ||
+        hipEventElapsedTime(&f, c->span_a, c->span_b) != hipSuccess)
+        return Q48_EHIP;
+    *ms = f;
+    return Q48_OK;
 }
 
 int q48_prof_enable(q48_ctx *c, int on)

@@ -32,6 +32,7 @@ struct q48_ctx {
     struct ProfRec { hipEvent_t a, b; double bytes; };
     ProfRec *prof;
     int prof_n, prof_cap;
+    hipEvent_t span_a, span_b;   // q48_timer_start / q48_timer_stop
 };
 
 // Grow the context workspace to at least `bytes` (stream-synchronising).

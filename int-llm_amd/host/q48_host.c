@@ -865,3 +865,43 @@ int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_t
             return i + 1;
     return n;
 }
+
+/* ---------------------------------------------------------------------- */
+/* measurement helper                                                      */
+/* ---------------------------------------------------------------------- */
+
+int q48h_gemv_sweep(q48h_model *m, int reps, int *launches, double *bytes)
+{
+    if (!m || reps < 0)
+        return Q48_EINVAL;
+    const q48h_config *c = &m->c;
+    q48_ctx *x = m->ctx;
+    int dim = c->dim, kvd = c->n_kv_heads * c->head_dim, ffn = c->ffn;
+    int n = 0;
+    double b = 0;
+#define GB(M, K, out) (b += 8.0 * ((double)(M) * (K) + (K) + (out)), ++n)
+    for (int r = 0; r < reps; ++r) {
+        for (int l = 0; l < c->n_layers; ++l) {
+            const int64_t *w = m->w + m->off_layers + (size_t)l * m->layer_elems;
+            TRY(q48_norm_gemv(x, m->qkv, w + m->lo_qkv, m->hidden, w + m->lo_an, m->r_attn,
+                              dim + 2 * kvd, dim));
+            GB(dim + 2 * kvd, dim, dim + 2 * kvd);
+            TRY(q48_gemv_residual_rms(x, m->hidden, w + m->lo_wo, m->attn, dim, dim, m->r_ffn));
+            GB(dim, dim, dim);
+            TRY(q48_norm_gemv_swiglu(x, m->h_ffn, w + m->lo_gu, m->hidden, w + m->lo_fn,
+                                     m->r_ffn, ffn, dim));
+            GB(2 * ffn, dim, ffn);
+            TRY(q48_gemv_residual_rms(x, m->hidden, w + m->lo_wd, m->h_ffn, dim, ffn, m->r_attn));
+            GB(dim, ffn, dim);
+        }
+        TRY(q48_norm_gemv(x, m->logits, m->w + m->off_lm, m->hidden, m->w + m->off_norm,
+                          m->r_attn, c->vocab, dim));
+        GB(c->vocab, dim, c->vocab);
+    }
+#undef GB
+    if (launches)
+        *launches = n;
+    if (bytes)
+        *bytes = b;
+    return Q48_OK;
+}

@@ -120,6 +120,13 @@ void q48h_model_set_fused(q48h_model *m, int fused);
 int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
                       q48h_stats *stats);
 
+/* Measurement helper: enqueue `reps` times the GEMV launches of one decode
+ * token (the four fused projections of every layer and the lm_head, in
+ * decode order, on the model's weights and activation buffers) and report
+ * their number and algorithmic bytes 8 (M K + K + outputs).  Overwrites the
+ * activations; run it after decoding. */
+int q48h_gemv_sweep(q48h_model *m, int reps, int *launches, double *bytes);
+
 #ifdef __cplusplus
 }
 #endif

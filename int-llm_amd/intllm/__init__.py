@@ -68,6 +68,8 @@ ABI_SIGNATURES = {
     "q48_graph_launch": [_P, _I],
     "q48_graph_drop": [_P],
     "q48_prof_enable": [_P, _I],
+    "q48_timer_start": [_P],
+    "q48_timer_stop": [_P, C.POINTER(C.c_double)],
     "q48_prof_read": [_P, _P, _I],
 }
 
@@ -271,6 +273,14 @@ class Context:
     def prof_enable(self, on: bool = True):
         check("q48_prof_enable", hip_lib().q48_prof_enable(self.h, int(on)))
 
+    def timer_start(self):
+        check("q48_timer_start", hip_lib().q48_timer_start(self.h))
+
+    def timer_stop(self) -> float:
+        ms = C.c_double()
+        check("q48_timer_stop", hip_lib().q48_timer_stop(self.h, C.byref(ms)))
+        return ms.value
+
     def prof_read(self, reset: bool = True) -> "Prof":
         p = Prof()
         check("q48_prof_read", hip_lib().q48_prof_read(self.h, C.byref(p), int(reset)))
@@ -330,6 +340,7 @@ HOST_SIGNATURES = {
     "q48h_decode_from": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(C.c_uint64),
                           C.POINTER(Stats)], C.c_int),
     "q48h_model_set_fused": ([_P, _I], None),
+    "q48h_gemv_sweep": ([_P, _I, C.POINTER(C.c_int), C.POINTER(C.c_double)], C.c_int),
     "q48h_decode_graph": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
 }
 
@@ -412,6 +423,12 @@ class HostModel:
         k = check("q48h_decode_graph", host_lib().q48h_decode_graph(
             self.h, token, start_pos, n, out, C.byref(st)))
         return list(out[:k]), list(out[:n]), st
+
+    def gemv_sweep(self, reps: int):
+        """Enqueue the decode GEMV sequence `reps` times: (launches, bytes)."""
+        n, b = C.c_int(), C.c_double()
+        check("q48h_gemv_sweep", host_lib().q48h_gemv_sweep(self.h, reps, C.byref(n), C.byref(b)))
+        return n.value, b.value
 
     def decode_from(self, token: int, start_pos: int, n: int, hashes: bool = True):
         out = (C.c_int * max(1, n))()
