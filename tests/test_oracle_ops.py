@@ -78,6 +78,14 @@ def test_rope_tables_and_apply_match_reference(oracle):
         oracle.q48o_rope_tables(c.ctypes.data, s.ctypes.data, hd, ms, th)
         e = g[f"{hd}x{ms}x{th}"]
         assert O.fnv(c) == e["cos"] and O.fnv(s) == e["sin"], (hd, ms)
+        # invariants: every (cos, sin) pair lies on the unit circle, position 0
+        # is the identity rotation, and frequency 0 turns by exactly pos radians
+        cf, sf = c / 2.0**48, s / 2.0**48
+        assert np.abs(cf * cf + sf * sf - 1.0).max() < 1e-9, (hd, ms)
+        assert np.abs(cf[: hd // 2] - 1.0).max() < 1e-9 and np.abs(sf[: hd // 2]).max() < 1e-9
+        pos = np.arange(ms)
+        ang = np.arctan2(sf.reshape(ms, hd // 2)[:, 0], cf.reshape(ms, hd // 2)[:, 0])
+        assert np.abs(np.angle(np.exp(1j * (ang - pos)))).max() < 1e-9, (hd, ms)
         if "apply" in e:
             v0 = O.synth("rope.vec", 1, hd, spec.SEED_OPS, spec.SIGMA_ACT, 0)
             for pos, want in enumerate(e["apply"]):
