@@ -246,7 +246,7 @@ def main():
                    "layers": 22, "dim": 2048, "heads": 32, "kv_heads": 4, "ffn": 5632,
                    "vocab": 32000, "prompt_tokens": len(prompt), "positions": [p0, p0 + args.steps]},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_gemv_v4 (q48_gemv family: the 89 fused GEMV launches of a "
+                     "kernel": "k_gemv_v5 (q48_gemv family: the 89 fused GEMV launches of a "
                                "decode token, back to back)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC,

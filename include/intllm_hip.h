@@ -181,10 +181,33 @@ int q48_norm_gemv_swiglu(q48_ctx *ctx, int64_t *out, const int64_t *Wgu, const i
 int q48_gemv_residual_rms(q48_ctx *ctx, int64_t *acc, const int64_t *W, const int64_t *x,
                           int M, int K, int64_t *r_out);
 
+/* The same fusions with the statistics left as partial sums: stats[2i],
+ * stats[2i + 1] (lo, hi words) hold the 128-bit sum of squares of rows
+ * 8i .. 8i+7 of the vector, Q48_STATS_WORDS(dim) int64 words in all.  The
+ * producer of a vector writes them with no cross-block step; every block of
+ * the consumer adds them up and derives r itself while its weight loads are
+ * in flight (same r, same bits as rmsnorm, llama_int.c:1048-1058). */
+#define Q48_STATS_WORDS(dim) (2 * (((dim) + 7) / 8))
+int q48_rms_stats(q48_ctx *ctx, int64_t *stats, const int64_t *x, int dim);
+/* out = table[token] (llama_int.c:2822-2824) and the partial sums of that row. */
+int q48_embed_stats(q48_ctx *ctx, int64_t *out, const int64_t *table, int token, int dim,
+                    int64_t *stats);
+/* y = W . rmsnorm(x, norm_w) with the statistics of x given as partial sums. */
+int q48_norm_gemv_stats(q48_ctx *ctx, int64_t *y, const int64_t *W, const int64_t *x,
+                        const int64_t *norm_w, const int64_t *stats, int M, int K);
+/* q48_rmsnorm_gemv_swiglu with the statistics of x given as partial sums. */
+int q48_norm_gemv_swiglu_stats(q48_ctx *ctx, int64_t *out, const int64_t *Wgu,
+                               const int64_t *x, const int64_t *norm_w,
+                               const int64_t *stats, int ffn, int K);
+/* acc += W . x (residual add), then the partial sums of the updated acc
+ * (dim M) into stats. */
+int q48_gemv_residual_stats(q48_ctx *ctx, int64_t *acc, const int64_t *W, const int64_t *x,
+                            int M, int K, int64_t *stats);
+
 /* ---- device-resident decode steps (graph replay) ---------------------------- */
 /* No reference counterpart: llama_int's generate (llama_int.c:3067-3135)
- * passes token and pos as C arguments each call.  In step mode q48_embed
- * and q48_embed_rms read the token, and q48_rope / q48_attn_decode(_rope) read pos, from a
+ * passes token and pos as C arguments each call.  In step mode q48_embed,
+ * q48_embed_rms and q48_embed_stats read the token, and q48_rope / q48_attn_decode(_rope) read pos, from a
  * device-side state {token, pos, count} instead of their arguments, and
  * q48_argmax_step writes the greedy token back into that state (pos += 1),
  * so one captured forward can be replayed for consecutive tokens with no

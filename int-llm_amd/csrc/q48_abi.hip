@@ -686,6 +686,86 @@ int q48_gemv_residual_rms(q48_ctx *c, int64_t *acc, const int64_t *W, const int6
     return launch_rc(q48_launch_rms_inv(c, r_out, nullptr, acc, nullptr, nullptr, 0, M));
 }
 
+int q48_rms_stats(q48_ctx *c, int64_t *stats, const int64_t *x, int dim)
+{
+    if (!c || !stats || !x || dim <= 0 || dim > kMaxDim)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_rms_stats(c, stats, nullptr, x, nullptr, nullptr, 0, dim));
+}
+
+int q48_embed_stats(q48_ctx *c, int64_t *out, const int64_t *table, int token, int dim,
+                    int64_t *stats)
+{
+    if (!c || !out || !table || !stats || dim <= 0 || dim > kMaxDim)
+        return Q48_EINVAL;
+    if (token < 0)
+        return Q48_ERANGE;
+    return launch_rc(q48_launch_rms_stats(c, stats, out, nullptr, table,
+                                          c->step_mode ? c->d_step : nullptr, token, dim));
+}
+
+// r from the partial sums into the context's scratch word (the fallbacks)
+static int stats_to_r(q48_ctx *c, const int64_t *stats, int dim, int64_t **r)
+{
+    *r = (int64_t *)(c->d_scalar + 16);   // bytes 64..71: clear of the argmax slot
+    return launch_rc(q48_launch_stats_r(c, *r, stats, dim));
+}
+
+int q48_norm_gemv_stats(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                        const int64_t *norm_w, const int64_t *stats, int M, int K)
+{
+    if (!c || bad_ptrs(y, W, x) || !norm_w || !stats || M <= 0 || K <= 0 || M > kMaxDim ||
+        K > kMaxDim)
+        return Q48_EINVAL;
+    if (q48_gemv_v2_ok(W, K)) {
+        int prc;
+        q48_ctx::ProfRec *pr = prof_begin(c, gemv_bytes(M, K, M), &prc);
+        if (prc)
+            return prc;
+        return prof_end(c, pr, launch_rc(q48_launch_gemv_fused(c, y, W, x, norm_w, stats,
+                                                               nullptr, M, K, 3, 0)));
+    }
+    int64_t *r;
+    int rc = stats_to_r(c, stats, K, &r);
+    return rc ? rc : q48_norm_gemv(c, y, W, x, norm_w, r, M, K);
+}
+
+int q48_norm_gemv_swiglu_stats(q48_ctx *c, int64_t *out, const int64_t *Wgu, const int64_t *x,
+                               const int64_t *norm_w, const int64_t *stats, int ffn, int K)
+{
+    if (!c || bad_ptrs(out, Wgu, x) || !norm_w || !stats || ffn <= 0 || K <= 0 ||
+        ffn > kMaxDim / 2 || K > kMaxDim)
+        return Q48_EINVAL;
+    if (q48_gemv_v2_ok(Wgu, K)) {
+        int prc;
+        q48_ctx::ProfRec *pr = prof_begin(c, gemv_bytes(2 * ffn, K, ffn), &prc);
+        if (prc)
+            return prc;
+        return prof_end(c, pr, launch_rc(q48_launch_gemv_fused(c, out, Wgu, x, norm_w, stats,
+                                                               nullptr, 2 * ffn, K, 3, 2)));
+    }
+    int64_t *r;
+    int rc = stats_to_r(c, stats, K, &r);
+    return rc ? rc : q48_norm_gemv_swiglu(c, out, Wgu, x, norm_w, r, ffn, K);
+}
+
+int q48_gemv_residual_stats(q48_ctx *c, int64_t *acc, const int64_t *W, const int64_t *x,
+                            int M, int K, int64_t *stats)
+{
+    if (!c || bad_ptrs(acc, W, x) || !stats || M <= 0 || K <= 0 || M > kMaxDim || K > kMaxDim)
+        return Q48_EINVAL;
+    if (q48_gemv_v2_ok(W, K)) {
+        int prc;
+        q48_ctx::ProfRec *pr = prof_begin(c, gemv_bytes(M, K, M), &prc);
+        if (prc)
+            return prc;
+        return prof_end(c, pr, launch_rc(q48_launch_gemv_fused(c, acc, W, x, nullptr, nullptr,
+                                                               stats, M, K, 0, 4)));
+    }
+    int rc = q48_gemv_residual(c, acc, W, x, M, K);
+    return rc ? rc : launch_rc(q48_launch_rms_stats(c, stats, nullptr, acc, nullptr, nullptr, 0, M));
+}
+
 // ---- decode-step state and graphs --------------------------------------------
 
 int q48_step_mode(q48_ctx *c, int on)

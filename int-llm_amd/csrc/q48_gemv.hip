@@ -147,7 +147,7 @@ __global__ __launch_bounds__(64 * RPB) void k_gemv(int64_t *__restrict__ y,
 }
 
 // ---------------------------------------------------------------------------
-// GEMV v4 (the decode kernel).
+// GEMV v5 (the decode kernel).
 //
 // Carry-free limbs.  x is shared by every row, so it is split once, when it
 // is staged, into three limbs of its flipped value X' = x ^ 2^63:
@@ -155,24 +155,33 @@ __global__ __launch_bounds__(64 * RPB) void k_gemv(int64_t *__restrict__ y,
 // and each weight into two 32-bit limbs of W' = w ^ 2^63.  Every partial
 // product x_i * w_j is below 2^54, so a 64-bit accumulator holds the sum of
 // up to 1024 of them exactly: six v_mad_u64_u32 per MAC and no carry
-// handling.  A lane sums at most K / 8 / NW <= 1023 products per
-// accumulator (K <= V4_MAX_K).  At the end
+// handling.  A lane sums 2 products per 16-element tile of its segment,
+// at most seg / 8 <= 192 per accumulator (K <= V2_MAX_K).  At the end
 //     S = a00 + 2^32 a01 + 2^22 a10 + 2^54 a11 + 2^43 a20 + 2^75 a21
 //         - 2^63 (sum w + sum x)                                 (mod 2^128)
 // (the offset-binary identity above), and y = (int64)(S >> 48).
 //
 // Layout.  8 rows per block, one 8-lane group per row (each load
 // instruction of a group reads one full 128-byte line of its row), NW
-// waves per block each taking one K-segment of all 8 rows.  Every lane has
-// UNR 16-byte weight loads in flight and the first batch is issued before
-// the prologue.  Each wave stages only its own segment of x, so no
-// block-wide barrier sits between the prologue and the loads; the segment
-// partials meet in LDS at the end.
+// waves per block each taking one K-segment of all 8 rows.  Each wave
+// stages only its own segment of x, so no block-wide barrier sits between
+// the prologue and the loads; the segment partials meet in LDS at the end.
+//
+// Latency.  A lane issues its x loads, then its first UNR weight tiles,
+// and only then waits, for x alone, to stage it: the weights arrive
+// meanwhile.  vmcnt retires loads in issue order, so that order and
+// unconditional (clamped) loads are what keep the compiler's waits partial.
+// For the decode shapes (16 or 44 tiles per wave) the tiles then flow
+// through a rotating window of UNR = 4 or 6 loads: multiply tile t, issue
+// tile t + UNR.  Issuing every tile up front instead stalls the wave on
+// the full memory pipeline with no work to overlap (measured: 10-20% slower).
 //
 // Prologues (the staged x is exactly what rmsnorm, llama_int.c:1048-1058,
 // would write):  PRO 0: x as given;  PRO 1: every block computes the
 // rmsnorm statistics of x itself and stages fp_mul(fp_mul(x, r), norm_w);
-// PRO 2: the same with r = *r_in, computed once by the producer of x.
+// PRO 2: the same with r = *r_in, computed once by the producer of x;
+// PRO 3: the same with r computed in the block from the producer's partial
+// sums of squares (r_in points at them: ceil(K / 8) 128-bit values).
 // Epilogues:  EPI 0 stores y;  EPI 1 adds y into `y` (the residual adds,
 // llama_int.c:1535, 1556);  EPI 2 reads W as [gate; up] (M = 2 ffn):
 // block b takes gate rows 4b..4b+3 (groups 0-3) and the matching up rows
@@ -180,7 +189,10 @@ __global__ __launch_bounds__(64 * RPB) void k_gemv(int64_t *__restrict__ y,
 // (llama_int.c:1549-1552);  EPI 3 is EPI 1 followed by the statistics of
 // the next rmsnorm of the updated vector: each block writes its partial sum
 // of squares, the last block to finish adds them all and writes
-// r = fp_inv_sqrt((int64)((ss >> 48) / M) + 2814749767) to *r_out.
+// r = fp_inv_sqrt((int64)((ss >> 48) / M) + 2814749767) to *r_out;
+// EPI 4 is EPI 1 followed by the block's partial sum of squares of its 8
+// new rows, stored at r_out[2 b], r_out[2 b + 1] (lo, hi) for a PRO 3
+// consumer: no atomics, no waits, no last block.
 // ---------------------------------------------------------------------------
 constexpr int V4_RB = 8;
 
@@ -234,8 +246,24 @@ __device__ __forceinline__ q48_u128 acc6_value(const Acc6 &A)
            ((q48_u128)A.ws << 63);
 }
 
-template <int NW, int UNR, int PRO, int EPI>
-__global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
+// One batch of UNR tiles of a lane (16 weights of a row per tile, two per
+// lane) against the staged x limbs, 12 v_mad_u64_u32 per tile; tiles at or
+// past nt are skipped (uniform branch).
+template <int UNR>
+__device__ __forceinline__ void mac_tiles(Acc6 &A, const uint32_t *xl,
+                                          const ulonglong2 (&w)[UNR], int t0, int nt)
+{
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+        if (t0 + u < nt) {
+            const uint32_t *p = xl + 48 * (t0 + u);
+            mac6(A, p[0], p[1], p[2], w[u].x);
+            mac6(A, p[3], p[4], p[5], w[u].y);
+        }
+}
+
+template <int NW, int UNR, int PRO, int EPI, int NTF>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void k_gemv_v5(int64_t *__restrict__ y,
                                                     const int64_t *__restrict__ W,
                                                     const int64_t *__restrict__ x,
                                                     const int64_t *__restrict__ norm_w,
@@ -251,7 +279,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
     __shared__ int64_t r_sh;
     __shared__ int last_sh;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // wave-uniform (scalar) so that the segment bounds and the tile loop
+    // branch uniformly
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 3, l8 = lane & 7;
     const int row0 = blockIdx.x * V4_RB;
     const int ffn = M >> 1;
@@ -262,38 +293,48 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
     const int pr = blockIdx.x * 4 + (g & 3);
     const int row = EPI == 2 ? (g < 4 ? pr : ffn + pr) : row0 + g;
     const bool live = EPI == 2 ? pr < ffn : row < M;
+    // rows past the end read row 0 (in bounds, never accumulated)
     const ulonglong2 *w2 =
         reinterpret_cast<const ulonglong2 *>(W + (size_t)(live ? row : 0) * K + k0) + l8;
-    const int nt = kn >> 4;
+    const int nt = kn >> 4;   // whole 16-element tiles of the segment
 
-    // first batch of weight loads, before anything waits
-    ulonglong2 wv[UNR];
-    const int nb0 = live ? min(UNR, nt) : 0;
+    // the residual rows this block adds to (EPI 1, 3, 4): read now, used last
+    constexpr bool RES = EPI == 1 || EPI == 3 || EPI == 4;
+    int64_t yres = 0;
+    if (RES && tid < V4_RB && row0 + tid < M)
+        yres = y[row0 + tid];
+
+    // PRO 3: the norm statistics arrive as the producer's per-8-row partial
+    // sums of squares (128-bit lo/hi pairs, ceil(K / 8) of them, at most 3
+    // per thread); their loads go out first, with the residual's
+    constexpr int PC = 3;
+    uint64_t plo[PC], phi[PC];
+    const int np = (K + 7) >> 3;
+    if (PRO == 3) {
+        const uint64_t *st = reinterpret_cast<const uint64_t *>(r_in);
 #pragma unroll
-    for (int u = 0; u < UNR; ++u)
-        if (u < nb0)
-            wv[u] = w2[u * 8];
-
-    // this lane's x (and norm weight) values of the segment: every load is
-    // issued before any is used, so the staging costs one L2 round trip
-    constexpr int XB = PRO ? 8 : 16;   // x values per lane per staging batch
-    int64_t xv[XB], nw[XB];
-    uint64_t xsum = 0;
-    uint32_t *xw = xs + (size_t)wave * seg * 3;
+        for (int c = 0; c < PC; ++c) {
+            const int i = min(tid + c * 64 * NW, np - 1);
+            plo[c] = st[2 * i];
+            phi[c] = st[2 * i + 1];
+        }
+    }
 
     int64_t r = 0;
     if (PRO == 1) {
-        // whole-x statistics in every block (ssq over K, 512 threads)
+        // whole-x statistics in every block (ssq over K, 64 NW threads)
+        constexpr int SB = 8;
         q48_u128 ss = 0;
-        for (int j0 = 0; j0 < K; j0 += 64 * NW * XB) {
+        for (int j0 = 0; j0 < K; j0 += 64 * NW * SB) {
+            int64_t v[SB];
 #pragma unroll
-            for (int b = 0; b < XB; ++b) {
+            for (int b = 0; b < SB; ++b) {
                 const int j = j0 + tid + b * 64 * NW;
-                xv[b] = j < K ? x[j] : 0;
+                v[b] = j < K ? x[j] : 0;
             }
 #pragma unroll
-            for (int b = 0; b < XB; ++b)
-                ss += (q48_u128)((q48_i128)xv[b] * xv[b]);
+            for (int b = 0; b < SB; ++b)
+                ss += (q48_u128)((q48_i128)v[b] * v[b]);
         }
         ss = block_sum128<64 * NW>(ss, red_lo, red_hi);
         if (tid == 0)
@@ -304,29 +345,80 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
         r = *r_in;
     }
 
-    // stage this wave's segment of x as limbs; sum x over the segment
-    for (int j0 = 0; j0 < kn; j0 += 64 * XB) {
+    // Issue order matters: vmcnt retires loads in issue order, so the x (and
+    // norm weight) loads of the first staging batch go out before the first
+    // batch of weights; staging then waits for x only while the weights are
+    // still in flight.  Every load below is unconditional (clamped index) so
+    // the wait counts stay static.
+    // (A wave with an empty segment or no whole tile reads element 0 of x
+    // and of W instead: in bounds, never used.)
+    constexpr int XB = PRO ? 8 : 16;   // x values per lane per staging batch
+    int64_t xv[XB], nw[XB];
+    const int xk = kn > 0 ? k0 : 0, xlast = max(kn - 1, 0);
 #pragma unroll
-        for (int b = 0; b < XB; ++b) {
-            const int j = j0 + lane + 64 * b;
-            xv[b] = j < kn ? x[k0 + j] : 0;
-            if (PRO != 0)
-                nw[b] = j < kn ? norm_w[k0 + j] : 0;
+    for (int b = 0; b < XB; ++b) {
+        const int j = min(lane + 64 * b, xlast);
+        xv[b] = x[xk + j];
+        if (PRO != 0)
+            nw[b] = norm_w[xk + j];
+    }
+    asm volatile("" ::: "memory");   // keep the x loads ahead of the weight loads
+    const ulonglong2 *wt = nt > 0 ? w2 : reinterpret_cast<const ulonglong2 *>(W);
+    const int tlast = max(nt - 1, 0), tstep = nt > 0 ? 8 : 0;
+    ulonglong2 wa[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+        wa[u] = wt[min(u, tlast) * tstep];
+    // nothing that waits on a load may be scheduled above this point
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (PRO == 3) {
+        q48_u128 ss = 0;
+#pragma unroll
+        for (int c = 0; c < PC; ++c) {
+            // masked, not branched: a branch would sink the load and wait on it
+            const uint64_t m = tid + c * 64 * NW < np ? ~0ull : 0ull;
+            ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
         }
+        ss = block_sum128<64 * NW>(ss, red_lo, red_hi);
+        if (tid == 0)
+            r_sh = rms_inv_of(ss, K);
+        __syncthreads();
+        r = r_sh;
+    }
+
+    // stage this wave's segment of x as limbs; sum x over the segment
+    uint64_t xsum = 0;
+    uint32_t *xw = xs + (size_t)wave * seg * 3;
+    auto stage = [&](int j0) {
 #pragma unroll
         for (int b = 0; b < XB; ++b) {
+            // the loaded value is used outside the branch so that its load
+            // is not sunk into it (a load there would wait for the weights)
             const int j = j0 + lane + 64 * b;
+            int64_t v = xv[b];
+            if (PRO != 0)
+                v = q48_mul(q48_mul(v, r), nw[b]);
+            v = j < kn ? v : 0;
+            xsum += (uint64_t)v;
             if (j < kn) {
-                int64_t v = xv[b];
-                if (PRO != 0)
-                    v = q48_mul(q48_mul(v, r), nw[b]);
                 const uint64_t X = (uint64_t)v ^ 0x8000000000000000ull;
                 xw[3 * j] = (uint32_t)X & 0x3FFFFFu;
                 xw[3 * j + 1] = (uint32_t)(X >> 22) & 0x1FFFFFu;
                 xw[3 * j + 2] = (uint32_t)(X >> 43);
-                xsum += (uint64_t)v;
             }
         }
+    };
+    stage(0);   // straight-line: the loads above stay where they are
+    for (int j0 = 64 * XB; j0 < kn; j0 += 64 * XB) {
+#pragma unroll
+        for (int b = 0; b < XB; ++b) {
+            const int j = min(j0 + lane + 64 * b, kn - 1);
+            xv[b] = x[k0 + j];
+            if (PRO != 0)
+                nw[b] = norm_w[k0 + j];
+        }
+        stage(j0);
     }
     xsum = (uint64_t)q48_wave_sum64((int64_t)xsum);
     // the segment is read only by the wave that wrote it
@@ -334,41 +426,41 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    // The first UNR tiles were issued before the staging; a segment of at
+    // most UNR tiles (K <= 8 * 16 * UNR) needs no further weight loads.
+    // Longer segments continue in batches of UNR (clamped, unconditional
+    // loads).  Rows past the end (reading row 0) accumulate too, without
+    // branching, and are never stored.
     Acc6 A = {0, 0, 0, 0, 0, 0, 0};
-    if (live) {
-        const uint32_t *xl = xw + 6 * l8;   // this lane's pair: 6 limbs per step of 16
+    const uint32_t *xl = xw + 6 * l8;   // this lane's pair: 6 limbs per tile of 16
+    if constexpr (NTF > 0) {
+        // every wave has exactly NTF tiles: a rotating window of UNR loads in
+        // flight, unrolled so that each wait is for one tile and each issue
+        // follows a multiply (the wave does useful work while the memory
+        // pipeline is full instead of stalling on a long run of issues)
 #pragma unroll
-        for (int u = 0; u < UNR; ++u)
-            if (u < nb0) {
-                const uint32_t *p = xl + 48 * u;
-                mac6(A, p[0], p[1], p[2], wv[u].x);
-                mac6(A, p[3], p[4], p[5], wv[u].y);
-            }
-        int t = nb0;
-        for (; t + UNR <= nt; t += UNR) {
+        for (int t = 0; t < NTF; ++t) {
+            const uint32_t *p = xl + 48 * t;
+            mac6(A, p[0], p[1], p[2], wa[t % UNR].x);
+            mac6(A, p[3], p[4], p[5], wa[t % UNR].y);
+            if (t + UNR < NTF)
+                wa[t % UNR] = w2[(t + UNR) * 8];
+        }
+    } else {
+        mac_tiles<UNR>(A, xl, wa, 0, nt);
+        for (int t0 = UNR; t0 < nt; t0 += UNR) {
 #pragma unroll
             for (int u = 0; u < UNR; ++u)
-                wv[u] = w2[(t + u) * 8];
-#pragma unroll
-            for (int u = 0; u < UNR; ++u) {
-                const uint32_t *p = xl + 48 * (t + u);
-                mac6(A, p[0], p[1], p[2], wv[u].x);
-                mac6(A, p[3], p[4], p[5], wv[u].y);
-            }
+                wa[u] = w2[min(t0 + u, nt - 1) * 8];
+            mac_tiles<UNR>(A, xl, wa, t0, nt);
         }
-        for (; t < nt; ++t) {
-            const ulonglong2 w1 = w2[t * 8];
-            const uint32_t *p = xl + 48 * t;
-            mac6(A, p[0], p[1], p[2], w1.x);
-            mac6(A, p[3], p[4], p[5], w1.y);
-        }
-        // segment tail: kn % 16 elements (even), one pair per lane
-        if (2 * l8 < (kn & 15)) {
-            const ulonglong2 w1 = w2[nt * 8];
-            const uint32_t *p = xl + 48 * nt;
-            mac6(A, p[0], p[1], p[2], w1.x);
-            mac6(A, p[3], p[4], p[5], w1.y);
-        }
+    }
+    // the kn % 16 elements (even) of the segment's end, one pair per lane
+    if (2 * l8 < (kn & 15)) {
+        const ulonglong2 w1 = w2[nt * 8];
+        const uint32_t *p = xl + 48 * nt;
+        mac6(A, p[0], p[1], p[2], w1.x);
+        mac6(A, p[3], p[4], p[5], w1.y);
     }
     q48_u128 S = acc6_value(A);
 #pragma unroll
@@ -383,6 +475,36 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
     }
     __syncthreads();
 
+    if (EPI == 4) {
+        // residual add, then this block's partial sum of squares of its 8 new
+        // rows for the consumer's PRO 3 (no cross-block step here)
+        if (tid < V4_RB) {
+            q48_u128 T = 0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+                T += ((q48_u128)part[w][tid][1] << 64) | part[w][tid][0];
+            const int64_t v = (int64_t)((q48_i128)T >> 48);
+            const int rr = row0 + tid;
+            int64_t h = 0;
+            if (rr < M) {
+                h = (int64_t)((uint64_t)yres + (uint64_t)v);
+                y[rr] = h;
+            }
+            q48_u128 sq = (q48_u128)((q48_i128)h * h);
+#pragma unroll
+            for (int off = 1; off < 8; off <<= 1) {
+                const uint64_t lo = (uint64_t)sq, hi = (uint64_t)(sq >> 64);
+                sq += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
+            }
+            if (tid == 0) {
+                uint64_t *st = reinterpret_cast<uint64_t *>(r_out);
+                st[2 * blockIdx.x] = (uint64_t)sq;
+                st[2 * blockIdx.x + 1] = (uint64_t)(sq >> 64);
+            }
+        }
+        return;
+    }
+
     if (EPI == 3) {
         // residual add, then this block's sum of squares of the new rows
         if (tid < V4_RB) {
@@ -394,7 +516,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
             const int rr = row0 + tid;
             int64_t h = 0;
             if (rr < M) {
-                h = (int64_t)((uint64_t)y[rr] + (uint64_t)v);
+                h = (int64_t)((uint64_t)yres + (uint64_t)v);
                 y[rr] = h;
             }
             q48_u128 sq = (q48_u128)((q48_i128)h * h);
@@ -404,11 +526,19 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
                 sq += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
             }
             if (tid == 0) {
+                // The partial goes out with agent-coherent (write-through)
+                // stores; waiting for them to complete before the ticket
+                // increment orders them before it for every block.  No other
+                // data is published through the ticket, so the L2 write-back
+                // and invalidate of a full agent-scope release/acquire are not
+                // needed: the last block reads the partials with
+                // agent-coherent loads.
                 __hip_atomic_store(&rms_part[2 * blockIdx.x], (uint64_t)sq, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(&rms_part[2 * blockIdx.x + 1], (uint64_t)(sq >> 64),
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const int ticket = __hip_atomic_fetch_add(rms_count, 1, __ATOMIC_ACQ_REL,
+                __builtin_amdgcn_s_waitcnt(0);
+                const int ticket = __hip_atomic_fetch_add(rms_count, 1, __ATOMIC_RELAXED,
                                                           __HIP_MEMORY_SCOPE_AGENT);
                 last_sh = ticket == (int)gridDim.x - 1;
             }
@@ -416,9 +546,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
         __syncthreads();
         if (!last_sh)
             return;
-        // last block: every partial is visible (the acquire of its ticket);
-        // the whole block adds them (integer sum: any order gives the bits)
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        // last block: every partial is visible (each was complete before its
+        // block's ticket); the whole block adds them (integer sum: any order
+        // gives the bits)
         q48_u128 ss = 0;
         for (unsigned b = tid; b < gridDim.x; b += 64 * NW) {
             const uint64_t lo =
@@ -448,7 +578,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_v4(int64_t *__restrict__ y,
             y[rr] = v;
     } else if (EPI == 1) {
         if (rr < M)
-            y[rr] = (int64_t)((uint64_t)y[rr] + (uint64_t)v);
+            y[rr] = (int64_t)((uint64_t)yres + (uint64_t)v);
     } else {
         // threads 0-3 hold gate rows, 4-7 the matching up rows
         const int64_t up = __shfl_down(v, 4, 64);
@@ -507,6 +637,58 @@ __global__ __launch_bounds__(256) void k_rms_inv(int64_t *__restrict__ r_out,
     }
 }
 
+// Partial sums of squares of x over rows 8i..8i+7 (stats[2i], stats[2i+1]
+// = lo, hi), the input of a PRO 3 consumer; with table != nullptr x is the
+// embedding row table[*d_token or token], copied to out first
+// (llama_int.c:2822-2824).
+__global__ __launch_bounds__(256) void k_rms_stats(int64_t *__restrict__ stats,
+                                                  int64_t *__restrict__ out,
+                                                  const int64_t *__restrict__ x,
+                                                  const int64_t *__restrict__ table,
+                                                  const int *__restrict__ d_token, int token,
+                                                  int dim)
+{
+    if (table) {
+        if (d_token)
+            token = *d_token;
+        x = table + (size_t)token * dim;
+    }
+    const int np = (dim + 7) >> 3;
+    for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < np; p += gridDim.x * blockDim.x) {
+        int64_t v[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const int i = 8 * p + b;
+            v[b] = i < dim ? x[i] : 0;
+        }
+        q48_u128 ss = 0;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const int i = 8 * p + b;
+            if (table && i < dim)
+                out[i] = v[b];
+            ss += (q48_u128)((q48_i128)v[b] * v[b]);
+        }
+        reinterpret_cast<uint64_t *>(stats)[2 * p] = (uint64_t)ss;
+        reinterpret_cast<uint64_t *>(stats)[2 * p + 1] = (uint64_t)(ss >> 64);
+    }
+}
+
+// r of the rmsnorm of a dim-vector from its partial sums (one block).
+__global__ __launch_bounds__(256) void k_stats_r(int64_t *__restrict__ r_out,
+                                                const int64_t *__restrict__ stats, int dim)
+{
+    __shared__ uint64_t red_lo[4], red_hi[4];
+    const int np = (dim + 7) >> 3;
+    const uint64_t *st = reinterpret_cast<const uint64_t *>(stats);
+    q48_u128 ss = 0;
+    for (int p = threadIdx.x; p < np; p += 256)
+        ss += ((q48_u128)st[2 * p + 1] << 64) | st[2 * p];
+    ss = block_sum128<256>(ss, red_lo, red_hi);
+    if (threadIdx.x == 0)
+        *r_out = rms_inv_of(ss, dim);
+}
+
 // out = fp_mul(fp_mul(x, *r), w): the per-element part of rmsnorm.
 __global__ __launch_bounds__(256) void k_rms_apply(int64_t *__restrict__ out,
                                                   const int64_t *__restrict__ x,
@@ -532,9 +714,20 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
         if (rc)
             return rc;
     }
-    hipLaunchKernelGGL((k_gemv_v4<NW, 8, PRO, EPI>), dim3(blocks), dim3(64 * NW), lds,
-                       c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count, M,
-                       K, seg);
+    // K = 2048 and K = 5632 (every wave: 16 or 44 whole tiles) take the
+    // unrolled rotating pipeline; other K the batched loop
+    if (K == NW * seg && seg == 16 * 16)
+        hipLaunchKernelGGL((k_gemv_v5<NW, 4, PRO, EPI, 16>), dim3(blocks), dim3(64 * NW), lds,
+                           c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
+                           M, K, seg);
+    else if (K == NW * seg && seg == 16 * 44)
+        hipLaunchKernelGGL((k_gemv_v5<NW, 6, PRO, EPI, 44>), dim3(blocks), dim3(64 * NW), lds,
+                           c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
+                           M, K, seg);
+    else
+        hipLaunchKernelGGL((k_gemv_v5<NW, 16, PRO, EPI, 0>), dim3(blocks), dim3(64 * NW), lds,
+                           c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
+                           M, K, seg);
     return (int)hipGetLastError();
 }
 
@@ -680,6 +873,11 @@ int q48_launch_gemv_fused(q48_ctx *c, int64_t *y, const int64_t *W, const int64_
     if (pro == 2)
         return epi == 2 ? launch_v4<2, 2>(c, y, W, x, norm_w, r_in, nullptr, M, K)
                         : launch_v4<2, 0>(c, y, W, x, norm_w, r_in, nullptr, M, K);
+    if (pro == 3)
+        return epi == 2 ? launch_v4<3, 2>(c, y, W, x, norm_w, r_in, nullptr, M, K)
+                        : launch_v4<3, 0>(c, y, W, x, norm_w, r_in, nullptr, M, K);
+    if (epi == 4)
+        return launch_v4<0, 4>(c, y, W, x, nullptr, nullptr, r_out, M, K);
     if (epi == 3)
         return launch_v4<0, 3>(c, y, W, x, nullptr, nullptr, r_out, M, K);
     return epi == 1 ? launch_v4<0, 1>(c, y, W, x, nullptr, nullptr, nullptr, M, K)
@@ -691,6 +889,21 @@ int q48_launch_rms_inv(q48_ctx *c, int64_t *r_out, int64_t *out, const int64_t *
 {
     hipLaunchKernelGGL(k_rms_inv, dim3(1), dim3(256), 0, c->stream, r_out, out, x, table,
                        d_token, token, dim);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_rms_stats(q48_ctx *c, int64_t *stats, int64_t *out, const int64_t *x,
+                         const int64_t *table, const int *d_token, int token, int dim)
+{
+    const int np = (dim + 7) / 8;
+    hipLaunchKernelGGL(k_rms_stats, dim3((np + 255) / 256), dim3(256), 0, c->stream, stats, out,
+                       x, table, d_token, token, dim);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_stats_r(q48_ctx *c, int64_t *r_out, const int64_t *stats, int dim)
+{
+    hipLaunchKernelGGL(k_stats_r, dim3(1), dim3(256), 0, c->stream, r_out, stats, dim);
     return (int)hipGetLastError();
 }
 

@@ -52,6 +52,9 @@ int q48_launch_rms_inv(q48_ctx *c, int64_t *r_out, int64_t *out, const int64_t *
                        const int64_t *table, const int *d_token, int token, int dim);
 int q48_launch_rms_apply(q48_ctx *c, int64_t *out, const int64_t *x, const int64_t *w,
                          const int64_t *r, int dim);
+int q48_launch_rms_stats(q48_ctx *c, int64_t *stats, int64_t *out, const int64_t *x,
+                         const int64_t *table, const int *d_token, int token, int dim);
+int q48_launch_stats_r(q48_ctx *c, int64_t *r_out, const int64_t *stats, int dim);
 // Grow the per-block partial sums of the rms epilogue to `blocks` entries.
 int q48_rms_reserve(q48_ctx *c, int blocks);
 int q48_launch_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X,

@@ -44,9 +44,12 @@ struct q48h_model {
     int64_t *hidden, *normed, *qkv, *attn, *o, *gu, *h_ffn, *mlp, *logits;
     int *d_tokens;              /* device: tokens of graph-replayed decode steps */
     int64_t *r_attn, *r_ffn;    /* device: rmsnorm statistics of hidden for the next norm */
+    int64_t *s_attn, *s_ffn;    /* device: the same as partial sums (Q48_STATS_WORDS) */
     int fused;                  /* 0: one op per kernel; 1: fused, norm statistics in
-                                   every consumer block; 2 (default): fused, statistics
-                                   once per vector by the producer */
+                                   every consumer block; 2: fused, statistics computed
+                                   once by the producer (last block); 3 (default):
+                                   fused, the producer leaves partial sums and every
+                                   consumer block finishes them */
     int graph_ready;            /* the context graph holds this model's decode step */
 };
 
@@ -190,8 +193,11 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
     size_t a_mlp = an; an += align_up(dim);
     size_t a_log = an; an += align_up((size_t)c->vocab);
     size_t a_r = an; an += ALIGN_ELEMS;
+    size_t sw = (size_t)Q48_STATS_WORDS(c->dim);
+    size_t a_sa = an; an += align_up(sw);
+    size_t a_sf = an; an += align_up(sw);
 
-    m->fused = 2;
+    m->fused = 3;
     if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->kc, kvn * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->vc, kvn * 8)) ||
@@ -211,6 +217,8 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
     m->logits = m->act + a_log;
     m->r_attn = m->act + a_r;
     m->r_ffn = m->act + a_r + 1;
+    m->s_attn = m->act + a_sa;
+    m->s_ffn = m->act + a_sf;
     if ((rc = q48_zero(ctx, m->w, weight_elems(m) * 8)) ||
         (rc = q48_zero(ctx, m->kc, kvn * 8)) || (rc = q48_zero(ctx, m->vc, kvn * 8)) ||
         (rc = q48_zero(ctx, m->act, an * 8)) ||
@@ -247,8 +255,8 @@ void q48h_model_free(q48h_model *m)
 
 void q48h_model_set_fused(q48h_model *m, int fused)
 {
-    if (fused < 0 || fused > 2)
-        fused = 2;
+    if (fused < 0 || fused > 3)
+        fused = 3;
     if (m && m->fused != fused) {
         m->fused = fused;
         if (m->graph_ready) {
@@ -610,7 +618,12 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
     const int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
     int64_t *q = m->qkv, *k = m->qkv + dim, *v = m->qkv + dim + kvd;
 
-    if (m->fused == 2) {
+    if (m->fused == 3) {
+        /* s_attn holds the partial sums of squares of hidden (from the
+         * embedding or the previous layer's down projection) */
+        TRY(q48_norm_gemv_stats(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an, m->s_attn,
+                                dim + 2 * kvd, dim));
+    } else if (m->fused == 2) {
         /* r_attn holds the statistics of hidden (from the embedding or the
          * previous layer's down projection) */
         TRY(q48_norm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an, m->r_attn,
@@ -621,7 +634,12 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
     }
     TRY(q48_attn_decode_rope(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
                              c->n_kv_heads, hd, c->max_seq));
-    if (m->fused == 2) {
+    if (m->fused == 3) {
+        TRY(q48_gemv_residual_stats(x, m->hidden, b + m->lo_wo, m->attn, dim, dim, m->s_ffn));
+        TRY(q48_norm_gemv_swiglu_stats(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn,
+                                       m->s_ffn, ffn, dim));
+        TRY(q48_gemv_residual_stats(x, m->hidden, b + m->lo_wd, m->h_ffn, dim, ffn, m->s_attn));
+    } else if (m->fused == 2) {
         TRY(q48_gemv_residual_rms(x, m->hidden, b + m->lo_wo, m->attn, dim, dim, m->r_ffn));
         TRY(q48_norm_gemv_swiglu(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn, m->r_ffn,
                                  ffn, dim));
@@ -664,7 +682,13 @@ static int layer_forward(q48h_model *m, int l, int pos)
 static int enqueue_forward(q48h_model *m, int token, int pos)
 {
     const q48h_config *c = &m->c;
-    if (m->fused == 2) {
+    if (m->fused == 3) {
+        TRY(q48_embed_stats(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim, m->s_attn));
+        for (int l = 0; l < c->n_layers; ++l)
+            TRY(layer_forward_fused(m, l, pos));
+        TRY(q48_norm_gemv_stats(m->ctx, m->logits, m->w + m->off_lm, m->hidden,
+                                m->w + m->off_norm, m->s_attn, c->vocab, c->dim));
+    } else if (m->fused == 2) {
         TRY(q48_embed_rms(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim, m->r_attn));
         for (int l = 0; l < c->n_layers; ++l)
             TRY(layer_forward_fused(m, l, pos));
@@ -883,19 +907,36 @@ int q48h_gemv_sweep(q48h_model *m, int reps, int *launches, double *bytes)
     for (int r = 0; r < reps; ++r) {
         for (int l = 0; l < c->n_layers; ++l) {
             const int64_t *w = m->w + m->off_layers + (size_t)l * m->layer_elems;
-            TRY(q48_norm_gemv(x, m->qkv, w + m->lo_qkv, m->hidden, w + m->lo_an, m->r_attn,
-                              dim + 2 * kvd, dim));
+            if (m->fused == 3) {
+                TRY(q48_norm_gemv_stats(x, m->qkv, w + m->lo_qkv, m->hidden, w + m->lo_an,
+                                        m->s_attn, dim + 2 * kvd, dim));
+                TRY(q48_gemv_residual_stats(x, m->hidden, w + m->lo_wo, m->attn, dim, dim,
+                                            m->s_ffn));
+                TRY(q48_norm_gemv_swiglu_stats(x, m->h_ffn, w + m->lo_gu, m->hidden,
+                                               w + m->lo_fn, m->s_ffn, ffn, dim));
+                TRY(q48_gemv_residual_stats(x, m->hidden, w + m->lo_wd, m->h_ffn, dim, ffn,
+                                            m->s_attn));
+            } else {
+                TRY(q48_norm_gemv(x, m->qkv, w + m->lo_qkv, m->hidden, w + m->lo_an,
+                                  m->r_attn, dim + 2 * kvd, dim));
+                TRY(q48_gemv_residual_rms(x, m->hidden, w + m->lo_wo, m->attn, dim, dim,
+                                          m->r_ffn));
+                TRY(q48_norm_gemv_swiglu(x, m->h_ffn, w + m->lo_gu, m->hidden, w + m->lo_fn,
+                                         m->r_ffn, ffn, dim));
+                TRY(q48_gemv_residual_rms(x, m->hidden, w + m->lo_wd, m->h_ffn, dim, ffn,
+                                          m->r_attn));
+            }
             GB(dim + 2 * kvd, dim, dim + 2 * kvd);
-            TRY(q48_gemv_residual_rms(x, m->hidden, w + m->lo_wo, m->attn, dim, dim, m->r_ffn));
             GB(dim, dim, dim);
-            TRY(q48_norm_gemv_swiglu(x, m->h_ffn, w + m->lo_gu, m->hidden, w + m->lo_fn,
-                                     m->r_ffn, ffn, dim));
             GB(2 * ffn, dim, ffn);
-            TRY(q48_gemv_residual_rms(x, m->hidden, w + m->lo_wd, m->h_ffn, dim, ffn, m->r_attn));
             GB(dim, ffn, dim);
         }
-        TRY(q48_norm_gemv(x, m->logits, m->w + m->off_lm, m->hidden, m->w + m->off_norm,
-                          m->r_attn, c->vocab, dim));
+        if (m->fused == 3)
+            TRY(q48_norm_gemv_stats(x, m->logits, m->w + m->off_lm, m->hidden,
+                                    m->w + m->off_norm, m->s_attn, c->vocab, dim));
+        else
+            TRY(q48_norm_gemv(x, m->logits, m->w + m->off_lm, m->hidden, m->w + m->off_norm,
+                              m->r_attn, c->vocab, dim));
         GB(c->vocab, dim, c->vocab);
     }
 #undef GB

@@ -108,8 +108,10 @@ int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_to
 
 /* Choose how a layer maps onto library ops (same bits in every mode):
  * 0 one op per reference step; 1 fused (5 launches per layer), every GEMV
- * that starts with a norm recomputes its statistics; 2 (default) fused, the
- * statistics computed once by the kernel that produced the vector. */
+ * that starts with a norm recomputes its statistics; 2 fused, the
+ * statistics computed once by the kernel that produced the vector (its last
+ * block); 3 (default) fused, the producer leaves per-block partial sums and
+ * each block of the consuming GEMV finishes them. */
 void q48h_model_set_fused(q48h_model *m, int fused);
 
 /* Greedy decode of n steps replayed from a captured graph: step i runs

@@ -59,6 +59,11 @@ ABI_SIGNATURES = {
     "q48_norm_gemv": [_P, _P, _P, _P, _P, _P, _I, _I],
     "q48_norm_gemv_swiglu": [_P, _P, _P, _P, _P, _P, _I, _I],
     "q48_gemv_residual_rms": [_P, _P, _P, _P, _I, _I, _P],
+    "q48_rms_stats": [_P, _P, _P, _I],
+    "q48_embed_stats": [_P, _P, _P, _I, _I, _P],
+    "q48_norm_gemv_stats": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "q48_norm_gemv_swiglu_stats": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "q48_gemv_residual_stats": [_P, _P, _P, _P, _I, _I, _P],
     "q48_step_mode": [_P, _I],
     "q48_step_set": [_P, _I, _I],
     "q48_step_get": [_P, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)],
@@ -123,6 +128,11 @@ def check(fn: str, rc: int) -> int:
     if rc < 0:
         raise Q48Error(fn, rc)
     return rc
+
+
+def stats_words(dim: int) -> int:
+    """Q48_STATS_WORDS(dim): int64 words of a partial-sums statistics buffer."""
+    return 2 * ((dim + 7) // 8)
 
 
 def i64(a) -> np.ndarray:
@@ -270,6 +280,27 @@ class Context:
         return check("q48_gemv_residual_rms",
                      hip_lib().q48_gemv_residual_rms(self.h, acc, W, x, M, K, r_out))
 
+    # statistics as per-8-row partial sums (stats_words(dim) int64 words)
+    def rms_stats(self, stats, x, dim):
+        return check("q48_rms_stats", hip_lib().q48_rms_stats(self.h, stats, x, dim))
+
+    def embed_stats(self, out, table, token, dim, stats):
+        return check("q48_embed_stats",
+                     hip_lib().q48_embed_stats(self.h, out, table, token, dim, stats))
+
+    def norm_gemv_stats(self, y, W, x, norm_w, stats, M, K):
+        return check("q48_norm_gemv_stats",
+                     hip_lib().q48_norm_gemv_stats(self.h, y, W, x, norm_w, stats, M, K))
+
+    def norm_gemv_swiglu_stats(self, out, Wgu, x, norm_w, stats, ffn, K):
+        return check("q48_norm_gemv_swiglu_stats",
+                     hip_lib().q48_norm_gemv_swiglu_stats(self.h, out, Wgu, x, norm_w, stats,
+                                                          ffn, K))
+
+    def gemv_residual_stats(self, acc, W, x, M, K, stats):
+        return check("q48_gemv_residual_stats",
+                     hip_lib().q48_gemv_residual_stats(self.h, acc, W, x, M, K, stats))
+
     def prof_enable(self, on: bool = True):
         check("q48_prof_enable", hip_lib().q48_prof_enable(self.h, int(on)))
 
@@ -412,7 +443,8 @@ class HostModel:
 
     def set_fused(self, mode: int):
         """0: one op per reference step; 1: fused with per-block norm
-        statistics; 2 (default): fused with producer-side statistics."""
+        statistics; 2: fused with producer-side statistics; 3 (default):
+        fused with producer partial sums finished by each consumer block."""
         host_lib().q48h_model_set_fused(self.h, int(mode))
 
     def decode_graph(self, token: int, start_pos: int, n: int):

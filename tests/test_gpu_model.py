@@ -144,10 +144,11 @@ def test_gemm_config4_vs_reference(ctx, T):
             b.free()
 
 
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1, 2])
 def test_tiny_generate_other_paths_bit_exact(ctx, mode):
-    """One library op per reference step (0) and the per-block-statistics
-    fusion (1) give the same stream as the default path."""
+    """One library op per reference step (0), the per-block-statistics
+    fusion (1) and the producer-statistics fusion (2) give the same stream
+    as the default path (partial sums finished by the consumer)."""
     g = golden("tiny_generate.json")
     m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
     try:

@@ -481,3 +481,100 @@ def test_gemv_residual_rms(ctx, oracle, M, K):
         assert int(dr.download()[0]) == rms_inv_exact(oracle, h), it
         dW.free()
         dx.free()
+
+
+# ---------------------------------------------------------------------------
+# statistics as per-8-row partial sums (producer) finished by the consumer
+# ---------------------------------------------------------------------------
+
+def stats_exact(x):
+    """Partial sums of squares of rows 8i..8i+7 as 128-bit (lo, hi) words,
+    computed with Python integers (the wrap of an int128 sum)."""
+    x = [int(v) for v in x]
+    out = []
+    for i in range(0, len(x), 8):
+        s = sum(v * v for v in x[i:i + 8]) % (1 << 128)
+        out += [spec.wrap64(s & ((1 << 64) - 1)), spec.wrap64(s >> 64)]
+    return np.array(out, dtype=np.int64)
+
+
+@pytest.mark.parametrize("dim", [1, 7, 256, 2048, 5000])
+def test_rms_stats_and_embed_stats(ctx, dim):
+    rng = np.random.default_rng(dim + 1)
+    table = (rng.standard_normal(3 * dim) * 2 * ONE).astype(np.int64)
+    table[0] = spec.INT64_MIN          # extreme squares wrap like the reference's int128
+    sw = intllm.stats_words(dim)
+    dt, do, ds = ctx.to_device(table), ctx.buffer(dim), ctx.buffer(sw)
+    say("embed_stats", dim)
+    ctx.embed_stats(do.ptr, dt.ptr, 2, dim, ds.ptr)
+    row = table[2 * dim:3 * dim]
+    assert np.array_equal(do.download(), row)
+    assert np.array_equal(ds.download(), stats_exact(row))
+    ctx.rms_stats(ds.ptr, dt.ptr, dim)
+    assert np.array_equal(ds.download(), stats_exact(table[:dim]))
+
+
+@pytest.mark.parametrize("M,K", [(2560, 2048), (32000, 2048), (64, 256), (9, 7681), (5, 129)])
+def test_norm_gemv_with_stats(ctx, oracle, M, K):
+    rng = np.random.default_rng(M * 7 + K)
+    W = (rng.standard_normal(M * K) * spec.SIGMA_W).astype(np.int64)
+    x = (rng.standard_normal(K) * 3 * ONE).astype(np.int64)
+    w = (rng.standard_normal(K) * ONE).astype(np.int64)
+    want = O.gemv(W, _rms(oracle, x, w), M, K)
+    dW, dx, dw, dy = ctx.to_device(W), ctx.to_device(x), ctx.to_device(w), ctx.buffer(M)
+    ds = ctx.buffer(intllm.stats_words(K))
+    say("norm_gemv_stats", M, K)
+    ctx.rms_stats(ds.ptr, dx.ptr, K)
+    ctx.norm_gemv_stats(dy.ptr, dW.ptr, dx.ptr, dw.ptr, ds.ptr, M, K)
+    assert np.array_equal(dy.download(), want)
+    for b in (dW, dx, dw, dy, ds):
+        b.free()
+
+
+@pytest.mark.parametrize("ffn,K", [(5632, 2048), (688, 256), (6, 7681)])
+def test_norm_gemv_swiglu_with_stats(ctx, oracle, ffn, K):
+    rng = np.random.default_rng(ffn + 5 * K)
+    W = (rng.standard_normal(2 * ffn * K) * spec.SIGMA_W * 20).astype(np.int64)
+    x = (rng.standard_normal(K) * ONE).astype(np.int64)
+    w = (rng.standard_normal(K) * ONE).astype(np.int64)
+    t = O.gemv(W, _rms(oracle, x, w), 2 * ffn, K)
+    want = np.empty(ffn, dtype=np.int64)
+    g, u = t[:ffn].copy(), t[ffn:].copy()
+    oracle.q48o_silu_mul(want.ctypes.data, g.ctypes.data, u.ctypes.data, ffn)
+    dW, dx, dw, do = ctx.to_device(W), ctx.to_device(x), ctx.to_device(w), ctx.buffer(ffn)
+    ds = ctx.buffer(intllm.stats_words(K))
+    say("norm_gemv_swiglu_stats", ffn, K)
+    ctx.rms_stats(ds.ptr, dx.ptr, K)
+    ctx.norm_gemv_swiglu_stats(do.ptr, dW.ptr, dx.ptr, dw.ptr, ds.ptr, ffn, K)
+    assert np.array_equal(do.download(), want)
+    for b in (dW, dx, dw, do, ds):
+        b.free()
+
+
+@pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 5632), (256, 688), (13, 40), (3, 7681)])
+def test_gemv_residual_stats(ctx, oracle, M, K):
+    """acc += W x and the partial sums of the new acc, three calls in a row,
+    then a consumer GEMV normalising acc with them."""
+    rng = np.random.default_rng(M + 13 * K)
+    h = (rng.standard_normal(M) * ONE).astype(np.int64)
+    dh, ds = ctx.to_device(h), ctx.buffer(intllm.stats_words(M))
+    for it in range(3):
+        W = (rng.standard_normal(M * K) * spec.SIGMA_W).astype(np.int64)
+        x = (rng.standard_normal(K) * ONE).astype(np.int64)
+        h = (h.view(np.uint64) + O.gemv(W, x, M, K).view(np.uint64)).view(np.int64)
+        dW, dx = ctx.to_device(W), ctx.to_device(x)
+        say("gemv_residual_stats", M, K, "call", it)
+        ctx.gemv_residual_stats(dh.ptr, dW.ptr, dx.ptr, M, K, ds.ptr)
+        assert np.array_equal(dh.download(), h), it
+        assert np.array_equal(ds.download(), stats_exact(h)), it
+        dW.free()
+        dx.free()
+    # the consumer side: the same r as rmsnorm of the updated vector
+    N = 24
+    Wn = (rng.standard_normal(N * M) * spec.SIGMA_W).astype(np.int64)
+    nw = (rng.standard_normal(M) * ONE).astype(np.int64)
+    dWn, dnw, dy = ctx.to_device(Wn), ctx.to_device(nw), ctx.buffer(N)
+    ctx.norm_gemv_stats(dy.ptr, dWn.ptr, dh.ptr, dnw.ptr, ds.ptr, N, M)
+    assert np.array_equal(dy.download(), O.gemv(Wn, _rms(oracle, h, nw), N, M))
+    for b in (dWn, dnw, dy, dh, ds):
+        b.free()
