@@ -161,6 +161,16 @@ int q48_attn_decode_rope(q48_ctx *ctx, int64_t *out, const int64_t *q,
                          int64_t *kcache, int64_t *vcache, const int64_t *k_new,
                          const int64_t *v_new, int layer, int pos, int n_heads,
                          int n_kv, int head_dim, int max_seq);
+/* q48_attn_decode_rope that also reads [prefetch, prefetch + prefetch_bytes)
+ * (16-byte aligned; typically the next op's weights, W_o) on the compute
+ * units the heads leave idle, so that the next op finds them in the
+ * device-side cache.  No reference counterpart (a scheduling hint: the
+ * results are those of q48_attn_decode_rope). */
+int q48_attn_decode_rope_prefetch(q48_ctx *ctx, int64_t *out, const int64_t *q,
+                                  int64_t *kcache, int64_t *vcache, const int64_t *k_new,
+                                  const int64_t *v_new, int layer, int pos, int n_heads,
+                                  int n_kv, int head_dim, int max_seq, const void *prefetch,
+                                  size_t prefetch_bytes);
 
 /* The same fusions with the rmsnorm statistics computed once per vector:
  * r = fp_inv_sqrt((int64)((sum x^2 >> 48) / dim) + 2814749767), the scalar

@@ -90,6 +90,10 @@ int q48_ctx_create(q48_ctx **out, int device)
     if (!c)
         return Q48_ENOMEM;
     c->device = device;
+    if (hipDeviceGetAttribute(&c->cu_count, hipDeviceAttributeMultiprocessorCount, device) !=
+            hipSuccess ||
+        c->cu_count <= 0)
+        c->cu_count = 1;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return Q48_EHIP;
@@ -374,7 +378,9 @@ int q48_rope_init(q48_ctx *c, int head_dim, int max_seq, int theta)
     c->rope_cos = c->rope_sin = nullptr;
     c->rope_head_dim = c->rope_max_seq = c->rope_theta = 0;
     size_t n = (size_t)max_seq * (head_dim / 2) * sizeof(int64_t);
-    if (hipMalloc(&c->rope_cos, n) != hipSuccess || hipMalloc(&c->rope_sin, n) != hipSuccess) {
+    // the sine table carries one more value: the attention score scale
+    if (hipMalloc(&c->rope_cos, n) != hipSuccess ||
+        hipMalloc(&c->rope_sin, n + sizeof(int64_t)) != hipSuccess) {
         (void)hipFree(c->rope_cos);
         c->rope_cos = c->rope_sin = nullptr;
         return Q48_ENOMEM;
@@ -411,7 +417,7 @@ int q48_attn_decode(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
     const int *dp = c->step_mode ? c->d_step + 1 : nullptr;
     int rc = head_dim % 8 == 0
                  ? q48_launch_attn_v2(c, out, q, kcache, vcache, k_new, v_new, layer, dp, pos,
-                                      n_heads, n_kv, head_dim, max_seq, 0)
+                                      n_heads, n_kv, head_dim, max_seq, 0, nullptr, 0)
                  : q48_launch_attn(c, out, q, kcache, vcache, k_new, v_new, layer, dp, pos,
                                    n_heads, n_kv, head_dim, max_seq);
     if (rc == Q48_ENOMEM)
@@ -576,6 +582,17 @@ int q48_attn_decode_rope(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kc
                          int64_t *vcache, const int64_t *k_new, const int64_t *v_new, int layer,
                          int pos, int n_heads, int n_kv, int head_dim, int max_seq)
 {
+    return q48_attn_decode_rope_prefetch(c, out, q, kcache, vcache, k_new, v_new, layer, pos,
+                                         n_heads, n_kv, head_dim, max_seq, nullptr, 0);
+}
+
+int q48_attn_decode_rope_prefetch(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
+                                  int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
+                                  int layer, int pos, int n_heads, int n_kv, int head_dim,
+                                  int max_seq, const void *prefetch, size_t prefetch_bytes)
+{
+    if (prefetch && ((uintptr_t)prefetch & 15))
+        return Q48_EINVAL;
     if (!c || !out || !q || !kcache || !vcache || !k_new || !v_new)
         return Q48_EINVAL;
     if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || head_dim <= 0 ||
@@ -587,7 +604,8 @@ int q48_attn_decode_rope(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kc
         return Q48_ERANGE;
     const int *dp = c->step_mode ? c->d_step + 1 : nullptr;
     int rc = q48_launch_attn_v2(c, out, q, kcache, vcache, k_new, v_new, layer, dp, pos, n_heads,
-                                n_kv, head_dim, max_seq, 1);
+                                n_kv, head_dim, max_seq, 1, prefetch,
+                                prefetch ? prefetch_bytes : 0);
     if (rc == Q48_ENOMEM)
         return rc;
     return launch_rc(rc);

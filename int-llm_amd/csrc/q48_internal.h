@@ -10,6 +10,7 @@
 
 struct q48_ctx {
     int device;
+    int cu_count;                // compute units of the device
     hipStream_t stream;
     q48_consts *consts;          // device: fp_math_init constants
     int64_t *rope_cos, *rope_sin; // device: [max_seq][head_dim/2]
@@ -42,9 +43,10 @@ int q48_ws_reserve(q48_ctx *c, size_t bytes);
 int q48_launch_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
                     int M, int K);
 bool q48_gemv_v2_ok(const int64_t *W, int K);
-// pro: 1 = rmsnorm(x, norm_w) prologue; epi: 0 store, 1 add into y, 2 SwiGLU pairs
-// pro: 0 none, 1 rmsnorm(x, norm_w) computed in every block, 2 with r = *r_in;
-// epi: 0 store, 1 add into y, 2 SwiGLU pairs, 3 add into y + rms statistics -> *r_out
+// pro: 0 none, 1 rmsnorm(x, norm_w) computed in every block, 2 with r = *r_in,
+//      3 with r from the partial sums at r_in;
+// epi: 0 store, 1 add into y, 2 SwiGLU pairs, 3 add into y + rms statistics -> *r_out,
+//      4 add into y + partial sums -> r_out
 int q48_launch_gemv_fused(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
                           const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
                           int K, int pro, int epi);
@@ -71,7 +73,8 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
 int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                        int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
                        int layer, const int *d_pos, int pos, int n_heads, int n_kv,
-                       int head_dim, int max_seq, int rope);
+                       int head_dim, int max_seq, int rope,
+                       const void *prefetch, size_t prefetch_bytes);
 int q48_launch_step_set(q48_ctx *c, int token, int pos);
 int q48_launch_step_argmax(q48_ctx *c, int *tokens, int cap, const int64_t *v, int n);
 int q48_launch_silu_mul_pairs(q48_ctx *c, int64_t *out, const int64_t *t, int n);

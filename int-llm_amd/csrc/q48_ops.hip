@@ -110,6 +110,8 @@ __global__ __launch_bounds__(256) void k_rope_init(int64_t *__restrict__ cos_t,
     q48_sincos(k, q48_mul(q48_from_int(pos), th), &c, &s);
     cos_t[idx] = c;
     sin_t[idx] = s;
+    if (idx == 0)   // the attention score scale, stored after the sine table
+        sin_t[(size_t)half * max_seq] = q48_inv_sqrt(q48_from_int(head_dim));
 }
 
 // ---------------------------------------------------------------------------
@@ -251,12 +253,35 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
     const int64_t *__restrict__ k_new, const int64_t *__restrict__ v_new,
     int64_t *__restrict__ scores, const int64_t *__restrict__ cos_t,
     const int64_t *__restrict__ sin_t, int layer, const int *__restrict__ d_pos, int pos,
-    int n_heads, int n_kv, int hd, int max_seq)
+    int n_heads, int n_kv, int hd, int max_seq, const ulonglong2 *__restrict__ pf,
+    size_t pf_n16)
 {
     __shared__ int64_t qs[256], ks[256], vs[256];
     __shared__ int64_t red[ATT_NT / 64];
     __shared__ int64_t part[ATT_NT];
     __shared__ int64_t sc_lds[LDS ? ATT_LDS_MAX : 1];
+    if ((int)blockIdx.x >= n_heads) {
+        // Blocks past the heads run on otherwise idle compute units while
+        // the heads' latency-bound chain runs: they read the next op's
+        // weights so that op finds them in the device-side cache (MALL).
+        // The values are only consumed by an empty asm statement.
+        const size_t stride = (size_t)(gridDim.x - n_heads) * ATT_NT;
+        size_t i = (size_t)(blockIdx.x - n_heads) * ATT_NT + threadIdx.x;
+        uint64_t acc = 0;
+        for (; i + 7 * stride < pf_n16; i += 8 * stride) {
+            ulonglong2 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                v[u] = pf[i + u * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                acc ^= v[u].x ^ v[u].y;
+        }
+        for (; i < pf_n16; i += stride)
+            acc ^= pf[i].x ^ pf[i].y;
+        asm volatile("" ::"v"(acc));
+        return;
+    }
     if (d_pos)
         pos = *d_pos;
     if (pos < 0 || pos >= max_seq)
@@ -367,6 +392,199 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
         for (int s2 = 0; s2 < slices; ++s2)
             o += (uint64_t)part[s2 * hd + d];
         out[(size_t)h * hd + d] = (int64_t)o;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention v3: k_attn_v2's computation with its memory round trips cut:
+//  - the K rows of the first two score passes are issued before RoPE, and
+//    each later pass is issued one pass ahead (two register buffers);
+//  - the first V batches are issued before the softmax, later ones one
+//    batch ahead, so the V pass rarely waits;
+//  - the score scale fp_inv_sqrt(fp_from_int(hd)) is read, not recomputed
+//    (k_rope_init stores it after the sine table).
+// Loads past the last position are clamped to it (in bounds, unused), so
+// every wait is for a known, static number of younger loads.  Rows at pos
+// are read from the cache and replaced by the block's own rotated k and v.
+// One block of 256 threads per query head; HD = 32, 64 or 128; at most
+// ATT_LDS_MAX positions.  Blocks past n_heads prefetch like k_attn_v2's.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_v3(
+    int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
+    int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
+    const int64_t *__restrict__ v_new, const int64_t *__restrict__ cos_t,
+    const int64_t *__restrict__ sin_t, const int64_t *__restrict__ scale_p, int layer,
+    const int *__restrict__ d_pos, int pos, int n_heads, int n_kv, int max_seq,
+    const ulonglong2 *__restrict__ pf, size_t pf_n16)
+{
+    constexpr int NT = 256, DPL = HD / 8, DP2 = DPL / 2, SL = NT / HD, NG = NT / 8, VB = 8;
+    __shared__ int64_t qs[HD], ks[HD], vs[HD];
+    __shared__ int64_t red[NT / 64];
+    __shared__ int64_t part[NT];
+    __shared__ int64_t sc[ATT_LDS_MAX];
+    if ((int)blockIdx.x >= n_heads) {
+        const size_t stride = (size_t)(gridDim.x - n_heads) * NT;
+        size_t i = (size_t)(blockIdx.x - n_heads) * NT + threadIdx.x;
+        uint64_t acc = 0;
+        for (; i + 7 * stride < pf_n16; i += 8 * stride) {
+            ulonglong2 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                v[u] = pf[i + u * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                acc ^= v[u].x ^ v[u].y;
+        }
+        for (; i < pf_n16; i += stride)
+            acc ^= pf[i].x ^ pf[i].y;
+        asm volatile("" ::"v"(acc));
+        return;
+    }
+    if (d_pos)
+        pos = *d_pos;
+    if (pos < 0 || pos >= max_seq)
+        return;   // uniform over the block: no barrier is skipped by part of it
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int group = n_heads / n_kv, kh = h / group;
+    const size_t kvd = (size_t)n_kv * HD;
+    const size_t base = (size_t)layer * max_seq;
+    const int S = pos + 1, half = HD / 2;
+    const int g = tid >> 3, l8 = tid & 7;
+    const int64_t scale = *scale_p;
+
+    // the RoPE inputs and the new v first (loads retire in issue order: the
+    // RoPE then waits for them alone), every thread loading (clamped index)
+    const int64_t *qh = q + (size_t)h * HD, *kn = k_new + (size_t)kh * HD;
+    const int i = min(tid, half - 1), j = min(tid, HD - 1);
+    int64_t c = cos_t[(size_t)pos * half + i];
+    int64_t sn = sin_t[(size_t)pos * half + i];
+    int64_t q0 = qh[i], q1 = qh[i + half];
+    int64_t k0 = kn[i], k1 = kn[i + half];
+    int64_t vn = v_new[(size_t)kh * HD + j];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // K rows of passes 0 and 1: lane l8 of group g holds dims [l8 DPL, +DPL)
+    const int64_t *kb0 = kcache + base * kvd + (size_t)kh * HD + l8 * DPL;
+    auto krow = [&](int t) {
+        return reinterpret_cast<const ulonglong2 *>(kb0 + (size_t)min(t, S - 1) * kvd);
+    };
+    ulonglong2 ka[DP2], kb[DP2];
+#pragma unroll
+    for (int d = 0; d < DP2; ++d)
+        ka[d] = krow(g)[d];
+#pragma unroll
+    for (int d = 0; d < DP2; ++d)
+        kb[d] = krow(g + NG)[d];
+    __builtin_amdgcn_sched_barrier(0);
+    // first use of the RoPE inputs here, after the K loads are out (else the
+    // compiler extends them to 128 bits, and waits for them, earlier)
+    asm volatile("" : "+v"(c), "+v"(sn), "+v"(q0), "+v"(q1), "+v"(k0), "+v"(k1), "+v"(vn));
+
+    // RoPE of q_h and the new k (rope_apply, llama_int.c:997-1008, 1392-1395);
+    // threads past half repeat the last pair (same values, same slots): no
+    // branch, so the loads above are not sunk into one
+    qs[i] = (int64_t)((uint64_t)q48_mul(q0, c) - (uint64_t)q48_mul(q1, sn));
+    qs[i + half] = (int64_t)((uint64_t)q48_mul(q1, c) + (uint64_t)q48_mul(q0, sn));
+    ks[i] = (int64_t)((uint64_t)q48_mul(k0, c) - (uint64_t)q48_mul(k1, sn));
+    ks[i + half] = (int64_t)((uint64_t)q48_mul(k1, c) + (uint64_t)q48_mul(k0, sn));
+    vs[j] = vn;
+    __syncthreads();
+    if (h % group == 0 && tid < HD) {
+        kcache[(base + pos) * kvd + (size_t)kh * HD + tid] = ks[tid];
+        vcache[(base + pos) * kvd + (size_t)kh * HD + tid] = vs[tid];
+    }
+
+    // scores s_t = fp_mul((sum_d q_d k_t,d) >> 48, scale), llama_int.c:1502-1512
+    const int64_t *qd = qs + l8 * DPL, *kd = ks + l8 * DPL;
+    int64_t mx = INT64_MIN;
+    auto score = [&](const ulonglong2 (&kr)[DP2], int t) {
+        const bool own = t == pos;
+        q48_u128 dot = 0;
+#pragma unroll
+        for (int d = 0; d < DP2; ++d) {
+            const int64_t a0 = own ? kd[2 * d] : (int64_t)kr[d].x;
+            const int64_t a1 = own ? kd[2 * d + 1] : (int64_t)kr[d].y;
+            dot += (q48_u128)((q48_i128)qd[2 * d] * a0);
+            dot += (q48_u128)((q48_i128)qd[2 * d + 1] * a1);
+        }
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            const uint64_t lo = (uint64_t)dot, hi = (uint64_t)(dot >> 64);
+            dot += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
+        }
+        if (t < S && l8 == 0) {
+            const int64_t s = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
+            sc[t] = s;
+            mx = s > mx ? s : mx;
+        }
+    };
+    for (int t0 = 0; t0 < S; t0 += 2 * NG) {
+        score(ka, t0 + g);
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            ka[d] = krow(t0 + 2 * NG + g)[d];
+        score(kb, t0 + NG + g);
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            kb[d] = krow(t0 + 3 * NG + g)[d];
+    }
+
+    // V batches 0 and 1 go out before the softmax: thread (d, sl) takes
+    // positions sl + SL i, VB of them per batch
+    const int d = tid % HD, sl = tid / HD;
+    const int64_t *vcol = vcache + base * kvd + (size_t)kh * HD + d;
+    auto vld = [&](int i) { return vcol[(size_t)min(sl + SL * i, S - 1) * kvd]; };
+    int64_t va[VB], vb[VB];
+#pragma unroll
+    for (int u = 0; u < VB; ++u)
+        va[u] = vld(u);
+#pragma unroll
+    for (int u = 0; u < VB; ++u)
+        vb[u] = vld(VB + u);
+
+    // softmax, llama_int.c:1060-1072
+    mx = block_max64<NT>(mx, red);
+    int64_t sum = 0;
+    for (int t = tid; t < S; t += NT) {
+        const int64_t e = q48_safe_exp((int64_t)((uint64_t)sc[t] - (uint64_t)mx));
+        sc[t] = e;
+        sum = (int64_t)((uint64_t)sum + (uint64_t)e);
+    }
+    sum = block_sum64<NT>(sum, red);
+    if (sum > 0)
+        for (int t = tid; t < S; t += NT)
+            sc[t] = q48_div(sc[t], sum);
+    __syncthreads();
+
+    // o[d] = sum_t fp_mul(p_t, v_t[d]), llama_int.c:1514-1529
+    uint64_t acc = 0;
+    auto vmac = [&](const int64_t (&vv)[VB], int i0) {
+#pragma unroll
+        for (int u = 0; u < VB; ++u) {
+            const int t = sl + SL * (i0 + u);
+            if (t < S)
+                acc += (uint64_t)q48_mul(sc[t], t == pos ? vs[d] : vv[u]);
+        }
+    };
+    for (int i0 = 0; sl + SL * i0 < S; i0 += 2 * VB) {
+        vmac(va, i0);
+#pragma unroll
+        for (int u = 0; u < VB; ++u)
+            va[u] = vld(i0 + 2 * VB + u);
+        vmac(vb, i0 + VB);
+#pragma unroll
+        for (int u = 0; u < VB; ++u)
+            vb[u] = vld(i0 + 3 * VB + u);
+    }
+    part[tid] = (int64_t)acc;
+    __syncthreads();
+    if (sl == 0) {
+        uint64_t o = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < SL; ++s2)
+            o += (uint64_t)part[s2 * HD + d];
+        out[(size_t)h * HD + d] = (int64_t)o;
     }
 }
 
@@ -609,8 +827,12 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
 int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                        int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
                        int layer, const int *d_pos, int pos, int n_heads, int n_kv,
-                       int head_dim, int max_seq, int rope)
+                       int head_dim, int max_seq, int rope, const void *prefetch,
+                       size_t prefetch_bytes)
 {
+    // prefetch blocks: one per compute unit the heads leave idle
+    const size_t pf_n16 = prefetch ? prefetch_bytes / 16 : 0;
+    const int pf_blocks = pf_n16 ? (c->cu_count > n_heads ? c->cu_count - n_heads : 1) : 0;
     const bool lds = max_seq <= ATT_LDS_MAX;
     if (!lds) {
         int rc = q48_ws_reserve(c, (size_t)n_heads * max_seq * sizeof(int64_t));
@@ -619,10 +841,23 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
     }
     int64_t *ws = (int64_t *)c->ws;
 #define ATT_LAUNCH(R, L)                                                                      \
-    hipLaunchKernelGGL((k_attn_v2<R, L>), dim3(n_heads), dim3(ATT_NT), 0, c->stream, out, q,   \
-                       kcache, vcache, k_new, v_new, ws, c->rope_cos, c->rope_sin, layer,     \
-                       d_pos, pos, n_heads, n_kv, head_dim, max_seq)
-    if (rope && lds)
+    hipLaunchKernelGGL((k_attn_v2<R, L>), dim3(n_heads + pf_blocks), dim3(ATT_NT), 0,         \
+                       c->stream, out, q, kcache, vcache, k_new, v_new, ws, c->rope_cos,      \
+                       c->rope_sin, layer, d_pos, pos, n_heads, n_kv, head_dim, max_seq,      \
+                       (const ulonglong2 *)prefetch, pf_n16)
+    const int64_t *scale_p = c->rope_sin + (size_t)c->rope_max_seq * (c->rope_head_dim / 2);
+#define ATT3_LAUNCH(HD)                                                                      \
+    hipLaunchKernelGGL((k_attn_v3<HD>), dim3(n_heads + pf_blocks), dim3(256), 0, c->stream,  \
+                       out, q, kcache, vcache, k_new, v_new, c->rope_cos, c->rope_sin,       \
+                       scale_p, layer, d_pos, pos, n_heads, n_kv, max_seq,                   \
+                       (const ulonglong2 *)prefetch, pf_n16)
+    if (rope && lds && head_dim == 64)
+        ATT3_LAUNCH(64);
+    else if (rope && lds && head_dim == 32)
+        ATT3_LAUNCH(32);
+    else if (rope && lds && head_dim == 128)
+        ATT3_LAUNCH(128);
+    else if (rope && lds)
         ATT_LAUNCH(1, 1);
     else if (rope)
         ATT_LAUNCH(1, 0);
@@ -631,6 +866,7 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
     else
         ATT_LAUNCH(0, 0);
 #undef ATT_LAUNCH
+#undef ATT3_LAUNCH
     return (int)hipGetLastError();
 }
 

@@ -51,6 +51,7 @@ struct q48h_model {
                                    fused, the producer leaves partial sums and every
                                    consumer block finishes them */
     int graph_ready;            /* the context graph holds this model's decode step */
+    int prefetch;               /* attention warms the cache with W_o (fused modes) */
 };
 
 /* ---------------------------------------------------------------------- */
@@ -198,6 +199,7 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
     size_t a_sf = an; an += align_up(sw);
 
     m->fused = 3;
+    m->prefetch = 1;
     if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->kc, kvn * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->vc, kvn * 8)) ||
@@ -259,6 +261,17 @@ void q48h_model_set_fused(q48h_model *m, int fused)
         fused = 3;
     if (m && m->fused != fused) {
         m->fused = fused;
+        if (m->graph_ready) {
+            q48_graph_drop(m->ctx);
+            m->graph_ready = 0;
+        }
+    }
+}
+
+void q48h_model_set_prefetch(q48h_model *m, int on)
+{
+    if (m && m->prefetch != (on != 0)) {
+        m->prefetch = on != 0;
         if (m->graph_ready) {
             q48_graph_drop(m->ctx);
             m->graph_ready = 0;
@@ -632,8 +645,13 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
         TRY(q48_rmsnorm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an,
                              dim + 2 * kvd, dim));
     }
-    TRY(q48_attn_decode_rope(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
-                             c->n_kv_heads, hd, c->max_seq));
+    if (m->prefetch)
+        TRY(q48_attn_decode_rope_prefetch(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
+                                          c->n_kv_heads, hd, c->max_seq, b + m->lo_wo,
+                                          (size_t)dim * dim * 8));
+    else
+        TRY(q48_attn_decode_rope(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
+                                 c->n_kv_heads, hd, c->max_seq));
     if (m->fused == 3) {
         TRY(q48_gemv_residual_stats(x, m->hidden, b + m->lo_wo, m->attn, dim, dim, m->s_ffn));
         TRY(q48_norm_gemv_swiglu_stats(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn,

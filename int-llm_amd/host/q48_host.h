@@ -114,6 +114,12 @@ int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_to
  * each block of the consuming GEMV finishes them. */
 void q48h_model_set_fused(q48h_model *m, int fused);
 
+/* In the fused modes, have each layer's attention launch also read that
+ * layer's W_o on the idle compute units (q48_attn_decode_rope_prefetch), so
+ * the O projection finds it in the device-side cache.  On by default; the
+ * bits do not depend on it. */
+void q48h_model_set_prefetch(q48h_model *m, int on);
+
 /* Greedy decode of n steps replayed from a captured graph: step i runs
  * forward(token_i, start_pos + i) and its argmax becomes token_{i+1} on the
  * device, with no host round trip between steps.  out_tokens[i] receives

@@ -54,6 +54,7 @@ ABI_SIGNATURES = {
     "q48_gemv_residual": [_P, _P, _P, _P, _I, _I],
     "q48_rmsnorm_gemv_swiglu": [_P, _P, _P, _P, _P, _I, _I],
     "q48_attn_decode_rope": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
+    "q48_attn_decode_rope_prefetch": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _SZ],
     "q48_rms_inv": [_P, _P, _P, _I],
     "q48_embed_rms": [_P, _P, _P, _I, _I, _P],
     "q48_norm_gemv": [_P, _P, _P, _P, _P, _P, _I, _I],
@@ -263,6 +264,11 @@ class Context:
         return check("q48_attn_decode_rope", hip_lib().q48_attn_decode_rope(
             self.h, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq))
 
+    def attn_decode_rope_prefetch(self, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq,
+                                  prefetch, nbytes):
+        return check("q48_attn_decode_rope_prefetch", hip_lib().q48_attn_decode_rope_prefetch(
+            self.h, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq, prefetch, nbytes))
+
     def rms_inv(self, r_out, x, dim):
         return check("q48_rms_inv", hip_lib().q48_rms_inv(self.h, r_out, x, dim))
 
@@ -371,6 +377,7 @@ HOST_SIGNATURES = {
     "q48h_decode_from": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(C.c_uint64),
                           C.POINTER(Stats)], C.c_int),
     "q48h_model_set_fused": ([_P, _I], None),
+    "q48h_model_set_prefetch": ([_P, _I], None),
     "q48h_gemv_sweep": ([_P, _I, C.POINTER(C.c_int), C.POINTER(C.c_double)], C.c_int),
     "q48h_decode_graph": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
 }
@@ -440,6 +447,10 @@ class HostModel:
         total = check("q48h_generate", host_lib().q48h_generate(
             self.h, p, len(prompt), max_new, out, hs, C.byref(n), C.byref(st)))
         return list(out[:total]), (list(hs[:n.value]) if hashes else None), st
+
+    def set_prefetch(self, on: bool):
+        """Warm the device cache with each layer's W_o during its attention."""
+        host_lib().q48h_model_set_prefetch(self.h, int(bool(on)))
 
     def set_fused(self, mode: int):
         """0: one op per reference step; 1: fused with per-block norm

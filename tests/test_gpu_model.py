@@ -144,16 +144,20 @@ def test_gemm_config4_vs_reference(ctx, T):
             b.free()
 
 
-@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("mode", [0, 1, 2, "noprefetch"])
 def test_tiny_generate_other_paths_bit_exact(ctx, mode):
     """One library op per reference step (0), the per-block-statistics
-    fusion (1) and the producer-statistics fusion (2) give the same stream
-    as the default path (partial sums finished by the consumer)."""
+    fusion (1), the producer-statistics fusion (2) and the default path
+    without the W_o prefetch give the same stream as the default path
+    (partial sums finished by the consumer, prefetch on)."""
     g = golden("tiny_generate.json")
     m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
     try:
         m.synth(g["seed"], threads())
-        m.set_fused(mode)
+        if mode == "noprefetch":
+            m.set_prefetch(False)
+        else:
+            m.set_fused(mode)
         say("tiny generate mode", mode)
         toks, hs, _ = m.generate(g["prompt"], g["max_new"])
         assert toks == g["tokens"]

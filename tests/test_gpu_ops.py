@@ -103,6 +103,17 @@ def test_device_div_random_vs_oracle(ctx, oracle):
     d = dev_eval(ctx, intllm.FP_DIV, a, b)
     want = np.array([oracle.q48o_fp_div(int(p), int(q)) for p, q in zip(a, b)], dtype=np.int64)
     assert np.array_equal(d, want)
+    # log-uniform magnitudes: every quotient size from 0 to 2^111 bits
+    n = 8192
+    ea, eb = rng.integers(0, 64, size=n), rng.integers(0, 64, size=n)
+    a = np.array([spec.wrap64(int(rng.integers(0, 1 << 62)) >> (62 - min(int(e), 62))) for e in ea],
+                 dtype=np.int64) * rng.choice([-1, 1], size=n)
+    b = np.array([max(1, int(rng.integers(0, 1 << 62)) >> (62 - min(int(e), 62))) for e in eb],
+                 dtype=np.int64) * rng.choice([-1, 1], size=n)
+    say("div log-uniform", n)
+    d = dev_eval(ctx, intllm.FP_DIV, a, b)
+    want = np.array([oracle.q48o_fp_div(int(p), int(q)) for p, q in zip(a, b)], dtype=np.int64)
+    assert np.array_equal(d, want)
 
 
 def gemv_dev(ctx, W, x, M, K, w_offset=0):
@@ -399,6 +410,13 @@ def test_attention_rope_fused(ctx, oracle, nh, nkv, hd, max_seq, positions):
                              max_seq)
         assert np.array_equal(do.download(), out), pos
         assert np.array_equal(dk.download(), kc) and np.array_equal(dv.download(), vc)
+        # the same with the idle compute units reading another buffer meanwhile
+        do2 = ctx.buffer(nh * hd)
+        ctx.attn_decode_rope_prefetch(do2.ptr, dq.ptr, dk.ptr, dv.ptr, dkn.ptr, dvn.ptr, 1, pos, nh,
+                                      nkv, hd, max_seq, dv.ptr, (vc.size * 8) // 16 * 16)
+        assert np.array_equal(do2.download(), out), pos
+        assert np.array_equal(dk.download(), kc) and np.array_equal(dv.download(), vc)
+        do2.free()
         for b in (dq, dkn, dvn, do):
             b.free()
 
