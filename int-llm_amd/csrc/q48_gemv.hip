@@ -307,7 +307,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     // PRO 3: the norm statistics arrive as the producer's per-8-row partial
     // sums of squares (128-bit lo/hi pairs, ceil(K / 8) of them, at most 3
     // per thread); their loads go out first, with the residual's
-    constexpr int PC = 3;
+    // np = K / 8 = 2 NW NTF partials over 64 NW threads when NTF is known
+    constexpr int PC = NTF > 0 ? (NTF + 31) / 32 : 3;
     uint64_t plo[PC], phi[PC];
     const int np = (K + 7) >> 3;
     if (PRO == 3) {
@@ -352,7 +353,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     // the wait counts stay static.
     // (A wave with an empty segment or no whole tile reads element 0 of x
     // and of W instead: in bounds, never used.)
-    constexpr int XB = PRO ? 8 : 16;   // x values per lane per staging batch
+    // x values per lane per staging batch: exactly the segment when every
+    // wave has NTF tiles (16 NTF elements), else 8 or 16 per batch
+    constexpr int XB = NTF > 0 ? (16 * NTF + 63) / 64 : (PRO ? 8 : 16);
     int64_t xv[XB], nw[XB];
     const int xk = kn > 0 ? k0 : 0, xlast = max(kn - 1, 0);
 #pragma unroll
