@@ -355,15 +355,31 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     // and of W instead: in bounds, never used.)
     // x values per lane per staging batch: exactly the segment when every
     // wave has NTF tiles (16 NTF elements), else 8 or 16 per batch
-    constexpr int XB = NTF > 0 ? (16 * NTF + 63) / 64 : (PRO ? 8 : 16);
-    int64_t xv[XB], nw[XB];
-    const int xk = kn > 0 ? k0 : 0, xlast = max(kn - 1, 0);
+    // With NTF known every wave's segment is exactly 16 NTF elements and x,
+    // norm_w are 16-byte aligned (checked on the host): a lane loads element
+    // pairs, 16 bytes at a time.  Otherwise single elements, 8 or 16 of them
+    // per lane per staging batch.
+    constexpr int XB = NTF > 0 ? (16 * NTF + 127) / 128 : (PRO ? 8 : 16);
+    constexpr int XW = NTF > 0 ? 2 : 1;   // elements per load
+    int64_t xv[XB * XW], nw[XB * XW];
+    const int xk = kn > 0 ? k0 : 0, xlast = max(kn - XW, 0);
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
-        const int j = min(lane + 64 * b, xlast);
-        xv[b] = x[xk + j];
-        if (PRO != 0)
-            nw[b] = norm_w[xk + j];
+        const int j = min(XW * lane + 64 * XW * b, xlast);
+        if constexpr (XW == 2) {
+            const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(x + xk + j);
+            xv[2 * b] = (int64_t)v.x;
+            xv[2 * b + 1] = (int64_t)v.y;
+            if (PRO != 0) {
+                const ulonglong2 w = *reinterpret_cast<const ulonglong2 *>(norm_w + xk + j);
+                nw[2 * b] = (int64_t)w.x;
+                nw[2 * b + 1] = (int64_t)w.y;
+            }
+        } else {
+            xv[b] = x[xk + j];
+            if (PRO != 0)
+                nw[b] = norm_w[xk + j];
+        }
     }
     asm volatile("" ::: "memory");   // keep the x loads ahead of the weight loads
     const ulonglong2 *wt = nt > 0 ? w2 : reinterpret_cast<const ulonglong2 *>(W);
@@ -395,10 +411,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     uint32_t *xw = xs + (size_t)wave * seg * 3;
     auto stage = [&](int j0) {
 #pragma unroll
-        for (int b = 0; b < XB; ++b) {
+        for (int b = 0; b < XB * XW; ++b) {
             // the loaded value is used outside the branch so that its load
             // is not sunk into it (a load there would wait for the weights)
-            const int j = j0 + lane + 64 * b;
+            const int j = j0 + XW * lane + 64 * XW * (b / XW) + b % XW;
             int64_t v = xv[b];
             if (PRO != 0)
                 v = q48_mul(q48_mul(v, r), nw[b]);
@@ -413,7 +429,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         }
     };
     stage(0);   // straight-line: the loads above stay where they are
-    for (int j0 = 64 * XB; j0 < kn; j0 += 64 * XB) {
+    for (int j0 = 64 * XB; NTF == 0 && j0 < kn; j0 += 64 * XB) {
 #pragma unroll
         for (int b = 0; b < XB; ++b) {
             const int j = min(j0 + lane + 64 * b, kn - 1);
@@ -719,11 +735,12 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
     }
     // K = 2048 and K = 5632 (every wave: 16 or 44 whole tiles) take the
     // unrolled rotating pipeline; other K the batched loop
-    if (K == NW * seg && seg == 16 * 16)
+    const bool al = ((uintptr_t)x & 15) == 0 && (PRO == 0 || ((uintptr_t)norm_w & 15) == 0);
+    if (al && K == NW * seg && seg == 16 * 16)
         hipLaunchKernelGGL((k_gemv_v5<NW, 4, PRO, EPI, 16>), dim3(blocks), dim3(64 * NW), lds,
                            c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
                            M, K, seg);
-    else if (K == NW * seg && seg == 16 * 44)
+    else if (al && K == NW * seg && seg == 16 * 44)
         hipLaunchKernelGGL((k_gemv_v5<NW, 6, PRO, EPI, 44>), dim3(blocks), dim3(64 * NW), lds,
                            c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
                            M, K, seg);
