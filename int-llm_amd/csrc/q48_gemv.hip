@@ -196,10 +196,19 @@ __global__ __launch_bounds__(64 * RPB) void k_gemv(int64_t *__restrict__ y,
 // ---------------------------------------------------------------------------
 constexpr int V4_RB = 8;
 
-// (ss >> 48) / dim + eps, then fp_inv_sqrt: the scalar part of rmsnorm.
+// (ss >> 48) / dim + eps, then fp_inv_sqrt: the scalar part of rmsnorm
+// (llama_int.c:1049-1055).  A power-of-two dim divides by shifting
+// (truncating, like the division, for a negative wrapped sum too).
 __device__ __forceinline__ int64_t rms_inv_of(q48_u128 ss, int dim)
 {
-    int64_t ms = (int64_t)q48_divs_128_64((q48_i128)ss >> 48, (int64_t)dim);
+    const q48_i128 a = (q48_i128)ss >> 48;
+    int64_t ms;
+    if ((dim & (dim - 1)) == 0) {
+        const int sh = __builtin_ctz((unsigned)dim);
+        ms = (int64_t)(a >= 0 ? a >> sh : -((-a) >> sh));
+    } else {
+        ms = (int64_t)q48_divs_128_64(a, (int64_t)dim);
+    }
     ms = (int64_t)((uint64_t)ms + 2814749767ull);
     return q48_inv_sqrt(ms);
 }
@@ -307,17 +316,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     // PRO 3: the norm statistics arrive as the producer's per-8-row partial
     // sums of squares (128-bit lo/hi pairs, ceil(K / 8) of them, at most 3
     // per thread); their loads go out first, with the residual's
-    // np = K / 8 = 2 NW NTF partials over 64 NW threads when NTF is known
-    constexpr int PC = NTF > 0 ? (NTF + 31) / 32 : 3;
+    // With NTF known each lane preloads np / 64 of the np = K / 8 = 2 NW NTF
+    // partials (16-byte aligned, checked on the host); otherwise they are
+    // read in a loop when needed.
+    constexpr int PC = NTF > 0 ? (2 * NW * NTF + 63) / 64 : 1;
     uint64_t plo[PC], phi[PC];
     const int np = (K + 7) >> 3;
-    if (PRO == 3) {
-        const uint64_t *st = reinterpret_cast<const uint64_t *>(r_in);
+    const uint64_t *st = reinterpret_cast<const uint64_t *>(r_in);
+    if (PRO == 3 && NTF > 0) {
 #pragma unroll
         for (int c = 0; c < PC; ++c) {
-            const int i = min(tid + c * 64 * NW, np - 1);
-            plo[c] = st[2 * i];
-            phi[c] = st[2 * i + 1];
+            const int i = min(lane + c * 64, np - 1);
+            const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(st + 2 * i);
+            plo[c] = v.x;
+            phi[c] = v.y;
         }
     }
 
@@ -392,18 +404,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     __builtin_amdgcn_sched_barrier(0);
 
     if (PRO == 3) {
+        // every wave adds all the partials itself (no block barrier) and
+        // every lane derives the same r
         q48_u128 ss = 0;
+        if constexpr (NTF > 0) {
 #pragma unroll
-        for (int c = 0; c < PC; ++c) {
-            // masked, not branched: a branch would sink the load and wait on it
-            const uint64_t m = tid + c * 64 * NW < np ? ~0ull : 0ull;
-            ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
+            for (int c = 0; c < PC; ++c) {
+                // masked, not branched: a branch would sink the load and wait
+                const uint64_t m = lane + c * 64 < np ? ~0ull : 0ull;
+                ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
+            }
+        } else {
+            for (int i = lane; i < np; i += 64)
+                ss += ((q48_u128)st[2 * i + 1] << 64) | st[2 * i];
         }
-        ss = block_sum128<64 * NW>(ss, red_lo, red_hi);
-        if (tid == 0)
-            r_sh = rms_inv_of(ss, K);
-        __syncthreads();
-        r = r_sh;
+        ss = q48_wave_sum128(ss);
+        r = rms_inv_of(ss, K);
     }
 
     // stage this wave's segment of x as limbs; sum x over the segment
@@ -735,7 +751,8 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
     }
     // K = 2048 and K = 5632 (every wave: 16 or 44 whole tiles) take the
     // unrolled rotating pipeline; other K the batched loop
-    const bool al = ((uintptr_t)x & 15) == 0 && (PRO == 0 || ((uintptr_t)norm_w & 15) == 0);
+    const bool al = ((uintptr_t)x & 15) == 0 && (PRO == 0 || ((uintptr_t)norm_w & 15) == 0) &&
+                    (PRO != 3 || ((uintptr_t)r_in & 15) == 0);
     if (al && K == NW * seg && seg == 16 * 16)
         hipLaunchKernelGGL((k_gemv_v5<NW, 4, PRO, EPI, 16>), dim3(blocks), dim3(64 * NW), lds,
                            c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,

@@ -549,6 +549,27 @@ def test_norm_gemv_with_stats(ctx, oracle, M, K):
         b.free()
 
 
+@pytest.mark.parametrize("K", [2048, 7681])
+def test_norm_gemv_stats_wrapped_sum(ctx, oracle, K):
+    """Sums of squares past 2^127 wrap negative in the reference's int128:
+    the normalised vector (and so the product) is then exactly zero."""
+    rng = np.random.default_rng(K)
+    M = 16
+    W = (rng.standard_normal(M * K) * spec.SIGMA_W).astype(np.int64)
+    x = (rng.standard_normal(K) * ONE).astype(np.int64)
+    x[:3] = spec.INT64_MIN
+    w = (rng.standard_normal(K) * ONE).astype(np.int64)
+    want = O.gemv(W, _rms(oracle, x, w), M, K)
+    dW, dx, dw, dy = ctx.to_device(W), ctx.to_device(x), ctx.to_device(w), ctx.buffer(M)
+    ds = ctx.buffer(intllm.stats_words(K))
+    say("norm_gemv_stats wrapped", M, K)
+    ctx.rms_stats(ds.ptr, dx.ptr, K)
+    ctx.norm_gemv_stats(dy.ptr, dW.ptr, dx.ptr, dw.ptr, ds.ptr, M, K)
+    assert np.array_equal(dy.download(), want)
+    for b in (dW, dx, dw, dy, ds):
+        b.free()
+
+
 @pytest.mark.parametrize("ffn,K", [(5632, 2048), (688, 256), (6, 7681)])
 def test_norm_gemv_swiglu_with_stats(ctx, oracle, ffn, K):
     rng = np.random.default_rng(ffn + 5 * K)
