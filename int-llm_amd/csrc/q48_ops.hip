@@ -588,6 +588,33 @@ __global__ __launch_bounds__(256) void k_attn_v3(
     }
 }
 
+// This thread's share of argmax (llama_int.c:2888-2893) over v[0..n) with
+// 1024 threads: elements tid + 1024 i, scanned in ascending order with a
+// strict > (the first maximum wins).  The loads of a batch of 32 are all
+// issued before any comparison: one memory round trip per batch instead of
+// one per element.
+__device__ __forceinline__ void argmax_scan(const int64_t *__restrict__ v, int n, int tid,
+                                            int64_t &best, int &idx)
+{
+    constexpr int B = 32;
+    for (int i0 = 0; i0 < n; i0 += 1024 * B) {
+        int64_t x[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int i = i0 + tid + 1024 * b;
+            x[b] = v[i < n ? i : n - 1];
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int i = i0 + tid + 1024 * b;
+            if (i < n && x[b] > best) {
+                best = x[b];
+                idx = i;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Decode-step state (graph replay): st[0] = token, st[1] = pos, st[2] =
 // number of tokens recorded.  k_step_argmax is argmax (llama_int.c:
@@ -612,13 +639,7 @@ __global__ __launch_bounds__(1024) void k_step_argmax(int *__restrict__ st,
     const int tid = threadIdx.x;
     int64_t best = INT64_MIN;
     int idx = n;
-    for (int i = tid; i < n; i += 1024) {
-        const int64_t x = v[i];
-        if (x > best) {
-            best = x;
-            idx = i;
-        }
-    }
+    argmax_scan(v, n, tid, best, idx);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         const int64_t ov = __shfl_xor(best, off, 64);
@@ -699,13 +720,7 @@ __global__ __launch_bounds__(1024) void k_argmax(int *__restrict__ out,
     const int tid = threadIdx.x;
     int64_t best = INT64_MIN;
     int idx = n;   // sentinel larger than any index
-    for (int i = tid; i < n; i += 1024) {
-        const int64_t x = v[i];
-        if (x > best) {   // strided ascending scan: keeps the first max
-            best = x;
-            idx = i;
-        }
-    }
+    argmax_scan(v, n, tid, best, idx);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         const int64_t ov = __shfl_xor(best, off, 64);
