@@ -343,7 +343,8 @@ def test_rmsnorm_gemv_fused(ctx, oracle, M, K):
         b.free()
 
 
-@pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 5632), (256, 688), (3, 7681), (7, 33)])
+@pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 5632), (256, 688), (3, 7681), (7, 33),
+                                 (4616, 2048)])
 def test_gemv_residual_fused(ctx, M, K):
     rng = np.random.default_rng(M * 3 + K)
     W = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=M * K, dtype=np.int64)
@@ -590,7 +591,8 @@ def test_norm_gemv_swiglu_with_stats(ctx, oracle, ffn, K):
         b.free()
 
 
-@pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 5632), (256, 688), (13, 40), (3, 7681)])
+@pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 5632), (256, 688), (13, 40), (3, 7681),
+                                 (5128, 2048)])
 def test_gemv_residual_stats(ctx, oracle, M, K):
     """acc += W x and the partial sums of the new acc, three calls in a row,
     then a consumer GEMV normalising acc with them."""
