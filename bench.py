@@ -35,8 +35,8 @@ sys.path.insert(0, str(ROOT / "tests"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline sweep, from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE runs scaled by the counters' reading for a copy kernel of known
-# size (profiles/k_gemv_v4_decode_tinyllama.md); re-measure when the kernel changes
-TRAFFIC = 93502843
+# size (profiles/k_gemv_v5_decode_tinyllama.md); re-measure when the kernel changes
+TRAFFIC = 93553554
 REF_CPU_MS_PER_TOK = 501.4   # reference decode, Zen 4, 1 thread
 
 
