@@ -161,6 +161,12 @@ int q48_attn_decode_rope(q48_ctx *ctx, int64_t *out, const int64_t *q,
                          int64_t *kcache, int64_t *vcache, const int64_t *k_new,
                          const int64_t *v_new, int layer, int pos, int n_heads,
                          int n_kv, int head_dim, int max_seq);
+/* First position at which q48_attn_decode_rope(_prefetch) serves a head with
+ * the split kernels (chunks of the cache over many compute units) instead
+ * of one block per head.  Kernels are chosen from the pos argument, also in
+ * step mode: a graph captured below this position keeps the one-block
+ * kernels as replays move past it (same bits, slower). */
+int q48_attn_split_min(void);
 /* q48_attn_decode_rope that also reads [prefetch, prefetch + prefetch_bytes)
  * (16-byte aligned; typically the next op's weights, W_o) on the compute
  * units the heads leave idle, so that the next op finds them in the

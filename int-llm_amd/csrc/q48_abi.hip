@@ -101,7 +101,7 @@ int q48_ctx_create(q48_ctx **out, int device)
     if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
         hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess ||
         hipMalloc(&c->d_step, 4 * sizeof(int)) != hipSuccess ||
-        hipMalloc(&c->rms_count, 64 * sizeof(int)) != hipSuccess) {
+        hipMalloc(&c->rms_count, 512 * sizeof(int)) != hipSuccess) {
         q48_ctx_destroy(c);
         return Q48_ENOMEM;
     }
@@ -109,7 +109,7 @@ int q48_ctx_create(q48_ctx **out, int device)
     if (rc == Q48_OK)
         rc = launch_rc(q48_launch_step_set(c, 0, 0));
     if (rc == Q48_OK)
-        rc = launch_rc(q48_launch_zero(c, c->rms_count, 64 * sizeof(int)));
+        rc = launch_rc(q48_launch_zero(c, c->rms_count, 512 * sizeof(int)));
     if (rc == Q48_OK)
         rc = hip_rc(hipStreamSynchronize(c->stream));
     if (rc != Q48_OK) {
@@ -585,6 +585,8 @@ int q48_attn_decode_rope(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kc
     return q48_attn_decode_rope_prefetch(c, out, q, kcache, vcache, k_new, v_new, layer, pos,
                                          n_heads, n_kv, head_dim, max_seq, nullptr, 0);
 }
+
+int q48_attn_split_min(void) { return q48_att_split_min(); }
 
 int q48_attn_decode_rope_prefetch(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                                   int64_t *vcache, const int64_t *k_new, const int64_t *v_new,

@@ -23,7 +23,8 @@ struct q48_ctx {
     void *tmp;                   // device temporaries of the unfused fallbacks
     size_t tmp_bytes;
     uint64_t *rms_part;          // device: per-block partial sums of squares (EPI 3)
-    int *rms_count;              // device: blocks finished (EPI 3), back to 0 after use
+    int *rms_count;              // device: tickets, back to 0 after use: [0] EPI 3 blocks
+                                 // finished, [256 + h] split-attention chunks of head h
     int rms_blocks;
     hipGraph_t graph;            // captured decode step
     hipGraphExec_t graph_exec;
@@ -70,6 +71,7 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
                     int64_t *kcache, int64_t *vcache, const int64_t *k_new,
                     const int64_t *v_new, int layer, const int *d_pos, int pos,
                     int n_heads, int n_kv, int head_dim, int max_seq);
+int q48_att_split_min();
 int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                        int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
                        int layer, const int *d_pos, int pos, int n_heads, int n_kv,

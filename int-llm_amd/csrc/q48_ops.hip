@@ -616,6 +616,234 @@ __device__ __forceinline__ void argmax_scan(const int64_t *__restrict__ v, int n
 }
 
 // ---------------------------------------------------------------------------
+// Split attention for long caches: the same exact computation spread over
+// (chunk of ATT_CH positions, head) blocks, so that a head's keys and values
+// stream through many compute units instead of one.  The reference's
+// softmax needs the global max before any exponential and the global sum
+// before any division, so:
+//  - k_attn_s1: each block rotates q_h / the new k (RoPE), scores its chunk
+//    into sc[h][t] and its chunk maximum into cmax[h][c], all with
+//    write-through stores; the last block of a head to finish (agent-scope
+//    ticket, taken after its stores completed) takes the global max, turns
+//    every score into e_t = fp_safe_exp(s_t - max), sums them (int64 wrap),
+//    stores p_t = fp_div(e_t, sum) when sum > 0, zeroes out[h] and resets
+//    the ticket (llama_int.c:1060-1072, 1502-1512);
+//  - k_attn_s2: each block adds sum_t fp_mul(p_t, v_t[d]) over its chunk
+//    into out[h][d] with 64-bit atomic adds: int64 wrap sums in any order,
+//    the bits of llama_int.c:1514-1529.
+// Blocks whose chunk starts past pos exit at once (the grid covers the
+// whole cache, so a captured graph stays valid as pos grows).
+// ---------------------------------------------------------------------------
+constexpr int ATT_CH = 256;        // positions per chunk
+constexpr int ATT_SPLIT_MIN = 512; // first position served by the split kernels
+constexpr int ATT_NCMAX = 128;   // chunks per head: max_seq <= 32768
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_s1(
+    int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
+    int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
+    const int64_t *__restrict__ v_new, const int64_t *__restrict__ cos_t,
+    const int64_t *__restrict__ sin_t, const int64_t *__restrict__ scale_p,
+    int64_t *__restrict__ sc, int64_t *__restrict__ cmax, int *__restrict__ tickets, int layer,
+    const int *__restrict__ d_pos, int pos, int n_heads, int n_kv, int max_seq)
+{
+    constexpr int NT = 256, DPL = HD / 8, DP2 = DPL / 2, NG = NT / 8;
+    __shared__ int64_t qs[HD], ks[HD], vs[HD];
+    __shared__ int64_t red[NT / 64];
+    __shared__ int last_sh;
+    if (d_pos)
+        pos = *d_pos;
+    if (pos < 0 || pos >= max_seq)
+        return;
+    const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int S = pos + 1, t0 = c * ATT_CH;
+    if (t0 >= S)
+        return;   // uniform: no barrier is skipped by part of the block
+    const int tend = min(t0 + ATT_CH, S);
+    const int nc = (S + ATT_CH - 1) / ATT_CH;
+    const int group = n_heads / n_kv, kh = h / group;
+    const size_t kvd = (size_t)n_kv * HD;
+    const size_t base = (size_t)layer * max_seq;
+    const int half = HD / 2;
+    const int g = tid >> 3, l8 = tid & 7;
+    const int64_t scale = *scale_p;
+    int64_t *sch = sc + (size_t)h * max_seq;
+
+    // RoPE inputs and the new v first, then the first two key passes
+    const int64_t *qh = q + (size_t)h * HD, *kn = k_new + (size_t)kh * HD;
+    const int i = min(tid, half - 1), j = min(tid, HD - 1);
+    int64_t cs = cos_t[(size_t)pos * half + i];
+    int64_t sn = sin_t[(size_t)pos * half + i];
+    int64_t q0 = qh[i], q1 = qh[i + half];
+    int64_t k0 = kn[i], k1 = kn[i + half];
+    int64_t vn = v_new[(size_t)kh * HD + j];
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t *kb0 = kcache + base * kvd + (size_t)kh * HD + l8 * DPL;
+    auto krow = [&](int t) {
+        return reinterpret_cast<const ulonglong2 *>(kb0 + (size_t)min(t, tend - 1) * kvd);
+    };
+    ulonglong2 ka[DP2], kb[DP2];
+#pragma unroll
+    for (int d = 0; d < DP2; ++d)
+        ka[d] = krow(t0 + g)[d];
+#pragma unroll
+    for (int d = 0; d < DP2; ++d)
+        kb[d] = krow(t0 + NG + g)[d];
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(cs), "+v"(sn), "+v"(q0), "+v"(q1), "+v"(k0), "+v"(k1), "+v"(vn));
+    qs[i] = (int64_t)((uint64_t)q48_mul(q0, cs) - (uint64_t)q48_mul(q1, sn));
+    qs[i + half] = (int64_t)((uint64_t)q48_mul(q1, cs) + (uint64_t)q48_mul(q0, sn));
+    ks[i] = (int64_t)((uint64_t)q48_mul(k0, cs) - (uint64_t)q48_mul(k1, sn));
+    ks[i + half] = (int64_t)((uint64_t)q48_mul(k1, cs) + (uint64_t)q48_mul(k0, sn));
+    vs[j] = vn;
+    __syncthreads();
+    if (h % group == 0 && c == pos / ATT_CH && tid < HD) {
+        kcache[(base + pos) * kvd + (size_t)kh * HD + tid] = ks[tid];
+        vcache[(base + pos) * kvd + (size_t)kh * HD + tid] = vs[tid];
+    }
+
+    // scores of the chunk (the row at pos is the block's own rotated k)
+    const int64_t *qd = qs + l8 * DPL, *kd = ks + l8 * DPL;
+    int64_t mx = INT64_MIN;
+    auto score = [&](const ulonglong2 (&kr)[DP2], int t) {
+        const bool own = t == pos;
+        q48_u128 dot = 0;
+#pragma unroll
+        for (int d = 0; d < DP2; ++d) {
+            const int64_t a0 = own ? kd[2 * d] : (int64_t)kr[d].x;
+            const int64_t a1 = own ? kd[2 * d + 1] : (int64_t)kr[d].y;
+            dot += (q48_u128)((q48_i128)qd[2 * d] * a0);
+            dot += (q48_u128)((q48_i128)qd[2 * d + 1] * a1);
+        }
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            const uint64_t lo = (uint64_t)dot, hi = (uint64_t)(dot >> 64);
+            dot += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
+        }
+        if (t < tend && l8 == 0) {
+            const int64_t sv = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
+            __hip_atomic_store(&sch[t], sv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            mx = sv > mx ? sv : mx;
+        }
+    };
+    for (int tt = t0; tt < tend; tt += 2 * NG) {
+        score(ka, tt + g);
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            ka[d] = krow(tt + 2 * NG + g)[d];
+        score(kb, tt + NG + g);
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            kb[d] = krow(tt + 3 * NG + g)[d];
+    }
+    mx = block_max64<NT>(mx, red);
+    if (tid == 0)
+        __hip_atomic_store(&cmax[(size_t)h * ATT_NCMAX + c], mx, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    // Every store above is write-through (agent scope); waiting for their
+    // completion before the ticket orders them before it for every block.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+        last_sh = __hip_atomic_fetch_add(&tickets[h], 1, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) == nc - 1;
+    __syncthreads();
+    if (!last_sh)
+        return;
+
+    // last block of head h: the softmax over all S positions
+    int64_t gm = INT64_MIN;
+    if (tid < nc)
+        gm = __hip_atomic_load(&cmax[(size_t)h * ATT_NCMAX + tid], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    gm = block_max64<NT>(gm, red);
+    int64_t sum = 0;
+    for (int t = tid; t < S; t += NT) {
+        const int64_t sv = __hip_atomic_load(&sch[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int64_t e = q48_safe_exp((int64_t)((uint64_t)sv - (uint64_t)gm));
+        sch[t] = e;   // re-read below by this same thread
+        sum = (int64_t)((uint64_t)sum + (uint64_t)e);
+    }
+    sum = block_sum64<NT>(sum, red);
+    if (sum > 0)
+        for (int t = tid; t < S; t += NT)
+            sch[t] = q48_div(sch[t], sum);
+    if (tid < HD)
+        out[(size_t)h * HD + tid] = 0;
+    if (tid == 0)
+        tickets[h] = 0;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_s2(int64_t *__restrict__ out,
+                                                const int64_t *__restrict__ vcache,
+                                                const int64_t *__restrict__ sc, int layer,
+                                                const int *__restrict__ d_pos, int pos,
+                                                int n_heads, int n_kv, int max_seq)
+{
+    constexpr int NT = 256, SL = NT / HD, VB = 8;
+    __shared__ int64_t part[NT];
+    if (d_pos)
+        pos = *d_pos;
+    if (pos < 0 || pos >= max_seq)
+        return;
+    const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int S = pos + 1, t0 = c * ATT_CH;
+    if (t0 >= S)
+        return;
+    const int tend = min(t0 + ATT_CH, S);
+    const int group = n_heads / n_kv, kh = h / group;
+    const size_t kvd = (size_t)n_kv * HD;
+    const int d = tid % HD, sl = tid / HD;
+    const int64_t *vcol = vcache + (size_t)layer * max_seq * kvd + (size_t)kh * HD + d;
+    const int64_t *ph = sc + (size_t)h * max_seq;
+    // positions t0 + sl + SL i of this thread, VB per batch, one batch ahead
+    auto tpos = [&](int i) { return min(t0 + sl + SL * i, tend - 1); };
+    int64_t va[VB], vb[VB], pa[VB], pb[VB];
+#pragma unroll
+    for (int u = 0; u < VB; ++u) {
+        va[u] = vcol[(size_t)tpos(u) * kvd];
+        pa[u] = ph[tpos(u)];
+    }
+#pragma unroll
+    for (int u = 0; u < VB; ++u) {
+        vb[u] = vcol[(size_t)tpos(VB + u) * kvd];
+        pb[u] = ph[tpos(VB + u)];
+    }
+    uint64_t acc = 0;
+    auto vmac = [&](const int64_t (&vv)[VB], const int64_t (&pp)[VB], int i0) {
+#pragma unroll
+        for (int u = 0; u < VB; ++u)
+            if (t0 + sl + SL * (i0 + u) < tend)
+                acc += (uint64_t)q48_mul(pp[u], vv[u]);
+    };
+    for (int i0 = 0; t0 + sl + SL * i0 < tend; i0 += 2 * VB) {
+        vmac(va, pa, i0);
+#pragma unroll
+        for (int u = 0; u < VB; ++u) {
+            va[u] = vcol[(size_t)tpos(i0 + 2 * VB + u) * kvd];
+            pa[u] = ph[tpos(i0 + 2 * VB + u)];
+        }
+        vmac(vb, pb, i0 + VB);
+#pragma unroll
+        for (int u = 0; u < VB; ++u) {
+            vb[u] = vcol[(size_t)tpos(i0 + 3 * VB + u) * kvd];
+            pb[u] = ph[tpos(i0 + 3 * VB + u)];
+        }
+    }
+    part[tid] = (int64_t)acc;
+    __syncthreads();
+    if (sl == 0) {
+        uint64_t o = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < SL; ++s2)
+            o += (uint64_t)part[s2 * HD + d];
+        __hip_atomic_fetch_add(reinterpret_cast<uint64_t *>(out) + (size_t)h * HD + d, o,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Decode-step state (graph replay): st[0] = token, st[1] = pos, st[2] =
 // number of tokens recorded.  k_step_argmax is argmax (llama_int.c:
 // 2888-2893) feeding the next step: token <- argmax, pos += 1, and the
@@ -839,6 +1067,8 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
     return (int)hipGetLastError();
 }
 
+int q48_att_split_min() { return ATT_SPLIT_MIN; }
+
 int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                        int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
                        int layer, const int *d_pos, int pos, int n_heads, int n_kv,
@@ -861,6 +1091,35 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
                        c->rope_sin, layer, d_pos, pos, n_heads, n_kv, head_dim, max_seq,      \
                        (const ulonglong2 *)prefetch, pf_n16)
     const int64_t *scale_p = c->rope_sin + (size_t)c->rope_max_seq * (c->rope_head_dim / 2);
+    // long caches: the split kernels (chunks of ATT_CH positions over many
+    // blocks) once the position reaches ATT_SPLIT_MIN; a captured graph
+    // keeps the kernels of the position it was captured at
+    if (rope && pos >= ATT_SPLIT_MIN && (head_dim == 32 || head_dim == 64 || head_dim == 128) &&
+        (max_seq + ATT_CH - 1) / ATT_CH <= ATT_NCMAX && n_heads <= 256) {
+        const size_t sc_n = (size_t)n_heads * max_seq, cm_n = (size_t)n_heads * ATT_NCMAX;
+        int rc = q48_ws_reserve(c, (sc_n + cm_n) * sizeof(int64_t));
+        if (rc)
+            return rc;
+        int64_t *sc = (int64_t *)c->ws, *cm = sc + sc_n;
+        int *tk = c->rms_count + 256;
+        const dim3 grid((max_seq + ATT_CH - 1) / ATT_CH, n_heads);
+#define ATTS_LAUNCH(HD)                                                                       \
+    do {                                                                                      \
+        hipLaunchKernelGGL((k_attn_s1<HD>), grid, dim3(256), 0, c->stream, out, q, kcache,   \
+                           vcache, k_new, v_new, c->rope_cos, c->rope_sin, scale_p, sc, cm,  \
+                           tk, layer, d_pos, pos, n_heads, n_kv, max_seq);                   \
+        hipLaunchKernelGGL((k_attn_s2<HD>), grid, dim3(256), 0, c->stream, out, vcache, sc,  \
+                           layer, d_pos, pos, n_heads, n_kv, max_seq);                       \
+    } while (0)
+        if (head_dim == 64)
+            ATTS_LAUNCH(64);
+        else if (head_dim == 32)
+            ATTS_LAUNCH(32);
+        else
+            ATTS_LAUNCH(128);
+#undef ATTS_LAUNCH
+        return (int)hipGetLastError();
+    }
 #define ATT3_LAUNCH(HD)                                                                      \
     hipLaunchKernelGGL((k_attn_v3<HD>), dim3(n_heads + pf_blocks), dim3(256), 0, c->stream,  \
                        out, q, kcache, vcache, k_new, v_new, c->rope_cos, c->rope_sin,       \

@@ -51,6 +51,7 @@ struct q48h_model {
                                    fused, the producer leaves partial sums and every
                                    consumer block finishes them */
     int graph_ready;            /* the context graph holds this model's decode step */
+    int graph_long;             /* ... captured at a position served by split attention */
     int prefetch;               /* attention warms the cache with W_o (fused modes) */
 };
 
@@ -864,6 +865,13 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
         rc = q48_argmax_step(x, m->logits, c->vocab, m->d_tokens, c->max_seq);
     if (rc == Q48_OK)
         rc = q48_sync(x);
+    /* attention picks its kernels by position (split from q48_attn_split_min):
+     * recapture when the step crosses that line */
+    const int want_long = pos >= q48_attn_split_min();
+    if (rc == Q48_OK && m->graph_ready && m->graph_long != want_long) {
+        rc = q48_graph_drop(x);
+        m->graph_ready = 0;
+    }
     if (rc == Q48_OK && !m->graph_ready) {
         rc = q48_graph_begin(x);
         if (rc == Q48_OK) {
@@ -873,8 +881,10 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
             rc = q48_graph_end(x);
             if (rc1)
                 rc = rc1;
-            if (rc == Q48_OK)
+            if (rc == Q48_OK) {
                 m->graph_ready = 1;
+                m->graph_long = want_long;
+            }
         }
     }
     q48_step_mode(x, 0);

@@ -54,6 +54,7 @@ ABI_SIGNATURES = {
     "q48_gemv_residual": [_P, _P, _P, _P, _I, _I],
     "q48_rmsnorm_gemv_swiglu": [_P, _P, _P, _P, _P, _I, _I],
     "q48_attn_decode_rope": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
+    "q48_attn_split_min": [],
     "q48_attn_decode_rope_prefetch": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _SZ],
     "q48_rms_inv": [_P, _P, _P, _I],
     "q48_embed_rms": [_P, _P, _P, _I, _I, _P],

@@ -130,6 +130,33 @@ def test_long_context_decode_bit_exact(ctx):
         m.free()
 
 
+def test_long_context_graph_decode_bit_exact(ctx):
+    """Config 5 through a graph captured at position 2048 (split attention),
+    then a short-context graph decode on the same model: the step graph is
+    recaptured whenever attention changes kernels, and both streams match
+    the reference's."""
+    g = golden("longctx_decode.json")
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    try:
+        say("longctx synth + kv fill")
+        m.synth(g["seed"], threads())
+        m.kv_fill_synth(g["kv_seed"], g["prefill"], threads())
+        say("longctx graph decode")
+        _, toks, _ = m.decode_graph(g["start_token"], g["prefill"], 24)
+        assert toks == g["tokens"][:24]
+        # back to the start of the cache: the graph drops back to one-block attention
+        gt = golden("tinyllama_generate.json")
+        assert gt["seed"] == g["seed"]
+        for pos, tok in enumerate(gt["prompt"]):
+            nxt, _ = m.forward(tok, pos, spec.TINYLLAMA[6], logits=False)
+        say("short graph decode after long")
+        _, toks2, _ = m.decode_graph(nxt, len(gt["prompt"]), 8)
+        ref = gt["tokens"][len(gt["prompt"]):]
+        assert [nxt] + toks2[:7] == ref[:8]
+    finally:
+        m.free()
+
+
 @pytest.mark.parametrize("T", spec.GEMM_TOKENS)
 def test_gemm_config4_vs_reference(ctx, T):
     g = golden("gemm.json")["shapes"]

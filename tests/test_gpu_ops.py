@@ -380,6 +380,9 @@ def test_rmsnorm_gemv_swiglu_fused(ctx, oracle, ffn, K):
 @pytest.mark.parametrize("nh,nkv,hd,max_seq,positions", [
     (8, 2, 32, 64, [0, 1, 63]),
     (32, 4, 64, 300, [0, 7, 299]),
+    # from position 512 on, the split (chunked) kernels: chunk edges 767/768
+    (32, 4, 64, 1300, [511, 512, 767, 768, 1299]),
+    (8, 2, 32, 600, [513, 599]),
 ])
 def test_attention_rope_fused(ctx, oracle, nh, nkv, hd, max_seq, positions):
     rng = np.random.default_rng(nh + hd + max_seq)
