@@ -757,17 +757,40 @@ __global__ __launch_bounds__(256) void k_attn_s1(
         gm = __hip_atomic_load(&cmax[(size_t)h * ATT_NCMAX + tid], __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     gm = block_max64<NT>(gm, red);
+    // 8 positions per thread per round, loads first, so that the exps and
+    // divisions of a thread are independent chains the core can interleave
+    constexpr int EB = 8;
     int64_t sum = 0;
-    for (int t = tid; t < S; t += NT) {
-        const int64_t sv = __hip_atomic_load(&sch[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int64_t e = q48_safe_exp((int64_t)((uint64_t)sv - (uint64_t)gm));
-        sch[t] = e;   // re-read below by this same thread
-        sum = (int64_t)((uint64_t)sum + (uint64_t)e);
+    for (int t0r = 0; t0r < S; t0r += NT * EB) {
+        int64_t sv[EB];
+#pragma unroll
+        for (int u = 0; u < EB; ++u)
+            sv[u] = __hip_atomic_load(&sch[min(t0r + tid + NT * u, S - 1)], __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int u = 0; u < EB; ++u) {
+            const int t = t0r + tid + NT * u;
+            if (t < S) {
+                const int64_t e = q48_safe_exp((int64_t)((uint64_t)sv[u] - (uint64_t)gm));
+                sch[t] = e;   // re-read below by this same thread
+                sum = (int64_t)((uint64_t)sum + (uint64_t)e);
+            }
+        }
     }
     sum = block_sum64<NT>(sum, red);
     if (sum > 0)
-        for (int t = tid; t < S; t += NT)
-            sch[t] = q48_div(sch[t], sum);
+        for (int t0r = 0; t0r < S; t0r += NT * EB) {
+            int64_t ev[EB];
+#pragma unroll
+            for (int u = 0; u < EB; ++u)
+                ev[u] = sch[min(t0r + tid + NT * u, S - 1)];
+#pragma unroll
+            for (int u = 0; u < EB; ++u) {
+                const int t = t0r + tid + NT * u;
+                if (t < S)
+                    sch[t] = q48_div(ev[u], sum);
+            }
+        }
     if (tid < HD)
         out[(size_t)h * HD + tid] = 0;
     if (tid == 0)
