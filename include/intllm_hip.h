@@ -73,6 +73,18 @@ int q48_gemv(q48_ctx *ctx, int64_t *y, const int64_t *W, const int64_t *x,
 int q48_gemm(q48_ctx *ctx, int64_t *Y, const int64_t *W, const int64_t *X,
              int T, int N, int K);
 
+/* q48_gemm with the kernel named: Q48_GEMM_VALU multiplies 32-bit limbs on
+ * the vector ALUs; Q48_GEMM_I8 splits both operands into int8 digits and
+ * multiplies them on the matrix cores (v_mfma_i32_32x32x32_i8); Q48_GEMM_AUTO
+ * is q48_gemm's choice.  All three give the same bits.  No reference
+ * counterpart: it exists so that callers and benchmarks can compare the two
+ * kernels on the same inputs. */
+#define Q48_GEMM_AUTO 0
+#define Q48_GEMM_VALU 1
+#define Q48_GEMM_I8   2
+int q48_gemm_ex(q48_ctx *ctx, int64_t *Y, const int64_t *W, const int64_t *X,
+                int T, int N, int K, int kernel);
+
 /* out = rmsnorm(x) * w.  Replaces rmsnorm (llama_int.c:1048-1058). */
 int q48_rmsnorm(q48_ctx *ctx, int64_t *out, const int64_t *x,
                 const int64_t *w, int dim);

@@ -343,17 +343,26 @@ int q48_prof_read(q48_ctx *c, q48_prof *out, int reset)
     return Q48_OK;
 }
 
-int q48_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int T, int N, int K)
+int q48_gemm_ex(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int T, int N,
+                int K, int kernel)
 {
     if (!c || !Y || !W || !X || T <= 0 || N <= 0 || K <= 0 || T > 65535 * 64 ||
-        N > kMaxDim || K > kMaxDim)
+        N > kMaxDim || K > kMaxDim || kernel < Q48_GEMM_AUTO || kernel > Q48_GEMM_I8)
         return Q48_EINVAL;
     if ((((uintptr_t)W | (uintptr_t)X | (uintptr_t)Y) & 7) != 0)
         return Q48_EINVAL;
-    int rc = q48_launch_gemm(c, Y, W, X, T, N, K);
+    if (kernel == Q48_GEMM_AUTO)
+        kernel = q48_gemm_auto_kernel(T, N, K);
+    int rc = kernel == Q48_GEMM_I8 ? q48_launch_gemm_i8(c, Y, W, X, T, N, K)
+                                   : q48_launch_gemm(c, Y, W, X, T, N, K);
     if (rc == Q48_ENOMEM)
         return rc;
     return launch_rc(rc);
+}
+
+int q48_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int T, int N, int K)
+{
+    return q48_gemm_ex(c, Y, W, X, T, N, K, Q48_GEMM_AUTO);
 }
 
 int q48_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *x, const int64_t *w, int dim)

@@ -1,0 +1,305 @@
+// q48_gemm.hip — token-batched Q16.48 GEMM on the int8 matrix cores (gfx950).
+//
+// Y[t][n] = (int64)((sum_k (int128)X[t][k] * W[n][k]) >> 48), per output
+// exactly matmul_vec (llama_int.c:1014-1046) applied to each token row.
+//
+// Digits.  Every int64 v is written v = S(v) + C with C = 0x0080808080808080
+// and S(v) = sum_i s_i 256^i, s_i the bytes of v ^ C read as int8 (bytes 0..6
+// are offset by 128, byte 7 is v's own signed top byte).  Then
+//   sum_k W X = sum_{a,b} 256^(a+b) P_ab + C sum_k W + C sum_k X - K C^2,
+//   P_ab = sum_k s_a(X_k) s_b(W_k),
+// an exact integer identity.  Only bits [48,112) of the sum are observable,
+// so the pair a = b = 7 (weight 2^112) is dropped and the remaining 63 int8
+// products are grouped by d = a + b into 14 int32 accumulators
+// Q_d = sum_{a+b=d} P_ab; |Q_d| <= 8 * 2^14 * K < 2^31 while K < 16384 per
+// accumulation run (longer K is split across blocks and summed in int128).
+//
+// Block: 4 waves, 64 tokens x 64 rows; wave w owns 32 tokens x 32 rows as 14
+// v_mfma_i32_32x32x32_i8 accumulators (224 registers).  Per k-step of 32
+// elements the block loads the int64 tiles, splits them into eight byte
+// planes in LDS (double-buffered), and every wave issues 63 MFMAs.
+#include "q48_internal.h"
+#include "../../include/intllm_hip.h"
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr uint64_t kDig = 0x0080808080808080ull;
+constexpr int MT = 64;             // tokens per block
+constexpr int MN = 64;             // rows per block
+constexpr int MK = 32;             // k per step (one MFMA's depth)
+constexpr int MAXK_RUN = 16352;    // k per accumulation run: |Q_d| < 2^31
+
+// byte planes of one stage: [limb][64 rows][32 bytes]
+constexpr int PLANE = MT * MK;     // 2048 B per limb
+constexpr int STAGE = 8 * PLANE;   // 16 KiB per operand
+
+// 4 x 4 byte transpose: out_j = [a_j, b_j, c_j, d_j] (v_perm_b32 selects
+// bytes 0-3 from its second operand and 4-7 from its first).
+__device__ __forceinline__ void tr4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                    uint32_t (&o)[4])
+{
+    const uint32_t t0 = __builtin_amdgcn_perm(b, a, 0x06020400u);   // a0 b0 a2 b2
+    const uint32_t t1 = __builtin_amdgcn_perm(b, a, 0x07030501u);   // a1 b1 a3 b3
+    const uint32_t t2 = __builtin_amdgcn_perm(d, c, 0x06020400u);   // c0 d0 c2 d2
+    const uint32_t t3 = __builtin_amdgcn_perm(d, c, 0x07030501u);   // c1 d1 c3 d3
+    o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    o[2] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+
+// Eight consecutive int64 of one row -> eight 8-byte digit words, limb a of
+// element e in byte e of word a, stored at plane a, row r, bytes [8q, 8q+8).
+__device__ __forceinline__ void split_store(uint8_t *stage, int r, int q,
+                                            const uint64_t (&v)[8])
+{
+    uint32_t l0[4], l1[4], h0[4], h1[4];
+    tr4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], l0);
+    tr4((uint32_t)v[4], (uint32_t)v[5], (uint32_t)v[6], (uint32_t)v[7], l1);
+    tr4((uint32_t)(v[0] >> 32), (uint32_t)(v[1] >> 32), (uint32_t)(v[2] >> 32),
+        (uint32_t)(v[3] >> 32), h0);
+    tr4((uint32_t)(v[4] >> 32), (uint32_t)(v[5] >> 32), (uint32_t)(v[6] >> 32),
+        (uint32_t)(v[7] >> 32), h1);
+    uint8_t *p = stage + r * MK + 8 * q;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+        *reinterpret_cast<uint2 *>(p + a * PLANE) =
+            make_uint2(l0[a] ^ 0x80808080u, l1[a] ^ 0x80808080u);
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+        *reinterpret_cast<uint2 *>(p + (4 + a) * PLANE) =
+            make_uint2(h0[a] ^ 0x80808080u, h1[a] ^ 0x80808080u);
+    *reinterpret_cast<uint2 *>(p + 7 * PLANE) = make_uint2(h0[3], h1[3]);
+}
+
+// Eight elements [k, k + 8) of a row; positions at or past kend read as C
+// (all digits zero, so they add nothing to any Q_d).
+template <bool VEC, bool TAIL>
+__device__ __forceinline__ void load8(uint64_t (&v)[8], const int64_t *row, int k, int kend)
+{
+    if (!TAIL && VEC) {
+        const ulonglong2 *p = reinterpret_cast<const ulonglong2 *>(row + k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const ulonglong2 u = p[e];
+            v[2 * e] = u.x;
+            v[2 * e + 1] = u.y;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            v[e] = (!TAIL || k + e < kend) ? (uint64_t)row[TAIL ? min(k + e, kend - 1) : k + e]
+                                           : kDig;
+    }
+}
+
+__device__ __forceinline__ void mfma_step(v16i (&acc)[14], const uint8_t *xs,
+                                          const uint8_t *ws, int lane)
+{
+    // lane l holds row l % 32 of its 32-row slice, bytes 16 (l / 32) .. +16
+    const int off = (lane & 31) * MK + 16 * (lane >> 5);
+    v4i A[8], B[8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        A[a] = *reinterpret_cast<const v4i *>(xs + a * PLANE + off);
+        B[a] = *reinterpret_cast<const v4i *>(ws + a * PLANE + off);
+    }
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+            if (a + b <= 13)
+                acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[a], B[b], acc[a + b], 0,
+                                                                   0, 0);
+}
+
+// grid (ceil(N/64), ceil(T/64), S): split z covers k-steps [z*spb, (z+1)*spb).
+// S == 1: Y gets the shifted result (with the digit corrections cw, cx);
+// S > 1: P[z][t][n] gets the int128 sum of Q_d 256^d (two uint64, lo first).
+template <bool VEC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__restrict__ W,
+          const int64_t *__restrict__ X, const uint64_t *__restrict__ cw,
+          const uint64_t *__restrict__ cx, int T, int N, int K, int spb)
+{
+    __shared__ __align__(16) uint8_t lds[2][2][STAGE];   // [stage][X, W]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n0 = blockIdx.x * MN, t0 = blockIdx.y * MT;
+    const int kbeg = blockIdx.z * spb * MK;
+    const int kend = max(kbeg, min(K, kbeg + spb * MK));
+    const int nfull = (kend - kbeg) / MK;
+    const bool tail = (kend - kbeg) % MK != 0;
+
+    // loader role: row r of both tiles, elements [8q, 8q + 8) of each step
+    const int r = tid >> 2, q = tid & 3;
+    const int64_t *xrow = X + (size_t)min(t0 + r, T - 1) * K;
+    const int64_t *wrow = W + (size_t)min(n0 + r, N - 1) * K;
+
+    v16i acc[14];
+#pragma unroll
+    for (int d = 0; d < 14; ++d)
+        acc[d] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+    const int wt = w >> 1, wn = w & 1;   // wave's token half, row half
+    uint64_t gx[8], gw[8];
+    if (nfull > 0) {
+        load8<VEC, false>(gx, xrow, kbeg + 8 * q, kend);
+        load8<VEC, false>(gw, wrow, kbeg + 8 * q, kend);
+        split_store(lds[0][0], r, q, gx);
+        split_store(lds[0][1], r, q, gw);
+    }
+    __syncthreads();
+    for (int s = 0; s < nfull; ++s) {
+        // next step's tiles (the last step re-reads its own: in bounds, unused)
+        const int kn = kbeg + min(s + 1, nfull - 1) * MK + 8 * q;
+        load8<VEC, false>(gx, xrow, kn, kend);
+        load8<VEC, false>(gw, wrow, kn, kend);
+        const uint8_t *st = &lds[s & 1][0][0];
+        mfma_step(acc, st + wt * 32 * MK, st + STAGE + wn * 32 * MK, lane);
+        split_store(lds[(s + 1) & 1][0], r, q, gx);
+        split_store(lds[(s + 1) & 1][1], r, q, gw);
+        __syncthreads();
+    }
+    if (tail) {
+        const int kt = kbeg + nfull * MK + 8 * q;
+        load8<VEC, true>(gx, xrow, kt, kend);
+        load8<VEC, true>(gw, wrow, kt, kend);
+        split_store(lds[nfull & 1][0], r, q, gx);
+        split_store(lds[nfull & 1][1], r, q, gw);
+        __syncthreads();
+        const uint8_t *st = &lds[nfull & 1][0][0];
+        mfma_step(acc, st + wt * 32 * MK, st + STAGE + wn * 32 * MK, lane);
+    }
+
+    // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32
+    const int n = n0 + 32 * wn + (lane & 31);
+    if (n >= N)
+        return;
+    q48_u128 cwn = 0;
+    if (gridDim.z == 1)
+        cwn = ((q48_u128)cw[2 * n + 1] << 64) | cw[2 * n];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int t = t0 + 32 * wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (t >= T)
+            continue;
+        q48_u128 tot = 0;
+#pragma unroll
+        for (int d = 13; d >= 0; --d)
+            tot = (tot << 8) + (q48_u128)(q48_i128)acc[d][i];
+        if (gridDim.z == 1) {
+            tot += cwn + (((q48_u128)cx[2 * t + 1] << 64) | cx[2 * t]);
+            Y[(size_t)t * N + n] = (int64_t)((q48_i128)tot >> 48);
+        } else {
+            uint64_t *p = P + 2 * (((size_t)blockIdx.z * T + t) * N + n);
+            *reinterpret_cast<ulonglong2 *>(p) = make_ulonglong2((uint64_t)tot,
+                                                                 (uint64_t)(tot >> 64));
+        }
+    }
+}
+
+// Y[t][n] = (sum_z P[z][t][n] + cw[n] + cx[t]) >> 48
+__global__ __launch_bounds__(256) void k_gemm_i8_reduce(int64_t *__restrict__ Y,
+                                                       const uint64_t *__restrict__ P,
+                                                       const uint64_t *__restrict__ cw,
+                                                       const uint64_t *__restrict__ cx,
+                                                       int T, int N, int S)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)T * N)
+        return;
+    const int t = (int)(i / N), n = (int)(i % N);
+    q48_u128 tot = (((q48_u128)cw[2 * n + 1] << 64) | cw[2 * n]) +
+                   (((q48_u128)cx[2 * t + 1] << 64) | cx[2 * t]);
+    for (int z = 0; z < S; ++z) {
+        const ulonglong2 u =
+            *reinterpret_cast<const ulonglong2 *>(P + 2 * ((size_t)z * T * N + i));
+        tot += ((q48_u128)u.y << 64) | u.x;
+    }
+    Y[i] = (int64_t)((q48_i128)tot >> 48);
+}
+
+// out[row] = C * sum_k A[row][k] (exact int128, mod 2^128), minus K C^2 when
+// sub_kc2: the digit corrections of the identity above.  One wave per row.
+__global__ __launch_bounds__(256) void k_digit_corr(uint64_t *__restrict__ out,
+                                                   const int64_t *__restrict__ A, int rows,
+                                                   int K, int sub_kc2)
+{
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows)
+        return;
+    const int64_t *p = A + (size_t)row * K;
+    q48_i128 s = 0;
+    for (int k = lane; k < K; k += 64)
+        s += p[k];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint64_t lo = (uint64_t)s, hi = (uint64_t)((q48_u128)s >> 64);
+        s += (q48_i128)(((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64));
+    }
+    if (lane == 0) {
+        q48_u128 v = (q48_u128)s * kDig;
+        if (sub_kc2)
+            v -= (q48_u128)kDig * kDig * (q48_u128)(uint64_t)K;
+        out[2 * row] = (uint64_t)v;
+        out[2 * row + 1] = (uint64_t)(v >> 64);
+    }
+}
+
+} // namespace
+
+int q48_gemm_auto_kernel(int T, int N, int K)
+{
+    (void)N;
+    (void)K;
+    return T >= 8 ? Q48_GEMM_I8 : Q48_GEMM_VALU;
+}
+
+int q48_gemm_i8_splits(int T, int N, int K, int cu_count)
+{
+    const int base = ((N + MN - 1) / MN) * ((T + MT - 1) / MT);
+    const int steps = (K + MK - 1) / MK;
+    const int min_s = (steps + MAXK_RUN / MK - 1) / (MAXK_RUN / MK);
+    int s = 1;
+    // split K while the grid is under one block per compute unit and every
+    // split keeps at least 8 steps
+    while (base * s < cu_count && steps / (2 * s) >= 8)
+        s *= 2;
+    return s > min_s ? s : min_s;
+}
+
+int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int T,
+                       int N, int K)
+{
+    const int S = q48_gemm_i8_splits(T, N, K, c->cu_count);
+    const int steps = (K + MK - 1) / MK;
+    const int spb = (steps + S - 1) / S;
+    const size_t corr = 16 * ((size_t)N + (size_t)T);
+    const size_t part = S > 1 ? 16 * (size_t)S * T * N : 0;
+    int rc = q48_ws_reserve(c, corr + part);
+    if (rc)
+        return rc;
+    uint64_t *cw = (uint64_t *)c->ws;
+    uint64_t *cx = cw + 2 * (size_t)N;
+    uint64_t *P = S > 1 ? cx + 2 * (size_t)T : nullptr;
+    hipLaunchKernelGGL(k_digit_corr, dim3((N + 3) / 4), dim3(256), 0, c->stream, cw, W, N, K, 1);
+    hipLaunchKernelGGL(k_digit_corr, dim3((T + 3) / 4), dim3(256), 0, c->stream, cx, X, T, K, 0);
+    const dim3 grid((N + MN - 1) / MN, (T + MT - 1) / MT, S);
+    const bool vec = K % 2 == 0 && (((uintptr_t)W | (uintptr_t)X) & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL((k_gemm_i8<true>), grid, dim3(256), 0, c->stream, Y, P, W, X, cw, cx,
+                           T, N, K, spb);
+    else
+        hipLaunchKernelGGL((k_gemm_i8<false>), grid, dim3(256), 0, c->stream, Y, P, W, X, cw,
+                           cx, T, N, K, spb);
+    if (S > 1) {
+        const size_t tn = (size_t)T * N;
+        hipLaunchKernelGGL(k_gemm_i8_reduce, dim3((unsigned)((tn + 255) / 256)), dim3(256), 0,
+                           c->stream, Y, P, cw, cx, T, N, S);
+    }
+    return (int)hipGetLastError();
+}

@@ -26,6 +26,9 @@ Q48_OK, Q48_EINVAL, Q48_ENOMEM, Q48_EHIP, Q48_ERANGE, Q48_ESTATE = 0, -1, -2, -3
 FP_MUL, FP_DIV, FP_SQRT, FP_SQRT_FAST, FP_INV_SQRT, FP_EXP, FP_LOG, FP_SINCOS, \
     FP_SIGMOID, FP_SILU, FP_SAFE_EXP, FP_EXP_DYADIC = range(12)
 
+# q48_gemm_ex kernels (include/intllm_hip.h)
+GEMM_AUTO, GEMM_VALU, GEMM_I8 = 0, 1, 2
+
 # ABI entry points and their argument types (include/intllm_hip.h)
 _P, _I, _SZ = C.c_void_p, C.c_int, C.c_size_t
 ABI_SIGNATURES = {
@@ -40,6 +43,7 @@ ABI_SIGNATURES = {
     "q48_sync": [_P],
     "q48_gemv": [_P, _P, _P, _P, _I, _I],
     "q48_gemm": [_P, _P, _P, _P, _I, _I, _I],
+    "q48_gemm_ex": [_P, _P, _P, _P, _I, _I, _I, _I],
     "q48_rmsnorm": [_P, _P, _P, _P, _I],
     "q48_rope_init": [_P, _I, _I, _I],
     "q48_rope": [_P, _P, _I, _I, _I],
@@ -213,8 +217,11 @@ class Context:
     def gemv(self, y, W, x, M, K):
         return check("q48_gemv", hip_lib().q48_gemv(self.h, y, W, x, M, K))
 
-    def gemm(self, Y, W, X, T, N, K):
-        return check("q48_gemm", hip_lib().q48_gemm(self.h, Y, W, X, T, N, K))
+    def gemm(self, Y, W, X, T, N, K, kernel=None):
+        """kernel: None (q48_gemm's choice), GEMM_VALU or GEMM_I8."""
+        if kernel is None:
+            return check("q48_gemm", hip_lib().q48_gemm(self.h, Y, W, X, T, N, K))
+        return check("q48_gemm_ex", hip_lib().q48_gemm_ex(self.h, Y, W, X, T, N, K, kernel))
 
     def rmsnorm(self, out, x, w, dim):
         return check("q48_rmsnorm", hip_lib().q48_rmsnorm(self.h, out, x, w, dim))

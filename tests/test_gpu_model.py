@@ -157,15 +157,17 @@ def test_long_context_graph_decode_bit_exact(ctx):
         m.free()
 
 
+@pytest.mark.parametrize("kernel", [pytest.param(intllm.GEMM_VALU, id="valu"),
+                                    pytest.param(intllm.GEMM_I8, id="i8")])
 @pytest.mark.parametrize("T", spec.GEMM_TOKENS)
-def test_gemm_config4_vs_reference(ctx, T):
+def test_gemm_config4_vs_reference(ctx, T, kernel):
     g = golden("gemm.json")["shapes"]
     for (N, K) in spec.GEMV_SHAPES:
         W = O.synth(spec.gemv_w_name(N, K), N, K, spec.SEED_GEMV, spec.SIGMA_W, 1)
         X = O.synth(spec.gemm_x_name(T, K), T, K, spec.SEED_GEMV, spec.SIGMA_ACT, 0)
         dW, dX, dY = ctx.to_device(W), ctx.to_device(X), ctx.buffer(T * N)
-        say("gemm config4", T, N, K)
-        ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K)
+        say("gemm config4", T, N, K, "kernel", kernel)
+        ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K, kernel)
         assert O.fnv(dY.download()) == g[f"{T}x{N}x{K}"]["fnv"], (T, N, K)
         for b in (dW, dX, dY):
             b.free()

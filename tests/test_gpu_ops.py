@@ -162,20 +162,57 @@ def test_gemv_random_vs_oracle(ctx, M, K):
         assert np.array_equal(gemv_dev(ctx, W, x, M, K, off), want), (M, K, off)
 
 
+GEMM_KERNELS = [pytest.param(intllm.GEMM_VALU, id="valu"), pytest.param(intllm.GEMM_I8, id="i8")]
+
+
+@pytest.mark.parametrize("kernel", GEMM_KERNELS)
 @pytest.mark.parametrize("T,N,K", [(1, 1, 1), (3, 5, 7), (64, 64, 16), (65, 70, 33),
-                                   (130, 129, 688), (128, 256, 2048)])
-def test_gemm_random_vs_oracle(ctx, oracle, T, N, K):
+                                   (130, 129, 688), (128, 256, 2048), (64, 64, 8192),
+                                   (70, 33, 1031), (200, 96, 96), (3, 5, 20000)])
+def test_gemm_random_vs_oracle(ctx, oracle, T, N, K, kernel):
+    """Full-range int64 operands.  The cases cover partial tiles, a k tail
+    (K not a multiple of 32), odd K (8-byte loads), K split across blocks
+    (64x64x8192: one tile, many splits) and K past one int32 accumulation
+    run of the int8 kernel (20000)."""
     rng = np.random.default_rng(T * 31 + N * 7 + K)
     W = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=N * K, dtype=np.int64)
     X = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=T * K, dtype=np.int64)
     want = np.empty(T * N, dtype=np.int64)
     oracle.q48o_gemm(want.ctypes.data, W.ctypes.data, X.ctypes.data, T, N, K)
     dW, dX, dY = ctx.to_device(W), ctx.to_device(X), ctx.buffer(T * N)
-    say("gemm", T, N, K)
-    ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K)
+    say("gemm", T, N, K, "kernel", kernel)
+    ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K, kernel)
     assert np.array_equal(dY.download(), want)
     for b in (dW, dX, dY):
         b.free()
+
+
+@pytest.mark.parametrize("kernel", GEMM_KERNELS)
+def test_gemm_extreme_digits(ctx, oracle, kernel):
+    """INT64_MIN has every int8 digit at -128 (the largest digit products);
+    with K = 16352 + 8 one block accumulates the longest int32 run the int8
+    kernel allows, then more.  Mixed INT64_MIN / INT64_MAX / 0 / -1 / C
+    operands exercise the digit offsets, and the unaligned views (one
+    element in) the 8-byte load path."""
+    T, N, K = 40, 36, 16360
+    rng = np.random.default_rng(11)
+    pool = np.array([spec.INT64_MIN, spec.INT64_MAX, 0, -1, 0x0080808080808080], dtype=np.int64)
+    for name, W, X in (
+        ("all-min", np.full(N * K, spec.INT64_MIN, np.int64), np.full(T * K, spec.INT64_MIN, np.int64)),
+        ("mixed", pool[rng.integers(0, 5, N * K)], pool[rng.integers(0, 5, T * K)]),
+    ):
+        want = np.empty(T * N, dtype=np.int64)
+        oracle.q48o_gemm(want.ctypes.data, W.ctypes.data, X.ctypes.data, T, N, K)
+        for off in (0, 1):
+            pad = np.zeros(off, dtype=np.int64)
+            dW = ctx.to_device(np.concatenate([pad, W]))
+            dX = ctx.to_device(np.concatenate([pad, X]))
+            dY = ctx.buffer(T * N + off)
+            say("gemm extreme", name, "offset", off, "kernel", kernel)
+            ctx.gemm(dY.at(off), dW.at(off), dX.at(off), T, N, K, kernel)
+            assert np.array_equal(dY.download()[off:], want), (name, off)
+            for b in (dW, dX, dY):
+                b.free()
 
 
 def test_rmsnorm(ctx, oracle):
