@@ -76,7 +76,8 @@ int q48_gemm(q48_ctx *ctx, int64_t *Y, const int64_t *W, const int64_t *X,
 /* q48_gemm with the kernel named: Q48_GEMM_VALU multiplies 32-bit limbs on
  * the vector ALUs; Q48_GEMM_I8 splits both operands into int8 digits and
  * multiplies them on the matrix cores (v_mfma_i32_32x32x32_i8); Q48_GEMM_AUTO
- * is q48_gemm's choice.  All three give the same bits.  No reference
+ * is q48_gemm's choice (the decode GEMV for T = 1, else Q48_GEMM_I8).  All
+ * give the same bits.  No reference
  * counterpart: it exists so that callers and benchmarks can compare the two
  * kernels on the same inputs. */
 #define Q48_GEMM_AUTO 0

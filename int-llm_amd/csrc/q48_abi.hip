@@ -351,10 +351,13 @@ int q48_gemm_ex(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int 
         return Q48_EINVAL;
     if ((((uintptr_t)W | (uintptr_t)X | (uintptr_t)Y) & 7) != 0)
         return Q48_EINVAL;
-    if (kernel == Q48_GEMM_AUTO)
-        kernel = q48_gemm_auto_kernel(T, N, K);
-    int rc = kernel == Q48_GEMM_I8 ? q48_launch_gemm_i8(c, Y, W, X, T, N, K)
-                                   : q48_launch_gemm(c, Y, W, X, T, N, K);
+    int rc;
+    if (kernel == Q48_GEMM_AUTO && T == 1)
+        rc = q48_launch_gemv(c, Y, W, X, N, K);   // one token: the decode GEMV
+    else if ((kernel == Q48_GEMM_AUTO ? q48_gemm_auto_kernel(T, N, K) : kernel) == Q48_GEMM_I8)
+        rc = q48_launch_gemm_i8(c, Y, W, X, T, N, K);
+    else
+        rc = q48_launch_gemm(c, Y, W, X, T, N, K);
     if (rc == Q48_ENOMEM)
         return rc;
     return launch_rc(rc);

