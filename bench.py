@@ -38,6 +38,15 @@ HBM_PEAK_GBS = 8000.0
 # size (profiles/k_gemv_v5_decode_tinyllama.md); re-measure when the kernel changes
 TRAFFIC = 93553554
 REF_CPU_MS_PER_TOK = 501.4   # reference decode, Zen 4, 1 thread
+# int8 GEMM: MI355X dense int8 MFMA peak; one Q16.48 MAC is 63 int8 products
+# (digit pairs a + b <= 13), 2 ops each
+I8_PEAK_OPS = 5.0e15
+I8_OPS_PER_MAC = 126
+# VALU GEMM: one Q16.48 MAC is four v_mad_u64_u32 (32 x 32 -> 64-bit limb
+# products); their rate on MI355X, measured with 16 independent chains per
+# lane and 16 waves per compute unit: 17.2e12 lane-ops/s (28 per clock per CU)
+VALU_MAD_PEAK = 17.2e12
+VALU_MADS_PER_MAC = 4
 
 
 def log(*a):
@@ -52,16 +61,14 @@ def gemv_shapes(ctx, spec, intllm, reps: int):
     """GB/s of q48_gemv per config-2 shape, rotating over distinct weight
     buffers totalling > 2 GiB so the 256 MB MALL cannot serve them; launches
     back to back between two HIP events on the library's stream."""
-    import numpy as np
-    import oracle_lib as O
     out = {}
     gold = json.loads((ROOT / "tests" / "golden" / "gemv.json").read_text())["shapes"]
     pool_bytes = 2_600_000_000
     pool = ctx.buffer(pool_bytes // 8)
     for (M, K) in spec.GEMV_SHAPES + spec.GEMV_FUSED:
-        W, x = spec.gemv_inputs_ref(O.synth, M, K) if (M, K) in spec.GEMV_SHAPES else (
-            O.synth(spec.gemv_w_name(M, K), M, K, spec.SEED_GEMV, spec.SIGMA_W, 1),
-            O.synth(spec.gemv_x_name(K), 1, K, spec.SEED_GEMV, spec.SIGMA_ACT, 0))
+        W, x = spec.gemv_inputs_ref(intllm.synth, M, K) if (M, K) in spec.GEMV_SHAPES else (
+            intllm.synth(spec.gemv_w_name(M, K), M, K, spec.SEED_GEMV, spec.SIGMA_W, 1),
+            intllm.synth(spec.gemv_x_name(K), 1, K, spec.SEED_GEMV, spec.SIGMA_ACT, 0))
         per = M * K + 64
         nbuf = max(1, min(64, (pool.n - 4096) // per))
         pool.upload(W)
@@ -80,7 +87,7 @@ def gemv_shapes(ctx, spec, intllm, reps: int):
         # result check against the committed golden vector for the real shapes
         ok = None
         if f"{M}x{K}" in gold:
-            ok = O.fnv(dy.download()) == gold[f"{M}x{K}"]["fnv"]
+            ok = intllm.fnv(dy.download()) == gold[f"{M}x{K}"]["fnv"]
         us = 1e3 * ms / n
         out[f"{M}x{K}"] = {"us": round(us, 2),
                            "GB_s": round(8.0 * (M * K + K + M) / (us * 1e-6) / 1e9, 1),
@@ -90,6 +97,50 @@ def gemv_shapes(ctx, spec, intllm, reps: int):
         log("gemv", M, K, out[f"{M}x{K}"])
     pool.free()
     return out
+
+
+def gemm_prefill(ctx, spec, intllm, reps: int):
+    """Config 4: q48_gemm at T in {128, 512, 2048} tokens on the config-2
+    shapes, with both kernels (int8 digits on the matrix cores, 32-bit limbs
+    on the vector ALUs).  Each output is hashed against the golden vector of
+    the reference's per-token matmul_vec; times are whole q48_gemm calls
+    (digit corrections and split-K reduction included) between two HIP
+    events on the library's stream."""
+    gold = json.loads((ROOT / "tests" / "golden" / "gemm.json").read_text())["shapes"]
+    out = {}
+    for (N, K) in spec.GEMV_SHAPES:
+        dW = ctx.to_device(intllm.synth(spec.gemv_w_name(N, K), N, K, spec.SEED_GEMV,
+                                        spec.SIGMA_W, 1, threads()))
+        for T in spec.GEMM_TOKENS:
+            dX = ctx.to_device(intllm.synth(spec.gemm_x_name(T, K), T, K, spec.SEED_GEMV,
+                                            spec.SIGMA_ACT, 0, threads()))
+            dY = ctx.buffer(T * N)
+            key = f"{T}x{N}x{K}"
+            macs = T * N * K
+            rec = {}
+            for name, kern, n in (("i8", intllm.GEMM_I8, reps), ("valu", intllm.GEMM_VALU, 1)):
+                ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K, kern)
+                rec[f"{name}_bit_exact"] = intllm.fnv(dY.download()) == gold[key]["fnv"]
+                ctx.timer_start()
+                for _ in range(n):
+                    ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K, kern)
+                us = 1e3 * ctx.timer_stop() / n
+                rec[f"{name}_us"] = round(us, 1)
+                rec[f"{name}_TMAC_s"] = round(macs / (us * 1e-6) / 1e12, 3)
+            rec["i8_frac"] = round(I8_OPS_PER_MAC * macs / (rec["i8_us"] * 1e-6) / I8_PEAK_OPS, 4)
+            rec["valu_frac"] = round(VALU_MADS_PER_MAC * macs / (rec["valu_us"] * 1e-6)
+                                     / VALU_MAD_PEAK, 4)
+            rec["speedup_i8_vs_valu"] = round(rec["valu_us"] / rec["i8_us"], 1)
+            out[key] = rec
+            log("gemm", key, rec)
+            dX.free()
+            dY.free()
+        dW.free()
+    return {"workload": "config 4: Q16.48 GEMM, T tokens x config-2 (N, K), W N(0,0.02) "
+                        "bf16-exact, X N(0,1) raw Q16.48",
+            "i8_peak_ops": I8_PEAK_OPS, "i8_ops_per_mac": I8_OPS_PER_MAC,
+            "valu_mad_peak": VALU_MAD_PEAK, "valu_mads_per_mac": VALU_MADS_PER_MAC,
+            "shapes": out}
 
 
 def cpu_baseline(spec, seconds: float, prompt):
@@ -163,6 +214,10 @@ def main():
                     help="config-5 (2048-position cache) decode steps timed; 0 skips")
     ap.add_argument("--gemv-reps", type=int, default=8,
                     help="decode-token GEMV sequences timed back to back for the roofline")
+    ap.add_argument("--gemm-reps", type=int, default=5,
+                    help="int8 GEMM calls timed per config-4 shape; 0 skips config 4")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="run only the config-4 GEMM measurement (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the Q16.48 decode path is "
@@ -171,6 +226,13 @@ def main():
 
     import intllm
     import spec
+
+    if args.gemm_only:
+        ctx = intllm.Context(0)
+        print(json.dumps({"gemm": gemm_prefill(ctx, spec, intllm, max(1, args.gemm_reps))}),
+              flush=True)
+        ctx.close()
+        return
 
     gold = json.loads((ROOT / "tests" / "golden" / "tinyllama_generate.json").read_text())
     gold_long = json.loads((ROOT / "tests" / "golden" / "longctx_decode.json").read_text())
@@ -256,6 +318,7 @@ def main():
     m.free()
 
     shapes = None if args.no_shapes else gemv_shapes(ctx, spec, intllm, reps=64)
+    gemm = gemm_prefill(ctx, spec, intllm, args.gemm_reps) if args.gemm_reps > 0 else None
     ctx.close()
 
     cpu = None if args.no_cpu else cpu_baseline(spec, args.cpu_seconds, prompt)
@@ -288,6 +351,7 @@ def main():
                      "launches_timed": launches},
         "cpu_baseline": cpu,
         "gemv_shapes": shapes,
+        "gemm_prefill": gemm,
         "long_context": longctx,
         "parity": parity,
     }

@@ -388,7 +388,27 @@ HOST_SIGNATURES = {
     "q48h_model_set_prefetch": ([_P, _I], None),
     "q48h_gemv_sweep": ([_P, _I, C.POINTER(C.c_int), C.POINTER(C.c_double)], C.c_int),
     "q48h_decode_graph": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
+    "q48s_fill_named": ([_P, C.c_int64, C.c_int64, C.c_uint64, C.c_char_p, C.c_int64, _I, _I],
+                        None),
+    "q48s_fnv_i64": ([C.c_uint64, _P, C.c_size_t], C.c_uint64),
 }
+
+FNV_OFFSET = 1469598103934665603
+
+
+def synth(name: str, rows: int, cols: int, seed: int, sigma: int, bf16: int,
+          threads: int = 8) -> np.ndarray:
+    """The host library's synthetic tensor `name` (q48_synth.h), flattened."""
+    a = np.empty(rows * cols, dtype=np.int64)
+    host_lib().q48s_fill_named(a.ctypes.data, rows, cols, seed, name.encode(), sigma, bf16,
+                               threads)
+    return a
+
+
+def fnv(arr) -> str:
+    """FNV-1a-64 of an int64 array (the hash the golden vectors record)."""
+    a = np.ascontiguousarray(arr, dtype=np.int64)
+    return "%016x" % host_lib().q48s_fnv_i64(FNV_OFFSET, a.ctypes.data, a.size)
 
 
 def host_lib() -> C.CDLL:
