@@ -139,7 +139,22 @@ __device__ __forceinline__ void mfma_step(v16i (&acc)[14], const uint8_t *xs,
     }
 }
 
-// grid (ceil(N/64), ceil(T/64), S): split z covers k-steps [z*spb, (z+1)*spb).
+// Tile of block b in a grid of nn row tiles x nt token tiles.  Blocks go
+// round-robin to the 8 XCDs (each with its own L2), so b is first renumbered
+// to give every XCD a contiguous range, and that range is walked in groups of
+// GROUP row tiles: a group's W tiles stay in cache while its token tiles pass.
+constexpr int GROUP = 8;
+__device__ __forceinline__ void tile_of(int b, int nn, int nt, int &n_tile, int &t_tile)
+{
+    const int total = nn * nt, q = total / 8, r = total % 8, x = b % 8, l = b / 8;
+    const int pid = x < r ? x * (q + 1) + l : r * (q + 1) + (x - r) * q + l;
+    const int per = GROUP * nt, g = pid / per, first = g * GROUP;
+    const int gs = min(nn - first, GROUP), in = pid - g * per;
+    n_tile = first + in % gs;
+    t_tile = in / gs;
+}
+
+// grid (ceil(N/64) * ceil(T/64), 1, S): split z covers k-steps [z*spb, (z+1)*spb).
 // S == 1: Y gets the shifted result (with the digit corrections cw, cx);
 // S > 1: P[z][t][n] gets the int128 sum of Q_d 256^d (two uint64, lo first).
 template <bool VEC>
@@ -150,7 +165,9 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
 {
     __shared__ __align__(16) uint8_t lds[2][2][STAGE];   // [stage][X, W]
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int n0 = blockIdx.x * MN, t0 = blockIdx.y * MT;
+    int n_tile, t_tile;
+    tile_of(blockIdx.x, (N + MN - 1) / MN, (T + MT - 1) / MT, n_tile, t_tile);
+    const int n0 = n_tile * MN, t0 = t_tile * MT;
     const int kbeg = blockIdx.z * spb * MK;
     const int kend = max(kbeg, min(K, kbeg + spb * MK));
     const int nfull = (kend - kbeg) / MK;
@@ -356,7 +373,7 @@ int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *
     uint64_t *P = S > 1 ? cx + 2 * (size_t)T : nullptr;
     hipLaunchKernelGGL(k_digit_corr, dim3((N + 3) / 4), dim3(256), 0, c->stream, cw, W, N, K, 1);
     hipLaunchKernelGGL(k_digit_corr, dim3((T + 3) / 4), dim3(256), 0, c->stream, cx, X, T, K, 0);
-    const dim3 grid((N + MN - 1) / MN, (T + MT - 1) / MT, S);
+    const dim3 grid(((N + MN - 1) / MN) * ((T + MT - 1) / MT), 1, S);
     const bool vec = K % 2 == 0 && (((uintptr_t)W | (uintptr_t)X) & 15) == 0;
     if (vec)
         hipLaunchKernelGGL((k_gemm_i8<true>), grid, dim3(256), 0, c->stream, Y, P, W, X, cw, cx,
