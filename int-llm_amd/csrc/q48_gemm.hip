@@ -6,9 +6,11 @@
 // Digits.  Every int64 v is written v = S(v) + C with C = 0x0080808080808080
 // and S(v) = sum_i s_i 256^i, s_i the bytes of v ^ C read as int8 (bytes 0..6
 // are offset by 128, byte 7 is v's own signed top byte).  Then
-//   sum_k W X = sum_{a,b} 256^(a+b) P_ab + C sum_k W + C sum_k X - K C^2,
+//   sum_k W X = sum_{a,b} 256^(a+b) P_ab + C sum_k S(W) + C sum_k S(X) + K C^2,
 //   P_ab = sum_k s_a(X_k) s_b(W_k),
-// an exact integer identity.  Only bits [48,112) of the sum are observable,
+// an exact integer identity over any k range; sum_k S(v) is the digit sums
+// sum_a 256^a sum_k s_a(v_k), counted with v_dot4_i32_i8 while the tiles are
+// split, so W and X are read once.  Only bits [48,112) are observable,
 // so the pair a = b = 7 (weight 2^112) is dropped and the remaining 63 int8
 // products are grouped by d = a + b into 14 int32 accumulators
 // Q_d = sum_{a+b=d} P_ab; |Q_d| <= 8 * 2^14 * K < 2^31 while K < 16384 per
@@ -33,6 +35,7 @@ constexpr int MT = 64;             // tokens per block
 constexpr int MN = 64;             // rows per block
 constexpr int MK = 32;             // k per step: one MFMA depth
 constexpr int MAXK_RUN = 16320;    // k per accumulation run: |Q_d| < 2^31
+constexpr int FUSE_BELOW_T = 1024; // token counts that count digit sums in the GEMM
 constexpr int NPAIR = MK / 32;     // (row, 8 elements) pieces per thread per operand
 constexpr int CH = MK / 16;        // 16-byte k chunks per row and limb
 
@@ -73,8 +76,11 @@ __device__ __forceinline__ Piece piece(int p)
 }
 
 // Eight consecutive int64 of one row -> eight 8-byte digit words, limb a of
-// element e in byte e of word a, stored at plane a.
-__device__ __forceinline__ void split_store(uint8_t *stage, int off, const uint64_t (&v)[8])
+// element e in byte e of word a, stored at plane a.  sum[a] += ones-weighted
+// sum of the eight limb-a digits (v_dot4_i32_i8; ones = 0x01010101 or 0).
+template <bool FUSE>
+__device__ __forceinline__ void split_store(uint8_t *stage, int off, const uint64_t (&v)[8],
+                                            int (&sum)[8], int ones)
 {
     uint32_t l0[4], l1[4], h0[4], h1[4];
     tr4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], l0);
@@ -84,15 +90,22 @@ __device__ __forceinline__ void split_store(uint8_t *stage, int off, const uint6
     tr4((uint32_t)(v[4] >> 32), (uint32_t)(v[5] >> 32), (uint32_t)(v[6] >> 32),
         (uint32_t)(v[7] >> 32), h1);
     uint8_t *p = stage + off;
+    uint2 d[8];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
-        *reinterpret_cast<uint2 *>(p + a * PLANE) =
-            make_uint2(l0[a] ^ 0x80808080u, l1[a] ^ 0x80808080u);
+        d[a] = make_uint2(l0[a] ^ 0x80808080u, l1[a] ^ 0x80808080u);
 #pragma unroll
     for (int a = 0; a < 3; ++a)
-        *reinterpret_cast<uint2 *>(p + (4 + a) * PLANE) =
-            make_uint2(h0[a] ^ 0x80808080u, h1[a] ^ 0x80808080u);
-    *reinterpret_cast<uint2 *>(p + 7 * PLANE) = make_uint2(h0[3], h1[3]);
+        d[4 + a] = make_uint2(h0[a] ^ 0x80808080u, h1[a] ^ 0x80808080u);
+    d[7] = make_uint2(h0[3], h1[3]);
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        *reinterpret_cast<uint2 *>(p + a * PLANE) = d[a];
+        if (FUSE) {
+            sum[a] = __builtin_amdgcn_sdot4((int)d[a].x, ones, sum[a], false);
+            sum[a] = __builtin_amdgcn_sdot4((int)d[a].y, ones, sum[a], false);
+        }
+    }
 }
 
 // Eight elements [k, k + 8) of a row; positions at or past kend read as C
@@ -155,15 +168,21 @@ __device__ __forceinline__ void tile_of(int b, int nn, int nt, int &n_tile, int 
 }
 
 // grid (ceil(N/64) * ceil(T/64), 1, S): split z covers k-steps [z*spb, (z+1)*spb).
-// S == 1: Y gets the shifted result (with the digit corrections cw, cx);
-// S > 1: P[z][t][n] gets the int128 sum of Q_d 256^d (two uint64, lo first).
-template <bool VEC>
+// FUSE: every block adds the digit corrections of its own k range (the digit
+// sums of its rows, counted while splitting them, and its length times C^2).
+// Otherwise cw[n] = C sum_k W - K C^2 and cx[t] = C sum_k X come from
+// k_digit_corr and are added once: here when S == 1, else by the reduction.
+// S == 1: Y gets the shifted result;
+// S > 1: P[z][t][n] gets the block's int128 partial sum (two uint64, lo first).
+template <bool VEC, bool FUSE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__restrict__ W,
           const int64_t *__restrict__ X, const uint64_t *__restrict__ cw,
           const uint64_t *__restrict__ cx, int T, int N, int K, int spb)
 {
     __shared__ __align__(16) uint8_t lds[2][2][STAGE];   // [stage][X, W]
+    __shared__ int dsum[2][64][8];                        // [X, W][row][limb] digit sums
+    __shared__ q48_u128 corr[2][64];                      // [X, W][row] corrections
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     int n_tile, t_tile;
     tile_of(blockIdx.x, (N + MN - 1) / MN, (T + MT - 1) / MT, n_tile, t_tile);
@@ -187,6 +206,15 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
 #pragma unroll
     for (int d = 0; d < 14; ++d)
         acc[d] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = tid; i < 2 * 64 * 8; i += 256)
+        (&dsum[0][0][0])[i] = 0;
+    int sx[NPAIR][8], sw[NPAIR][8];
+#pragma unroll
+    for (int j = 0; j < NPAIR; ++j)
+#pragma unroll
+        for (int a = 0; a < 8; ++a)
+            sx[j][a] = sw[j][a] = 0;
+    constexpr int ONES = 0x01010101;
 
     const int wt = w >> 1, wn = w & 1;   // wave's token slice, row slice
     typedef uint64_t Regs[NPAIR][8];
@@ -197,11 +225,11 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
             load8<VEC, false>(gw[j], wrow[j], k, kend);
         }
     };
-    auto store = [&](int st, const Regs &gx, const Regs &gw) {
+    auto store = [&](int st, const Regs &gx, const Regs &gw, int ones) {
 #pragma unroll
         for (int j = 0; j < NPAIR; ++j) {
-            split_store(lds[st][0], pc[j].off, gx[j]);
-            split_store(lds[st][1], pc[j].off, gw[j]);
+            split_store<FUSE>(lds[st][0], pc[j].off, gx[j], sx[j], ones);
+            split_store<FUSE>(lds[st][1], pc[j].off, gw[j], sw[j], ones);
         }
     };
     // Steps go two ahead: step s multiplies stage s & 1, splits step s + 1
@@ -212,7 +240,7 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
     if (nfull > 0) {
         load(gx0, gw0, kbeg);
         load(gx1, gw1, kbeg + min(1, last) * MK);
-        store(0, gx0, gw0);
+        store(0, gx0, gw0, ONES);
     }
     __syncthreads();
     auto step = [&](int s, Regs &lx, Regs &lw, const Regs &cx_, const Regs &cw_) {
@@ -221,7 +249,8 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t *st = &lds[s & 1][0][0];
         mfma_step(acc, st + wt * SLICE, st + STAGE + wn * SLICE, lane);
-        store((s + 1) & 1, cx_, cw_);
+        // the last step splits a clamped re-read: stored, never used, not summed
+        store((s + 1) & 1, cx_, cw_, s + 1 < nfull ? ONES : 0);
         // operand reads first, then the MFMAs with the digit split of the
         // next step interleaved (its data arrived a step ago)
 #pragma unroll
@@ -250,30 +279,60 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
             load8<VEC, true>(gx0[j], xrow[j], kt, kend - pc[j].k8);
             load8<VEC, true>(gw0[j], wrow[j], kt, kend - pc[j].k8);
         }
-        store(nfull & 1, gx0, gw0);
+        store(nfull & 1, gx0, gw0, ONES);
         __syncthreads();
         const uint8_t *st = &lds[nfull & 1][0][0];
         mfma_step(acc, st + wt * SLICE, st + STAGE + wn * SLICE, lane);
     }
 
+    // Digit corrections of this k range: per row, C * sum_k S(v) =
+    // C * sum_a 256^a (digit sum of limb a); W rows also carry len * C^2.
+    if (FUSE) {
+#pragma unroll
+        for (int j = 0; j < NPAIR; ++j)
+#pragma unroll
+            for (int a = 0; a < 8; ++a) {
+                atomicAdd(&dsum[0][pc[j].r][a], sx[j][a]);
+                atomicAdd(&dsum[1][pc[j].r][a], sw[j][a]);
+            }
+    }
+    __syncthreads();
+    if (FUSE && tid < 128) {
+        const int op = tid >> 6, row = tid & 63;
+        q48_u128 sum = 0;
+#pragma unroll
+        for (int a = 7; a >= 0; --a)
+            sum = (sum << 8) + (q48_u128)(q48_i128)dsum[op][row][a];
+        q48_u128 v = sum * kDig;
+        if (op == 1)
+            v += (q48_u128)kDig * kDig * (q48_u128)(uint64_t)(kend - kbeg);
+        corr[op][row] = v;
+    }
+    __syncthreads();
+
     // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32
-    const int n = n0 + 32 * wn + (lane & 31);
+    const int nl = 32 * wn + (lane & 31), n = n0 + nl;
     if (n >= N)
         return;
     q48_u128 cwn = 0;
-    if (gridDim.z == 1)
+    if (FUSE)
+        cwn = corr[1][nl];
+    else if (gridDim.z == 1)
         cwn = ((q48_u128)cw[2 * n + 1] << 64) | cw[2 * n];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const int t = t0 + 32 * wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        const int tl = 32 * wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3), t = t0 + tl;
         if (t >= T)
             continue;
         q48_u128 tot = 0;
 #pragma unroll
         for (int d = 13; d >= 0; --d)
             tot = (tot << 8) + (q48_u128)(q48_i128)acc[d][i];
-        if (gridDim.z == 1) {
+        if (FUSE)
+            tot += cwn + corr[0][tl];
+        else if (gridDim.z == 1)
             tot += cwn + (((q48_u128)cx[2 * t + 1] << 64) | cx[2 * t]);
+        if (gridDim.z == 1) {
             Y[(size_t)t * N + n] = (int64_t)((q48_i128)tot >> 48);
         } else {
             uint64_t *p = P + 2 * (((size_t)blockIdx.z * T + t) * N + n);
@@ -283,7 +342,7 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
     }
 }
 
-// Y[t][n] = (sum_z P[z][t][n] + cw[n] + cx[t]) >> 48
+// Y[t][n] = (sum_z P[z][t][n] (+ cw[n] + cx[t] when given)) >> 48
 __global__ __launch_bounds__(256) void k_gemm_i8_reduce(int64_t *__restrict__ Y,
                                                        const uint64_t *__restrict__ P,
                                                        const uint64_t *__restrict__ cw,
@@ -293,9 +352,12 @@ __global__ __launch_bounds__(256) void k_gemm_i8_reduce(int64_t *__restrict__ Y,
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (size_t)T * N)
         return;
-    const int t = (int)(i / N), n = (int)(i % N);
-    q48_u128 tot = (((q48_u128)cw[2 * n + 1] << 64) | cw[2 * n]) +
-                   (((q48_u128)cx[2 * t + 1] << 64) | cx[2 * t]);
+    q48_u128 tot = 0;
+    if (cw) {
+        const int t = (int)(i / N), n = (int)(i % N);
+        tot = (((q48_u128)cw[2 * n + 1] << 64) | cw[2 * n]) +
+              (((q48_u128)cx[2 * t + 1] << 64) | cx[2 * t]);
+    }
     for (int z = 0; z < S; ++z) {
         const ulonglong2 u =
             *reinterpret_cast<const ulonglong2 *>(P + 2 * ((size_t)z * T * N + i));
@@ -363,24 +425,46 @@ int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *
     const int S = q48_gemm_i8_splits(T, N, K, c->cu_count);
     const int steps = (K + MK - 1) / MK;
     const int spb = (steps + S - 1) / S;
-    const size_t corr = 16 * ((size_t)N + (size_t)T);
+    // short token counts count the digit sums inside the GEMM (W is read
+    // once); long ones amortise a separate pass over W and X, which keeps
+    // 32 v_dot4 per step out of the MFMA loop
+    const bool fuse = T < FUSE_BELOW_T;
+    const size_t corr = fuse ? 0 : 16 * ((size_t)N + (size_t)T);
     const size_t part = S > 1 ? 16 * (size_t)S * T * N : 0;
-    int rc = q48_ws_reserve(c, corr + part);
-    if (rc)
-        return rc;
-    uint64_t *cw = (uint64_t *)c->ws;
-    uint64_t *cx = cw + 2 * (size_t)N;
-    uint64_t *P = S > 1 ? cx + 2 * (size_t)T : nullptr;
-    hipLaunchKernelGGL(k_digit_corr, dim3((N + 3) / 4), dim3(256), 0, c->stream, cw, W, N, K, 1);
-    hipLaunchKernelGGL(k_digit_corr, dim3((T + 3) / 4), dim3(256), 0, c->stream, cx, X, T, K, 0);
+    uint64_t *cw = nullptr, *cx = nullptr, *P = nullptr;
+    if (corr + part) {
+        int rc = q48_ws_reserve(c, corr + part);
+        if (rc)
+            return rc;
+        uint64_t *ws = (uint64_t *)c->ws;
+        if (!fuse) {
+            cw = ws;
+            cx = cw + 2 * (size_t)N;
+            ws = cx + 2 * (size_t)T;
+        }
+        if (S > 1)
+            P = ws;
+        if (!fuse) {
+            hipLaunchKernelGGL(k_digit_corr, dim3((N + 3) / 4), dim3(256), 0, c->stream, cw, W,
+                               N, K, 1);
+            hipLaunchKernelGGL(k_digit_corr, dim3((T + 3) / 4), dim3(256), 0, c->stream, cx, X,
+                               T, K, 0);
+        }
+    }
     const dim3 grid(((N + MN - 1) / MN) * ((T + MT - 1) / MT), 1, S);
     const bool vec = K % 2 == 0 && (((uintptr_t)W | (uintptr_t)X) & 15) == 0;
-    if (vec)
-        hipLaunchKernelGGL((k_gemm_i8<true>), grid, dim3(256), 0, c->stream, Y, P, W, X, cw, cx,
-                           T, N, K, spb);
+#define GEMM_I8_LAUNCH(V, F)                                                                 \
+    hipLaunchKernelGGL((k_gemm_i8<V, F>), grid, dim3(256), 0, c->stream, Y, P, W, X, cw, cx, T, \
+                       N, K, spb)
+    if (vec && fuse)
+        GEMM_I8_LAUNCH(true, true);
+    else if (vec)
+        GEMM_I8_LAUNCH(true, false);
+    else if (fuse)
+        GEMM_I8_LAUNCH(false, true);
     else
-        hipLaunchKernelGGL((k_gemm_i8<false>), grid, dim3(256), 0, c->stream, Y, P, W, X, cw,
-                           cx, T, N, K, spb);
+        GEMM_I8_LAUNCH(false, false);
+#undef GEMM_I8_LAUNCH
     if (S > 1) {
         const size_t tn = (size_t)T * N;
         hipLaunchKernelGGL(k_gemm_i8_reduce, dim3((unsigned)((tn + 255) / 256)), dim3(256), 0,

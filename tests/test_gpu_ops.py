@@ -168,12 +168,14 @@ GEMM_KERNELS = [pytest.param(intllm.GEMM_VALU, id="valu"), pytest.param(intllm.G
 @pytest.mark.parametrize("kernel", GEMM_KERNELS)
 @pytest.mark.parametrize("T,N,K", [(1, 1, 1), (3, 5, 7), (64, 64, 16), (65, 70, 33),
                                    (130, 129, 688), (128, 256, 2048), (64, 64, 8192),
-                                   (70, 33, 1031), (200, 96, 96), (3, 5, 20000)])
+                                   (70, 33, 1031), (200, 96, 96), (3, 5, 20000),
+                                   (1030, 37, 1031), (1024, 64, 8192)])
 def test_gemm_random_vs_oracle(ctx, oracle, T, N, K, kernel):
     """Full-range int64 operands.  The cases cover partial tiles, a k tail
     (K not a multiple of 32), odd K (8-byte loads), K split across blocks
-    (64x64x8192: one tile, many splits) and K past one int32 accumulation
-    run of the int8 kernel (20000)."""
+    (64x64x8192: one tile, many splits), K past one int32 accumulation run of
+    the int8 kernel (20000), and T >= 1024, where the int8 kernel takes its
+    digit corrections from a separate pass (alone and with K splits)."""
     rng = np.random.default_rng(T * 31 + N * 7 + K)
     W = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=N * K, dtype=np.int64)
     X = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=T * K, dtype=np.int64)
