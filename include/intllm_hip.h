@@ -180,6 +180,12 @@ int q48_attn_decode_rope(q48_ctx *ctx, int64_t *out, const int64_t *q,
  * step mode: a graph captured below this position keeps the one-block
  * kernels as replays move past it (same bits, slower). */
 int q48_attn_split_min(void);
+
+/* Long normed GEMVs (more than two rounds of 8-row groups: gate|up, lm_head)
+ * run as persistent blocks that loop over row groups (on: the default), or
+ * one block per group (off).  Same bits either way.  No reference
+ * counterpart: a scheduling choice of this library. */
+int q48_set_gemv_persistent(q48_ctx *ctx, int on);
 /* q48_attn_decode_rope that also reads [prefetch, prefetch + prefetch_bytes)
  * (16-byte aligned; typically the next op's weights, W_o) on the compute
  * units the heads leave idle, so that the next op finds them in the

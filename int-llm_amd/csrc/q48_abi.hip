@@ -90,6 +90,7 @@ int q48_ctx_create(q48_ctx **out, int device)
     if (!c)
         return Q48_ENOMEM;
     c->device = device;
+    c->gemv_persistent = 1;
     if (hipDeviceGetAttribute(&c->cu_count, hipDeviceAttributeMultiprocessorCount, device) !=
             hipSuccess ||
         c->cu_count <= 0)
@@ -110,6 +111,8 @@ int q48_ctx_create(q48_ctx **out, int device)
         rc = launch_rc(q48_launch_step_set(c, 0, 0));
     if (rc == Q48_OK)
         rc = launch_rc(q48_launch_zero(c, c->rms_count, 512 * sizeof(int)));
+    if (rc == Q48_OK)
+        rc = launch_rc(q48_launch_zero(c, c->d_scalar, 64 * sizeof(int)));
     if (rc == Q48_OK)
         rc = hip_rc(hipStreamSynchronize(c->stream));
     if (rc != Q48_OK) {
@@ -599,6 +602,14 @@ int q48_attn_decode_rope(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kc
 }
 
 int q48_attn_split_min(void) { return q48_att_split_min(); }
+
+int q48_set_gemv_persistent(q48_ctx *c, int on)
+{
+    if (!c)
+        return Q48_EINVAL;
+    c->gemv_persistent = on != 0;
+    return Q48_OK;
+}
 
 int q48_attn_decode_rope_prefetch(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                                   int64_t *vcache, const int64_t *k_new, const int64_t *v_new,

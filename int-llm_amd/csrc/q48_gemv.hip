@@ -623,6 +623,183 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     }
 }
 
+// ---------------------------------------------------------------------------
+// k_gemv_p6: the persistent form of k_gemv_v5 for the long projections whose
+// blocks would otherwise repeat a costly prologue in lockstep rounds (the
+// normed gate|up with SwiGLU, the normed lm_head).  Block b takes the row
+// groups b, b + G, b + 2G, ... (G = gridDim.x):
+//  - the norm statistics, r and the staged x limbs are computed once per
+//    block, not once per 8 rows;
+//  - the next group's first UNR weight tiles are issued during the current
+//    group's last ones, so the weight stream does not stop between groups;
+//  - EPI 2 keeps each group's gate/up pre-activations in LDS and applies
+//    SwiGLU to all of them after the last group (one latency chain per
+//    block instead of one per group).
+// Every wave has exactly NTF tiles (K = 16 NTF NW, checked on the host).
+// Results are those of k_gemv_v5 (same sums, same epilogue arithmetic).
+// ---------------------------------------------------------------------------
+constexpr int P6_MAXG = 16;   // row groups per block at most
+
+template <int NW, int UNR, int PRO, int EPI, int NTF>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void
+k_gemv_p6(int64_t *__restrict__ y, const int64_t *__restrict__ W,
+          const int64_t *__restrict__ x, const int64_t *__restrict__ norm_w,
+          const int64_t *__restrict__ r_in, int M, int K, int seg)
+{
+    static_assert(NTF > 0 && (PRO == 0 || PRO == 3) && (EPI == 0 || EPI == 2), "p6 forms");
+    extern __shared__ __align__(16) uint32_t xs[];   // 3 limbs per staged x
+    __shared__ uint64_t part[2][NW][V4_RB][2];
+    __shared__ int64_t pre[P6_MAXG][V4_RB];          // EPI 2: gate (0-3) / up (4-7)
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 3, l8 = lane & 7;
+    const int ffn = M >> 1;
+    const int k0 = wave * seg;
+    const int ngroups = EPI == 2 ? (ffn + 3) / 4 : (M + V4_RB - 1) / V4_RB;
+
+    // this lane's weight row in group grp (EPI 2: gate rows 4 grp + g, then
+    // up rows ffn + 4 grp + g - 4); rows past the end read row 0 (in bounds,
+    // never stored)
+    auto wrow = [&](int grp) {
+        const int pr = grp * 4 + (g & 3);
+        const int row = EPI == 2 ? (g < 4 ? pr : ffn + pr) : grp * V4_RB + g;
+        const bool live = EPI == 2 ? pr < ffn : row < M;
+        return reinterpret_cast<const ulonglong2 *>(W + (size_t)(live ? row : 0) * K + k0) + l8;
+    };
+
+    // PRO 3 partial sums first, then x (and the norm weights), then the
+    // first group's weight tiles: vmcnt retires in issue order
+    constexpr int PC = (2 * NW * NTF + 63) / 64;
+    uint64_t plo[PC], phi[PC];
+    const int np = (K + 7) >> 3;
+    const uint64_t *st = reinterpret_cast<const uint64_t *>(r_in);
+    if (PRO == 3) {
+#pragma unroll
+        for (int c = 0; c < PC; ++c) {
+            const int i = min(lane + c * 64, np - 1);
+            const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(st + 2 * i);
+            plo[c] = v.x;
+            phi[c] = v.y;
+        }
+    }
+    constexpr int XB = (16 * NTF + 127) / 128;
+    int64_t xv[2 * XB], nw[2 * XB];
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+        const int j = min(2 * lane + 128 * b, seg - 2);
+        const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(x + k0 + j);
+        xv[2 * b] = (int64_t)v.x;
+        xv[2 * b + 1] = (int64_t)v.y;
+        if (PRO != 0) {
+            const ulonglong2 w = *reinterpret_cast<const ulonglong2 *>(norm_w + k0 + j);
+            nw[2 * b] = (int64_t)w.x;
+            nw[2 * b + 1] = (int64_t)w.y;
+        }
+    }
+    asm volatile("" ::: "memory");   // keep the x loads ahead of the weight loads
+    int grp = blockIdx.x;
+    const ulonglong2 *w2 = wrow(grp < ngroups ? grp : 0);
+    ulonglong2 wa[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+        wa[u] = w2[u * 8];
+    __builtin_amdgcn_sched_barrier(0);
+
+    int64_t r = 0;
+    if (PRO == 3) {
+        q48_u128 ss = 0;
+#pragma unroll
+        for (int c = 0; c < PC; ++c) {
+            const uint64_t m = lane + c * 64 < np ? ~0ull : 0ull;
+            ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
+        }
+        ss = q48_wave_sum128(ss);
+        r = rms_inv_of(ss, K);
+    }
+
+    // stage this wave's segment of x as limbs; sum x over the segment
+    uint64_t xsum = 0;
+    uint32_t *xw = xs + (size_t)wave * seg * 3;
+#pragma unroll
+    for (int b = 0; b < 2 * XB; ++b) {
+        const int j = 2 * lane + 128 * (b / 2) + b % 2;
+        int64_t v = xv[b];
+        if (PRO != 0)
+            v = q48_mul(q48_mul(v, r), nw[b]);
+        v = j < seg ? v : 0;
+        xsum += (uint64_t)v;
+        if (j < seg) {
+            const uint64_t X = (uint64_t)v ^ 0x8000000000000000ull;
+            xw[3 * j] = (uint32_t)X & 0x3FFFFFu;
+            xw[3 * j + 1] = (uint32_t)(X >> 22) & 0x1FFFFFu;
+            xw[3 * j + 2] = (uint32_t)(X >> 43);
+        }
+    }
+    xsum = (uint64_t)q48_wave_sum64((int64_t)xsum);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const uint32_t *xl = xw + 6 * l8;
+    int i = 0;
+    for (; grp < ngroups; grp += gridDim.x, ++i) {
+        const int nxt = grp + (int)gridDim.x;
+        // the next group's rows (this group's again after the last: in
+        // bounds, never used)
+        const ulonglong2 *w2n = wrow(nxt < ngroups ? nxt : grp);
+        Acc6 A = {0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < NTF; ++t) {
+            const uint32_t *p = xl + 48 * t;
+            mac6(A, p[0], p[1], p[2], wa[t % UNR].x);
+            mac6(A, p[3], p[4], p[5], wa[t % UNR].y);
+            if (t + UNR < NTF)
+                wa[t % UNR] = w2[(t + UNR) * 8];
+            else
+                wa[t % UNR] = w2n[(t + UNR - NTF) * 8];
+        }
+        w2 = w2n;
+        q48_u128 S = acc6_value(A);
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            const uint64_t lo = (uint64_t)S, hi = (uint64_t)(S >> 64);
+            S += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
+        }
+        if (l8 == 0) {
+            S -= (q48_u128)xsum << 63;
+            part[i & 1][wave][g][0] = (uint64_t)S;
+            part[i & 1][wave][g][1] = (uint64_t)(S >> 64);
+        }
+        // partial sums double-buffered by group: one barrier per group
+        __syncthreads();
+        if (tid < V4_RB) {
+            q48_u128 T = 0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+                T += ((q48_u128)part[i & 1][w][tid][1] << 64) | part[i & 1][w][tid][0];
+            const int64_t v = (int64_t)((q48_i128)T >> 48);
+            if (EPI == 0) {
+                const int rr = grp * V4_RB + tid;
+                if (rr < M)
+                    y[rr] = v;
+            } else {
+                pre[i][tid] = v;
+            }
+        }
+    }
+    if (EPI == 2) {
+        __syncthreads();
+        // SwiGLU of every pair this block produced, one pair per thread
+        if (tid < 4 * i) {
+            const int gi = tid >> 2, q = tid & 3;
+            const int pi = ((int)blockIdx.x + gi * (int)gridDim.x) * 4 + q;
+            if (pi < ffn)
+                y[pi] = q48_mul(q48_silu(pre[gi][q]), pre[gi][4 + q]);
+        }
+    }
+}
+
 // Standalone rmsnorm statistics r of x (one block): for the fallbacks and
 // for the first hidden vector of a token.  With table != nullptr it also
 // copies table[*d_token or token] to out first (the embedding row,
@@ -753,6 +930,16 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
     // unrolled rotating pipeline; other K the batched loop
     const bool al = ((uintptr_t)x & 15) == 0 && (PRO == 0 || ((uintptr_t)norm_w & 15) == 0) &&
                     (PRO != 3 || ((uintptr_t)r_in & 15) == 0);
+    // more row groups than two rounds of blocks: the persistent form
+    if constexpr ((PRO == 0 || PRO == 3) && (EPI == 0 || EPI == 2)) {
+        const int grid = 2 * c->cu_count;
+        if (al && K == NW * seg && seg == 16 * 16 && blocks > 2 * grid &&
+            blocks <= P6_MAXG * grid && c->gemv_persistent) {
+            hipLaunchKernelGGL((k_gemv_p6<NW, 4, PRO, EPI, 16>), dim3(grid), dim3(64 * NW), lds,
+                               c->stream, y, W, x, norm_w, r_in, M, K, seg);
+            return (int)hipGetLastError();
+        }
+    }
     if (al && K == NW * seg && seg == 16 * 16)
         hipLaunchKernelGGL((k_gemv_v5<NW, 4, PRO, EPI, 16>), dim3(blocks), dim3(64 * NW), lds,
                            c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,

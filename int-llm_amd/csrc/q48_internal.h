@@ -11,6 +11,7 @@
 struct q48_ctx {
     int device;
     int cu_count;                // compute units of the device
+    int gemv_persistent;         // long normed GEMVs take k_gemv_p6 (default on)
     hipStream_t stream;
     q48_consts *consts;          // device: fp_math_init constants
     int64_t *rope_cos, *rope_sin; // device: [max_seq][head_dim/2]

@@ -7,41 +7,9 @@
 // arithmetic is integer, and every reduction is an integer sum (mod 2^64
 // or 2^128) or a max, so the parallel order cannot change a bit.
 #include "q48_internal.h"
+#include "q48_attn.hpp"
 
 namespace {
-
-// Sum an int64 (wrapping) across a block of NT threads; every thread gets it.
-template <int NT>
-__device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t *red)
-{
-    v = q48_wave_sum64(v);
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __syncthreads();
-    if (lane == 0)
-        red[w] = v;
-    __syncthreads();
-    uint64_t t = 0;
-#pragma unroll
-    for (int i = 0; i < NT / 64; ++i)
-        t += (uint64_t)red[i];
-    return (int64_t)t;
-}
-
-template <int NT>
-__device__ __forceinline__ int64_t block_max64(int64_t v, int64_t *red)
-{
-    v = q48_wave_max64(v);
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __syncthreads();
-    if (lane == 0)
-        red[w] = v;
-    __syncthreads();
-    int64_t t = red[0];
-#pragma unroll
-    for (int i = 1; i < NT / 64; ++i)
-        t = red[i] > t ? red[i] : t;
-    return t;
-}
 
 // ---------------------------------------------------------------------------
 // fp_math_init on the device (fp_math.h:833-858)
@@ -244,7 +212,6 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_decode(
 // pos is read from *d_pos when given (graph replay of a decode step).
 // hd must be a multiple of 8 and divide 256 (checked on the host).
 // ---------------------------------------------------------------------------
-constexpr int ATT_LDS_MAX = 4096;   // positions whose scores fit in LDS (32 KiB)
 
 template <int ROPE, int LDS>
 __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
@@ -396,18 +363,10 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
 }
 
 // ---------------------------------------------------------------------------
-// Attention v3: k_attn_v2's computation with its memory round trips cut:
-//  - the K rows of the first two score passes are issued before RoPE, and
-//    each later pass is issued one pass ahead (two register buffers);
-//  - the first V batches are issued before the softmax, later ones one
-//    batch ahead, so the V pass rarely waits;
-//  - the score scale fp_inv_sqrt(fp_from_int(hd)) is read, not recomputed
-//    (k_rope_init stores it after the sine table).
-// Loads past the last position are clamped to it (in bounds, unused), so
-// every wait is for a known, static number of younger loads.  Rows at pos
-// are read from the cache and replaced by the block's own rotated k and v.
-// One block of 256 threads per query head; HD = 32, 64 or 128; at most
-// ATT_LDS_MAX positions.  Blocks past n_heads prefetch like k_attn_v2's.
+// Attention v3: k_attn_v2's computation with its memory round trips cut
+// (attn_v3_head, q48_attn.hpp).  One block of 256 threads per query head;
+// HD = 32, 64 or 128; at most ATT_LDS_MAX positions.  Blocks past n_heads
+// prefetch like k_attn_v2's.
 // ---------------------------------------------------------------------------
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_v3(
@@ -418,11 +377,7 @@ __global__ __launch_bounds__(256) void k_attn_v3(
     const int *__restrict__ d_pos, int pos, int n_heads, int n_kv, int max_seq,
     const ulonglong2 *__restrict__ pf, size_t pf_n16)
 {
-    constexpr int NT = 256, DPL = HD / 8, DP2 = DPL / 2, SL = NT / HD, NG = NT / 8, VB = 8;
-    __shared__ int64_t qs[HD], ks[HD], vs[HD];
-    __shared__ int64_t red[NT / 64];
-    __shared__ int64_t part[NT];
-    __shared__ int64_t sc[ATT_LDS_MAX];
+    constexpr int NT = 256;
     if ((int)blockIdx.x >= n_heads) {
         const size_t stride = (size_t)(gridDim.x - n_heads) * NT;
         size_t i = (size_t)(blockIdx.x - n_heads) * NT + threadIdx.x;
@@ -441,151 +396,9 @@ __global__ __launch_bounds__(256) void k_attn_v3(
         asm volatile("" ::"v"(acc));
         return;
     }
-    if (d_pos)
-        pos = *d_pos;
-    if (pos < 0 || pos >= max_seq)
-        return;   // uniform over the block: no barrier is skipped by part of it
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int group = n_heads / n_kv, kh = h / group;
-    const size_t kvd = (size_t)n_kv * HD;
-    const size_t base = (size_t)layer * max_seq;
-    const int S = pos + 1, half = HD / 2;
-    const int g = tid >> 3, l8 = tid & 7;
-    const int64_t scale = *scale_p;
-
-    // the RoPE inputs and the new v first (loads retire in issue order: the
-    // RoPE then waits for them alone), every thread loading (clamped index)
-    const int64_t *qh = q + (size_t)h * HD, *kn = k_new + (size_t)kh * HD;
-    const int i = min(tid, half - 1), j = min(tid, HD - 1);
-    int64_t c = cos_t[(size_t)pos * half + i];
-    int64_t sn = sin_t[(size_t)pos * half + i];
-    int64_t q0 = qh[i], q1 = qh[i + half];
-    int64_t k0 = kn[i], k1 = kn[i + half];
-    int64_t vn = v_new[(size_t)kh * HD + j];
-    __builtin_amdgcn_sched_barrier(0);
-
-    // K rows of passes 0 and 1: lane l8 of group g holds dims [l8 DPL, +DPL)
-    const int64_t *kb0 = kcache + base * kvd + (size_t)kh * HD + l8 * DPL;
-    auto krow = [&](int t) {
-        return reinterpret_cast<const ulonglong2 *>(kb0 + (size_t)min(t, S - 1) * kvd);
-    };
-    ulonglong2 ka[DP2], kb[DP2];
-#pragma unroll
-    for (int d = 0; d < DP2; ++d)
-        ka[d] = krow(g)[d];
-#pragma unroll
-    for (int d = 0; d < DP2; ++d)
-        kb[d] = krow(g + NG)[d];
-    __builtin_amdgcn_sched_barrier(0);
-    // first use of the RoPE inputs here, after the K loads are out (else the
-    // compiler extends them to 128 bits, and waits for them, earlier)
-    asm volatile("" : "+v"(c), "+v"(sn), "+v"(q0), "+v"(q1), "+v"(k0), "+v"(k1), "+v"(vn));
-
-    // RoPE of q_h and the new k (rope_apply, llama_int.c:997-1008, 1392-1395);
-    // threads past half repeat the last pair (same values, same slots): no
-    // branch, so the loads above are not sunk into one
-    qs[i] = (int64_t)((uint64_t)q48_mul(q0, c) - (uint64_t)q48_mul(q1, sn));
-    qs[i + half] = (int64_t)((uint64_t)q48_mul(q1, c) + (uint64_t)q48_mul(q0, sn));
-    ks[i] = (int64_t)((uint64_t)q48_mul(k0, c) - (uint64_t)q48_mul(k1, sn));
-    ks[i + half] = (int64_t)((uint64_t)q48_mul(k1, c) + (uint64_t)q48_mul(k0, sn));
-    vs[j] = vn;
-    __syncthreads();
-    if (h % group == 0 && tid < HD) {
-        kcache[(base + pos) * kvd + (size_t)kh * HD + tid] = ks[tid];
-        vcache[(base + pos) * kvd + (size_t)kh * HD + tid] = vs[tid];
-    }
-
-    // scores s_t = fp_mul((sum_d q_d k_t,d) >> 48, scale), llama_int.c:1502-1512
-    const int64_t *qd = qs + l8 * DPL, *kd = ks + l8 * DPL;
-    int64_t mx = INT64_MIN;
-    auto score = [&](const ulonglong2 (&kr)[DP2], int t) {
-        const bool own = t == pos;
-        q48_u128 dot = 0;
-#pragma unroll
-        for (int d = 0; d < DP2; ++d) {
-            const int64_t a0 = own ? kd[2 * d] : (int64_t)kr[d].x;
-            const int64_t a1 = own ? kd[2 * d + 1] : (int64_t)kr[d].y;
-            dot += (q48_u128)((q48_i128)qd[2 * d] * a0);
-            dot += (q48_u128)((q48_i128)qd[2 * d + 1] * a1);
-        }
-#pragma unroll
-        for (int off = 1; off < 8; off <<= 1) {
-            const uint64_t lo = (uint64_t)dot, hi = (uint64_t)(dot >> 64);
-            dot += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
-        }
-        if (t < S && l8 == 0) {
-            const int64_t s = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
-            sc[t] = s;
-            mx = s > mx ? s : mx;
-        }
-    };
-    for (int t0 = 0; t0 < S; t0 += 2 * NG) {
-        score(ka, t0 + g);
-#pragma unroll
-        for (int d = 0; d < DP2; ++d)
-            ka[d] = krow(t0 + 2 * NG + g)[d];
-        score(kb, t0 + NG + g);
-#pragma unroll
-        for (int d = 0; d < DP2; ++d)
-            kb[d] = krow(t0 + 3 * NG + g)[d];
-    }
-
-    // V batches 0 and 1 go out before the softmax: thread (d, sl) takes
-    // positions sl + SL i, VB of them per batch
-    const int d = tid % HD, sl = tid / HD;
-    const int64_t *vcol = vcache + base * kvd + (size_t)kh * HD + d;
-    auto vld = [&](int i) { return vcol[(size_t)min(sl + SL * i, S - 1) * kvd]; };
-    int64_t va[VB], vb[VB];
-#pragma unroll
-    for (int u = 0; u < VB; ++u)
-        va[u] = vld(u);
-#pragma unroll
-    for (int u = 0; u < VB; ++u)
-        vb[u] = vld(VB + u);
-
-    // softmax, llama_int.c:1060-1072
-    mx = block_max64<NT>(mx, red);
-    int64_t sum = 0;
-    for (int t = tid; t < S; t += NT) {
-        const int64_t e = q48_safe_exp((int64_t)((uint64_t)sc[t] - (uint64_t)mx));
-        sc[t] = e;
-        sum = (int64_t)((uint64_t)sum + (uint64_t)e);
-    }
-    sum = block_sum64<NT>(sum, red);
-    if (sum > 0)
-        for (int t = tid; t < S; t += NT)
-            sc[t] = q48_div(sc[t], sum);
-    __syncthreads();
-
-    // o[d] = sum_t fp_mul(p_t, v_t[d]), llama_int.c:1514-1529
-    uint64_t acc = 0;
-    auto vmac = [&](const int64_t (&vv)[VB], int i0) {
-#pragma unroll
-        for (int u = 0; u < VB; ++u) {
-            const int t = sl + SL * (i0 + u);
-            if (t < S)
-                acc += (uint64_t)q48_mul(sc[t], t == pos ? vs[d] : vv[u]);
-        }
-    };
-    for (int i0 = 0; sl + SL * i0 < S; i0 += 2 * VB) {
-        vmac(va, i0);
-#pragma unroll
-        for (int u = 0; u < VB; ++u)
-            va[u] = vld(i0 + 2 * VB + u);
-        vmac(vb, i0 + VB);
-#pragma unroll
-        for (int u = 0; u < VB; ++u)
-            vb[u] = vld(i0 + 3 * VB + u);
-    }
-    part[tid] = (int64_t)acc;
-    __syncthreads();
-    if (sl == 0) {
-        uint64_t o = 0;
-#pragma unroll
-        for (int s2 = 0; s2 < SL; ++s2)
-            o += (uint64_t)part[s2 * HD + d];
-        out[(size_t)h * HD + d] = (int64_t)o;
-    }
+    attn_v3_head<HD, ATT_LDS_MAX, false>(out, q, kcache, vcache, k_new, v_new, cos_t, sin_t,
+                                         scale_p, layer, d_pos, pos, n_heads, n_kv, max_seq,
+                                         (int)blockIdx.x);
 }
 
 // This thread's share of argmax (llama_int.c:2888-2893) over v[0..n) with

@@ -905,8 +905,20 @@ int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_t
         return 0;
     double t0 = now_s();
     TRY(first_step_and_capture(m, token, start_pos));
-    TRY(q48_graph_launch(m->ctx, n - 1));
-    TRY(q48_memcpy_d2h(m->ctx, out_tokens, m->d_tokens, (size_t)n * sizeof(int)));
+    /* a graph serves one attention kernel class: a run that crosses the
+     * position where attention changes kernels is replayed in two parts,
+     * the second from a graph captured at that position */
+    const int B = q48_attn_split_min();
+    int k = n;
+    if (start_pos < B && start_pos + n > B)
+        k = B - start_pos;
+    TRY(q48_graph_launch(m->ctx, k - 1));
+    TRY(q48_memcpy_d2h(m->ctx, out_tokens, m->d_tokens, (size_t)k * sizeof(int)));
+    if (k < n) {
+        TRY(first_step_and_capture(m, out_tokens[k - 1], B));
+        TRY(q48_graph_launch(m->ctx, n - k - 1));
+        TRY(q48_memcpy_d2h(m->ctx, out_tokens + k, m->d_tokens, (size_t)(n - k) * sizeof(int)));
+    }
     if (st) {
         st->decode_s += now_s() - t0;
         st->decode_tokens += n;

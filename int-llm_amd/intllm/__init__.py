@@ -44,6 +44,8 @@ ABI_SIGNATURES = {
     "q48_gemv": [_P, _P, _P, _P, _I, _I],
     "q48_gemm": [_P, _P, _P, _P, _I, _I, _I],
     "q48_gemm_ex": [_P, _P, _P, _P, _I, _I, _I, _I],
+    "q48_set_gemv_persistent": [_P, _I],
+
     "q48_rmsnorm": [_P, _P, _P, _P, _I],
     "q48_rope_init": [_P, _I, _I, _I],
     "q48_rope": [_P, _P, _I, _I, _I],
@@ -217,6 +219,9 @@ class Context:
     def gemv(self, y, W, x, M, K):
         return check("q48_gemv", hip_lib().q48_gemv(self.h, y, W, x, M, K))
 
+    def set_gemv_persistent(self, on: bool):
+        return check("q48_set_gemv_persistent", hip_lib().q48_set_gemv_persistent(self.h, int(on)))
+
     def gemm(self, Y, W, X, T, N, K, kernel=None):
         """kernel: None (q48_gemm's choice), GEMM_VALU or GEMM_I8."""
         if kernel is None:
@@ -386,6 +391,7 @@ HOST_SIGNATURES = {
                           C.POINTER(Stats)], C.c_int),
     "q48h_model_set_fused": ([_P, _I], None),
     "q48h_model_set_prefetch": ([_P, _I], None),
+
     "q48h_gemv_sweep": ([_P, _I, C.POINTER(C.c_int), C.POINTER(C.c_double)], C.c_int),
     "q48h_decode_graph": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
     "q48s_fill_named": ([_P, C.c_int64, C.c_int64, C.c_uint64, C.c_char_p, C.c_int64, _I, _I],
@@ -479,6 +485,7 @@ class HostModel:
     def set_prefetch(self, on: bool):
         """Warm the device cache with each layer's W_o during its attention."""
         host_lib().q48h_model_set_prefetch(self.h, int(bool(on)))
+
 
     def set_fused(self, mode: int):
         """0: one op per reference step; 1: fused with per-block norm

@@ -195,6 +195,37 @@ def test_tiny_generate_other_paths_bit_exact(ctx, mode):
         m.free()
 
 
+def test_graph_decode_across_split_position(ctx, oracle):
+    """A graph-replayed run that crosses position 512, where attention changes
+    kernels (one block per head below it, split attention from it on): the
+    run is replayed from two captured graphs and equals the eager per-token
+    decode and the oracle's decode."""
+    g = golden("tiny_generate.json")
+    cfg = intllm.Config(*g["config"])
+    start, n, tok0 = 500, 24, 7
+    m = intllm.HostModel(ctx, cfg)
+    try:
+        m.synth(g["seed"], threads())
+        m.kv_fill_synth(spec.SEED_KV, start, threads())
+        say("graph decode across 512")
+        _, steps, _ = m.decode_graph(tok0, start, n)
+        say("eager decode across 512")
+        eager, _, _ = m.decode_from(tok0, start, n, hashes=False)
+    finally:
+        m.free()
+    ocfg = O.Config(*g["config"])
+    om = oracle.q48o_model_synth(C.byref(ocfg), g["seed"], threads())
+    try:
+        oracle.q48o_kv_fill_synth(om, spec.SEED_KV, start, threads())
+        out = (C.c_int * n)()
+        k = oracle.q48o_decode_from(om, tok0, start, n, out, None)
+        ref = list(out[:k])
+    finally:
+        oracle.q48o_model_free(om)
+    assert eager[:k] == ref
+    assert steps[:k] == ref
+
+
 def test_tiny_graph_decode_replays(ctx):
     """Graph-replayed decode: several launches of the captured step, with
     eager work and host synchronisation between the calls, each continuing

@@ -633,6 +633,43 @@ def test_norm_gemv_swiglu_with_stats(ctx, oracle, ffn, K):
         b.free()
 
 
+@pytest.mark.parametrize("persistent", [True, False])
+@pytest.mark.parametrize("M,ffn", [(32000, 0), (9001, 0), (0, 5632), (0, 4097)])
+def test_long_normed_gemv_persistent(ctx, oracle, M, ffn, persistent):
+    """The normed lm_head / gate|up shapes with more row groups than two rounds
+    of blocks: persistent blocks looping over row groups (the default) and one
+    block per group both give the oracle's bits, with a partial last group
+    (9001 rows, ffn 4097)."""
+    K = 2048
+    rows = M or 2 * ffn
+    rng = np.random.default_rng(rows + 3 * K + persistent)
+    W = (rng.standard_normal(rows * K) * spec.SIGMA_W * 20).astype(np.int64)
+    x = (rng.standard_normal(K) * ONE).astype(np.int64)
+    w = (rng.standard_normal(K) * ONE).astype(np.int64)
+    t = O.gemv(W, _rms(oracle, x, w), rows, K)
+    if ffn:
+        want = np.empty(ffn, dtype=np.int64)
+        g, u = t[:ffn].copy(), t[ffn:].copy()
+        oracle.q48o_silu_mul(want.ctypes.data, g.ctypes.data, u.ctypes.data, ffn)
+    else:
+        want = t
+    dW, dx, dw = ctx.to_device(W), ctx.to_device(x), ctx.to_device(w)
+    dy, ds = ctx.buffer(want.size), ctx.buffer(intllm.stats_words(K))
+    ctx.set_gemv_persistent(persistent)
+    try:
+        say("long normed gemv", M, ffn, "persistent", persistent)
+        ctx.rms_stats(ds.ptr, dx.ptr, K)
+        if ffn:
+            ctx.norm_gemv_swiglu_stats(dy.ptr, dW.ptr, dx.ptr, dw.ptr, ds.ptr, ffn, K)
+        else:
+            ctx.norm_gemv_stats(dy.ptr, dW.ptr, dx.ptr, dw.ptr, ds.ptr, M, K)
+        assert np.array_equal(dy.download(), want)
+    finally:
+        ctx.set_gemv_persistent(True)
+    for b in (dW, dx, dw, dy, ds):
+        b.free()
+
+
 @pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 5632), (256, 688), (13, 40), (3, 7681),
                                  (5128, 2048)])
 def test_gemv_residual_stats(ctx, oracle, M, K):
