@@ -647,6 +647,9 @@ k_gemv_p6(int64_t *__restrict__ y, const int64_t *__restrict__ W,
           const int64_t *__restrict__ r_in, int M, int K, int seg)
 {
     static_assert(NTF > 0 && (PRO == 0 || PRO == 3) && (EPI == 0 || EPI == 2), "p6 forms");
+    // the window crosses into the next group in the slots it frees: tile t of
+    // the next group must land in slot t % UNR
+    static_assert(NTF % UNR == 0, "p6 window must divide the tiles");
     extern __shared__ __align__(16) uint32_t xs[];   // 3 limbs per staged x
     __shared__ uint64_t part[2][NW][V4_RB][2];
     __shared__ int64_t pre[P6_MAXG][V4_RB];          // EPI 2: gate (0-3) / up (4-7)
