@@ -35,8 +35,8 @@ sys.path.insert(0, str(ROOT / "tests"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline sweep, from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE runs scaled by the counters' reading for a copy kernel of known
-# size (profiles/k_gemv_v5_decode_tinyllama.md); re-measure when the kernel changes
-TRAFFIC = 93553554
+# size (profiles/k_gemv_decode_tinyllama.md); re-measure when the kernel changes
+TRAFFIC = 93496847
 REF_CPU_MS_PER_TOK = 501.4   # reference decode, Zen 4, 1 thread
 # int8 GEMM: MI355X dense int8 MFMA peak; one Q16.48 MAC is 63 int8 products
 # (digit pairs a + b <= 13), 2 ops each
@@ -342,8 +342,8 @@ def main():
                    "layers": 22, "dim": 2048, "heads": 32, "kv_heads": 4, "ffn": 5632,
                    "vocab": 32000, "prompt_tokens": len(prompt), "positions": [p0, p0 + args.steps]},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_gemv_v5 (q48_gemv family: the 89 fused GEMV launches of a "
-                               "decode token, back to back)",
+                     "kernel": "k_gemv_v5 / k_gemv_p6 (q48_gemv family: the 89 fused GEMV "
+                               "launches of a decode token, back to back)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC,
                      "avg_launch_us": round(avg_us, 3),

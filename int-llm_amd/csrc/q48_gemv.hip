@@ -748,9 +748,9 @@ k_gemv_p6(int64_t *__restrict__ y, const int64_t *__restrict__ W,
     int i = 0;
     for (; grp < ngroups; grp += gridDim.x, ++i) {
         const int nxt = grp + (int)gridDim.x;
-        // the next group's rows (this group's again after the last: in
-        // bounds, never used)
-        const ulonglong2 *w2n = wrow(nxt < ngroups ? nxt : grp);
+        // the next group's rows; after the last group, group 0's (read by
+        // every block there, so they stay in cache: in bounds, never used)
+        const ulonglong2 *w2n = wrow(nxt < ngroups ? nxt : 0);
         Acc6 A = {0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < NTF; ++t) {
