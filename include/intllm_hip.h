@@ -239,6 +239,34 @@ int q48_norm_gemv_swiglu_stats(q48_ctx *ctx, int64_t *out, const int64_t *Wgu,
 int q48_gemv_residual_stats(q48_ctx *ctx, int64_t *acc, const int64_t *W, const int64_t *x,
                             int M, int K, int64_t *stats);
 
+/* ---- bfloat16-resident weights ------------------------------------------
+ * The reference's .mgwc format (llama_int.c:1906-1929) keeps weights as
+ * their bfloat16 bits and expands them with bfloat16_to_q1648
+ * (safetensors.h:115-152) at load.  These GEMVs keep the bits in device
+ * memory (2 bytes per weight) and expand each one in the kernel with the
+ * same rule, so for weights that are bfloat16 values the results are the
+ * int64-weight results, bit for bit, from a quarter of the weight bytes.
+ * W is [M][K] uint16, 16-byte aligned; x, norm_w and stats 16-byte aligned;
+ * K a multiple of 512 (else Q48_EINVAL).  No reference counterpart beyond
+ * the format: the reference expands at load time. */
+
+/* out[i] = the bfloat16 bits b with bfloat16_to_q1648(b) == in[i], for n
+ * elements; *inexact = 1 (host int) when some in[i] has no such b (then the
+ * weights must stay int64).  Synchronises. */
+int q48_bf16_pack(q48_ctx *ctx, uint16_t *out, const int64_t *in, size_t n, int *inexact);
+/* q48_gemv on bfloat16 weights. */
+int q48_gemv_bf16(q48_ctx *ctx, int64_t *y, const uint16_t *W, const int64_t *x, int M, int K);
+/* q48_norm_gemv_stats on bfloat16 weights. */
+int q48_norm_gemv_stats_bf16(q48_ctx *ctx, int64_t *y, const uint16_t *W, const int64_t *x,
+                             const int64_t *norm_w, const int64_t *stats, int M, int K);
+/* q48_norm_gemv_swiglu_stats on bfloat16 weights (Wgu is [2 ffn][K]). */
+int q48_norm_gemv_swiglu_stats_bf16(q48_ctx *ctx, int64_t *out, const uint16_t *Wgu,
+                                    const int64_t *x, const int64_t *norm_w,
+                                    const int64_t *stats, int ffn, int K);
+/* q48_gemv_residual_stats on bfloat16 weights. */
+int q48_gemv_residual_stats_bf16(q48_ctx *ctx, int64_t *acc, const uint16_t *W,
+                                 const int64_t *x, int M, int K, int64_t *stats);
+
 /* ---- device-resident decode steps (graph replay) ---------------------------- */
 /* No reference counterpart: llama_int's generate (llama_int.c:3067-3135)
  * passes token and pos as C arguments each call.  In step mode q48_embed,

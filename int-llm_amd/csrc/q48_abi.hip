@@ -913,3 +913,87 @@ int q48_graph_drop(q48_ctx *c)
 }
 
 } // extern "C"
+
+/* ---- bfloat16-resident weights ------------------------------------------ */
+
+namespace {
+double gemv_bytes_bf16(int M, int K, int out)
+{
+    return 2.0 * (double)M * K + 8.0 * ((double)K + out);
+}
+// x, norm_w, stats 16-byte aligned, W 16-byte aligned, K a multiple of 512
+bool bad_bf16(const void *y, const void *W, const void *x, const void *nw, const void *st, int K)
+{
+    return !y || !W || !x || ((uintptr_t)y & 7) || ((uintptr_t)W & 15) || ((uintptr_t)x & 15) ||
+           (nw && ((uintptr_t)nw & 15)) || (st && ((uintptr_t)st & 15)) || !q48_gemv_bf16_ok(K);
+}
+int bf16_fused(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
+               const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M, int K, int pro,
+               int epi, double bytes)
+{
+    int prc;
+    q48_ctx::ProfRec *pr = prof_begin(c, bytes, &prc);
+    if (prc)
+        return prc;
+    const int rc = q48_launch_gemv_fused_bf16(c, y, W, x, norm_w, r_in, r_out, M, K, pro, epi);
+    return prof_end(c, pr, rc < 0 ? Q48_EINVAL : launch_rc(rc));
+}
+} // namespace
+
+int q48_bf16_pack(q48_ctx *c, uint16_t *out, const int64_t *in, size_t n, int *inexact)
+{
+    if (!c || !out || !in || !inexact || ((uintptr_t)in & 7) || ((uintptr_t)out & 1))
+        return Q48_EINVAL;
+    int *flag = c->d_scalar + 40;
+    int rc = launch_rc(q48_launch_zero(c, flag, sizeof(int)));
+    if (rc)
+        return rc;
+    if (n) {
+        rc = launch_rc(q48_launch_bf16_pack(c, out, in, n, flag));
+        if (rc)
+            return rc;
+    }
+    int f = 0;
+    if (hipMemcpyAsync(&f, flag, sizeof(int), hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q48_EHIP;
+    *inexact = f != 0;
+    return Q48_OK;
+}
+
+int q48_gemv_bf16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x, int M, int K)
+{
+    if (!c || bad_bf16(y, W, x, nullptr, nullptr, K) || M <= 0 || M > kMaxDim)
+        return Q48_EINVAL;
+    return bf16_fused(c, y, W, x, nullptr, nullptr, nullptr, M, K, 0, 0, gemv_bytes_bf16(M, K, M));
+}
+
+int q48_norm_gemv_stats_bf16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
+                             const int64_t *norm_w, const int64_t *stats, int M, int K)
+{
+    if (!c || !norm_w || !stats || bad_bf16(y, W, x, norm_w, stats, K) || M <= 0 ||
+        M > kMaxDim)
+        return Q48_EINVAL;
+    return bf16_fused(c, y, W, x, norm_w, stats, nullptr, M, K, 3, 0, gemv_bytes_bf16(M, K, M));
+}
+
+int q48_norm_gemv_swiglu_stats_bf16(q48_ctx *c, int64_t *out, const uint16_t *Wgu,
+                                    const int64_t *x, const int64_t *norm_w,
+                                    const int64_t *stats, int ffn, int K)
+{
+    if (!c || !norm_w || !stats || bad_bf16(out, Wgu, x, norm_w, stats, K) || ffn <= 0 ||
+        ffn > kMaxDim / 2)
+        return Q48_EINVAL;
+    return bf16_fused(c, out, Wgu, x, norm_w, stats, nullptr, 2 * ffn, K, 3, 2,
+                      gemv_bytes_bf16(2 * ffn, K, ffn));
+}
+
+int q48_gemv_residual_stats_bf16(q48_ctx *c, int64_t *acc, const uint16_t *W, const int64_t *x,
+                                 int M, int K, int64_t *stats)
+{
+    if (!c || !stats || bad_bf16(acc, W, x, nullptr, stats, K) || M <= 0 || M > kMaxDim)
+        return Q48_EINVAL;
+    return bf16_fused(c, acc, W, x, nullptr, nullptr, stats, M, K, 0, 4,
+                      gemv_bytes_bf16(M, K, M));
+}
+

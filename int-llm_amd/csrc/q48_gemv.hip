@@ -255,25 +255,77 @@ __device__ __forceinline__ q48_u128 acc6_value(const Acc6 &A)
            ((q48_u128)A.ws << 63);
 }
 
-// One batch of UNR tiles of a lane (16 weights of a row per tile, two per
-// lane) against the staged x limbs, 12 v_mad_u64_u32 per tile; tiles at or
+// bfloat16_to_q1648 (safetensors.h:115-152), bit for bit: zero and subnormal
+// exponents give 0, exponent 255 gives +-32000 << 48, otherwise (128 + m)
+// shifted by e - 86 (left shifts wrap mod 2^64, right shifts truncate,
+// shifts of 64 or more give 0), then the sign (two's complement negation).
+// Branch-free (selects and masks only): it runs once per weight inside the
+// unrolled GEMV loop.
+__device__ __forceinline__ int64_t q48_bf16(uint32_t b)
+{
+    const int e = (int)((b >> 7) & 0xffu);
+    const uint64_t sig = 128u + (b & 0x7fu);
+    const int sh = e - 86;
+    const uint64_t lft = sig << (sh & 63), rgt = sig >> ((-sh) & 63);
+    const uint64_t left = 0ull - (uint64_t)(sh >= 0);
+    // a shift of 64 or more either way, or a zero / subnormal exponent: 0
+    const uint64_t ok = 0ull - (uint64_t)((unsigned)(sh + 63) < 127u && e != 0);
+    uint64_t r = (rgt ^ ((lft ^ rgt) & left)) & ok;
+    const uint64_t inf = 0ull - (uint64_t)(e == 0xff);
+    r = (r & ~inf) | (((uint64_t)32000 << 48) & inf);
+    const uint64_t neg = 0ull - (uint64_t)(b >> 15);
+    return (int64_t)((r ^ neg) - neg);
+}
+
+// Weight formats of the decode GEMVs: WT 0 = int64 Q16.48 (a 128-byte tile of
+// a row is 16 weights, 2 per lane); WT 1 = bfloat16 bits (a tile is 64
+// weights, 8 per lane), expanded exactly with q48_bf16.  A wave's segment is
+// TE[WT] * NTF elements.
+template <int WT> struct WFmt;
+template <> struct WFmt<0> { static constexpr int ES = 8, TE = 16; };
+template <> struct WFmt<1> { static constexpr int ES = 2, TE = 64; };
+
+// One 128-byte tile t of this lane's row against the staged x limbs (3 per
+// element at xw[3 j]).
+template <int WT>
+__device__ __forceinline__ void mac_tile(Acc6 &A, const uint32_t *xw, int l8, int t, ulonglong2 w)
+{
+    if constexpr (WT == 0) {
+        const uint32_t *p = xw + 6 * l8 + 48 * t;
+        mac6(A, p[0], p[1], p[2], w.x);
+        mac6(A, p[3], p[4], p[5], w.y);
+    } else {
+        // one tile at a time: without the barrier the scheduler hoists the
+        // limb reads and expansions of every tile and runs out of registers
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t *p = xw + 3 * (64 * t + 8 * l8);
+        const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)(w.x >> 32), (uint32_t)w.y,
+                               (uint32_t)(w.y >> 32)};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            mac6(A, p[3 * e], p[3 * e + 1], p[3 * e + 2],
+                 (uint64_t)q48_bf16((u[e >> 1] >> (16 * (e & 1))) & 0xffffu));
+            if (e & 1)
+                __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// One batch of UNR tiles of a lane against the staged x limbs; tiles at or
 // past nt are skipped (uniform branch).
-template <int UNR>
-__device__ __forceinline__ void mac_tiles(Acc6 &A, const uint32_t *xl,
+template <int UNR, int WT>
+__device__ __forceinline__ void mac_tiles(Acc6 &A, const uint32_t *xw, int l8,
                                           const ulonglong2 (&w)[UNR], int t0, int nt)
 {
 #pragma unroll
     for (int u = 0; u < UNR; ++u)
-        if (t0 + u < nt) {
-            const uint32_t *p = xl + 48 * (t0 + u);
-            mac6(A, p[0], p[1], p[2], w[u].x);
-            mac6(A, p[3], p[4], p[5], w[u].y);
-        }
+        if (t0 + u < nt)
+            mac_tile<WT>(A, xw, l8, t0 + u, w[u]);
 }
 
-template <int NW, int UNR, int PRO, int EPI, int NTF>
+template <int NW, int UNR, int PRO, int EPI, int NTF, int WT = 0>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void k_gemv_v5(int64_t *__restrict__ y,
-                                                    const int64_t *__restrict__ W,
+                                                    const void *__restrict__ Wv,
                                                     const int64_t *__restrict__ x,
                                                     const int64_t *__restrict__ norm_w,
                                                     const int64_t *__restrict__ r_in,
@@ -303,9 +355,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     const int row = EPI == 2 ? (g < 4 ? pr : ffn + pr) : row0 + g;
     const bool live = EPI == 2 ? pr < ffn : row < M;
     // rows past the end read row 0 (in bounds, never accumulated)
-    const ulonglong2 *w2 =
-        reinterpret_cast<const ulonglong2 *>(W + (size_t)(live ? row : 0) * K + k0) + l8;
-    const int nt = kn >> 4;   // whole 16-element tiles of the segment
+    constexpr int ES = WFmt<WT>::ES, SEGC = WFmt<WT>::TE * NTF;
+    const ulonglong2 *w2 = reinterpret_cast<const ulonglong2 *>(
+                               static_cast<const char *>(Wv) +
+                               ((size_t)(live ? row : 0) * K + k0) * ES) + l8;
+    const int nt = kn / WFmt<WT>::TE;   // whole tiles of the segment
 
     // the residual rows this block adds to (EPI 1, 3, 4): read now, used last
     constexpr bool RES = EPI == 1 || EPI == 3 || EPI == 4;
@@ -319,7 +373,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     // With NTF known each lane preloads np / 64 of the np = K / 8 = 2 NW NTF
     // partials (16-byte aligned, checked on the host); otherwise they are
     // read in a loop when needed.
-    constexpr int PC = NTF > 0 ? (2 * NW * NTF + 63) / 64 : 1;
+    constexpr int PC = NTF > 0 ? (NW * SEGC / 8 + 63) / 64 : 1;
     uint64_t plo[PC], phi[PC];
     const int np = (K + 7) >> 3;
     const uint64_t *st = reinterpret_cast<const uint64_t *>(r_in);
@@ -371,7 +425,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     // norm_w are 16-byte aligned (checked on the host): a lane loads element
     // pairs, 16 bytes at a time.  Otherwise single elements, 8 or 16 of them
     // per lane per staging batch.
-    constexpr int XB = NTF > 0 ? (16 * NTF + 127) / 128 : (PRO ? 8 : 16);
+    constexpr int XB = NTF > 0 ? (SEGC + 127) / 128 : (PRO ? 8 : 16);
     constexpr int XW = NTF > 0 ? 2 : 1;   // elements per load
     int64_t xv[XB * XW], nw[XB * XW];
     const int xk = kn > 0 ? k0 : 0, xlast = max(kn - XW, 0);
@@ -394,7 +448,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         }
     }
     asm volatile("" ::: "memory");   // keep the x loads ahead of the weight loads
-    const ulonglong2 *wt = nt > 0 ? w2 : reinterpret_cast<const ulonglong2 *>(W);
+    const ulonglong2 *wt = nt > 0 ? w2 : reinterpret_cast<const ulonglong2 *>(Wv);
     const int tlast = max(nt - 1, 0), tstep = nt > 0 ? 8 : 0;
     ulonglong2 wa[UNR];
 #pragma unroll
@@ -475,23 +529,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         // pipeline is full instead of stalling on a long run of issues)
 #pragma unroll
         for (int t = 0; t < NTF; ++t) {
-            const uint32_t *p = xl + 48 * t;
-            mac6(A, p[0], p[1], p[2], wa[t % UNR].x);
-            mac6(A, p[3], p[4], p[5], wa[t % UNR].y);
+            mac_tile<WT>(A, xw, l8, t, wa[t % UNR]);
             if (t + UNR < NTF)
                 wa[t % UNR] = w2[(t + UNR) * 8];
         }
     } else {
-        mac_tiles<UNR>(A, xl, wa, 0, nt);
+        mac_tiles<UNR, WT>(A, xw, l8, wa, 0, nt);
         for (int t0 = UNR; t0 < nt; t0 += UNR) {
 #pragma unroll
             for (int u = 0; u < UNR; ++u)
                 wa[u] = w2[min(t0 + u, nt - 1) * 8];
-            mac_tiles<UNR>(A, xl, wa, t0, nt);
+            mac_tiles<UNR, WT>(A, xw, l8, wa, t0, nt);
         }
     }
     // the kn % 16 elements (even) of the segment's end, one pair per lane
-    if (2 * l8 < (kn & 15)) {
+    if (WT == 0 && 2 * l8 < (kn & 15)) {
         const ulonglong2 w1 = w2[nt * 8];
         const uint32_t *p = xl + 48 * nt;
         mac6(A, p[0], p[1], p[2], w1.x);
@@ -640,9 +692,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
 // ---------------------------------------------------------------------------
 constexpr int P6_MAXG = 16;   // row groups per block at most
 
-template <int NW, int UNR, int PRO, int EPI, int NTF>
+template <int NW, int UNR, int PRO, int EPI, int NTF, int WT = 0>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void
-k_gemv_p6(int64_t *__restrict__ y, const int64_t *__restrict__ W,
+k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
           const int64_t *__restrict__ x, const int64_t *__restrict__ norm_w,
           const int64_t *__restrict__ r_in, int M, int K, int seg)
 {
@@ -650,6 +702,7 @@ k_gemv_p6(int64_t *__restrict__ y, const int64_t *__restrict__ W,
     // the window crosses into the next group in the slots it frees: tile t of
     // the next group must land in slot t % UNR
     static_assert(NTF % UNR == 0, "p6 window must divide the tiles");
+    constexpr int ES = WFmt<WT>::ES, SEGC = WFmt<WT>::TE * NTF;
     extern __shared__ __align__(16) uint32_t xs[];   // 3 limbs per staged x
     __shared__ uint64_t part[2][NW][V4_RB][2];
     __shared__ int64_t pre[P6_MAXG][V4_RB];          // EPI 2: gate (0-3) / up (4-7)
@@ -668,12 +721,14 @@ k_gemv_p6(int64_t *__restrict__ y, const int64_t *__restrict__ W,
         const int pr = grp * 4 + (g & 3);
         const int row = EPI == 2 ? (g < 4 ? pr : ffn + pr) : grp * V4_RB + g;
         const bool live = EPI == 2 ? pr < ffn : row < M;
-        return reinterpret_cast<const ulonglong2 *>(W + (size_t)(live ? row : 0) * K + k0) + l8;
+        return reinterpret_cast<const ulonglong2 *>(static_cast<const char *>(Wv) +
+                                                    ((size_t)(live ? row : 0) * K + k0) * ES) +
+               l8;
     };
 
     // PRO 3 partial sums first, then x (and the norm weights), then the
     // first group's weight tiles: vmcnt retires in issue order
-    constexpr int PC = (2 * NW * NTF + 63) / 64;
+    constexpr int PC = (NW * SEGC / 8 + 63) / 64;
     uint64_t plo[PC], phi[PC];
     const int np = (K + 7) >> 3;
     const uint64_t *st = reinterpret_cast<const uint64_t *>(r_in);
@@ -686,7 +741,7 @@ k_gemv_p6(int64_t *__restrict__ y, const int64_t *__restrict__ W,
             phi[c] = v.y;
         }
     }
-    constexpr int XB = (16 * NTF + 127) / 128;
+    constexpr int XB = (SEGC + 127) / 128;
     int64_t xv[2 * XB], nw[2 * XB];
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
@@ -744,7 +799,6 @@ k_gemv_p6(int64_t *__restrict__ y, const int64_t *__restrict__ W,
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    const uint32_t *xl = xw + 6 * l8;
     int i = 0;
     for (; grp < ngroups; grp += gridDim.x, ++i) {
         const int nxt = grp + (int)gridDim.x;
@@ -754,9 +808,7 @@ k_gemv_p6(int64_t *__restrict__ y, const int64_t *__restrict__ W,
         Acc6 A = {0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < NTF; ++t) {
-            const uint32_t *p = xl + 48 * t;
-            mac6(A, p[0], p[1], p[2], wa[t % UNR].x);
-            mac6(A, p[3], p[4], p[5], wa[t % UNR].y);
+            mac_tile<WT>(A, xw, l8, t, wa[t % UNR]);
             if (t + UNR < NTF)
                 wa[t % UNR] = w2[(t + UNR) * 8];
             else
@@ -958,6 +1010,59 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
     return (int)hipGetLastError();
 }
 
+// The bfloat16-weight forms (WT 1): every wave takes K / 512 whole tiles of 64
+// weights (K a multiple of 512), x and norm_w 16-byte aligned; other shapes
+// are refused (Q48_EINVAL from the caller).  Long normed projections take the
+// persistent form like the int64 weights.
+template <int PRO, int EPI, int NTF>
+static int launch_b16_ntf(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
+                          const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
+                          int K)
+{
+    constexpr int NW = 8, UNR = NTF < 4 ? NTF : 4;
+    const int seg = K / NW;
+    const size_t lds = (size_t)seg * NW * 3 * sizeof(uint32_t);
+    const int blocks = EPI == 2 ? (M / 2 + 3) / 4 : (M + V4_RB - 1) / V4_RB;
+    if constexpr ((PRO == 0 || PRO == 3) && (EPI == 0 || EPI == 2) && NTF % UNR == 0) {
+        const int grid = 2 * c->cu_count;
+        if (blocks > 2 * grid && blocks <= P6_MAXG * grid && c->gemv_persistent) {
+            hipLaunchKernelGGL((k_gemv_p6<NW, UNR, PRO, EPI, NTF, 1>), dim3(grid),
+                               dim3(64 * NW), lds, c->stream, y, W, x, norm_w, r_in, M, K, seg);
+            return (int)hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((k_gemv_v5<NW, UNR, PRO, EPI, NTF, 1>), dim3(blocks), dim3(64 * NW), lds,
+                       c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count, M,
+                       K, seg);
+    return (int)hipGetLastError();
+}
+
+template <int PRO, int EPI>
+static int launch_b16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
+                      const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M, int K)
+{
+    switch (K) {
+    case 512:
+        return launch_b16_ntf<PRO, EPI, 1>(c, y, W, x, norm_w, r_in, r_out, M, K);
+    case 1024:
+        return launch_b16_ntf<PRO, EPI, 2>(c, y, W, x, norm_w, r_in, r_out, M, K);
+    case 2048:
+        return launch_b16_ntf<PRO, EPI, 4>(c, y, W, x, norm_w, r_in, r_out, M, K);
+    default: {
+        // other K (a multiple of 512): batches of 4 tiles in a loop (an
+        // unrolled chain of more tiles runs out of registers)
+        constexpr int NW = 8;
+        const int seg = K / NW;
+        const size_t lds = (size_t)seg * NW * 3 * sizeof(uint32_t);
+        const int blocks = EPI == 2 ? (M / 2 + 3) / 4 : (M + V4_RB - 1) / V4_RB;
+        hipLaunchKernelGGL((k_gemv_v5<NW, 4, PRO, EPI, 0, 1>), dim3(blocks), dim3(64 * NW), lds,
+                           c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
+                           M, K, seg);
+        return (int)hipGetLastError();
+    }
+    }
+}
+
 // Per-row sums mod 2^64 (one wave per row): the 2^63 correction terms of
 // the flipped-limb GEMM.
 __global__ __launch_bounds__(256) void k_rowsum(uint64_t *__restrict__ out,
@@ -1109,6 +1214,57 @@ int q48_launch_gemv_fused(q48_ctx *c, int64_t *y, const int64_t *W, const int64_
         return launch_v4<0, 3>(c, y, W, x, nullptr, nullptr, r_out, M, K);
     return epi == 1 ? launch_v4<0, 1>(c, y, W, x, nullptr, nullptr, nullptr, M, K)
                     : launch_v4<0, 0>(c, y, W, x, nullptr, nullptr, nullptr, M, K);
+}
+
+bool q48_gemv_bf16_ok(int K) { return K > 0 && K % 512 == 0 && K <= V2_MAX_K; }
+
+int q48_launch_gemv_fused_bf16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
+                               const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
+                               int K, int pro, int epi)
+{
+    if (pro == 3)
+        return epi == 2 ? launch_b16<3, 2>(c, y, W, x, norm_w, r_in, nullptr, M, K)
+                        : launch_b16<3, 0>(c, y, W, x, norm_w, r_in, nullptr, M, K);
+    if (epi == 4)
+        return launch_b16<0, 4>(c, y, W, x, nullptr, nullptr, r_out, M, K);
+    return launch_b16<0, 0>(c, y, W, x, nullptr, nullptr, nullptr, M, K);
+}
+
+// int64 -> bfloat16 bits where exact: b is the candidate with 8 significant
+// bits (bfloat16_to_q1648's exponent rule inverted), then q48_bf16(b) == v
+// is checked; any element that does not round-trip sets *inexact.
+__global__ __launch_bounds__(256) void k_bf16_pack(uint16_t *__restrict__ out,
+                                                  const int64_t *__restrict__ in, size_t n,
+                                                  int *__restrict__ inexact)
+{
+    bool bad = false;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * 256) {
+        const int64_t v = in[i];
+        uint32_t b = 0;
+        if (v != 0) {
+            const uint64_t mag = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
+            const int p = 63 - __builtin_clzll(mag);
+            const int sh = p - 7;   // shift of the 8-bit significand
+            const uint32_t sig = sh >= 0 ? (uint32_t)(mag >> sh) : (uint32_t)(mag << (-sh));
+            const int e = sh + 86;
+            b = (v < 0 ? 0x8000u : 0u) | ((uint32_t)(e & 0xff) << 7) | (sig & 0x7fu);
+            if (e < 1 || e > 254)
+                bad = true;
+        }
+        bad |= q48_bf16(b) != v;
+        out[i] = (uint16_t)b;
+    }
+    if (bad)
+        __hip_atomic_store(inexact, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+int q48_launch_bf16_pack(q48_ctx *c, uint16_t *out, const int64_t *in, size_t n, int *inexact)
+{
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(k_bf16_pack, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256),
+                       0, c->stream, out, in, n, inexact);
+    return (int)hipGetLastError();
 }
 
 int q48_launch_rms_inv(q48_ctx *c, int64_t *r_out, int64_t *out, const int64_t *x,

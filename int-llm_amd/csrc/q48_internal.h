@@ -52,6 +52,14 @@ bool q48_gemv_v2_ok(const int64_t *W, int K);
 int q48_launch_gemv_fused(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
                           const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
                           int K, int pro, int epi);
+// the same fused GEMVs on bfloat16 weight bits (pro 0/3, epi 0/2/4; K =
+// 512, 1024, 2048 or 5632: q48_gemv_bf16_ok); -1 for other K
+bool q48_gemv_bf16_ok(int K);
+int q48_launch_gemv_fused_bf16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
+                               const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
+                               int K, int pro, int epi);
+// out[i] = the bfloat16 bits of in[i] where exact; *inexact = 1 otherwise
+int q48_launch_bf16_pack(q48_ctx *c, uint16_t *out, const int64_t *in, size_t n, int *inexact);
 int q48_launch_rms_inv(q48_ctx *c, int64_t *r_out, int64_t *out, const int64_t *x,
                        const int64_t *table, const int *d_token, int token, int dim);
 int q48_launch_rms_apply(q48_ctx *c, int64_t *out, const int64_t *x, const int64_t *w,

@@ -53,6 +53,9 @@ struct q48h_model {
     int graph_ready;            /* the context graph holds this model's decode step */
     int graph_long;             /* ... captured at a position served by split attention */
     int prefetch;               /* attention warms the cache with W_o (fused modes) */
+    uint16_t *wb;               /* device: bfloat16 bits of the projection matrices and
+                                   lm_head, at the element offsets of w (else NULL) */
+    int bf16;                   /* mode 3 reads the matrices from wb */
 };
 
 /* ---------------------------------------------------------------------- */
@@ -242,10 +245,75 @@ int q48h_model_create(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg)
     return model_alloc(out, ctx, cfg, 0);
 }
 
+static void drop_graph(q48h_model *m)
+{
+    if (m->graph_ready) {
+        q48_graph_drop(m->ctx);
+        m->graph_ready = 0;
+    }
+}
+
+/* Forget the bfloat16 copy of the weights (they are about to change). */
+static void drop_bf16(q48h_model *m)
+{
+    if (m->wb) {
+        q48_free(m->ctx, m->wb);
+        m->wb = NULL;
+    }
+    if (m->bf16) {
+        m->bf16 = 0;
+        drop_graph(m);
+    }
+}
+
+int q48h_model_set_bf16(q48h_model *m, int on)
+{
+    if (!m)
+        return Q48_EINVAL;
+    on = on != 0;
+    if (on && !m->wb) {
+        const q48h_config *c = &m->c;
+        int kvd = c->n_kv_heads * c->head_dim;
+        if (c->dim % 512 || c->ffn % 512)
+            return Q48_EINVAL;   /* the bfloat16 GEMVs take K = 512 j */
+        int mrc = q48_malloc(m->ctx, (void **)&m->wb, weight_elems(m) * 2);
+        if (mrc)
+            return mrc;
+        /* the four projections of every layer and lm_head; each must be
+         * bfloat16 values exactly, else the weights stay int64 only */
+        struct { size_t off, n; } t[4];
+        int inexact = 0, rc = Q48_OK;
+        for (int l = 0; l < c->n_layers && !rc && !inexact; ++l) {
+            size_t b = m->off_layers + (size_t)l * m->layer_elems;
+            t[0].off = b + m->lo_qkv; t[0].n = (size_t)(c->dim + 2 * kvd) * c->dim;
+            t[1].off = b + m->lo_wo;  t[1].n = (size_t)c->dim * c->dim;
+            t[2].off = b + m->lo_gu;  t[2].n = (size_t)2 * c->ffn * c->dim;
+            t[3].off = b + m->lo_wd;  t[3].n = (size_t)c->dim * c->ffn;
+            for (int i = 0; i < 4 && !rc && !inexact; ++i)
+                rc = q48_bf16_pack(m->ctx, m->wb + t[i].off, m->w + t[i].off, t[i].n,
+                                   &inexact);
+        }
+        if (!rc && !inexact)
+            rc = q48_bf16_pack(m->ctx, m->wb + m->off_lm, m->w + m->off_lm,
+                               (size_t)c->vocab * c->dim, &inexact);
+        if (rc || inexact) {
+            q48_free(m->ctx, m->wb);
+            m->wb = NULL;
+            return rc ? rc : Q48_EINVAL;
+        }
+    }
+    if (m->bf16 != on) {
+        m->bf16 = on;
+        drop_graph(m);
+    }
+    return Q48_OK;
+}
+
 void q48h_model_free(q48h_model *m)
 {
     if (!m)
         return;
+    q48_free(m->ctx, m->wb);
     q48_free(m->ctx, m->w);
     q48_free(m->ctx, m->kc);
     q48_free(m->ctx, m->vc);
@@ -340,6 +408,7 @@ int q48h_upload(q48h_model *m, const char *name, const int64_t *host, int64_t n)
     int64_t want;
     if (tensor_slot(m, name, &dst, &want) || n != want)
         return Q48_EINVAL;
+    drop_bf16(m);   /* the bfloat16 copy would be stale */
     return q48_memcpy_h2d(m->ctx, dst, host, (size_t)n * 8);
 }
 
@@ -632,7 +701,11 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
     const int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
     int64_t *q = m->qkv, *k = m->qkv + dim, *v = m->qkv + dim + kvd;
 
-    if (m->fused == 3) {
+    const uint16_t *bb = m->bf16 ? m->wb + m->off_layers + (size_t)l * m->layer_elems : NULL;
+    if (m->fused == 3 && bb) {
+        TRY(q48_norm_gemv_stats_bf16(x, m->qkv, bb + m->lo_qkv, m->hidden, b + m->lo_an,
+                                     m->s_attn, dim + 2 * kvd, dim));
+    } else if (m->fused == 3) {
         /* s_attn holds the partial sums of squares of hidden (from the
          * embedding or the previous layer's down projection) */
         TRY(q48_norm_gemv_stats(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an, m->s_attn,
@@ -653,7 +726,14 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
     else
         TRY(q48_attn_decode_rope(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
                                  c->n_kv_heads, hd, c->max_seq));
-    if (m->fused == 3) {
+    if (m->fused == 3 && bb) {
+        TRY(q48_gemv_residual_stats_bf16(x, m->hidden, bb + m->lo_wo, m->attn, dim, dim,
+                                         m->s_ffn));
+        TRY(q48_norm_gemv_swiglu_stats_bf16(x, m->h_ffn, bb + m->lo_gu, m->hidden, b + m->lo_fn,
+                                            m->s_ffn, ffn, dim));
+        TRY(q48_gemv_residual_stats_bf16(x, m->hidden, bb + m->lo_wd, m->h_ffn, dim, ffn,
+                                         m->s_attn));
+    } else if (m->fused == 3) {
         TRY(q48_gemv_residual_stats(x, m->hidden, b + m->lo_wo, m->attn, dim, dim, m->s_ffn));
         TRY(q48_norm_gemv_swiglu_stats(x, m->h_ffn, b + m->lo_gu, m->hidden, b + m->lo_fn,
                                        m->s_ffn, ffn, dim));
@@ -705,8 +785,12 @@ static int enqueue_forward(q48h_model *m, int token, int pos)
         TRY(q48_embed_stats(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim, m->s_attn));
         for (int l = 0; l < c->n_layers; ++l)
             TRY(layer_forward_fused(m, l, pos));
-        TRY(q48_norm_gemv_stats(m->ctx, m->logits, m->w + m->off_lm, m->hidden,
-                                m->w + m->off_norm, m->s_attn, c->vocab, c->dim));
+        if (m->bf16)
+            TRY(q48_norm_gemv_stats_bf16(m->ctx, m->logits, m->wb + m->off_lm, m->hidden,
+                                         m->w + m->off_norm, m->s_attn, c->vocab, c->dim));
+        else
+            TRY(q48_norm_gemv_stats(m->ctx, m->logits, m->w + m->off_lm, m->hidden,
+                                    m->w + m->off_norm, m->s_attn, c->vocab, c->dim));
     } else if (m->fused == 2) {
         TRY(q48_embed_rms(m->ctx, m->hidden, m->w + m->off_embed, token, c->dim, m->r_attn));
         for (int l = 0; l < c->n_layers; ++l)
@@ -943,11 +1027,23 @@ int q48h_gemv_sweep(q48h_model *m, int reps, int *launches, double *bytes)
     int dim = c->dim, kvd = c->n_kv_heads * c->head_dim, ffn = c->ffn;
     int n = 0;
     double b = 0;
-#define GB(M, K, out) (b += 8.0 * ((double)(M) * (K) + (K) + (out)), ++n)
+    const int wb16 = m->fused == 3 && m->bf16;
+    const double wbytes = wb16 ? 2.0 : 8.0;
+#define GB(M, K, out) (b += wbytes * (double)(M) * (K) + 8.0 * ((double)(K) + (out)), ++n)
     for (int r = 0; r < reps; ++r) {
         for (int l = 0; l < c->n_layers; ++l) {
             const int64_t *w = m->w + m->off_layers + (size_t)l * m->layer_elems;
-            if (m->fused == 3) {
+            const uint16_t *bw = wb16 ? m->wb + m->off_layers + (size_t)l * m->layer_elems : NULL;
+            if (wb16) {
+                TRY(q48_norm_gemv_stats_bf16(x, m->qkv, bw + m->lo_qkv, m->hidden, w + m->lo_an,
+                                             m->s_attn, dim + 2 * kvd, dim));
+                TRY(q48_gemv_residual_stats_bf16(x, m->hidden, bw + m->lo_wo, m->attn, dim, dim,
+                                                 m->s_ffn));
+                TRY(q48_norm_gemv_swiglu_stats_bf16(x, m->h_ffn, bw + m->lo_gu, m->hidden,
+                                                    w + m->lo_fn, m->s_ffn, ffn, dim));
+                TRY(q48_gemv_residual_stats_bf16(x, m->hidden, bw + m->lo_wd, m->h_ffn, dim, ffn,
+                                                 m->s_attn));
+            } else if (m->fused == 3) {
                 TRY(q48_norm_gemv_stats(x, m->qkv, w + m->lo_qkv, m->hidden, w + m->lo_an,
                                         m->s_attn, dim + 2 * kvd, dim));
                 TRY(q48_gemv_residual_stats(x, m->hidden, w + m->lo_wo, m->attn, dim, dim,
@@ -971,7 +1067,10 @@ int q48h_gemv_sweep(q48h_model *m, int reps, int *launches, double *bytes)
             GB(2 * ffn, dim, ffn);
             GB(dim, ffn, dim);
         }
-        if (m->fused == 3)
+        if (wb16)
+            TRY(q48_norm_gemv_stats_bf16(x, m->logits, m->wb + m->off_lm, m->hidden,
+                                         m->w + m->off_norm, m->s_attn, c->vocab, dim));
+        else if (m->fused == 3)
             TRY(q48_norm_gemv_stats(x, m->logits, m->w + m->off_lm, m->hidden,
                                     m->w + m->off_norm, m->s_attn, c->vocab, dim));
         else

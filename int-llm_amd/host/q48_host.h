@@ -120,6 +120,14 @@ void q48h_model_set_fused(q48h_model *m, int fused);
  * bits do not depend on it. */
 void q48h_model_set_prefetch(q48h_model *m, int on);
 
+/* Mode 3 with the projection matrices and lm_head read as bfloat16 bits
+ * (the reference's .mgwc representation, llama_int.c:1906-1929): on packs a
+ * device copy of them (2 bytes per weight, kept until the weights change)
+ * and uses it; the results are bit-identical to the int64 weights.
+ * Returns Q48_EINVAL, and changes nothing, when a weight is not exactly a
+ * bfloat16 value or dim or ffn is not a multiple of 512. */
+int q48h_model_set_bf16(q48h_model *m, int on);
+
 /* Greedy decode of n steps replayed from a captured graph: step i runs
  * forward(token_i, start_pos + i) and its argmax becomes token_{i+1} on the
  * device, with no host round trip between steps.  out_tokens[i] receives

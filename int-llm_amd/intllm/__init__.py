@@ -44,6 +44,11 @@ ABI_SIGNATURES = {
     "q48_gemv": [_P, _P, _P, _P, _I, _I],
     "q48_gemm": [_P, _P, _P, _P, _I, _I, _I],
     "q48_gemm_ex": [_P, _P, _P, _P, _I, _I, _I, _I],
+    "q48_bf16_pack": [_P, _P, _P, _SZ, C.POINTER(C.c_int)],
+    "q48_gemv_bf16": [_P, _P, _P, _P, _I, _I],
+    "q48_norm_gemv_stats_bf16": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "q48_norm_gemv_swiglu_stats_bf16": [_P, _P, _P, _P, _P, _P, _I, _I],
+    "q48_gemv_residual_stats_bf16": [_P, _P, _P, _P, _I, _I, _P],
     "q48_set_gemv_persistent": [_P, _I],
 
     "q48_rmsnorm": [_P, _P, _P, _P, _I],
@@ -219,6 +224,27 @@ class Context:
     def gemv(self, y, W, x, M, K):
         return check("q48_gemv", hip_lib().q48_gemv(self.h, y, W, x, M, K))
 
+    def bf16_pack(self, out, inp, n) -> bool:
+        """Pack n int64 at inp into bfloat16 bits at out; False if any is inexact."""
+        flag = C.c_int()
+        check("q48_bf16_pack", hip_lib().q48_bf16_pack(self.h, out, inp, n, C.byref(flag)))
+        return flag.value == 0
+
+    def gemv_bf16(self, y, W, x, M, K):
+        return check("q48_gemv_bf16", hip_lib().q48_gemv_bf16(self.h, y, W, x, M, K))
+
+    def norm_gemv_stats_bf16(self, y, W, x, norm_w, stats, M, K):
+        return check("q48_norm_gemv_stats_bf16",
+                     hip_lib().q48_norm_gemv_stats_bf16(self.h, y, W, x, norm_w, stats, M, K))
+
+    def norm_gemv_swiglu_stats_bf16(self, out, Wgu, x, norm_w, stats, ffn, K):
+        return check("q48_norm_gemv_swiglu_stats_bf16", hip_lib().q48_norm_gemv_swiglu_stats_bf16(
+            self.h, out, Wgu, x, norm_w, stats, ffn, K))
+
+    def gemv_residual_stats_bf16(self, acc, W, x, M, K, stats):
+        return check("q48_gemv_residual_stats_bf16",
+                     hip_lib().q48_gemv_residual_stats_bf16(self.h, acc, W, x, M, K, stats))
+
     def set_gemv_persistent(self, on: bool):
         return check("q48_set_gemv_persistent", hip_lib().q48_set_gemv_persistent(self.h, int(on)))
 
@@ -391,6 +417,7 @@ HOST_SIGNATURES = {
                           C.POINTER(Stats)], C.c_int),
     "q48h_model_set_fused": ([_P, _I], None),
     "q48h_model_set_prefetch": ([_P, _I], None),
+    "q48h_model_set_bf16": ([_P, _I], C.c_int),
 
     "q48h_gemv_sweep": ([_P, _I, C.POINTER(C.c_int), C.POINTER(C.c_double)], C.c_int),
     "q48h_decode_graph": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
@@ -486,6 +513,10 @@ class HostModel:
         """Warm the device cache with each layer's W_o during its attention."""
         host_lib().q48h_model_set_prefetch(self.h, int(bool(on)))
 
+
+    def set_bf16(self, on: bool):
+        """Read the projection matrices and lm_head as bfloat16 bits (mode 3)."""
+        check("q48h_model_set_bf16", host_lib().q48h_model_set_bf16(self.h, int(bool(on))))
 
     def set_fused(self, mode: int):
         """0: one op per reference step; 1: fused with per-block norm

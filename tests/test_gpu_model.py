@@ -271,3 +271,56 @@ def test_tinyllama_graph_decode_bit_exact(ctx):
         print(f"graph decode {1e3 * st.decode_s / max(1, st.decode_tokens):.3f} ms/tok", flush=True)
     finally:
         m.free()
+
+
+def test_tinyllama_bf16_weights_bit_exact(ctx):
+    """Config 3 with the projection matrices and lm_head read as bfloat16 bits
+    (2 bytes per weight): the same 128-token stream and per-step logits
+    hashes as the reference, eager and graph-replayed."""
+    g = golden("tinyllama_generate.json")
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    try:
+        say("tinyllama synth, bf16 pack")
+        m.synth(g["seed"], threads())
+        m.set_bf16(True)
+        say("tinyllama bf16 generate")
+        toks, hs, _ = m.generate(g["prompt"], g["max_new"])
+        assert toks == g["tokens"]
+        assert ["%016x" % h for h in hs] == g["step_fnv"]
+        prompt, ref = g["prompt"], g["tokens"]
+        for pos, tok in enumerate(prompt):
+            nxt, _ = m.forward(tok, pos, spec.TINYLLAMA[6], logits=False)
+        say("tinyllama bf16 graph decode")
+        toks2, _, _ = m.decode_graph(nxt, len(prompt), 32)
+        assert [nxt] + toks2[:31] == ref[len(prompt):len(prompt) + 32]
+    finally:
+        m.free()
+
+
+def test_bf16_weights_refused_when_not_applicable(ctx):
+    """The tiny model (dim 256) has no bfloat16 GEMV shape, and weights that
+    are not bfloat16 values cannot be packed: both refuse, and the model
+    keeps decoding with its int64 weights."""
+    g = golden("tiny_generate.json")
+    m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
+    try:
+        m.synth(g["seed"], threads())
+        with pytest.raises(intllm.Q48Error):
+            m.set_bf16(True)
+        toks, _, _ = m.generate(g["prompt"], g["max_new"])
+        assert toks == g["tokens"]
+    finally:
+        m.free()
+    cfg = intllm.config(intllm.TINY, dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024,
+                        vocab=512, n_layers=1)
+    m = intllm.HostModel(ctx, cfg)
+    try:
+        m.synth(3, threads())
+        m.set_bf16(True)      # synthetic weights are bfloat16 values
+        m.set_bf16(False)
+        wo = np.full(512 * 512, 0x123456789, dtype=np.int64)
+        m.upload("model.layers.0.self_attn.o_proj.weight", wo)
+        with pytest.raises(intllm.Q48Error):
+            m.set_bf16(True)
+    finally:
+        m.free()

@@ -698,3 +698,108 @@ def test_gemv_residual_stats(ctx, oracle, M, K):
     assert np.array_equal(dy.download(), O.gemv(Wn, _rms(oracle, h, nw), N, M))
     for b in (dWn, dnw, dy, dh, ds):
         b.free()
+
+
+# ---- bfloat16-resident weights ----------------------------------------------
+
+def _bf16_values(oracle, bits):
+    return np.array([oracle.q48s_bf16_to_q48(int(b)) for b in bits], dtype=np.int64)
+
+
+def test_bf16_pack_every_pattern(ctx, oracle):
+    """Every one of the 65536 bfloat16 patterns, converted by the reference
+    rule (safetensors.h:115-152), packs back to bits that convert to the same
+    int64; a value with more than 8 significant bits is reported inexact."""
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    vals = _bf16_values(oracle, bits)
+    dv = ctx.to_device(vals)
+    db = ctx.buffer(vals.size // 4)   # 2 bytes per element
+    say("bf16 pack, all patterns")
+    assert ctx.bf16_pack(db.ptr, dv.ptr, vals.size)
+    packed = db.download().view(np.uint16)
+    assert np.array_equal(_bf16_values(oracle, packed), vals)
+    bad = ctx.to_device(np.array([0, ONE, 0x123456789, -ONE], dtype=np.int64))
+    assert not ctx.bf16_pack(db.ptr, bad.ptr, 4)
+    for b in (dv, db, bad):
+        b.free()
+
+
+def test_bf16_gemv_every_pattern(ctx, oracle):
+    """The in-kernel expansion on every bfloat16 pattern (zero, subnormal,
+    wrapping left shifts, truncating right shifts, shifts past 64, +-Inf/NaN
+    clamps): a 128 x 512 matrix holding all 65536 patterns against random x,
+    equal to the int64 GEMV of the expanded matrix and to the oracle."""
+    M, K = 128, 512
+    rng = np.random.default_rng(5)
+    bits = rng.permutation(np.arange(1 << 16, dtype=np.uint16))
+    W = _bf16_values(oracle, bits)
+    x = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=K, dtype=np.int64)
+    want = O.gemv(W, x, M, K)
+    dWb = ctx.buffer(M * K // 4)
+    dWb.upload(bits.view(np.int64))
+    dx, dy = ctx.to_device(x), ctx.buffer(M)
+    say("bf16 gemv, all patterns")
+    ctx.gemv_bf16(dy.ptr, dWb.ptr, dx.ptr, M, K)
+    assert np.array_equal(dy.download(), want)
+    for b in (dWb, dx, dy):
+        b.free()
+
+
+def _bf16_matrix(rng, rows, cols):
+    """bfloat16 bits of model-like weights: sign, exponents around 2^-6 (N(0,
+    0.02)-sized) with a spread, any mantissa."""
+    e = np.clip(rng.normal(121, 4, rows * cols).round(), 1, 140).astype(np.uint16)
+    m = rng.integers(0, 128, rows * cols, dtype=np.uint16)
+    s = rng.integers(0, 2, rows * cols, dtype=np.uint16)
+    return (s << 15) | (e << 7) | m
+
+
+@pytest.mark.parametrize("persistent", [True, False])
+@pytest.mark.parametrize("M,K", [(2560, 2048), (2048, 5632), (9001, 2048), (32000, 2048),
+                                 (100, 512), (1030, 1024)])
+def test_bf16_gemv_forms_equal_int64(ctx, oracle, M, K, persistent):
+    """Every fused form on bfloat16 weights (plain, normed with partial-sum
+    statistics, residual add with the next statistics, gate|up + SwiGLU)
+    gives the bits of the same form on the expanded int64 weights, with the
+    persistent row-group loop on and off."""
+    rng = np.random.default_rng(M * 3 + K)
+    bits = _bf16_matrix(rng, M, K)
+    lut = _bf16_values(oracle, np.arange(1 << 16, dtype=np.uint16))
+    W = lut[bits]
+    x = (rng.standard_normal(K) * ONE).astype(np.int64)
+    nw = (rng.standard_normal(K) * ONE).astype(np.int64)
+    h0 = (rng.standard_normal(M) * ONE).astype(np.int64)
+    dW, dWb = ctx.to_device(W), ctx.buffer((M * K + 3) // 4)
+    dWb.upload(np.concatenate([bits, np.zeros((-M * K) % 4, np.uint16)]).view(np.int64))
+    dx, dnw = ctx.to_device(x), ctx.to_device(nw)
+    ds = ctx.buffer(intllm.stats_words(K) + 2)
+    ctx.rms_stats(ds.ptr, dx.ptr, K)
+    ya, yb = ctx.buffer(M), ctx.buffer(M)
+    ctx.set_gemv_persistent(persistent)
+    try:
+        say("bf16 forms", M, K, "persistent", persistent)
+        ctx.gemv(ya.ptr, dW.ptr, dx.ptr, M, K)
+        ctx.gemv_bf16(yb.ptr, dWb.ptr, dx.ptr, M, K)
+        assert np.array_equal(ya.download(), yb.download()), "plain"
+        ctx.norm_gemv_stats(ya.ptr, dW.ptr, dx.ptr, dnw.ptr, ds.ptr, M, K)
+        ctx.norm_gemv_stats_bf16(yb.ptr, dWb.ptr, dx.ptr, dnw.ptr, ds.ptr, M, K)
+        assert np.array_equal(ya.download(), yb.download()), "normed"
+        if M % 2 == 0:
+            ffn = M // 2
+            ctx.norm_gemv_swiglu_stats(ya.ptr, dW.ptr, dx.ptr, dnw.ptr, ds.ptr, ffn, K)
+            ctx.norm_gemv_swiglu_stats_bf16(yb.ptr, dWb.ptr, dx.ptr, dnw.ptr, ds.ptr, ffn, K)
+            assert np.array_equal(ya.download(ffn), yb.download(ffn)), "swiglu"
+        sa, sb = ctx.buffer(intllm.stats_words(M) + 2), ctx.buffer(intllm.stats_words(M) + 2)
+        ya.upload(h0)
+        yb.upload(h0)
+        ctx.gemv_residual_stats(ya.ptr, dW.ptr, dx.ptr, M, K, sa.ptr)
+        ctx.gemv_residual_stats_bf16(yb.ptr, dWb.ptr, dx.ptr, M, K, sb.ptr)
+        assert np.array_equal(ya.download(), yb.download()), "residual"
+        n = intllm.stats_words(M)
+        assert np.array_equal(sa.download(n), sb.download(n)), "residual stats"
+        for b in (sa, sb):
+            b.free()
+    finally:
+        ctx.set_gemv_persistent(True)
+    for b in (dW, dWb, dx, dnw, ds, ya, yb):
+        b.free()
