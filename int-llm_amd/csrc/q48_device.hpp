@@ -246,11 +246,16 @@ __device__ __forceinline__ int64_t q48_inv_sqrt(int64_t x)
         int64_t y2 = (int64_t)(((q48_i128)y * y) >> 48);
         int64_t xy2 = (int64_t)(((q48_i128)xn * y2) >> 48);
         int64_t factor = three - xy2;
-        y = (int64_t)(((q48_i128)y * factor) >> 49);
-        if (y <= 0) {
+        const int64_t yn = (int64_t)(((q48_i128)y * factor) >> 49);
+        if (yn <= 0) {
             y = 1;
             break;
         }
+        // a fixed point: every remaining step maps y to itself (usually
+        // reached after 4-6 of the 8 steps)
+        if (yn == y)
+            break;
+        y = yn;
     }
     if (k >= 0) {
         int64_t r = y >> k;
@@ -414,27 +419,77 @@ __device__ __forceinline__ int64_t q48_silu(int64_t x)
 // Wave-level reductions (wave64)
 // ---------------------------------------------------------------------------
 
-// 128-bit two's-complement sum across the 64 lanes of a wave; every lane
-// returns the total.  Integer addition mod 2^128 is associative, so the
-// butterfly order gives the same bits as the reference's serial loop.
-__device__ __forceinline__ q48_u128 q48_wave_sum128(q48_u128 v)
+// Lane moves within a row of 16 lanes by DPP (no LDS round trip, unlike a
+// shuffle): every lane reads the lane given by the control word.
+constexpr int Q48_DPP_XOR1 = 0xB1;          // quad_perm [1,0,3,2]
+constexpr int Q48_DPP_XOR2 = 0x4E;          // quad_perm [2,3,0,1]
+constexpr int Q48_DPP_HALF_MIRROR = 0x141;  // lane i <- 7 - i within 8 lanes
+constexpr int Q48_DPP_MIRROR = 0x140;       // lane i <- 15 - i within 16 lanes
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t q48_dpp64(uint64_t v)
 {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        uint64_t lo = (uint64_t)v, hi = (uint64_t)(v >> 64);
-        uint64_t olo = __shfl_xor(lo, off, 64);
-        uint64_t ohi = __shfl_xor(hi, off, 64);
-        v += ((q48_u128)ohi << 64) | olo;
-    }
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf,
+                                                              0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32),
+                                                              CTRL, 0xf, 0xf, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+template <int CTRL>
+__device__ __forceinline__ q48_u128 q48_dpp128(q48_u128 v)
+{
+    return ((q48_u128)q48_dpp64<CTRL>((uint64_t)(v >> 64)) << 64) |
+           q48_dpp64<CTRL>((uint64_t)v);
+}
+
+// 128-bit sum over each aligned group of 8 lanes; every lane of the group
+// returns the group's total (all 8 lanes must be active).  After the two
+// quad exchanges each lane holds its quad's sum; the half-row mirror pairs
+// every lane with a lane of the other quad.
+__device__ __forceinline__ q48_u128 q48_sum8_u128(q48_u128 v)
+{
+    v += q48_dpp128<Q48_DPP_XOR1>(v);
+    v += q48_dpp128<Q48_DPP_XOR2>(v);
+    v += q48_dpp128<Q48_DPP_HALF_MIRROR>(v);
     return v;
 }
 
-__device__ __forceinline__ int64_t q48_wave_sum64(int64_t v)
+// 128-bit two's-complement sum across the 64 lanes of a wave (all active);
+// every lane returns the total.  Integer addition mod 2^128 is associative,
+// so any order gives the bits of the reference's serial loop.  Rows of 16
+// lanes are summed by DPP, then the four row sums are read as scalars.
+__device__ __forceinline__ q48_u128 q48_wave_sum128(q48_u128 v)
 {
+    v = q48_sum8_u128(v);
+    v += q48_dpp128<Q48_DPP_MIRROR>(v);
+    q48_u128 t = 0;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-        v = (int64_t)((uint64_t)v + (uint64_t)__shfl_xor(v, off, 64));
-    return v;
+    for (int r = 0; r < 4; ++r) {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            w[k] = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> (32 * k)), 16 * r);
+        t += ((q48_u128)(((uint64_t)w[3] << 32) | w[2]) << 64) | (((uint64_t)w[1] << 32) | w[0]);
+    }
+    return t;
+}
+
+__device__ __forceinline__ int64_t q48_wave_sum64(int64_t x)
+{
+    uint64_t v = (uint64_t)x;
+    v += q48_dpp64<Q48_DPP_XOR1>(v);
+    v += q48_dpp64<Q48_DPP_XOR2>(v);
+    v += q48_dpp64<Q48_DPP_HALF_MIRROR>(v);
+    v += q48_dpp64<Q48_DPP_MIRROR>(v);
+    uint64_t t = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 16 * r);
+        t += ((uint64_t)hi << 32) | lo;
+    }
+    return (int64_t)t;
 }
 
 __device__ __forceinline__ int64_t q48_wave_max64(int64_t v)

@@ -380,11 +380,7 @@ __global__ __launch_bounds__(256) void k_digit_corr(uint64_t *__restrict__ out,
     q48_i128 s = 0;
     for (int k = lane; k < K; k += 64)
         s += p[k];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const uint64_t lo = (uint64_t)s, hi = (uint64_t)((q48_u128)s >> 64);
-        s += (q48_i128)(((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64));
-    }
+    s = (q48_i128)q48_wave_sum128((q48_u128)s);
     if (lane == 0) {
         q48_u128 v = (q48_u128)s * kDig;
         if (sub_kc2)

@@ -213,6 +213,14 @@ __device__ __forceinline__ int64_t rms_inv_of(q48_u128 ss, int dim)
     return q48_inv_sqrt(ms);
 }
 
+// Marks a value as used here, in every wave, so that the compiler computes
+// it (and waits for its loads) at this point instead of sinking the work
+// into the one branch that reads it.
+__device__ __forceinline__ void q48_keep128(q48_u128 v)
+{
+    asm volatile("" ::"v"((uint64_t)v), "v"((uint64_t)(v >> 64)));
+}
+
 // 128-bit sum over the block (NT threads); result valid in thread 0.
 template <int NT>
 __device__ __forceinline__ q48_u128 block_sum128(q48_u128 v, uint64_t *red_lo, uint64_t *red_hi)
@@ -230,6 +238,8 @@ __device__ __forceinline__ q48_u128 block_sum128(q48_u128 v, uint64_t *red_lo, u
             t += ((q48_u128)red_hi[w] << 64) | red_lo[w];
     return t;
 }
+
+typedef unsigned short q48_u16x2 __attribute__((ext_vector_type(2)));
 
 struct Acc6 {
     uint64_t a00, a01, a10, a11, a20, a21, ws;
@@ -286,7 +296,9 @@ template <> struct WFmt<0> { static constexpr int ES = 8, TE = 16; };
 template <> struct WFmt<1> { static constexpr int ES = 2, TE = 64; };
 
 // One 128-byte tile t of this lane's row against the staged x limbs (3 per
-// element at xw[3 j]).
+// element at xw[3 j]).  For the bfloat16 weights this is the general form,
+// every pattern expanded by q48_bf16; the staged top limb is signed there
+// (see b16_tile_fast) and is moved back to offset binary for mac6.
 template <int WT>
 __device__ __forceinline__ void mac_tile(Acc6 &A, const uint32_t *xw, int l8, int t, ulonglong2 w)
 {
@@ -303,7 +315,7 @@ __device__ __forceinline__ void mac_tile(Acc6 &A, const uint32_t *xw, int l8, in
                                (uint32_t)(w.y >> 32)};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            mac6(A, p[3 * e], p[3 * e + 1], p[3 * e + 2],
+            mac6(A, p[3 * e], p[3 * e + 1], p[3 * e + 2] + 0x100000u,
                  (uint64_t)q48_bf16((u[e >> 1] >> (16 * (e & 1))) & 0xffffu));
             if (e & 1)
                 __builtin_amdgcn_sched_barrier(0);
@@ -311,16 +323,75 @@ __device__ __forceinline__ void mac_tile(Acc6 &A, const uint32_t *xw, int l8, in
     }
 }
 
-// One batch of UNR tiles of a lane against the staged x limbs; tiles at or
-// past nt are skipped (uniform branch).
-template <int UNR, int WT>
-__device__ __forceinline__ void mac_tiles(Acc6 &A, const uint32_t *xw, int l8,
-                                          const ulonglong2 (&w)[UNR], int t0, int nt)
+// Fast form of the bfloat16 tiles.  A pattern with exponent e in [103, 126]
+// has the Q16.48 value w = t 2^17 with t = s (128 + m) 2^(e - 103), an
+// integer of at most 31 bits: t is the pattern read as an f32 with 31 added
+// to its exponent, converted exactly by v_cvt_i32_f32.  Then
+// w x = (t x0 + t x1 2^22 + t x2s 2^43) 2^17 with x split into the limbs x0
+// (22 bits), x1 (21 bits) and the signed top limb x2s, three signed 32 x 32
+// multiply-adds per weight into 64-bit sums (a lane sums at most K / 64
+// <= 192 products below 2^53: no overflow).  Every other pattern (zero and
+// subnormal, |w| < 2^-24, |w| >= 1, inf, NaN) is caught by a range check
+// folded into a running packed 16-bit maximum: 2 b mod 2^16 drops the sign,
+// and 2 b - (103 << 8) wraps to at least 24 << 8 outside the window.  A
+// wave whose check fails recomputes its tiles with mac_tile<1>.
+struct Acc3 {
+    int64_t f0, f1, f2, g0, g1, g2;   // even / odd weights of a pair
+};
+constexpr uint32_t B16_EXP = 31u << 23;                 // 2^31 in the f32 exponent
+constexpr unsigned short B16_DLO = (unsigned short)(0x10000 - (103 << 8));
+constexpr unsigned B16_DMAX = (24u << 8) - 1;           // largest in-window value
+
+__device__ __forceinline__ void b16_tile_fast(Acc3 &F, q48_u16x2 &chk, const uint32_t *xw,
+                                              int l8, int t, ulonglong2 w)
 {
+    __builtin_amdgcn_sched_barrier(0);
+    // 8 elements x 3 limbs = 96 bytes at a 96-byte multiple of the 16-byte
+    // aligned segment: six 16-byte reads
+    const uint4 *p4 = reinterpret_cast<const uint4 *>(xw + 3 * (64 * t + 8 * l8));
+    uint4 q4[6];
 #pragma unroll
-    for (int u = 0; u < UNR; ++u)
-        if (t0 + u < nt)
-            mac_tile<WT>(A, xw, l8, t0 + u, w[u]);
+    for (int i = 0; i < 6; ++i)
+        q4[i] = p4[i];
+    const int32_t *q = reinterpret_cast<const int32_t *>(q4);
+    const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)(w.x >> 32), (uint32_t)w.y,
+                           (uint32_t)(w.y >> 32)};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const q48_u16x2 d = __builtin_bit_cast(q48_u16x2, u[h]) * (q48_u16x2)(2) +
+                            (q48_u16x2)(B16_DLO);
+        chk = __builtin_elementwise_max(chk, d);
+        const int32_t ta = (int32_t)__builtin_bit_cast(float, (u[h] << 16) + B16_EXP);
+        const int32_t tb = (int32_t)__builtin_bit_cast(float, (u[h] & 0xffff0000u) + B16_EXP);
+        F.f0 += (int64_t)ta * q[6 * h];
+        F.f1 += (int64_t)ta * q[6 * h + 1];
+        F.f2 += (int64_t)ta * q[6 * h + 2];
+        F.g0 += (int64_t)tb * q[6 * h + 3];
+        F.g1 += (int64_t)tb * q[6 * h + 4];
+        F.g2 += (int64_t)tb * q[6 * h + 5];
+    }
+}
+
+// Pins the fast sums in registers before the wave's range check: otherwise
+// the compiler sinks the fast multiply-adds below the check and keeps every
+// tile's staged limbs live across it.
+__device__ __forceinline__ void b16_pin(Acc3 &F)
+{
+    asm volatile("" : "+v"(F.f0), "+v"(F.f1), "+v"(F.f2), "+v"(F.g0), "+v"(F.g1), "+v"(F.g2));
+}
+
+// true on every lane when no lane of the wave saw a pattern outside the window
+__device__ __forceinline__ bool b16_wave_ok(q48_u16x2 chk)
+{
+    const unsigned m = chk.x > chk.y ? chk.x : chk.y;
+    return __builtin_amdgcn_ballot_w64(m > B16_DMAX) == 0;
+}
+
+__device__ __forceinline__ q48_u128 acc3_value(const Acc3 &F)
+{
+    const q48_i128 v = (q48_i128)F.f0 + (q48_i128)F.g0 + (((q48_i128)F.f1 + F.g1) << 22) +
+                       (((q48_i128)F.f2 + F.g2) << 43);
+    return (q48_u128)v << 17;
 }
 
 template <int NW, int UNR, int PRO, int EPI, int NTF, int WT = 0>
@@ -458,8 +529,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     __builtin_amdgcn_sched_barrier(0);
 
     if (PRO == 3) {
-        // every wave adds all the partials itself (no block barrier) and
-        // every lane derives the same r
+        // every wave adds the partials (cheap; it keeps their loads first in
+        // every wave), wave 0 alone derives r and the others meet it at the
+        // barrier: the chain of 64 x 64-bit products inside rms_inv_of is
+        // issue-bound, and run by every wave it would contend for the SIMDs
         q48_u128 ss = 0;
         if constexpr (NTF > 0) {
 #pragma unroll
@@ -473,7 +546,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                 ss += ((q48_u128)st[2 * i + 1] << 64) | st[2 * i];
         }
         ss = q48_wave_sum128(ss);
-        r = rms_inv_of(ss, K);
+        q48_keep128(ss);
+        if (wave == 0) {
+            const int64_t rv = rms_inv_of(ss, K);
+            if (lane == 0)
+                r_sh = rv;
+        }
+        __syncthreads();
+        r = r_sh;
     }
 
     // stage this wave's segment of x as limbs; sum x over the segment
@@ -494,7 +574,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                 const uint64_t X = (uint64_t)v ^ 0x8000000000000000ull;
                 xw[3 * j] = (uint32_t)X & 0x3FFFFFu;
                 xw[3 * j + 1] = (uint32_t)(X >> 22) & 0x1FFFFFu;
-                xw[3 * j + 2] = (uint32_t)(X >> 43);
+                // bfloat16 weights: the signed top limb (b16_tile_fast)
+                xw[3 * j + 2] = WT == 1 ? (uint32_t)(v >> 43) : (uint32_t)(X >> 43);
             }
         }
     };
@@ -521,6 +602,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     // loads).  Rows past the end (reading row 0) accumulate too, without
     // branching, and are never stored.
     Acc6 A = {0, 0, 0, 0, 0, 0, 0};
+    Acc3 F = {0, 0, 0, 0, 0, 0};
+    q48_u16x2 chk = {0, 0};
+    // one tile: the int64 weights, or the fast form of the bfloat16 ones
+    auto tile = [&](int t, ulonglong2 w) {
+        if constexpr (WT == 0)
+            mac_tile<0>(A, xw, l8, t, w);
+        else
+            b16_tile_fast(F, chk, xw, l8, t, w);
+    };
     const uint32_t *xl = xw + 6 * l8;   // this lane's pair: 6 limbs per tile of 16
     if constexpr (NTF > 0) {
         // every wave has exactly NTF tiles: a rotating window of UNR loads in
@@ -529,34 +619,54 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         // pipeline is full instead of stalling on a long run of issues)
 #pragma unroll
         for (int t = 0; t < NTF; ++t) {
-            mac_tile<WT>(A, xw, l8, t, wa[t % UNR]);
+            tile(t, wa[t % UNR]);
             if (t + UNR < NTF)
                 wa[t % UNR] = w2[(t + UNR) * 8];
         }
     } else {
-        mac_tiles<UNR, WT>(A, xw, l8, wa, 0, nt);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u)
+            if (u < nt)
+                tile(u, wa[u]);
         for (int t0 = UNR; t0 < nt; t0 += UNR) {
 #pragma unroll
             for (int u = 0; u < UNR; ++u)
                 wa[u] = w2[min(t0 + u, nt - 1) * 8];
-            mac_tiles<UNR, WT>(A, xw, l8, wa, t0, nt);
+#pragma unroll
+            for (int u = 0; u < UNR; ++u)
+                if (t0 + u < nt)
+                    tile(t0 + u, wa[u]);
         }
     }
-    // the kn % 16 elements (even) of the segment's end, one pair per lane
-    if (WT == 0 && 2 * l8 < (kn & 15)) {
-        const ulonglong2 w1 = w2[nt * 8];
-        const uint32_t *p = xl + 48 * nt;
-        mac6(A, p[0], p[1], p[2], w1.x);
-        mac6(A, p[3], p[4], p[5], w1.y);
+    // bfloat16: a pattern outside the fast window anywhere in the wave's
+    // tiles sends the wave through the general expansion (rare)
+    bool fast = false;
+    q48_u128 S;
+    if constexpr (WT == 1) {
+        b16_pin(F);
+        fast = b16_wave_ok(chk);
+        if (fast) {
+            S = acc3_value(F);
+        } else {
+#pragma unroll 1
+            for (int t = 0; t < nt; ++t)
+                mac_tile<1>(A, xw, l8, t, w2[t * 8]);
+            S = acc6_value(A);
+        }
+    } else {
+        // the kn % 16 elements (even) of the segment's end, one pair per lane
+        if (2 * l8 < (kn & 15)) {
+            const ulonglong2 w1 = w2[nt * 8];
+            const uint32_t *p = xl + 48 * nt;
+            mac6(A, p[0], p[1], p[2], w1.x);
+            mac6(A, p[3], p[4], p[5], w1.y);
+        }
+        S = acc6_value(A);
     }
-    q48_u128 S = acc6_value(A);
-#pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-        const uint64_t lo = (uint64_t)S, hi = (uint64_t)(S >> 64);
-        S += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
-    }
+    S = q48_sum8_u128(S);
     if (l8 == 0) {
-        S -= (q48_u128)xsum << 63;
+        if (!fast)
+            S -= (q48_u128)xsum << 63;
         part[wave][g][0] = (uint64_t)S;
         part[wave][g][1] = (uint64_t)(S >> 64);
     }
@@ -578,11 +688,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                 y[rr] = h;
             }
             q48_u128 sq = (q48_u128)((q48_i128)h * h);
-#pragma unroll
-            for (int off = 1; off < 8; off <<= 1) {
-                const uint64_t lo = (uint64_t)sq, hi = (uint64_t)(sq >> 64);
-                sq += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
-            }
+            sq = q48_sum8_u128(sq);
             if (tid == 0) {
                 uint64_t *st = reinterpret_cast<uint64_t *>(r_out);
                 st[2 * blockIdx.x] = (uint64_t)sq;
@@ -607,11 +713,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                 y[rr] = h;
             }
             q48_u128 sq = (q48_u128)((q48_i128)h * h);
-#pragma unroll
-            for (int off = 1; off < 8; off <<= 1) {
-                const uint64_t lo = (uint64_t)sq, hi = (uint64_t)(sq >> 64);
-                sq += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
-            }
+            sq = q48_sum8_u128(sq);
             if (tid == 0) {
                 // The partial goes out with agent-coherent (write-through)
                 // stores; waiting for them to complete before the ticket
@@ -706,6 +808,7 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
     extern __shared__ __align__(16) uint32_t xs[];   // 3 limbs per staged x
     __shared__ uint64_t part[2][NW][V4_RB][2];
     __shared__ int64_t pre[P6_MAXG][V4_RB];          // EPI 2: gate (0-3) / up (4-7)
+    __shared__ int64_t r_sh;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -766,6 +869,7 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
 
     int64_t r = 0;
     if (PRO == 3) {
+        // wave 0 derives r for the block (as in k_gemv_v5)
         q48_u128 ss = 0;
 #pragma unroll
         for (int c = 0; c < PC; ++c) {
@@ -773,7 +877,14 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
             ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
         }
         ss = q48_wave_sum128(ss);
-        r = rms_inv_of(ss, K);
+        q48_keep128(ss);
+        if (wave == 0) {
+            const int64_t rv = rms_inv_of(ss, K);
+            if (lane == 0)
+                r_sh = rv;
+        }
+        __syncthreads();
+        r = r_sh;
     }
 
     // stage this wave's segment of x as limbs; sum x over the segment
@@ -791,7 +902,7 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
             const uint64_t X = (uint64_t)v ^ 0x8000000000000000ull;
             xw[3 * j] = (uint32_t)X & 0x3FFFFFu;
             xw[3 * j + 1] = (uint32_t)(X >> 22) & 0x1FFFFFu;
-            xw[3 * j + 2] = (uint32_t)(X >> 43);
+            xw[3 * j + 2] = WT == 1 ? (uint32_t)(v >> 43) : (uint32_t)(X >> 43);
         }
     }
     xsum = (uint64_t)q48_wave_sum64((int64_t)xsum);
@@ -806,23 +917,42 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
         // every block there, so they stay in cache: in bounds, never used)
         const ulonglong2 *w2n = wrow(nxt < ngroups ? nxt : 0);
         Acc6 A = {0, 0, 0, 0, 0, 0, 0};
+        Acc3 F = {0, 0, 0, 0, 0, 0};
+        q48_u16x2 chk = {0, 0};
 #pragma unroll
         for (int t = 0; t < NTF; ++t) {
-            mac_tile<WT>(A, xw, l8, t, wa[t % UNR]);
+            if constexpr (WT == 0)
+                mac_tile<0>(A, xw, l8, t, wa[t % UNR]);
+            else
+                b16_tile_fast(F, chk, xw, l8, t, wa[t % UNR]);
             if (t + UNR < NTF)
                 wa[t % UNR] = w2[(t + UNR) * 8];
             else
                 wa[t % UNR] = w2n[(t + UNR - NTF) * 8];
         }
-        w2 = w2n;
-        q48_u128 S = acc6_value(A);
-#pragma unroll
-        for (int off = 1; off < 8; off <<= 1) {
-            const uint64_t lo = (uint64_t)S, hi = (uint64_t)(S >> 64);
-            S += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
+        // bfloat16 outside the fast window: this group again, general form
+        // (the next group's tiles stay in the window)
+        bool fast = false;
+        q48_u128 S;
+        if constexpr (WT == 1) {
+            b16_pin(F);
+            fast = b16_wave_ok(chk);
+            if (fast) {
+                S = acc3_value(F);
+            } else {
+#pragma unroll 1
+                for (int t = 0; t < NTF; ++t)
+                    mac_tile<1>(A, xw, l8, t, w2[t * 8]);
+                S = acc6_value(A);
+            }
+        } else {
+            S = acc6_value(A);
         }
+        w2 = w2n;
+        S = q48_sum8_u128(S);
         if (l8 == 0) {
-            S -= (q48_u128)xsum << 63;
+            if (!fast)
+                S -= (q48_u128)xsum << 63;
             part[i & 1][wave][g][0] = (uint64_t)S;
             part[i & 1][wave][g][1] = (uint64_t)(S >> 64);
         }
@@ -1019,11 +1149,13 @@ static int launch_b16_ntf(q48_ctx *c, int64_t *y, const uint16_t *W, const int64
                           const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
                           int K)
 {
-    constexpr int NW = 8, UNR = NTF < 4 ? NTF : 4;
+    // the window: every tile of the segment in flight when it divides no
+    // other way (11 tiles for K = 5632), else 4
+    constexpr int NW = 8, UNR = NTF < 4 ? NTF : NTF % 4 == 0 ? 4 : NTF;
     const int seg = K / NW;
     const size_t lds = (size_t)seg * NW * 3 * sizeof(uint32_t);
     const int blocks = EPI == 2 ? (M / 2 + 3) / 4 : (M + V4_RB - 1) / V4_RB;
-    if constexpr ((PRO == 0 || PRO == 3) && (EPI == 0 || EPI == 2) && NTF % UNR == 0) {
+    if constexpr ((PRO == 0 || PRO == 3) && (EPI == 0 || EPI == 2) && UNR <= 4 && NTF % UNR == 0) {
         const int grid = 2 * c->cu_count;
         if (blocks > 2 * grid && blocks <= P6_MAXG * grid && c->gemv_persistent) {
             hipLaunchKernelGGL((k_gemv_p6<NW, UNR, PRO, EPI, NTF, 1>), dim3(grid),
@@ -1048,6 +1180,11 @@ static int launch_b16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *
         return launch_b16_ntf<PRO, EPI, 2>(c, y, W, x, norm_w, r_in, r_out, M, K);
     case 2048:
         return launch_b16_ntf<PRO, EPI, 4>(c, y, W, x, norm_w, r_in, r_out, M, K);
+    case 5632:
+        // all 11 tiles in flight: registers allow it without the norm prologue
+        if constexpr (PRO == 0)
+            return launch_b16_ntf<PRO, EPI, 11>(c, y, W, x, norm_w, r_in, r_out, M, K);
+        [[fallthrough]];
     default: {
         // other K (a multiple of 512): batches of 4 tiles in a loop (an
         // unrolled chain of more tiles runs out of registers)

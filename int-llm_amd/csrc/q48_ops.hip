@@ -308,11 +308,7 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
                 dot += (q48_u128)((q48_i128)qd[d + 1] * a1);
             }
         }
-#pragma unroll
-        for (int off = 1; off < 8; off <<= 1) {
-            const uint64_t lo = (uint64_t)dot, hi = (uint64_t)(dot >> 64);
-            dot += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
-        }
+        dot = q48_sum8_u128(dot);
         if (t < S && l8 == 0) {
             const int64_t s = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
             sc[t] = s;
@@ -528,11 +524,7 @@ __global__ __launch_bounds__(256) void k_attn_s1(
             dot += (q48_u128)((q48_i128)qd[2 * d] * a0);
             dot += (q48_u128)((q48_i128)qd[2 * d + 1] * a1);
         }
-#pragma unroll
-        for (int off = 1; off < 8; off <<= 1) {
-            const uint64_t lo = (uint64_t)dot, hi = (uint64_t)(dot >> 64);
-            dot += ((q48_u128)__shfl_xor(hi, off, 64) << 64) | __shfl_xor(lo, off, 64);
-        }
+        dot = q48_sum8_u128(dot);
         if (t < tend && l8 == 0) {
             const int64_t sv = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
             __hip_atomic_store(&sch[t], sv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -745,25 +745,44 @@ def test_bf16_gemv_every_pattern(ctx, oracle):
         b.free()
 
 
-def _bf16_matrix(rng, rows, cols):
+def _bf16_matrix(rng, rows, cols, mode="wide"):
     """bfloat16 bits of model-like weights: sign, exponents around 2^-6 (N(0,
-    0.02)-sized) with a spread, any mantissa."""
-    e = np.clip(rng.normal(121, 4, rows * cols).round(), 1, 140).astype(np.uint16)
-    m = rng.integers(0, 128, rows * cols, dtype=np.uint16)
-    s = rng.integers(0, 2, rows * cols, dtype=np.uint16)
-    return (s << 15) | (e << 7) | m
+    0.02)-sized), any mantissa.  The kernels take a fast path for exponents
+    103..126 (2^-24 <= |w| < 1) and recompute a wave's tiles exactly when any
+    weight lies outside:
+      wide:   exponents 1..140, spread 4 (most waves see an outlier);
+      window: exponents 103..126 only (every wave fast);
+      mixed:  window, plus an outlier (zero, subnormal, tiny, |w| >= 1,
+              inf/NaN) at about 1 in 20000 weights, so fast and recomputed
+              waves meet in one launch."""
+    n = rows * cols
+    if mode == "wide":
+        e = np.clip(rng.normal(121, 4, n).round(), 1, 140)
+    else:
+        e = np.clip(rng.normal(119, 3, n).round(), 103, 126)
+    e = e.astype(np.uint16)
+    m = rng.integers(0, 128, n, dtype=np.uint16)
+    s = rng.integers(0, 2, n, dtype=np.uint16)
+    bits = (s << 15) | (e << 7) | m
+    if mode == "mixed":
+        at = rng.choice(n, size=max(1, n // 20000), replace=False)
+        bits[at] = rng.choice(np.array([0x0000, 0x8000, 0x0011, 0x3300, 0xb380, 0x3f80,
+                                        0xbfc0, 0x4500, 0x7f80, 0xffc1, 0x3f7f, 0xbf7f], np.uint16), at.size)
+    return bits
 
 
+@pytest.mark.parametrize("mode", ["wide", "window", "mixed"])
 @pytest.mark.parametrize("persistent", [True, False])
 @pytest.mark.parametrize("M,K", [(2560, 2048), (2048, 5632), (9001, 2048), (32000, 2048),
                                  (100, 512), (1030, 1024)])
-def test_bf16_gemv_forms_equal_int64(ctx, oracle, M, K, persistent):
+def test_bf16_gemv_forms_equal_int64(ctx, oracle, M, K, persistent, mode):
     """Every fused form on bfloat16 weights (plain, normed with partial-sum
     statistics, residual add with the next statistics, gate|up + SwiGLU)
     gives the bits of the same form on the expanded int64 weights, with the
-    persistent row-group loop on and off."""
-    rng = np.random.default_rng(M * 3 + K)
-    bits = _bf16_matrix(rng, M, K)
+    persistent row-group loop on and off, on the fast path, the exact
+    recomputation and a mixture of both."""
+    rng = np.random.default_rng(M * 3 + K + 7 * len(mode))
+    bits = _bf16_matrix(rng, M, K, mode)
     lut = _bf16_values(oracle, np.arange(1 << 16, dtype=np.uint16))
     W = lut[bits]
     x = (rng.standard_normal(K) * ONE).astype(np.int64)
@@ -777,7 +796,7 @@ def test_bf16_gemv_forms_equal_int64(ctx, oracle, M, K, persistent):
     ya, yb = ctx.buffer(M), ctx.buffer(M)
     ctx.set_gemv_persistent(persistent)
     try:
-        say("bf16 forms", M, K, "persistent", persistent)
+        say("bf16 forms", M, K, "persistent", persistent, mode)
         ctx.gemv(ya.ptr, dW.ptr, dx.ptr, M, K)
         ctx.gemv_bf16(yb.ptr, dWb.ptr, dx.ptr, M, K)
         assert np.array_equal(ya.download(), yb.download()), "plain"
