@@ -216,6 +216,8 @@ def main():
                     help="decode-token GEMV sequences timed back to back for the roofline")
     ap.add_argument("--gemm-reps", type=int, default=5,
                     help="int8 GEMM calls timed per config-4 shape; 0 skips config 4")
+    ap.add_argument("--no-bf16", action="store_true",
+                    help="skip the bfloat16-resident-weights decode measurement")
     ap.add_argument("--gemm-only", action="store_true",
                     help="run only the config-4 GEMM measurement (for profiling)")
     args = ap.parse_args()
@@ -271,11 +273,6 @@ def main():
     ms = 1e3 * dt / args.steps
     log(f"decode {ms:.3f} ms/tok")
 
-    # token stream vs the reference's (golden), over the tokens both have
-    ref_new = gold["tokens"][len(prompt):]
-    n_cmp = min(len(ref_new), len(toks))
-    parity = {"tokens_compared": n_cmp, "tokens_match_reference": toks[:n_cmp] == ref_new[:n_cmp]}
-
     p0 = len(prompt) + args.warmup
     # roofline of the dominant kernel (q48_gemv): the GEMV launches of one
     # decode token, in decode order on the model's own weights, timed back to
@@ -288,6 +285,41 @@ def main():
     avg_us = 1e3 * gemv_ms / launches
     bytes_per_launch = gbytes / launches
     achieved = bytes_per_launch / (avg_us * 1e-6) / 1e9
+
+    # the same greedy stream continued with bfloat16-resident weights (2 B
+    # per weight, expanded exactly in the kernels; same bits): the tokens
+    # join the parity check below
+    bf16 = None
+    if not args.no_bf16:
+        m.set_bf16(True)
+        _, steps, _ = m.decode_graph(toks[-1], pos, args.warmup)
+        toks += steps
+        pos += args.warmup
+        ctx.sync()
+        b0 = pos
+        t0 = time.perf_counter()
+        _, steps, _ = m.decode_graph(toks[-1], pos, args.steps)
+        ctx.sync()
+        bms = 1e3 * (time.perf_counter() - t0) / args.steps
+        toks += steps
+        pos += args.steps
+        m.gemv_sweep(1)
+        ctx.timer_start()
+        bl, bgb = m.gemv_sweep(args.gemv_reps)
+        bus = 1e3 * ctx.timer_stop() / bl
+        bach = bgb / bl / (bus * 1e-6) / 1e9
+        m.set_bf16(False)
+        log(f"bf16-resident decode {bms:.3f} ms/tok")
+        bf16 = {"workload": "config 3 with bfloat16-resident weights (2.07 GB read per token)",
+                "tok_s": round(1e3 / bms, 2), "ms_per_tok": round(bms, 4),
+                "positions": [b0, b0 + args.steps],
+                "gemv_avg_launch_us": round(bus, 3), "gemv_achieved_GBs": round(bach, 1),
+                "gemv_frac": round(bach / HBM_PEAK_GBS, 4)}
+
+    # token stream vs the reference's (golden), over the tokens both have
+    ref_new = gold["tokens"][len(prompt):]
+    n_cmp = min(len(ref_new), len(toks))
+    parity = {"tokens_compared": n_cmp, "tokens_match_reference": toks[:n_cmp] == ref_new[:n_cmp]}
 
     # config 5: the cache pre-filled to 2048 positions, then greedy decode
     # steps replayed from the graph (the golden stream covers 256 of them)
@@ -353,6 +385,7 @@ def main():
         "gemv_shapes": shapes,
         "gemm_prefill": gemm,
         "long_context": longctx,
+        "bf16_resident": bf16,
         "parity": parity,
     }
     print(json.dumps(line), flush=True)

@@ -719,7 +719,13 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
         TRY(q48_rmsnorm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an,
                              dim + 2 * kvd, dim));
     }
-    if (m->prefetch)
+    /* the attention's spare blocks warm the cache with W_o, read next (in
+     * the format the next GEMV reads) */
+    if (m->prefetch && bb)
+        TRY(q48_attn_decode_rope_prefetch(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
+                                          c->n_kv_heads, hd, c->max_seq, bb + m->lo_wo,
+                                          (size_t)dim * dim * 2));
+    else if (m->prefetch)
         TRY(q48_attn_decode_rope_prefetch(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
                                           c->n_kv_heads, hd, c->max_seq, b + m->lo_wo,
                                           (size_t)dim * dim * 8));
