@@ -281,6 +281,28 @@ int q48_step_get(q48_ctx *ctx, int *token, int *pos, int *count);  /* syncs */
 /* argmax (llama_int.c:2888-2893) of v[0..n) into the state; the token is
  * also stored at d_tokens[count] while count < cap. */
 int q48_argmax_step(q48_ctx *ctx, const int64_t *v, int n, int *d_tokens, int cap);
+
+
+/* ---- sampling (sample_token, llama_int.c:2958-3039) --------------------- */
+/* rng_seed (llama_int.c:2909-2920): the xoroshiro128+ state of a seed
+ * (SplitMix64), computed on the host.  Upload it to a device buffer of two
+ * uint64 words for q48_sample / q48_sample_step. */
+void q48_rng_seed(uint64_t seed, uint64_t state[2]);
+/* sample_token on device logits[0..vocab): temperature (Q16.48), top_k
+ * (0 = off), top_p (Q16.48, ONE = off), and one rng_next draw from the
+ * device state rng[2], advanced in place.  Below a temperature of 0.01 it is
+ * argmax and draws nothing, as the reference.  The token goes to *token
+ * (host; the call synchronises). */
+int q48_sample(q48_ctx *ctx, const int64_t *logits, int vocab, int64_t temperature,
+               int top_k, int64_t top_p, uint64_t *rng, int *token);
+/* The same into the decode-step state (as q48_argmax_step): stream-ordered,
+ * graph-capturable once q48_sample_reserve has sized the workspace. */
+int q48_sample_step(q48_ctx *ctx, const int64_t *logits, int vocab, int64_t temperature,
+                    int top_k, int64_t top_p, uint64_t *rng, int *d_tokens, int cap);
+/* Size the sampling workspace for `vocab` logits (synchronises; not during
+ * capture). */
+int q48_sample_reserve(q48_ctx *ctx, int vocab);
+
 /* Capture the ops enqueued between begin and end into the context's graph. */
 int q48_graph_begin(q48_ctx *ctx);
 int q48_graph_end(q48_ctx *ctx);

@@ -137,6 +137,7 @@ int q48_ctx_destroy(q48_ctx *c)
     (void)hipFree(c->d_step);
     (void)hipFree(c->rms_count);
     (void)hipFree(c->rms_part);
+    (void)hipFree(c->smp);
     (void)hipFree(c->tmp);
     if (c->graph_exec)
         (void)hipGraphExecDestroy(c->graph_exec);
@@ -851,6 +852,88 @@ int q48_argmax_step(q48_ctx *c, const int64_t *v, int n, int *d_tokens, int cap)
     if (!c || !v || n <= 0 || cap < 0 || (cap > 0 && !d_tokens))
         return Q48_EINVAL;
     return launch_rc(q48_launch_step_argmax(c, d_tokens, cap, v, n));
+}
+
+void q48_rng_seed(uint64_t seed, uint64_t state[2])
+{
+    // rng_seed, llama_int.c:2909-2920: SplitMix64 of seed and of
+    // seed + 0x9E3779B97F4A7C15; an all-zero state becomes (1, 0)
+    auto mix = [](uint64_t z) {
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    };
+    if (!state)
+        return;
+    state[0] = mix(seed);
+    state[1] = mix(seed + 0x9E3779B97F4A7C15ull);
+    if (state[0] == 0 && state[1] == 0)
+        state[0] = 1;
+}
+
+int q48_sample_reserve(q48_ctx *c, int vocab)
+{
+    if (!c || vocab <= 0)
+        return Q48_EINVAL;
+    const size_t words = q48_sample_ws_words(vocab);
+    if (words <= c->smp_words)
+        return Q48_OK;
+    if (c->capturing)
+        return Q48_ESTATE;
+    if (c->smp) {
+        if (hipStreamSynchronize(c->stream) != hipSuccess)
+            return Q48_EHIP;
+        (void)hipFree(c->smp);
+        c->smp = nullptr;
+        c->smp_words = 0;
+    }
+    if (hipMalloc(&c->smp, words * sizeof(int64_t)) != hipSuccess)
+        return Q48_ENOMEM;
+    c->smp_words = words;
+    return Q48_OK;
+}
+
+// greedy below a temperature of 0.01 (llama_int.c:2962-2964)
+static bool sample_greedy(int64_t temperature)
+{
+    return temperature <= 0 || temperature < ((int64_t)1 << 48) / 100;
+}
+
+int q48_sample(q48_ctx *c, const int64_t *logits, int vocab, int64_t temperature, int top_k,
+               int64_t top_p, uint64_t *rng, int *token)
+{
+    if (!c || !logits || vocab <= 0 || !token || (!rng && !sample_greedy(temperature)))
+        return Q48_EINVAL;
+    if (c->capturing)
+        return Q48_ESTATE;
+    if (sample_greedy(temperature))
+        return q48_argmax(c, logits, vocab, token);
+    int rc = q48_sample_reserve(c, vocab);
+    if (rc)
+        return rc;
+    rc = launch_rc(q48_launch_sample(c, c->smp, logits, vocab, temperature, top_k, top_p, rng,
+                                     c->d_scalar, nullptr, 0));
+    if (rc)
+        return rc;
+    if (hipMemcpyAsync(token, c->d_scalar, sizeof(int), hipMemcpyDeviceToHost, c->stream) !=
+        hipSuccess)
+        return Q48_EHIP;
+    return hip_rc(hipStreamSynchronize(c->stream));
+}
+
+int q48_sample_step(q48_ctx *c, const int64_t *logits, int vocab, int64_t temperature,
+                    int top_k, int64_t top_p, uint64_t *rng, int *d_tokens, int cap)
+{
+    if (!c || !logits || vocab <= 0 || cap < 0 || !d_tokens ||
+        (!rng && !sample_greedy(temperature)))
+        return Q48_EINVAL;
+    if (sample_greedy(temperature))
+        return q48_argmax_step(c, logits, vocab, d_tokens, cap);
+    int rc = q48_sample_reserve(c, vocab);
+    if (rc)
+        return rc;
+    return launch_rc(q48_launch_sample(c, c->smp, logits, vocab, temperature, top_k, top_p, rng,
+                                       nullptr, d_tokens, cap));
 }
 
 int q48_graph_begin(q48_ctx *c)

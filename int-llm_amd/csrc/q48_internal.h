@@ -27,6 +27,8 @@ struct q48_ctx {
     int *rms_count;              // device: tickets, back to 0 after use: [0] EPI 3 blocks
                                  // finished, [256 + h] split-attention chunks of head h
     int rms_blocks;
+    int64_t *smp;                // device: sampling workspace (q48_sample_ws_words)
+    size_t smp_words;
     hipGraph_t graph;            // captured decode step
     hipGraphExec_t graph_exec;
     int capturing;
@@ -102,6 +104,12 @@ int q48_launch_add(q48_ctx *c, int64_t *acc, const int64_t *d, int n);
 int q48_launch_embed(q48_ctx *c, int64_t *out, const int64_t *table,
                      const int *d_token, int token, int dim);
 int q48_launch_argmax(q48_ctx *c, int *d_out, const int64_t *v, int n);
+// sample_token: the sampling workspace size in int64 words for n logits, and
+// the kernel chain (greedy temperatures are the caller's: argmax); with
+// tokens != nullptr the token goes to the decode-step state
+size_t q48_sample_ws_words(int n);
+int q48_launch_sample(q48_ctx *c, int64_t *ws, const int64_t *logits, int n, int64_t temperature,
+                      int top_k, int64_t top_p, uint64_t *rng, int *out_tok, int *tokens, int cap);
 int q48_launch_zero(q48_ctx *c, void *p, size_t bytes);
 int q48_launch_math_init(q48_ctx *c);
 int q48_launch_fp_eval(q48_ctx *c, int func, const int64_t *x,

@@ -43,6 +43,11 @@ struct q48h_model {
     int64_t *act;               /* device activations */
     int64_t *hidden, *normed, *qkv, *attn, *o, *gu, *h_ffn, *mlp, *logits;
     int *d_tokens;              /* device: tokens of graph-replayed decode steps */
+    /* sampling (sample_token, llama_int.c:2958-3039); greedy while
+     * temperature < ONE / 100 */
+    int64_t temperature, top_p;
+    int top_k;
+    uint64_t *d_rng;            /* device: xoroshiro128+ state */
     int64_t *r_attn, *r_ffn;    /* device: rmsnorm statistics of hidden for the next norm */
     int64_t *s_attn, *s_ffn;    /* device: the same as partial sums (Q48_STATS_WORDS) */
     int fused;                  /* 0: one op per kernel; 1: fused, norm statistics in
@@ -319,9 +324,49 @@ void q48h_model_free(q48h_model *m)
     q48_free(m->ctx, m->vc);
     q48_free(m->ctx, m->act);
     q48_free(m->ctx, m->d_tokens);
+    q48_free(m->ctx, m->d_rng);
     if (m->graph_ready)
         q48_graph_drop(m->ctx);
     free(m);
+}
+
+int q48h_model_set_sampling(q48h_model *m, int64_t temperature, int top_k, int64_t top_p,
+                            uint64_t seed)
+{
+    if (!m)
+        return Q48_EINVAL;
+    int rc;
+    if (!m->d_rng && (rc = q48_malloc(m->ctx, (void **)&m->d_rng, 2 * sizeof(uint64_t))))
+        return rc;
+    uint64_t st[2];
+    q48_rng_seed(seed, st);
+    if ((rc = q48_memcpy_h2d(m->ctx, m->d_rng, st, sizeof st)))
+        return rc;
+    if ((rc = q48_sync(m->ctx)))
+        return rc;
+    m->temperature = temperature;
+    m->top_k = top_k;
+    m->top_p = top_p;
+    drop_graph(m);   /* the parameters are arguments of the captured kernels */
+    return Q48_OK;
+}
+
+/* The next token from the logits on the device: sample_token with the
+ * model's parameters (argmax below a temperature of 0.01). */
+static int select_token(q48h_model *m, int *next)
+{
+    if (m->temperature >= Q48_ONE / 100)
+        return q48_sample(m->ctx, m->logits, m->c.vocab, m->temperature, m->top_k, m->top_p,
+                          m->d_rng, next);
+    return q48_argmax(m->ctx, m->logits, m->c.vocab, next);
+}
+
+static int select_token_step(q48h_model *m)
+{
+    if (m->temperature >= Q48_ONE / 100)
+        return q48_sample_step(m->ctx, m->logits, m->c.vocab, m->temperature, m->top_k,
+                               m->top_p, m->d_rng, m->d_tokens, m->c.max_seq);
+    return q48_argmax_step(m->ctx, m->logits, m->c.vocab, m->d_tokens, m->c.max_seq);
 }
 
 void q48h_model_set_fused(q48h_model *m, int fused)
@@ -828,7 +873,7 @@ int q48h_forward(q48h_model *m, int token, int pos, int64_t *logits, int *next)
         return Q48_ERANGE;
     TRY(enqueue_forward(m, token, pos));
     if (next)
-        TRY(q48_argmax(m->ctx, m->logits, c->vocab, next));
+        TRY(select_token(m, next));
     if (logits)
         TRY(q48_memcpy_d2h(m->ctx, logits, m->logits, (size_t)c->vocab * 8));
     if (!next && !logits)
@@ -858,7 +903,9 @@ int q48h_generate(q48h_model *m, const int *prompt, int prompt_len, int max_new,
     double t0 = now_s();
     for (int pos = 0; pos < prompt_len && rc == Q48_OK; ++pos) {
         int next;
-        rc = q48h_forward(m, out_tokens[pos], pos, logits, &next);
+        /* the token is chosen (and a sample drawn) at the last prompt
+         * position only (llama_int.c:3087-3090) */
+        rc = q48h_forward(m, out_tokens[pos], pos, logits, pos == prompt_len - 1 ? &next : NULL);
         if (rc)
             break;
         if (step_hash)
@@ -938,21 +985,20 @@ int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_to
 /* graph-replayed greedy decode                                            */
 /* ---------------------------------------------------------------------- */
 
-/* Run decode step 0 eagerly in step mode (forward(token, pos), device
- * argmax recorded as tokens[0]) -- workspaces reach their size outside any
+/* Run decode step 0 eagerly in step mode (forward(token, pos), the device
+ * token choice -- argmax or sample_token -- recorded as tokens[0]) -- workspaces reach their size outside any
  * capture -- then capture the same step into the context graph.  Kernels
  * read token / pos from the device step state, so the graph serves every
  * later position. */
 static int first_step_and_capture(q48h_model *m, int token, int pos)
 {
     q48_ctx *x = m->ctx;
-    const q48h_config *c = &m->c;
     TRY(q48_step_mode(x, 1));
     int rc = q48_step_set(x, token, pos);
     if (rc == Q48_OK)
         rc = enqueue_forward(m, token, pos);
     if (rc == Q48_OK)
-        rc = q48_argmax_step(x, m->logits, c->vocab, m->d_tokens, c->max_seq);
+        rc = select_token_step(m);
     if (rc == Q48_OK)
         rc = q48_sync(x);
     /* attention picks its kernels by position (split from q48_attn_split_min):
@@ -967,7 +1013,7 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
         if (rc == Q48_OK) {
             int rc1 = enqueue_forward(m, token, pos);
             if (rc1 == Q48_OK)
-                rc1 = q48_argmax_step(x, m->logits, c->vocab, m->d_tokens, c->max_seq);
+                rc1 = select_token_step(m);
             rc = q48_graph_end(x);
             if (rc1)
                 rc = rc1;

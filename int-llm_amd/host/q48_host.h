@@ -128,10 +128,19 @@ void q48h_model_set_prefetch(q48h_model *m, int on);
  * bfloat16 value or dim or ffn is not a multiple of 512. */
 int q48h_model_set_bf16(q48h_model *m, int on);
 
-/* Greedy decode of n steps replayed from a captured graph: step i runs
- * forward(token_i, start_pos + i) and its argmax becomes token_{i+1} on the
- * device, with no host round trip between steps.  out_tokens[i] receives
- * the argmax of step i.  Returns the number of steps up to and including
+/* Token selection by sample_token (llama_int.c:2958-3039) instead of argmax
+ * for q48h_forward's next, q48h_generate, q48h_decode_from and
+ * q48h_decode_graph: temperature and top_p in Q16.48 (top_p >= ONE: off),
+ * top_k (0: off), the rng seeded by rng_seed(seed) (llama_int.c:2909-2920)
+ * and advanced by each draw.  A temperature below ONE / 100 is greedy (the
+ * default). */
+int q48h_model_set_sampling(q48h_model *m, int64_t temperature, int top_k, int64_t top_p,
+                            uint64_t seed);
+
+/* Decode of n steps replayed from a captured graph: step i runs
+ * forward(token_i, start_pos + i) and its argmax (or, with sampling set,
+ * its sample_token draw) becomes token_{i+1} on the device, with no host
+ * round trip between steps.  out_tokens[i] receives the token of step i.  Returns the number of steps up to and including
  * the first EOS (generate stops there, llama_int.c:3111), or n. */
 int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
                       q48h_stats *stats);

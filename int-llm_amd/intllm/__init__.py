@@ -59,6 +59,9 @@ ABI_SIGNATURES = {
     "q48_add": [_P, _P, _P, _I],
     "q48_embed": [_P, _P, _P, _I, _I],
     "q48_argmax": [_P, _P, _I, C.POINTER(C.c_int)],
+    "q48_sample": [_P, _P, _I, C.c_int64, _I, C.c_int64, _P, C.POINTER(C.c_int)],
+    "q48_sample_step": [_P, _P, _I, C.c_int64, _I, C.c_int64, _P, _P, _I],
+    "q48_sample_reserve": [_P, _I],
     "q48_rope_tables": [_P, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)],
     "q48_fp_eval": [_P, _I, _P, _P, _P, _P, _I],
     "q48_rmsnorm_gemv": [_P, _P, _P, _P, _P, _I, _I],
@@ -126,6 +129,8 @@ def hip_lib() -> C.CDLL:
             fn.restype = C.c_int
         lib.q48_strerror.argtypes = [C.c_int]
         lib.q48_strerror.restype = C.c_char_p
+        lib.q48_rng_seed.argtypes = [C.c_uint64, C.POINTER(C.c_uint64)]
+        lib.q48_rng_seed.restype = None
         _hip = lib
     return _hip
 
@@ -281,6 +286,14 @@ class Context:
         check("q48_argmax", hip_lib().q48_argmax(self.h, v, n, C.byref(r)))
         return r.value
 
+    def sample(self, v, n, temperature, top_k, top_p, rng) -> int:
+        """sample_token (llama_int.c:2958-3039) of device logits v[0..n);
+        rng: device pointer to the 2-word xoroshiro128+ state."""
+        r = C.c_int()
+        check("q48_sample", hip_lib().q48_sample(self.h, v, n, temperature, top_k, top_p, rng,
+                                                 C.byref(r)))
+        return r.value
+
     def zero(self, p, nbytes):
         return check("q48_zero", hip_lib().q48_zero(self.h, p, nbytes))
 
@@ -418,6 +431,7 @@ HOST_SIGNATURES = {
     "q48h_model_set_fused": ([_P, _I], None),
     "q48h_model_set_prefetch": ([_P, _I], None),
     "q48h_model_set_bf16": ([_P, _I], C.c_int),
+    "q48h_model_set_sampling": ([_P, C.c_int64, _I, C.c_int64, C.c_uint64], C.c_int),
 
     "q48h_gemv_sweep": ([_P, _I, C.POINTER(C.c_int), C.POINTER(C.c_double)], C.c_int),
     "q48h_decode_graph": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
@@ -491,12 +505,19 @@ class HostModel:
     def kv_pointers(self):
         return host_lib().q48h_kv_keys(self.h), host_lib().q48h_kv_values(self.h)
 
-    def forward(self, token: int, pos: int, vocab: int, logits: bool = True):
+    def forward(self, token: int, pos: int, vocab: int, logits: bool = True,
+                choose: bool = True):
+        """llama_forward; with choose, also the next token (argmax, or a
+        sample_token draw when sampling is set); else next is None."""
         out = np.empty(vocab, dtype=np.int64) if logits else None
         nxt = C.c_int()
         check("q48h_forward", host_lib().q48h_forward(
-            self.h, token, pos, out.ctypes.data if logits else None, C.byref(nxt)))
-        return nxt.value, out
+            self.h, token, pos, out.ctypes.data if logits else None,
+            C.byref(nxt) if choose else None))
+        return (nxt.value if choose else None), out
+
+    def kv_reset(self):
+        check("q48h_kv_reset", host_lib().q48h_kv_reset(self.h))
 
     def generate(self, prompt, max_new: int, hashes: bool = True):
         p = (C.c_int * len(prompt))(*prompt)
@@ -517,6 +538,13 @@ class HostModel:
     def set_bf16(self, on: bool):
         """Read the projection matrices and lm_head as bfloat16 bits (mode 3)."""
         check("q48h_model_set_bf16", host_lib().q48h_model_set_bf16(self.h, int(bool(on))))
+
+    def set_sampling(self, temperature: int, top_k: int = 0, top_p: int = 1 << 48,
+                     seed: int = 0):
+        """sample_token instead of argmax (temperature >= ONE / 100); the rng
+        is seeded by rng_seed(seed)."""
+        check("q48h_model_set_sampling", host_lib().q48h_model_set_sampling(
+            self.h, int(temperature), int(top_k), int(top_p), int(seed) & ((1 << 64) - 1)))
 
     def set_fused(self, mode: int):
         """0: one op per reference step; 1: fused with per-block norm
@@ -553,3 +581,10 @@ def gpu_available() -> bool:
     if os.environ.get("HIP_VISIBLE_DEVICES", None) == "":
         return False
     return os.path.exists("/dev/kfd")
+
+
+def rng_seed(seed: int) -> list:
+    """rng_seed (llama_int.c:2909-2920): the 2-word xoroshiro128+ state."""
+    st = (C.c_uint64 * 2)()
+    hip_lib().q48_rng_seed(int(seed) & ((1 << 64) - 1), st)
+    return [st[0], st[1]]

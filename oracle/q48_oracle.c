@@ -810,3 +810,178 @@ int q48o_decode_from(q48o_model *m, int token, int start_pos, int n,
     free(logits);
     return steps;
 }
+
+/* ======================================================================
+ * Sampling (llama_int.c:2895-3039)
+ * ==================================================================== */
+
+static uint64_t splitmix_step(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+/* rng_seed, llama_int.c:2909-2920 */
+void q48o_rng_seed(uint64_t seed, uint64_t s[2])
+{
+    s[0] = splitmix_step(seed);
+    s[1] = splitmix_step(seed + 0x9E3779B97F4A7C15ULL);
+    if (s[0] == 0 && s[1] == 0)
+        s[0] = 1;
+}
+
+static uint64_t rotl64(uint64_t v, int k) { return (v << k) | (v >> (64 - k)); }
+
+/* rng_next, llama_int.c:2922-2929 (xoroshiro128+) */
+uint64_t q48o_rng_next(uint64_t s[2])
+{
+    const uint64_t a = s[0];
+    uint64_t b = s[1];
+    const uint64_t out = a + b;
+    b ^= a;
+    s[0] = rotl64(a, 55) ^ b ^ (b << 14);
+    s[1] = rotl64(b, 36);
+    return out;
+}
+
+static int cmp_desc_i64(const void *pa, const void *pb)
+{
+    const int64_t a = *(const int64_t *)pa, b = *(const int64_t *)pb;
+    return (a < b) - (a > b);
+}
+
+typedef struct {
+    int64_t p;
+    int i;
+} prob_idx;
+
+/* descending probability, ascending index among equal ones: the order in
+ * which the reference's repeated first-maximum search (llama_int.c:2998-
+ * 3007) takes the entries */
+static int cmp_prob_idx(const void *pa, const void *pb)
+{
+    const prob_idx *a = (const prob_idx *)pa, *b = (const prob_idx *)pb;
+    if (a->p != b->p)
+        return a->p > b->p ? -1 : 1;
+    return (a->i > b->i) - (a->i < b->i);
+}
+
+/* sample_token, llama_int.c:2958-3039 */
+int q48o_sample(const int64_t *logits, int n, int64_t temperature, int top_k,
+                int64_t top_p, uint64_t s[2])
+{
+    /* 2963-2964: greedy below a temperature of 0.01 */
+    if (temperature <= 0 || temperature < Q48_ONE / 100)
+        return q48o_argmax(logits, n);
+    int64_t *w = (int64_t *)malloc((size_t)n * 8);
+    /* 2970-2971: logits / T */
+    for (int i = 0; i < n; ++i)
+        w[i] = q48o_fp_div(logits[i], temperature);
+    /* 2974-2987: the k-th largest value (duplicates counted) is the
+     * threshold; smaller values become INT64_MIN / 2 */
+    if (top_k > 0 && top_k < n) {
+        int64_t *srt = (int64_t *)malloc((size_t)n * 8);
+        memcpy(srt, w, (size_t)n * 8);
+        qsort(srt, (size_t)n, 8, cmp_desc_i64);
+        const int64_t thr = srt[top_k - 1];
+        free(srt);
+        for (int i = 0; i < n; ++i)
+            if (w[i] < thr)
+                w[i] = INT64_MIN / 2;
+    }
+    /* 2990: softmax in place */
+    q48o_softmax(w, n);
+    /* 2993-3023: nucleus.  The reference takes, while the running sum is
+     * below top_p, the largest remaining positive probability (first index
+     * among equals); the same entries in the same order are the prefix of
+     * the positive probabilities sorted by (value desc, index asc).  Kept
+     * entries are renormalised by their (wrapping) sum, the rest zeroed. */
+    if (top_p > 0 && top_p < Q48_ONE) {
+        prob_idx *o = (prob_idx *)malloc((size_t)n * sizeof(prob_idx));
+        int np = 0;
+        for (int i = 0; i < n; ++i)
+            if (w[i] > 0) {
+                o[np].p = w[i];
+                o[np].i = i;
+                np++;
+            }
+        qsort(o, (size_t)np, sizeof(prob_idx), cmp_prob_idx);
+        uint8_t *keep = (uint8_t *)calloc((size_t)n, 1);
+        int64_t cum = 0;
+        for (int k = 0; k < np && cum < top_p; ++k) {
+            cum = (int64_t)((uint64_t)cum + (uint64_t)o[k].p);
+            keep[o[k].i] = 1;
+        }
+        free(o);
+        int64_t sum = 0;
+        for (int i = 0; i < n; ++i) {
+            if (!keep[i])
+                w[i] = 0;
+            sum = (int64_t)((uint64_t)sum + (uint64_t)w[i]);
+        }
+        free(keep);
+        if (sum > 0)
+            for (int i = 0; i < n; ++i)
+                if (w[i] > 0)
+                    w[i] = q48o_fp_div(w[i], sum);
+    }
+    /* 3027-3036: r in [0, ONE) from the top 48 bits of one draw; the first
+     * index whose running (wrapping) sum exceeds r, else the argmax */
+    const int64_t r = (int64_t)(q48o_rng_next(s) >> 16);
+    int64_t cum = 0;
+    int sel = -1;
+    for (int i = 0; i < n; ++i) {
+        cum = (int64_t)((uint64_t)cum + (uint64_t)w[i]);
+        if (cum > r) {
+            sel = i;
+            break;
+        }
+    }
+    if (sel < 0)
+        sel = q48o_argmax(w, n);
+    free(w);
+    return sel;
+}
+
+/* generate, llama_int.c:3067-3135 with sampling parameters */
+int q48o_generate_sampled(q48o_model *m, const int *prompt, int prompt_len,
+                          int max_new, int *out_tokens, uint64_t *step_hash,
+                          int *n_steps, int64_t temperature, int top_k,
+                          int64_t top_p, uint64_t seed)
+{
+    uint64_t s[2];
+    q48o_rng_seed(seed, s);
+    int vocab = m->c.vocab, steps = 0;
+    int64_t *logits = (int64_t *)malloc((size_t)vocab * 8);
+    q48o_kv_reset(m);
+    memcpy(out_tokens, prompt, (size_t)prompt_len * sizeof(int));
+    int total = prompt_len;
+    for (int pos = 0; pos < prompt_len; ++pos) {
+        if (q48o_forward(m, out_tokens[pos], pos, logits) != 0) {
+            free(logits);
+            return -1;
+        }
+        if (step_hash)
+            step_hash[steps] = q48s_fnv_i64(FNV_OFF, logits, (size_t)vocab);
+        steps++;
+        if (pos == prompt_len - 1)
+            out_tokens[total++] = q48o_sample(logits, vocab, temperature, top_k, top_p, s);
+    }
+    for (int i = 1; i < max_new; ++i) {
+        int pos = prompt_len + i - 1;
+        if (q48o_forward(m, out_tokens[pos], pos, logits) != 0)
+            break;
+        if (step_hash)
+            step_hash[steps] = q48s_fnv_i64(FNV_OFF, logits, (size_t)vocab);
+        steps++;
+        int next = q48o_sample(logits, vocab, temperature, top_k, top_p, s);
+        if (next == LLAMA_EOS)
+            break;
+        out_tokens[total++] = next;
+    }
+    free(logits);
+    if (n_steps)
+        *n_steps = steps;
+    return total;
+}

@@ -98,6 +98,24 @@ int q48o_generate(q48o_model *m, const int *prompt, int prompt_len,
 int q48o_decode_from(q48o_model *m, int token, int start_pos, int n,
                      int *out_tokens, uint64_t *step_hash);
 
+/* ---- sampling (llama_int.c:2895-3039) ----------------------------------- */
+/* rng_seed (llama_int.c:2909-2920): SplitMix64 of seed and of
+ * seed + 0x9E3779B97F4A7C15 into the two state words; (0, 0) -> (1, 0). */
+void     q48o_rng_seed(uint64_t seed, uint64_t s[2]);
+/* rng_next (llama_int.c:2922-2929): xoroshiro128+ (55/14/36). */
+uint64_t q48o_rng_next(uint64_t s[2]);
+/* sample_token (llama_int.c:2958-3039): argmax when temperature < ONE/100
+ * (or <= 0); otherwise temperature, top-k mask, softmax, top-p nucleus and
+ * one draw of rng_next.  s is advanced in place when a draw is made. */
+int q48o_sample(const int64_t *logits, int n, int64_t temperature, int top_k,
+                int64_t top_p, uint64_t s[2]);
+/* generate (llama_int.c:3067-3135) with sampling parameters sp (rng seeded
+ * by rng_seed(seed)); step_hash as in q48o_generate. */
+int q48o_generate_sampled(q48o_model *m, const int *prompt, int prompt_len,
+                          int max_new, int *out_tokens, uint64_t *step_hash,
+                          int *n_steps, int64_t temperature, int top_k,
+                          int64_t top_p, uint64_t seed);
+
 #ifdef __cplusplus
 }
 #endif

@@ -272,3 +272,54 @@ void q48r_model_free_mgw(void *mm)
     free(m->scratch_buf);
     free(m);
 }
+
+/* ---- sampling: the reference's own rng and sample_token ---------------- */
+void q48r_rng_seed(uint64_t seed, uint64_t s[2])
+{
+    rng_state_t r;
+    rng_seed(&r, seed);
+    s[0] = r.s[0];
+    s[1] = r.s[1];
+}
+
+uint64_t q48r_rng_next(uint64_t s[2])
+{
+    rng_state_t r = {{s[0], s[1]}};
+    uint64_t v = rng_next(&r);
+    s[0] = r.s[0];
+    s[1] = r.s[1];
+    return v;
+}
+
+/* sample_token (llama_int.c:2958-3039) with the given parameters and rng
+ * state; the state is written back. */
+int q48r_sample(const int64_t *logits, int n, int64_t temperature, int top_k,
+                int64_t top_p, uint64_t s[2])
+{
+    sample_params_t sp;
+    memset(&sp, 0, sizeof sp);
+    sp.temperature = temperature;
+    sp.top_k = top_k;
+    sp.top_p = top_p;
+    sp.rng.s[0] = s[0];
+    sp.rng.s[1] = s[1];
+    int tok = sample_token(logits, n, &sp);
+    s[0] = sp.rng.s[0];
+    s[1] = sp.rng.s[1];
+    return tok;
+}
+
+/* The reference's generate() with sampling (rng_seed(seed), as its CLI
+ * does for --seed, llama_int.c:4776-4790). */
+int q48r_generate_sampled(void *mm, const int *prompt, int plen, int max_new,
+                          int *out, int64_t temperature, int top_k,
+                          int64_t top_p, uint64_t seed)
+{
+    sample_params_t sp;
+    memset(&sp, 0, sizeof sp);
+    sp.temperature = temperature;
+    sp.top_k = top_k;
+    sp.top_p = top_p;
+    rng_seed(&sp.rng, seed);
+    return generate((llama_model_t *)mm, prompt, plen, max_new, out, &sp);
+}

@@ -66,6 +66,10 @@ def ref():
         "q48s_tokens": ([P, I, U, I, I], None),
         "q48s_fnv_i64": ([U, P, C.c_size_t], U),
         "q48r_bf16_to_q48": ([C.c_uint16], C.c_int64),
+        "q48r_rng_seed": ([U, P], None),
+        "q48r_rng_next": ([P], U),
+        "q48r_sample": ([P, I, C.c_int64, I, C.c_int64, P], I),
+        "q48r_generate_sampled": ([P, P, I, I, P, C.c_int64, I, C.c_int64, U], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(lib, name)
@@ -317,6 +321,84 @@ def gen_gemm():
                                   "sequential prefill 3081-3092) via oracle/ref_harness.c",
                         "inputs": "W as gemv.json, X[T][K] sigma 1 raw Q16.48",
                         "shapes": res})
+
+
+def sample_cases():
+    """The sampling grid: every parameter combination on 512 logits of each
+    kind, and a subset on 32000 (the TinyLlama vocabulary)."""
+    cases = []
+    for kind in spec.SAMPLE_KINDS:
+        for ti, T in enumerate(spec.SAMPLE_TEMPS):
+            for ki, k in enumerate(spec.SAMPLE_TOPK):
+                for pi, p in enumerate(spec.SAMPLE_TOPP):
+                    seed = 1000 * ti + 100 * ki + 10 * pi + spec.SAMPLE_KINDS.index(kind)
+                    cases.append((kind, seed, 512, T, 511 if k is None else k, p))
+                    if kind in ("gauss", "ties") and ti in (3, 5) and ki in (0, 4) and pi in (0, 3, 4):
+                        cases.append((kind, seed, 32000, T, 31999 if k is None else k, p))
+    return cases
+
+
+def gen_sample():
+    # rng_seed / rng_next streams
+    rng = {}
+    for seed in (0, 1, 42, 0x9E3779B97F4A7C15, 2**64 - 1):
+        s = (C.c_uint64 * 2)()
+        R.q48r_rng_seed(seed, s)
+        st = ["%016x" % s[0], "%016x" % s[1]]
+        rng[str(seed)] = {"state": st, "next": ["%016x" % R.q48r_rng_next(s) for _ in range(8)]}
+    out = []
+    t = time.time()
+    for (kind, seed, n, T, k, p) in sample_cases():
+        x = spec.sample_logits(kind, seed, n)
+        s = (C.c_uint64 * 2)()
+        R.q48r_rng_seed(seed * 7919 + 1, s)
+        s_in = [s[0], s[1]]
+        tok = R.q48r_sample(x.ctypes.data, n, T, k, p, s)
+        out.append({"kind": kind, "seed": seed, "n": n, "T": T, "top_k": k, "top_p": p,
+                    "rng_in": ["%016x" % v for v in s_in], "token": tok,
+                    "rng_out": ["%016x" % s[0], "%016x" % s[1]]})
+    print(f"  {len(out)} sample_token cases in {time.time() - t:.1f}s", flush=True)
+    # generate() with sampling, tiny model
+    gens = []
+    prompt = spec.prompt(spec.SEED_TINY, 16, spec.TINY[6])
+    cfg = RefCfg(*spec.TINY)
+    m = model(cfg, spec.SEED_TINY)
+    for (T, k, p, seed) in spec.SAMPLE_GEN:
+        cap = len(prompt) + 32 + 1
+        pr = (C.c_int * len(prompt))(*prompt)
+        o = (C.c_int * cap)()
+        total = R.q48r_generate_sampled(m, pr, len(prompt), 32, o, T, k, p, seed)
+        gens.append({"T": T, "top_k": k, "top_p": p, "seed": seed, "tokens": list(o[:total])})
+    R.q48r_model_free(m)
+    write("sample.json", {
+        "source": "rng_seed / rng_next / sample_token / generate(sp) "
+                  "(llama_int.c:2909-2929, 2958-3039, 3067-3135) via oracle/ref_harness.c",
+        "logits": "tests/spec.py sample_logits(kind, seed, n); rng_in = rng_seed(seed * 7919 + 1)",
+        "rng": rng, "cases": out,
+        "generate_tiny": {"config": list(spec.TINY), "seed": spec.SEED_TINY,
+                          "prompt": prompt, "max_new": 32, "runs": gens}})
+
+
+def gen_sample_tl():
+    """generate() with sampling on the TinyLlama-shape model (config 3):
+    32-token prompt, 16 sampled tokens."""
+    prompt = spec.prompt(spec.SEED_TL, 32, spec.TINYLLAMA[6])
+    cfg = RefCfg(*spec.TINYLLAMA)
+    m = model(cfg, spec.SEED_TL)
+    T, k, p, seed = spec.SAMPLE_GEN_TL
+    cap = len(prompt) + 16 + 1
+    pr = (C.c_int * len(prompt))(*prompt)
+    o = (C.c_int * cap)()
+    t = time.time()
+    total = R.q48r_generate_sampled(m, pr, len(prompt), 16, o, T, k, p, seed)
+    tg = time.time() - t
+    R.q48r_model_free(m)
+    write("sample_tinyllama.json", {
+        "source": "generate(sp) (llama_int.c:3067-3135, sample_token 2958-3039) via "
+                  "oracle/ref_harness.c",
+        "config": list(spec.TINYLLAMA), "seed": spec.SEED_TL, "prompt": prompt, "max_new": 16,
+        "T": T, "top_k": k, "top_p": p, "rng_seed": seed, "tokens": list(o[:total]),
+        "ref_cpu_s": round(tg, 1)})
 
 
 R = None

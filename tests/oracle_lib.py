@@ -51,6 +51,9 @@ _SIG = {
     "q48o_forward": ([P, I, I, P], I),
     "q48o_generate": ([P, P, I, I, P, P, P], I),
     "q48o_decode_from": ([P, I, I, I, P, P], I),
+    "q48o_rng_seed": ([U, P], None), "q48o_rng_next": ([P], U),
+    "q48o_sample": ([P, I, I64, I, I64, P], I),
+    "q48o_generate_sampled": ([P, P, I, I, P, P, P, I64, I, I64, U], I),
     "q48s_fill": ([P, I64, I64, U, I64, I, I], None),
     "q48s_tensor_seed": ([U, C.c_char_p], U),
     "q48s_fnv_i64": ([U, P, C.c_size_t], U),
@@ -124,6 +127,16 @@ class Model:
         total = load().q48o_generate(self.h, p, len(prompt), max_new, out, hs, C.byref(n))
         return list(out[:total]), ["%016x" % v for v in hs[:n.value]]
 
+    def generate_sampled(self, prompt, max_new, temperature, top_k, top_p, seed):
+        cap = len(prompt) + max_new + 1
+        p = (C.c_int * len(prompt))(*prompt)
+        out = (C.c_int * cap)()
+        hs = (C.c_uint64 * cap)()
+        n = C.c_int()
+        total = load().q48o_generate_sampled(self.h, p, len(prompt), max_new, out, hs,
+                                             C.byref(n), temperature, top_k, top_p, seed)
+        return list(out[:total]), ["%016x" % v for v in hs[:n.value]]
+
     def forward(self, token, pos):
         lg = np.empty(self.cfg.vocab, dtype=np.int64)
         rc = load().q48o_forward(self.h, token, pos, lg.ctypes.data)
@@ -134,3 +147,17 @@ class Model:
         hs = (C.c_uint64 * n)()
         steps = load().q48o_decode_from(self.h, token, start, n, out, hs)
         return list(out[:steps]), ["%016x" % v for v in hs[:steps]]
+
+
+def rng_seed(seed: int) -> list[int]:
+    s = (C.c_uint64 * 2)()
+    load().q48o_rng_seed(seed & ((1 << 64) - 1), s)
+    return [s[0], s[1]]
+
+
+def sample(logits: np.ndarray, temperature: int, top_k: int, top_p: int, state: list[int]):
+    """sample_token on the oracle: (token, state after)."""
+    s = (C.c_uint64 * 2)(*state)
+    x = np.ascontiguousarray(logits, dtype=np.int64)
+    tok = load().q48o_sample(x.ctypes.data, x.size, temperature, top_k, top_p, s)
+    return tok, [s[0], s[1]]

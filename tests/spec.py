@@ -192,3 +192,44 @@ def rmsnorm_inputs(synth, dim: int):
 def softmax_inputs(synth, n: int):
     """Scores of spread ~4 so the +-10 clamp of fp_safe_exp is exercised."""
     return synth(f"softmax.x.{n}", 1, n, SEED_OPS, 4 * ONE, 0)
+
+
+# ---- sampling (sample_token, llama_int.c:2958-3039) ------------------------
+SAMPLE_KINDS = ("gauss", "ties", "peaked", "extreme")
+
+
+def sample_logits(kind: str, seed: int, n: int) -> np.ndarray:
+    """Deterministic logits for the sampling cases, from integer draws only
+    (identical on every host):
+      gauss    sum of four uniforms, spread about 3.0
+      ties     eight distinct levels: top-k thresholds and nucleus cuts
+               fall inside runs of equal values
+      peaked   one dominant logit (+12) over a spread of about 1.0
+      extreme  large magnitudes (up to +-30000) and the int64 extremes:
+               temperature division wraps, exp clamps at +-10"""
+    rng = np.random.default_rng(seed)
+    u = rng.integers(-(ONE // 2), ONE // 2, size=(4, n), dtype=np.int64)
+    if kind == "gauss":
+        return (u.sum(axis=0) * 3).astype(np.int64)
+    if kind == "ties":
+        lv = rng.integers(-4 * ONE, 4 * ONE, size=8, dtype=np.int64)
+        return lv[rng.integers(0, 8, size=n)]
+    if kind == "peaked":
+        v = u.sum(axis=0)
+        v[rng.integers(0, n)] += 12 * ONE
+        return v.astype(np.int64)
+    v = (u.sum(axis=0) * 30000).astype(np.int64)
+    v[rng.integers(0, n, size=4)] = [INT64_MAX, INT64_MIN, INT64_MAX - 1, 1]
+    return v
+
+
+# (temperature, top_k, top_p) in Q16.48 / counts; None top_k = n - 1
+SAMPLE_TEMPS = [0, ONE // 200, ONE // 100, ONE * 3 // 10, ONE * 7 // 10, ONE,
+                ONE * 3 // 2, 3 * ONE]
+SAMPLE_TOPK = [0, 1, 2, 10, 50, None]
+SAMPLE_TOPP = [0, ONE // 20, ONE // 2, ONE * 9 // 10, ONE - ONE // 1000, ONE]
+
+# generate() with sampling on the tiny model: (temperature, top_k, top_p, seed)
+SAMPLE_GEN = [(ONE * 8 // 10, 40, ONE * 9 // 10, 7), (ONE, 0, ONE, 11),
+              (ONE // 2, 5, ONE // 2, 3), (ONE * 3 // 2, 0, ONE * 95 // 100, 12345)]
+SAMPLE_GEN_TL = (ONE * 8 // 10, 40, ONE * 9 // 10, 2024)

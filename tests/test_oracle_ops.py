@@ -151,3 +151,59 @@ def test_generate_stops_at_max_seq(oracle):
         assert len(hs) <= 20 and len(toks) <= 21
     finally:
         m.free()
+
+
+def test_rng_matches_reference(oracle):
+    """rng_seed (SplitMix64) and rng_next (xoroshiro128+), llama_int.c:2909-2929,
+    against the reference's own streams."""
+    g = golden("sample.json")["rng"]
+    for seed, v in g.items():
+        st = O.rng_seed(int(seed))
+        assert ["%016x" % w for w in st] == v["state"]
+        s = (C.c_uint64 * 2)(*st)
+        assert ["%016x" % O.load().q48o_rng_next(s) for _ in range(8)] == v["next"]
+
+
+def test_sample_token_matches_reference(oracle):
+    """sample_token (llama_int.c:2958-3039) on 1176 cases: four logit kinds
+    (spread, runs of ties, one dominant logit, extreme magnitudes that wrap in
+    the temperature division) x temperatures on both sides of the 0.01
+    greedy floor x top-k (off, 1, 2, 10, 50, n - 1) x top-p (off, 0.05, 0.5,
+    0.9, 0.999, 1.0): the token and the rng state after it equal the
+    reference's."""
+    for c in golden("sample.json")["cases"]:
+        x = spec.sample_logits(c["kind"], c["seed"], c["n"])
+        st = [int(v, 16) for v in c["rng_in"]]
+        tok, st2 = O.sample(x, c["T"], c["top_k"], c["top_p"], st)
+        assert tok == c["token"], c
+        assert ["%016x" % v for v in st2] == c["rng_out"], c
+
+
+def test_sample_token_properties(oracle):
+    """Closed forms the reference fixes, on fresh logits: below the 0.01
+    floor it is argmax and draws nothing; top_k = 1 always gives the first
+    maximum (every other logit is masked to exp(-inf) = 0); with top_p under
+    the largest probability only that entry survives."""
+    rng = np.random.default_rng(99)
+    for _ in range(50):
+        n = int(rng.integers(2, 700))
+        x = rng.integers(-8 * ONE, 8 * ONE, size=n, dtype=np.int64)
+        st = O.rng_seed(int(rng.integers(0, 2**63)))
+        am = int(np.argmax(x))
+        assert O.sample(x, ONE // 100 - 1, 0, ONE, st) == (am, st)
+        assert O.sample(x, ONE // 2, 1, ONE, st)[0] == am
+        assert O.sample(x, ONE, 0, 1, st)[0] == am
+
+
+def test_generate_sampled_matches_reference(oracle):
+    """generate() with sampling parameters (llama_int.c:3067-3135) on the tiny
+    model: four (temperature, top-k, top-p, seed) settings, 32 new tokens."""
+    g = golden("sample.json")["generate_tiny"]
+    m = O.Model(spec.TINY, g["seed"])
+    try:
+        for r in g["runs"]:
+            toks, _ = m.generate_sampled(g["prompt"], g["max_new"], r["T"], r["top_k"],
+                                         r["top_p"], r["seed"])
+            assert toks == r["tokens"], r
+    finally:
+        m.free()
