@@ -216,6 +216,8 @@ def main():
                     help="decode-token GEMV sequences timed back to back for the roofline")
     ap.add_argument("--gemm-reps", type=int, default=5,
                     help="int8 GEMM calls timed per config-4 shape; 0 skips config 4")
+    ap.add_argument("--no-sample", action="store_true",
+                    help="skip the sampled-decode measurement")
     ap.add_argument("--no-bf16", action="store_true",
                     help="skip the bfloat16-resident-weights decode measurement")
     ap.add_argument("--gemm-only", action="store_true",
@@ -316,6 +318,28 @@ def main():
                 "gemv_avg_launch_us": round(bus, 3), "gemv_achieved_GBs": round(bach, 1),
                 "gemv_frac": round(bach / HBM_PEAK_GBS, 4)}
 
+    # sampled decode (row f4): the same graph-replayed steps with
+    # sample_token on the device (T 0.8, top-k 40, top-p 0.9) instead of
+    # argmax; the tokens are not the greedy stream, so they stay out of the
+    # parity check (tests/test_gpu_sample.py pins them)
+    sampled = None
+    if not args.no_sample:
+        T, k, p_, seed = spec.SAMPLE_GEN_TL
+        m.set_sampling(T, k, p_, seed)
+        st_tok, _, _ = m.decode_graph(toks[-1], pos, args.warmup)
+        ctx.sync()
+        s0 = pos + args.warmup
+        t0 = time.perf_counter()
+        m.decode_graph(st_tok[-1] if st_tok else toks[-1], s0, args.steps)
+        ctx.sync()
+        sms = 1e3 * (time.perf_counter() - t0) / args.steps
+        m.set_sampling(0)
+        log(f"sampled decode {sms:.3f} ms/tok")
+        sampled = {"workload": "config 3 decode, int64 weights, sample_token on the device "
+                               "(temperature 0.8, top-k 40, top-p 0.9)",
+                   "tok_s": round(1e3 / sms, 2), "ms_per_tok": round(sms, 4),
+                   "positions": [s0, s0 + args.steps]}
+
     # token stream vs the reference's (golden), over the tokens both have
     ref_new = gold["tokens"][len(prompt):]
     n_cmp = min(len(ref_new), len(toks))
@@ -386,6 +410,7 @@ def main():
         "gemm_prefill": gemm,
         "long_context": longctx,
         "bf16_resident": bf16,
+        "sampled_decode": sampled,
         "parity": parity,
     }
     print(json.dumps(line), flush=True)

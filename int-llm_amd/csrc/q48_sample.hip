@@ -136,22 +136,128 @@ __device__ __forceinline__ void blk_argmax(int64_t &v, int &idx, int64_t *redv, 
         }
 }
 
-// exclusive prefix sum (mod 2^64) over the threads of the block in order
+// exclusive prefix sum (mod 2^64) over the threads of the block in order:
+// a scan inside each wave, then the wave totals (tmp holds NT / 64 words)
 template <int NT>
 __device__ __forceinline__ uint64_t blk_excl_scan(uint64_t v, uint64_t *tmp)
 {
-    const int tid = threadIdx.x;
-    __syncthreads();
-    tmp[tid] = v;
-    __syncthreads();
-    // Hillis-Steele inclusive scan over NT entries
-    for (int off = 1; off < NT; off <<= 1) {
-        const uint64_t o = tid >= off ? tmp[tid - off] : 0;
-        __syncthreads();
-        tmp[tid] += o;
-        __syncthreads();
+    const int tid = threadIdx.x, lane = tid & 63;
+    uint64_t incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint64_t o = __shfl_up(incl, off, 64);
+        if (lane >= off)
+            incl += o;
     }
-    return tmp[tid] - v;
+    __syncthreads();
+    if (lane == 63)
+        tmp[tid >> 6] = incl;
+    __syncthreads();
+    uint64_t before = 0;
+    for (int w = 0; w < (tid >> 6); ++w)
+        before += tmp[w];
+    return before + incl - v;
+}
+
+// Walks of the radix selections, one wave (threads 0-63, all active): lane
+// l holds buckets 4 l .. 4 l + 3 of the 256.  The bucket where the k-th
+// largest lies (counts from the top: above < k <= above + cnt[b]) ...
+__device__ __forceinline__ void walk_count(const int *cnt, int nb, int k, int *out_b,
+                                           int *out_krem)
+{
+    const int l = threadIdx.x;
+    int c[4], tot = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        c[j] = 4 * l + j < nb ? cnt[4 * l + j] : 0;
+        tot += c[j];
+    }
+    int incl = tot;   // sum over lanes >= l
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_down(incl, off, 64);
+        if (l + off < 64)
+            incl += o;
+    }
+    int above = incl - tot;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+        if (above < k && k <= above + c[j]) {
+            *out_b = 4 * l + j;
+            *out_krem = k - above;
+        }
+        above += c[j];
+    }
+}
+
+// ... and the highest bucket whose sum from the top reaches top_p (sums
+// start at base; -1 when even the whole range stays below)
+__device__ __forceinline__ void walk_sum(const int *cnt, const unsigned long long *sum, int nb,
+                                         uint64_t base, int64_t top_p, int *out_b,
+                                         uint64_t *out_above, int *out_ties)
+{
+    const int l = threadIdx.x;
+    uint64_t sm[4], tot = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        sm[j] = 4 * l + j < nb ? sum[4 * l + j] : 0;
+        tot += sm[j];
+    }
+    uint64_t incl = tot;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint64_t o = __shfl_down(incl, off, 64);
+        if (l + off < 64)
+            incl += o;
+    }
+    uint64_t above = base + incl - tot;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+        if ((int64_t)above < top_p && (int64_t)(above + sm[j]) >= top_p) {
+            *out_b = 4 * l + j;
+            *out_above = above;
+            *out_ties = cnt[4 * l + j];
+        }
+        above += sm[j];
+    }
+}
+
+// Passes of the single-block kernels over n values: the loads of a batch of
+// SMP_U go out before any is used (one memory round trip per batch instead
+// of one per element).  pass_strided visits i = tid, tid + SMP_B, ...;
+// pass_chunk visits [lo, hi) in index order.
+constexpr int SMP_U = 16;
+
+template <class F>
+__device__ __forceinline__ void pass_strided(const int64_t *a, int n, F f)
+{
+    for (int i0 = threadIdx.x; i0 < n; i0 += SMP_B * SMP_U) {
+        int64_t v[SMP_U];
+#pragma unroll
+        for (int u = 0; u < SMP_U; ++u) {
+            const int i = i0 + u * SMP_B;
+            v[u] = a[i < n ? i : n - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < SMP_U; ++u)
+            if (i0 + u * SMP_B < n)
+                f(i0 + u * SMP_B, v[u]);
+    }
+}
+
+template <class F>
+__device__ __forceinline__ void pass_chunk(const int64_t *a, int lo, int hi, F f)
+{
+    for (int i0 = lo; i0 < hi; i0 += SMP_U) {
+        int64_t v[SMP_U];
+#pragma unroll
+        for (int u = 0; u < SMP_U; ++u)
+            v[u] = a[i0 + u < hi ? i0 + u : hi - 1];
+#pragma unroll
+        for (int u = 0; u < SMP_U; ++u)
+            if (i0 + u < hi)
+                f(i0 + u, v[u]);
+    }
 }
 
 // ---- 1: w = fp_div(logit, T) (llama_int.c:2970-2971), block max / min ----
@@ -185,8 +291,9 @@ __global__ __launch_bounds__(SMP_B) void k_smp_topk(int64_t *__restrict__ base, 
 {
     __shared__ int64_t red[SMP_B / 64];
     __shared__ int hist[256];
+    __shared__ int whist[16][256];
     __shared__ uint64_t sel_prefix;
-    __shared__ int sel_krem;
+    __shared__ int sel_krem, sel_krem2, sel_b;
     SmpWs s = smp_ws(base, n);
     const int tid = threadIdx.x;
     int64_t mx = INT64_MIN, mn = INT64_MAX;
@@ -199,33 +306,46 @@ __global__ __launch_bounds__(SMP_B) void k_smp_topk(int64_t *__restrict__ base, 
 
     int64_t thr = INT64_MIN;
     if (top_k > 0 && top_k < n) {
+        // keys w - min (unsigned, order-preserving), only the bits below
+        // the range's top bit; one histogram per wave (LDS atomics of a
+        // whole wave on one bucket would serialise), 8 bits a pass
+        const uint64_t range = (uint64_t)mx - (uint64_t)mn;
+        const int top = range ? 64 - __builtin_clzll(range) : 0;
+        const int wave = tid >> 6;
         if (tid == 0) {
             sel_prefix = 0;
             sel_krem = top_k;
         }
-        uint64_t mask = 0;
-        for (int shift = 56; shift >= 0; shift -= 8) {
-            for (int b = tid; b < 256; b += SMP_B)
-                hist[b] = 0;
+        for (int hi = top; hi > 0; hi -= 8) {
+            const int lo = hi > 8 ? hi - 8 : 0, width = hi - lo;
+            for (int b = tid; b < 16 * 256; b += SMP_B)
+                whist[b >> 8][b & 255] = 0;
             __syncthreads();
             const uint64_t prefix = sel_prefix;
-            for (int i = tid; i < n; i += SMP_B) {
-                const uint64_t key = (uint64_t)s.w[i] ^ 0x8000000000000000ull;
-                if ((key & mask) == prefix)
-                    atomicAdd(&hist[(key >> shift) & 255], 1);
+            pass_strided(s.w, n, [&](int, int64_t w) {
+                const uint64_t key = (uint64_t)w - (uint64_t)mn;
+                if (hi >= 64 || (key >> hi) == prefix)
+                    atomicAdd(&whist[wave][(key >> lo) & ((1u << width) - 1)], 1);
+            });
+            __syncthreads();
+            if (tid < 256) {
+                int h = 0;
+#pragma unroll
+                for (int w = 0; w < 16; ++w)
+                    h += whist[w][tid];
+                hist[tid] = h;
             }
+            __syncthreads();
+            if (tid < 64)
+                walk_count(hist, 1 << width, sel_krem, &sel_b, &sel_krem2);
             __syncthreads();
             if (tid == 0) {
-                int krem = sel_krem, b = 255;
-                for (; b > 0 && krem > hist[b]; --b)
-                    krem -= hist[b];
-                sel_krem = krem;
-                sel_prefix = prefix | ((uint64_t)b << shift);
+                sel_krem = sel_krem2;
+                sel_prefix = (prefix << width) | (uint64_t)sel_b;
             }
-            mask |= (uint64_t)255 << shift;
             __syncthreads();
         }
-        thr = (int64_t)(sel_prefix ^ 0x8000000000000000ull);
+        thr = (int64_t)((uint64_t)mn + sel_prefix);
     }
     if (tid == 0) {
         // masked entries (w < thr: some exist when thr > min w) become
@@ -298,6 +418,80 @@ __global__ __launch_bounds__(SMP_T) void k_smp_div(int64_t *__restrict__ base, i
             s.p[i] = q48_div(s.p[i], sum);
 }
 
+// First index i (index order) at which the running sum of val(a[j]), j <= i,
+// exceeds `target` (strict) or reaches it: INT_MAX if none.  Requires
+// val >= 0 with no wrap (a monotone running sum).  Each wave first sums a
+// contiguous range of the array with coalesced loads; the range where the
+// sum crosses is then split over the lanes of one wave, and one lane walks
+// its piece.  All threads of the block call it; every thread gets the
+// result.
+template <class F>
+__device__ __forceinline__ int first_crossing(const int64_t *a, int n, F val, uint64_t target,
+                                              bool strict, uint64_t *wtot, int *res)
+{
+    constexpr int NWV = SMP_B / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int R = (n + NWV - 1) / NWV;
+    const int w0 = min(n, wave * R), w1 = min(n, w0 + R);
+    uint64_t t = 0;
+    for (int j0 = w0 + lane; j0 < w1; j0 += 64 * SMP_U) {
+        int64_t v[SMP_U];
+#pragma unroll
+        for (int u = 0; u < SMP_U; ++u)
+            v[u] = a[min(j0 + 64 * u, w1 - 1)];
+#pragma unroll
+        for (int u = 0; u < SMP_U; ++u)
+            if (j0 + 64 * u < w1)
+                t += val(v[u]);
+    }
+    t = (uint64_t)q48_wave_sum64((int64_t)t);
+    __syncthreads();
+    if (lane == 0)
+        wtot[wave] = t;
+    __syncthreads();
+    // the crossing wave and the sum before it (identical in every thread)
+    auto crossed = [&](uint64_t s) { return strict ? s > target : s >= target; };
+    uint64_t before = 0;
+    int wc = -1;
+    for (int w = 0; w < NWV && wc < 0; ++w) {
+        if (crossed(before + wtot[w]))
+            wc = w;
+        else
+            before += wtot[w];
+    }
+    if (tid == 0)
+        *res = INT_MAX;
+    __syncthreads();
+    if (wc >= 0 && wave == wc) {
+        const int S = (R + 63) / 64;
+        const int l0 = min(w1, w0 + lane * S), l1 = min(w1, l0 + S);
+        uint64_t ls = 0;
+        pass_chunk(a, l0, l1, [&](int, int64_t v) { ls += val(v); });
+        uint64_t incl = ls;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint64_t o = __shfl_up(incl, off, 64);
+            if (lane >= off)
+                incl += o;
+        }
+        // the lane whose piece holds the crossing walks it
+        uint64_t run = before + incl - ls;
+        if (!crossed(run) && crossed(run + ls)) {
+            int found = INT_MAX;
+            pass_chunk(a, l0, l1, [&](int i, int64_t v) {
+                if (found == INT_MAX) {
+                    run += val(v);
+                    if (crossed(run))
+                        found = i;
+                }
+            });
+            *res = found;
+        }
+    }
+    __syncthreads();
+    return *res;
+}
+
 // ---- 5: nucleus (llama_int.c:2993-3023) and the draw (3027-3036) ----------
 // One block; thread t owns the index chunk [t C, (t + 1) C).  Step mode
 // (st != nullptr, as k_step_argmax): the token feeds the next decode step.
@@ -309,66 +503,191 @@ __global__ __launch_bounds__(SMP_B) void k_smp_pick(int64_t *__restrict__ base, 
 {
     __shared__ int64_t redv[SMP_B / 64];
     __shared__ int redi[SMP_B / 64];
-    __shared__ uint64_t scan[SMP_B];
+    __shared__ uint64_t scan[SMP_B / 64];
     __shared__ int hcnt[256];
     __shared__ unsigned long long hsum[256];
+    __shared__ int wcnt[16][256];
+    __shared__ unsigned long long wsum[16][256];
     __shared__ uint64_t cut_prefix;
-    __shared__ uint64_t cut_above;
-    __shared__ int cut_all, cut_ties;
+    __shared__ uint64_t cut_above, cut_above2;
+    __shared__ int cut_all, cut_ties, cut_b;
     __shared__ int64_t r_sh;
+    __shared__ int cross_i;
+    __shared__ int64_t cv[SMP_B];
+    __shared__ int ci[SMP_B];
+    __shared__ int ccount;
     SmpWs s = smp_ws(base, n);
     const int tid = threadIdx.x;
     const int C = (n + SMP_B - 1) / SMP_B;
     const int lo = min(n, tid * C), hi = min(n, lo + C);
     int64_t *p = s.p;
+    const bool nucleus = top_p > 0 && top_p < Q48_ONE;
+    const bool exact = s.st[ST_EXACT] != 0;
 
-    if (top_p > 0 && top_p < Q48_ONE) {
-        if (s.st[ST_EXACT]) {
+    // Few positive probabilities (top-k on, or a peaked softmax): gather
+    // them, with their indices, into LDS and finish there, one per thread
+    if (exact) {
+        if (tid == 0)
+            ccount = 0;
+        __syncthreads();
+        const int lane = tid & 63;
+        for (int i0 = tid; i0 < n; i0 += SMP_B * SMP_U) {
+            int64_t v[SMP_U];
+#pragma unroll
+            for (int u = 0; u < SMP_U; ++u)
+                v[u] = p[min(i0 + u * SMP_B, n - 1)];
+#pragma unroll
+            for (int u = 0; u < SMP_U; ++u) {
+                const bool pos = i0 + u * SMP_B < n && v[u] > 0;
+                const uint64_t m = __ballot(pos);
+                if (m) {
+                    const int leader = __ffsll((unsigned long long)m) - 1;
+                    int b0 = 0;
+                    if (lane == leader)
+                        b0 = atomicAdd(&ccount, __popcll(m));
+                    b0 = __shfl(b0, leader, 64);
+                    const int k = b0 + __popcll(m & ((1ull << lane) - 1));
+                    if (pos && k < SMP_B) {
+                        cv[k] = v[u];
+                        ci[k] = i0 + u * SMP_B;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (exact && ccount <= SMP_B) {
+        const int K = ccount;
+        const bool have = tid < K;
+        const int64_t v = have ? cv[tid] : 0;
+        const int ix = have ? ci[tid] : INT_MAX;
+        bool keep = have;
+        if (nucleus) {
+            // kept while the sum of the entries before it in the order
+            // (p desc, index asc) is below top_p: a prefix of that order
+            uint64_t before = 0;
+            for (int j = 0; j < K; ++j) {
+                const int64_t w = cv[j];
+                if (w > v || (w == v && ci[j] < ix))
+                    before += (uint64_t)w;
+            }
+            keep = have && (int64_t)before < top_p;
+        }
+        int64_t q = keep ? v : 0;
+        if (nucleus) {
+            const int64_t sum = (int64_t)blk_sum<SMP_B>((uint64_t)q, redv);
+            if (sum > 0 && q > 0)
+                q = q48_div(q, sum);
+        }
+        __syncthreads();
+        cv[tid] = q;   // slots past K hold 0
+        __syncthreads();
+        if (tid == 0) {
+            const uint64_t a = rng[0];
+            uint64_t b = rng[1];
+            const uint64_t d = a + b;
+            b ^= a;
+            rng[0] = ((a << 55) | (a >> 9)) ^ b ^ (b << 14);
+            rng[1] = (b << 36) | (b >> 28);
+            r_sh = (int64_t)(d >> 16);
+        }
+        __syncthreads();
+        // the running sum in index order reaches each entry's own index;
+        // zero entries elsewhere add nothing
+        uint64_t cum = 0;
+        for (int j = 0; j < K; ++j)
+            if (ci[j] <= ix)
+                cum += (uint64_t)cv[j];
+        int first = have && (int64_t)cum > r_sh ? ix : INT_MAX;
+        int64_t dummy = 0;
+        blk_argmax<SMP_B>(dummy, first, redv, redi);
+        int tok = first;
+        if (tok == INT_MAX) {
+            // argmax of the whole vector: the first largest entry, or index 0
+            // when every entry is 0
+            int64_t bv = have ? q : INT64_MIN;
+            int bi = have ? ix : INT_MAX;
+            blk_argmax<SMP_B>(bv, bi, redv, redi);
+            tok = bi != INT_MAX && bv > 0 ? bi : 0;
+        }
+        if (tid == 0) {
+            if (st) {
+                st[0] = tok;
+                st[1] = st[1] + 1;
+                const int k = st[2];
+                if (k < cap)
+                    tokens[k] = tok;
+                st[2] = k + 1;
+            } else {
+                *out_tok = tok;
+            }
+        }
+        return;
+    }
+
+    if (nucleus) {
+        if (exact) {
             // every p in [0, ONE], sum <= ONE: the kept set is the top of
             // the order (p desc, index asc) up to the first running sum
             // >= top_p.  Radix search for the cut value p*, carrying the
             // sum above the current bucket.
+            // keys p (>= 0) below the top bit of the largest; per-wave
+            // histograms of counts and sums, 8 bits a pass
+            int64_t pm = 0;
+            pass_strided(p, n, [&](int, int64_t v) { pm = v > pm ? v : pm; });
+            pm = blk_max<SMP_B>(pm, redv);
+            const int top = pm > 0 ? 64 - __builtin_clzll((uint64_t)pm) : 0;
+            const int wave = tid >> 6;
             if (tid == 0) {
                 cut_prefix = 0;
                 cut_above = 0;
-                cut_all = 0;
+                cut_all = top == 0;
             }
-            uint64_t mask = 0;
-            for (int shift = 48; shift >= 0; shift -= 8) {
-                for (int b = tid; b < 256; b += SMP_B) {
-                    hcnt[b] = 0;
-                    hsum[b] = 0;
+            __syncthreads();
+            for (int hi = top; hi > 0 && !cut_all; hi -= 8) {
+                const int lo = hi > 8 ? hi - 8 : 0, width = hi - lo;
+                for (int b = tid; b < 16 * 256; b += SMP_B) {
+                    wcnt[b >> 8][b & 255] = 0;
+                    wsum[b >> 8][b & 255] = 0;
                 }
                 __syncthreads();
-                if (cut_all)
-                    break;
                 const uint64_t prefix = cut_prefix;
-                for (int i = lo; i < hi; ++i) {
-                    const uint64_t v = (uint64_t)p[i];
-                    if ((int64_t)v > 0 && (v & mask) == prefix) {
-                        const int b = (int)((v >> shift) & 255);
-                        atomicAdd(&hcnt[b], 1);
-                        atomicAdd(&hsum[b], (unsigned long long)v);
+                pass_strided(p, n, [&](int, int64_t sv) {
+                    const uint64_t v = (uint64_t)sv;
+                    if (sv > 0 && (hi >= 64 || (v >> hi) == prefix)) {
+                        const int b = (int)((v >> lo) & ((1u << width) - 1));
+                        atomicAdd(&wcnt[wave][b], 1);
+                        atomicAdd(&wsum[wave][b], (unsigned long long)v);
                     }
+                });
+                __syncthreads();
+                if (tid < 256) {
+                    int c = 0;
+                    unsigned long long t = 0;
+#pragma unroll
+                    for (int w = 0; w < 16; ++w) {
+                        c += wcnt[w][tid];
+                        t += wsum[w][tid];
+                    }
+                    hcnt[tid] = c;
+                    hsum[tid] = t;
                 }
+                __syncthreads();
+                if (tid == 0)
+                    cut_b = -1;
+                __syncthreads();
+                if (tid < 64)
+                    walk_sum(hcnt, hsum, 1 << width, cut_above, top_p, &cut_b, &cut_above2,
+                             &cut_ties);
                 __syncthreads();
                 if (tid == 0) {
-                    uint64_t above = cut_above;
-                    int b = 255;
-                    for (; b >= 0; --b) {
-                        if ((int64_t)(above + hsum[b]) >= top_p)
-                            break;
-                        above += hsum[b];
-                    }
-                    if (b < 0) {
+                    if (cut_b < 0) {
                         cut_all = 1;   // all positive mass below top_p: keep it all
                     } else {
-                        cut_above = above;
-                        cut_prefix = prefix | ((uint64_t)b << shift);
-                        cut_ties = hcnt[b];
+                        cut_above = cut_above2;
+                        cut_prefix = (prefix << width) | (uint64_t)cut_b;
                     }
                 }
-                mask |= (uint64_t)255 << shift;
                 __syncthreads();
             }
             __syncthreads();
@@ -382,25 +701,17 @@ __global__ __launch_bounds__(SMP_B) void k_smp_pick(int64_t *__restrict__ base, 
                 m = (int64_t)((need + (uint64_t)pc - 1) / (uint64_t)pc);
                 m = m < cut_ties ? m : cut_ties;
             }
-            // rank of each tie: ties before this chunk, then in the chunk
-            int my_ties = 0;
-            if (!keep_all)
-                for (int i = lo; i < hi; ++i)
-                    my_ties += p[i] == pc;
-            int64_t rank = (int64_t)blk_excl_scan<SMP_B>((uint64_t)my_ties, scan);
-            for (int i = lo; i < hi; ++i) {
-                const int64_t v = p[i];
-                bool keep;
-                if (keep_all) {
-                    keep = v > 0;
-                } else if (v == pc) {
-                    keep = rank < m;
-                    ++rank;
-                } else {
-                    keep = v > pc;
-                }
+            // the m-th tie in index order is the last one kept (all of them
+            // when m is their count)
+            int last_tie = INT_MAX;
+            if (!keep_all && m < cut_ties)
+                last_tie = first_crossing(
+                    p, n, [pc](int64_t v) -> uint64_t { return v == pc; }, (uint64_t)m, false,
+                    scan, &cross_i);
+            pass_strided(p, n, [&](int i, int64_t v) {
+                const bool keep = keep_all ? v > 0 : v > pc || (v == pc && i <= last_tie);
                 p[i] = keep ? v : 0;
-            }
+            });
         } else {
             // the reference's own loop: while the running sum is below
             // top_p, take the largest positive entry (first index among
@@ -409,11 +720,12 @@ __global__ __launch_bounds__(SMP_B) void k_smp_pick(int64_t *__restrict__ base, 
             while (cum < top_p) {
                 int64_t bv = INT64_MIN;
                 int bi = INT_MAX;
-                for (int i = lo; i < hi; ++i)
-                    if (p[i] > 0 && (bi == INT_MAX || p[i] > bv)) {
-                        bv = p[i];
+                pass_chunk(p, lo, hi, [&](int i, int64_t v) {
+                    if (v > 0 && (bi == INT_MAX || v > bv)) {
+                        bv = v;
                         bi = i;
                     }
+                });
                 blk_argmax<SMP_B>(bv, bi, redv, redi);
                 if (bi == INT_MAX)
                     break;
@@ -423,18 +735,20 @@ __global__ __launch_bounds__(SMP_B) void k_smp_pick(int64_t *__restrict__ base, 
                     p[bi] = (int64_t)(0 - (uint64_t)bv);
                 __syncthreads();
             }
-            for (int i = lo; i < hi; ++i)
-                p[i] = p[i] < 0 ? (int64_t)(0 - (uint64_t)p[i]) : 0;
+            pass_chunk(p, lo, hi, [&](int i, int64_t v) {
+                p[i] = v < 0 ? (int64_t)(0 - (uint64_t)v) : 0;
+            });
         }
         // renormalise the kept entries by their (wrapping) sum
+        __syncthreads();
         uint64_t part = 0;
-        for (int i = lo; i < hi; ++i)
-            part += (uint64_t)p[i];
+        pass_strided(p, n, [&](int, int64_t v) { part += (uint64_t)v; });
         const int64_t sum = (int64_t)blk_sum<SMP_B>(part, redv);
         if (sum > 0)
-            for (int i = lo; i < hi; ++i)
-                if (p[i] > 0)
-                    p[i] = q48_div(p[i], sum);
+            pass_strided(p, n, [&](int i, int64_t v) {
+                if (v > 0)
+                    p[i] = q48_div(v, sum);
+            });
     }
 
     // the draw: r in [0, ONE) from one rng_next (llama_int.c:2922-2929)
@@ -450,35 +764,41 @@ __global__ __launch_bounds__(SMP_B) void k_smp_pick(int64_t *__restrict__ base, 
     __syncthreads();
     const int64_t r = r_sh;
     // first index whose running (wrapping) sum exceeds r
-    uint64_t part = 0;
-    for (int i = lo; i < hi; ++i)
-        part += (uint64_t)p[i];
-    uint64_t run = blk_excl_scan<SMP_B>(part, scan);
-    int first = INT_MAX;
-    for (int i = lo; i < hi; ++i) {
-        run += (uint64_t)p[i];
-        if ((int64_t)run > r) {
-            first = i;
-            break;
-        }
-    }
-    int64_t dummy = 0;
-    int fi = first;
-    {
+    __syncthreads();
+    int tok;
+    if (s.st[ST_EXACT]) {
+        // every value >= 0 and the sum at most ONE: a monotone running sum
+        tok = first_crossing(
+            p, n, [](int64_t v) -> uint64_t { return (uint64_t)v; }, (uint64_t)r, true, scan,
+            &cross_i);
+    } else {
+        uint64_t part = 0;
+        pass_chunk(p, lo, hi, [&](int, int64_t v) { part += (uint64_t)v; });
+        uint64_t run = blk_excl_scan<SMP_B>(part, scan);
+        int first = INT_MAX;
+        pass_chunk(p, lo, hi, [&](int i, int64_t v) {
+            if (first == INT_MAX) {
+                run += (uint64_t)v;
+                if ((int64_t)run > r)
+                    first = i;
+            }
+        });
         // minimum index over the block (values equal: argmax picks the
         // smaller index)
-        blk_argmax<SMP_B>(dummy, fi, redv, redi);
+        int64_t dummy = 0;
+        blk_argmax<SMP_B>(dummy, first, redv, redi);
+        tok = first;
     }
-    int tok = fi;
     if (tok == INT_MAX) {
         // rounding left the mass below r: the first maximum (argmax)
         int64_t bv = INT64_MIN;
         int bi = INT_MAX;
-        for (int i = lo; i < hi; ++i)
-            if (bi == INT_MAX || p[i] > bv) {
-                bv = p[i];
+        pass_chunk(p, lo, hi, [&](int i, int64_t v) {
+            if (bi == INT_MAX || v > bv) {
+                bv = v;
                 bi = i;
             }
+        });
         blk_argmax<SMP_B>(bv, bi, redv, redi);
         tok = bi == INT_MAX ? 0 : bi;
     }
