@@ -283,6 +283,32 @@ int q48_step_get(q48_ctx *ctx, int *token, int *pos, int *count);  /* syncs */
 int q48_argmax_step(q48_ctx *ctx, const int64_t *v, int n, int *d_tokens, int cap);
 
 
+/* ---- batched prefill ------------------------------------------------------ */
+/* No reference counterpart as a batch: llama_int's prefill calls
+ * llama_forward once per prompt token (llama_int.c:3081-3092).  These are the
+ * per-token ops of transformer_layer_forward over T rows (token t at
+ * position p0 + t), for a prefill whose projections are q48_gemm; each row
+ * gets the reference's bits for its token.  Row-major [T][...] buffers. */
+/* hidden[t] = embed[d_tokens[t]] (llama_int.c:2822-2824; ids on the device,
+ * range-checked by the caller). */
+int q48_embed_rows(q48_ctx *ctx, int64_t *H, const int64_t *table, const int *d_tokens, int T,
+                   int dim);
+/* rmsnorm (llama_int.c:1048-1058) of every row. */
+int q48_rmsnorm_rows(q48_ctx *ctx, int64_t *out, const int64_t *X, const int64_t *w, int T,
+                     int dim);
+/* RoPE (llama_int.c:997-1008, 1392-1395) of the q and k heads of every
+ * [q | k | v] row in place, then the KV store (1414-1416) at p0 + t. */
+int q48_rope_store_rows(q48_ctx *ctx, int64_t *QKV, int64_t *kcache, int64_t *vcache, int layer,
+                        int p0, int T, int n_heads, int n_kv, int head_dim, int max_seq);
+/* Exact causal attention (llama_int.c:1433, 1502-1529) of the rotated q of
+ * every row over cache positions 0 .. p0 + t (stored by
+ * q48_rope_store_rows); out[T][n_heads * head_dim].  p0 + T at most 4096. */
+int q48_attn_prefill(q48_ctx *ctx, int64_t *out, const int64_t *QKV, int64_t *kcache,
+                     int64_t *vcache, int layer, int p0, int T, int n_heads, int n_kv,
+                     int head_dim, int max_seq);
+/* SwiGLU (llama_int.c:1549-1552) of every [gate | up] row: out[T][ffn]. */
+int q48_silu_mul_rows(q48_ctx *ctx, int64_t *out, const int64_t *GU, int T, int ffn);
+
 /* ---- sampling (sample_token, llama_int.c:2958-3039) --------------------- */
 /* rng_seed (llama_int.c:2909-2920): the xoroshiro128+ state of a seed
  * (SplitMix64), computed on the host.  Upload it to a device buffer of two

@@ -638,6 +638,66 @@ int q48_attn_decode_rope_prefetch(q48_ctx *c, int64_t *out, const int64_t *q, in
 }
 
 
+// ---- batched prefill rows -------------------------------------------------------
+
+static bool heads_ok(int n_heads, int n_kv, int head_dim)
+{
+    return n_heads > 0 && n_kv > 0 && n_heads % n_kv == 0 &&
+           (head_dim == 32 || head_dim == 64 || head_dim == 128);
+}
+
+int q48_embed_rows(q48_ctx *c, int64_t *H, const int64_t *table, const int *d_tokens, int T,
+                   int dim)
+{
+    if (!c || !H || !table || !d_tokens || T <= 0 || dim <= 0 || dim > kMaxDim)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_pf_embed(c, H, table, d_tokens, T, dim));
+}
+
+int q48_rmsnorm_rows(q48_ctx *c, int64_t *out, const int64_t *X, const int64_t *w, int T,
+                     int dim)
+{
+    if (!c || !out || !X || !w || T <= 0 || dim <= 0 || dim > kMaxDim)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_pf_rmsnorm(c, out, X, w, T, dim));
+}
+
+int q48_rope_store_rows(q48_ctx *c, int64_t *QKV, int64_t *kcache, int64_t *vcache, int layer,
+                        int p0, int T, int n_heads, int n_kv, int head_dim, int max_seq)
+{
+    if (!c || !QKV || !kcache || !vcache || T <= 0 || layer < 0 || max_seq <= 0 ||
+        !heads_ok(n_heads, n_kv, head_dim))
+        return Q48_EINVAL;
+    if (!c->rope_cos || head_dim != c->rope_head_dim || max_seq > c->rope_max_seq)
+        return Q48_ESTATE;
+    if (p0 < 0 || p0 + T > max_seq)
+        return Q48_ERANGE;
+    return launch_rc(q48_launch_pf_rope_store(c, QKV, kcache, vcache, layer, p0, T, n_heads,
+                                              n_kv, head_dim, max_seq));
+}
+
+int q48_attn_prefill(q48_ctx *c, int64_t *out, const int64_t *QKV, int64_t *kcache,
+                     int64_t *vcache, int layer, int p0, int T, int n_heads, int n_kv,
+                     int head_dim, int max_seq)
+{
+    if (!c || !out || !QKV || !kcache || !vcache || T <= 0 || layer < 0 || max_seq <= 0 ||
+        !heads_ok(n_heads, n_kv, head_dim))
+        return Q48_EINVAL;
+    if (!c->rope_cos || head_dim != c->rope_head_dim || max_seq > c->rope_max_seq)
+        return Q48_ESTATE;
+    if (p0 < 0 || p0 + T > max_seq || p0 + T > q48_att_lds_max())
+        return Q48_ERANGE;
+    return launch_rc(q48_launch_pf_attn(c, out, QKV, kcache, vcache, layer, p0, T, n_heads, n_kv,
+                                        head_dim, max_seq));
+}
+
+int q48_silu_mul_rows(q48_ctx *c, int64_t *out, const int64_t *GU, int T, int ffn)
+{
+    if (!c || !out || !GU || T <= 0 || ffn <= 0 || ffn > kMaxDim)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_pf_silu(c, out, GU, T, ffn));
+}
+
 // ---- norm statistics computed once per vector ---------------------------------
 
 int q48_rms_inv(q48_ctx *c, int64_t *r_out, const int64_t *x, int dim)

@@ -59,8 +59,10 @@ constexpr int ATT_LDS_MAX = 4096;   // positions whose scores fit in LDS (32 KiB
 // are read from the cache and replaced by the block's own rotated k and v.
 // HD = 32, 64 or 128; at most SMAX positions (scores in LDS).  COH: the
 // output goes out with agent-coherent (write-through) stores, for a consumer
-// on other compute units in the same kernel.
-template <int HD, int SMAX, bool COH>
+// on other compute units in the same kernel.  PRE (batched prefill): q_h is
+// already rotated and the key and value at pos are already in the cache
+// (k_new, v_new, cos_t, sin_t unused); the rest is the same arithmetic.
+template <int HD, int SMAX, bool COH, bool PRE = false>
 __device__ __forceinline__ void attn_v3_head(
     int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
     int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
@@ -85,46 +87,63 @@ __device__ __forceinline__ void attn_v3_head(
     const int g = tid >> 3, l8 = tid & 7;
     const int64_t scale = *scale_p;
 
-    // the RoPE inputs and the new v first (loads retire in issue order: the
-    // RoPE then waits for them alone), every thread loading (clamped index)
-    const int64_t *qh = q + (size_t)h * HD, *kn = k_new + (size_t)kh * HD;
-    const int i = min(tid, half - 1), j = min(tid, HD - 1);
-    int64_t c = cos_t[(size_t)pos * half + i];
-    int64_t sn = sin_t[(size_t)pos * half + i];
-    int64_t q0 = qh[i], q1 = qh[i + half];
-    int64_t k0 = kn[i], k1 = kn[i + half];
-    int64_t vn = v_new[(size_t)kh * HD + j];
-    __builtin_amdgcn_sched_barrier(0);
-
-    // K rows of passes 0 and 1: lane l8 of group g holds dims [l8 DPL, +DPL)
     const int64_t *kb0 = kcache + base * kvd + (size_t)kh * HD + l8 * DPL;
     auto krow = [&](int t) {
         return reinterpret_cast<const ulonglong2 *>(kb0 + (size_t)min(t, S - 1) * kvd);
     };
     ulonglong2 ka[DP2], kb[DP2];
+    if constexpr (PRE) {
+        const int j = min(tid, HD - 1);
+        const int64_t qv = q[(size_t)h * HD + j];
+        const int64_t kv = kcache[(base + pos) * kvd + (size_t)kh * HD + j];
+        const int64_t vv = vcache[(base + pos) * kvd + (size_t)kh * HD + j];
 #pragma unroll
-    for (int d = 0; d < DP2; ++d)
-        ka[d] = krow(g)[d];
+        for (int d = 0; d < DP2; ++d)
+            ka[d] = krow(g)[d];
 #pragma unroll
-    for (int d = 0; d < DP2; ++d)
-        kb[d] = krow(g + NG)[d];
-    __builtin_amdgcn_sched_barrier(0);
-    // first use of the RoPE inputs here, after the K loads are out (else the
-    // compiler extends them to 128 bits, and waits for them, earlier)
-    asm volatile("" : "+v"(c), "+v"(sn), "+v"(q0), "+v"(q1), "+v"(k0), "+v"(k1), "+v"(vn));
+        for (int d = 0; d < DP2; ++d)
+            kb[d] = krow(g + NG)[d];
+        qs[j] = qv;
+        ks[j] = kv;
+        vs[j] = vv;
+        __syncthreads();
+    } else {
+        // the RoPE inputs and the new v first (loads retire in issue order: the
+        // RoPE then waits for them alone), every thread loading (clamped index)
+        const int64_t *qh = q + (size_t)h * HD, *kn = k_new + (size_t)kh * HD;
+        const int i = min(tid, half - 1), j = min(tid, HD - 1);
+        int64_t c = cos_t[(size_t)pos * half + i];
+        int64_t sn = sin_t[(size_t)pos * half + i];
+        int64_t q0 = qh[i], q1 = qh[i + half];
+        int64_t k0 = kn[i], k1 = kn[i + half];
+        int64_t vn = v_new[(size_t)kh * HD + j];
+        __builtin_amdgcn_sched_barrier(0);
 
-    // RoPE of q_h and the new k (rope_apply, llama_int.c:997-1008, 1392-1395);
-    // threads past half repeat the last pair (same values, same slots): no
-    // branch, so the loads above are not sunk into one
-    qs[i] = (int64_t)((uint64_t)q48_mul(q0, c) - (uint64_t)q48_mul(q1, sn));
-    qs[i + half] = (int64_t)((uint64_t)q48_mul(q1, c) + (uint64_t)q48_mul(q0, sn));
-    ks[i] = (int64_t)((uint64_t)q48_mul(k0, c) - (uint64_t)q48_mul(k1, sn));
-    ks[i + half] = (int64_t)((uint64_t)q48_mul(k1, c) + (uint64_t)q48_mul(k0, sn));
-    vs[j] = vn;
-    __syncthreads();
-    if (h % group == 0 && tid < HD) {
-        kcache[(base + pos) * kvd + (size_t)kh * HD + tid] = ks[tid];
-        vcache[(base + pos) * kvd + (size_t)kh * HD + tid] = vs[tid];
+        // K rows of passes 0 and 1: lane l8 of group g holds dims [l8 DPL, +DPL)
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            ka[d] = krow(g)[d];
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            kb[d] = krow(g + NG)[d];
+        __builtin_amdgcn_sched_barrier(0);
+        // first use of the RoPE inputs here, after the K loads are out (else the
+        // compiler extends them to 128 bits, and waits for them, earlier)
+        asm volatile("" : "+v"(c), "+v"(sn), "+v"(q0), "+v"(q1), "+v"(k0), "+v"(k1), "+v"(vn));
+
+        // RoPE of q_h and the new k (rope_apply, llama_int.c:997-1008, 1392-1395);
+        // threads past half repeat the last pair (same values, same slots): no
+        // branch, so the loads above are not sunk into one
+        qs[i] = (int64_t)((uint64_t)q48_mul(q0, c) - (uint64_t)q48_mul(q1, sn));
+        qs[i + half] = (int64_t)((uint64_t)q48_mul(q1, c) + (uint64_t)q48_mul(q0, sn));
+        ks[i] = (int64_t)((uint64_t)q48_mul(k0, c) - (uint64_t)q48_mul(k1, sn));
+        ks[i + half] = (int64_t)((uint64_t)q48_mul(k1, c) + (uint64_t)q48_mul(k0, sn));
+        vs[j] = vn;
+        __syncthreads();
+        if (h % group == 0 && tid < HD) {
+            kcache[(base + pos) * kvd + (size_t)kh * HD + tid] = ks[tid];
+            vcache[(base + pos) * kvd + (size_t)kh * HD + tid] = vs[tid];
+        }
     }
 
     // scores s_t = fp_mul((sum_d q_d k_t,d) >> 48, scale), llama_int.c:1502-1512

@@ -90,6 +90,7 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
                     const int64_t *v_new, int layer, const int *d_pos, int pos,
                     int n_heads, int n_kv, int head_dim, int max_seq);
 int q48_att_split_min();
+int q48_att_lds_max();   // positions a single-block attention keeps in LDS
 int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                        int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
                        int layer, const int *d_pos, int pos, int n_heads, int n_kv,
@@ -104,6 +105,18 @@ int q48_launch_add(q48_ctx *c, int64_t *acc, const int64_t *d, int n);
 int q48_launch_embed(q48_ctx *c, int64_t *out, const int64_t *table,
                      const int *d_token, int token, int dim);
 int q48_launch_argmax(q48_ctx *c, int *d_out, const int64_t *v, int n);
+// batched prefill rows (q48_prefill.hip)
+int q48_launch_pf_embed(q48_ctx *c, int64_t *H, const int64_t *table, const int *tokens, int T,
+                        int dim);
+int q48_launch_pf_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *X, const int64_t *w, int T,
+                          int dim);
+int q48_launch_pf_rope_store(q48_ctx *c, int64_t *QKV, int64_t *kcache, int64_t *vcache,
+                             int layer, int p0, int T, int n_heads, int n_kv, int hd,
+                             int max_seq);
+int q48_launch_pf_attn(q48_ctx *c, int64_t *out, const int64_t *QKV, int64_t *kcache,
+                       int64_t *vcache, int layer, int p0, int T, int n_heads, int n_kv, int hd,
+                       int max_seq);
+int q48_launch_pf_silu(q48_ctx *c, int64_t *out, const int64_t *GU, int T, int ffn);
 // sample_token: the sampling workspace size in int64 words for n logits, and
 // the kernel chain (greedy temperatures are the caller's: argmax); with
 // tokens != nullptr the token goes to the decode-step state

@@ -33,6 +33,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(int64_t *__restrict__ out,
     __shared__ uint64_t red_lo[4], red_hi[4];
     __shared__ int64_t r_sh;
     const int tid = threadIdx.x;
+    x += (size_t)blockIdx.x * dim;   // one row per block
+    out += (size_t)blockIdx.x * dim;
     q48_u128 ss = 0;
     for (int i = tid; i < dim; i += 256) {
         int64_t v = x[i];
@@ -862,6 +864,13 @@ int q48_launch_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *x,
     return (int)hipGetLastError();
 }
 
+int q48_launch_pf_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *X, const int64_t *w, int T,
+                          int dim)
+{
+    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), 0, c->stream, out, X, w, dim);
+    return (int)hipGetLastError();
+}
+
 int q48_launch_rope_init(q48_ctx *c)
 {
     const long n = (long)(c->rope_head_dim / 2) * c->rope_max_seq;
@@ -896,6 +905,7 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
 }
 
 int q48_att_split_min() { return ATT_SPLIT_MIN; }
+int q48_att_lds_max() { return ATT_LDS_MAX; }
 
 int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                        int64_t *vcache, const int64_t *k_new, const int64_t *v_new,

@@ -61,6 +61,9 @@ struct q48h_model {
     uint16_t *wb;               /* device: bfloat16 bits of the projection matrices and
                                    lm_head, at the element offsets of w (else NULL) */
     int bf16;                   /* mode 3 reads the matrices from wb */
+    int batched_prefill;        /* generate's prompt through q48h_prefill (default) */
+    int64_t *pf;                /* device: batched-prefill rows (grown on demand) */
+    size_t pf_words;
 };
 
 /* ---------------------------------------------------------------------- */
@@ -209,6 +212,7 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
 
     m->fused = 3;
     m->prefetch = 1;
+    m->batched_prefill = 1;
     if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->kc, kvn * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->vc, kvn * 8)) ||
@@ -325,6 +329,7 @@ void q48h_model_free(q48h_model *m)
     q48_free(m->ctx, m->act);
     q48_free(m->ctx, m->d_tokens);
     q48_free(m->ctx, m->d_rng);
+    q48_free(m->ctx, m->pf);
     if (m->graph_ready)
         q48_graph_drop(m->ctx);
     free(m);
@@ -888,6 +893,86 @@ static double now_s(void)
     return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
 }
 
+void q48h_model_set_batched_prefill(q48h_model *m, int on)
+{
+    if (m)
+        m->batched_prefill = on != 0;
+}
+
+int q48h_prefill(q48h_model *m, const int *tokens, int T, int p0, int64_t *logits_all,
+                 int *next)
+{
+    if (!m || !tokens || T <= 0)
+        return Q48_EINVAL;
+    const q48h_config *c = &m->c;
+    const int dim = c->dim, hd = c->head_dim, kvd = c->n_kv_heads * hd, ffn = c->ffn;
+    const int V = c->vocab, nq = dim + 2 * kvd;
+    if (p0 < 0 || p0 + T > c->max_seq)
+        return Q48_ERANGE;
+    for (int t = 0; t < T; ++t)
+        if (tokens[t] < 0 || tokens[t] >= V)
+            return Q48_ERANGE;
+    q48_ctx *x = m->ctx;
+    /* one row per token at a time past what a single-block attention keeps
+     * in LDS (or for one token) */
+    if (T == 1 || p0 + T > 4096 || !(hd == 32 || hd == 64 || hd == 128)) {
+        for (int t = 0; t < T; ++t) {
+            TRY(enqueue_forward(m, tokens[t], p0 + t));
+            if (logits_all)
+                TRY(q48_memcpy_d2h(x, logits_all + (size_t)t * V, m->logits, (size_t)V * 8));
+        }
+        if (next)
+            TRY(select_token(m, next));
+        return q48_sync(x);
+    }
+    /* rows: H, XN, QKV, ATT, D, GU, HF, logits (all T, or the last), ids */
+    const size_t nlog = logits_all ? (size_t)T * V : (size_t)V;
+    const size_t need = (size_t)T * (4 * (size_t)dim + nq + 3 * (size_t)ffn) + nlog +
+                        ((size_t)T + 1) / 2;
+    if (need > m->pf_words) {
+        TRY(q48_sync(x));
+        q48_free(x, m->pf);
+        m->pf = NULL;
+        m->pf_words = 0;
+        TRY(q48_malloc(x, (void **)&m->pf, need * 8));
+        m->pf_words = need;
+    }
+    int64_t *H = m->pf, *XN = H + (size_t)T * dim, *QKV = XN + (size_t)T * dim;
+    int64_t *ATT = QKV + (size_t)T * nq, *D = ATT + (size_t)T * dim;
+    int64_t *GU = D + (size_t)T * dim, *HF = GU + (size_t)T * 2 * ffn;
+    int64_t *LG = HF + (size_t)T * ffn;
+    int *ids = (int *)(LG + nlog);
+    TRY(q48_memcpy_h2d(x, ids, tokens, (size_t)T * sizeof(int)));
+    TRY(q48_embed_rows(x, H, m->w + m->off_embed, ids, T, dim));
+    for (int l = 0; l < c->n_layers; ++l) {
+        const int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
+        TRY(q48_rmsnorm_rows(x, XN, H, b + m->lo_an, T, dim));
+        TRY(q48_gemm(x, QKV, b + m->lo_qkv, XN, T, nq, dim));
+        TRY(q48_rope_store_rows(x, QKV, m->kc, m->vc, l, p0, T, c->n_heads, c->n_kv_heads, hd,
+                                c->max_seq));
+        TRY(q48_attn_prefill(x, ATT, QKV, m->kc, m->vc, l, p0, T, c->n_heads, c->n_kv_heads, hd,
+                             c->max_seq));
+        TRY(q48_gemm(x, D, b + m->lo_wo, ATT, T, dim, dim));
+        TRY(q48_add(x, H, D, T * dim));
+        TRY(q48_rmsnorm_rows(x, XN, H, b + m->lo_fn, T, dim));
+        TRY(q48_gemm(x, GU, b + m->lo_gu, XN, T, 2 * ffn, dim));
+        TRY(q48_silu_mul_rows(x, HF, GU, T, ffn));
+        TRY(q48_gemm(x, D, b + m->lo_wd, HF, T, dim, ffn));
+        TRY(q48_add(x, H, D, T * dim));
+    }
+    TRY(q48_rmsnorm_rows(x, XN, H, m->w + m->off_norm, T, dim));
+    if (logits_all) {
+        TRY(q48_gemm(x, LG, m->w + m->off_lm, XN, T, V, dim));
+        TRY(q48_memcpy_d2d(x, m->logits, LG + (size_t)(T - 1) * V, (size_t)V * 8));
+        TRY(q48_memcpy_d2h(x, logits_all, LG, (size_t)T * V * 8));
+    } else {
+        TRY(q48_gemv(x, m->logits, m->w + m->off_lm, XN + (size_t)(T - 1) * dim, V, dim));
+    }
+    if (next)
+        TRY(select_token(m, next));
+    return q48_sync(x);
+}
+
 int q48h_generate(q48h_model *m, const int *prompt, int prompt_len, int max_new,
                   int *out_tokens, uint64_t *step_hash, int *n_steps, q48h_stats *st)
 {
@@ -901,18 +986,37 @@ int q48h_generate(q48h_model *m, const int *prompt, int prompt_len, int max_new,
     memcpy(out_tokens, prompt, (size_t)prompt_len * sizeof(int));
     int total = prompt_len;
     double t0 = now_s();
-    for (int pos = 0; pos < prompt_len && rc == Q48_OK; ++pos) {
+    if (rc == Q48_OK && m->batched_prefill && prompt_len > 1) {
+        /* the prompt in one batched pass: the same cache and logits */
+        int64_t *all = step_hash ? (int64_t *)malloc((size_t)prompt_len * vocab * 8) : NULL;
         int next;
-        /* the token is chosen (and a sample drawn) at the last prompt
-         * position only (llama_int.c:3087-3090) */
-        rc = q48h_forward(m, out_tokens[pos], pos, logits, pos == prompt_len - 1 ? &next : NULL);
-        if (rc)
-            break;
-        if (step_hash)
-            step_hash[steps] = q48s_fnv_i64(FNV_OFF, logits, (size_t)vocab);
-        steps++;
-        if (pos == prompt_len - 1)
+        if (step_hash && !all)
+            rc = Q48_ENOMEM;
+        if (rc == Q48_OK)
+            rc = q48h_prefill(m, out_tokens, prompt_len, 0, all, &next);
+        if (rc == Q48_OK) {
+            for (int pos = 0; pos < prompt_len; ++pos, ++steps)
+                if (step_hash)
+                    step_hash[steps] = q48s_fnv_i64(FNV_OFF, all + (size_t)pos * vocab,
+                                                    (size_t)vocab);
             out_tokens[total++] = next;
+        }
+        free(all);
+    } else {
+        for (int pos = 0; pos < prompt_len && rc == Q48_OK; ++pos) {
+            int next;
+            /* the token is chosen (and a sample drawn) at the last prompt
+             * position only (llama_int.c:3087-3090) */
+            rc = q48h_forward(m, out_tokens[pos], pos, logits,
+                              pos == prompt_len - 1 ? &next : NULL);
+            if (rc)
+                break;
+            if (step_hash)
+                step_hash[steps] = q48s_fnv_i64(FNV_OFF, logits, (size_t)vocab);
+            steps++;
+            if (pos == prompt_len - 1)
+                out_tokens[total++] = next;
+        }
     }
     double t1 = now_s();
     int dec0 = total;

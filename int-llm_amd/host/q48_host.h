@@ -101,6 +101,19 @@ int q48h_generate(q48h_model *m, const int *prompt, int prompt_len, int max_new,
                   int *out_tokens, uint64_t *step_hash, int *n_steps,
                   q48h_stats *stats);
 
+/* Batched prefill (no reference counterpart as a batch: llama_int's prefill
+ * calls llama_forward per token, llama_int.c:3081-3092): the forward of
+ * tokens[0..T) at positions p0 .. p0 + T - 1 as row ops and q48_gemm
+ * projections, filling the KV cache exactly as T forward calls do.
+ * logits_all (host, may be NULL) receives the T logits rows; next (may be
+ * NULL) the token chosen from the last row (argmax or sample_token).  Past
+ * position 4096, or for T = 1, the tokens go one forward call at a time. */
+int q48h_prefill(q48h_model *m, const int *tokens, int T, int p0, int64_t *logits_all,
+                 int *next);
+/* q48h_generate's prompt through q48h_prefill (1, the default) or one
+ * forward call per token (0); the bits are the same. */
+void q48h_model_set_batched_prefill(q48h_model *m, int on);
+
 /* Greedy decode from an already filled cache: forward(token, start_pos),
  * then n - 1 more steps, stopping after EOS (long-context configuration). */
 int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_tokens,

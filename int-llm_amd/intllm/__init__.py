@@ -432,6 +432,8 @@ HOST_SIGNATURES = {
     "q48h_model_set_prefetch": ([_P, _I], None),
     "q48h_model_set_bf16": ([_P, _I], C.c_int),
     "q48h_model_set_sampling": ([_P, C.c_int64, _I, C.c_int64, C.c_uint64], C.c_int),
+    "q48h_model_set_batched_prefill": ([_P, _I], None),
+    "q48h_prefill": ([_P, C.POINTER(C.c_int), _I, _I, _P, C.POINTER(C.c_int)], C.c_int),
 
     "q48h_gemv_sweep": ([_P, _I, C.POINTER(C.c_int), C.POINTER(C.c_double)], C.c_int),
     "q48h_decode_graph": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
@@ -515,6 +517,22 @@ class HostModel:
             self.h, token, pos, out.ctypes.data if logits else None,
             C.byref(nxt) if choose else None))
         return (nxt.value if choose else None), out
+
+    def prefill(self, tokens, p0: int, vocab: int, logits: bool = True, choose: bool = True):
+        """q48h_prefill: tokens at positions p0.. in one batched pass; returns
+        (next token or None, the T logits rows or None)."""
+        T = len(tokens)
+        t = (C.c_int * T)(*tokens)
+        out = np.empty((T, vocab), dtype=np.int64) if logits else None
+        nxt = C.c_int()
+        check("q48h_prefill", host_lib().q48h_prefill(
+            self.h, t, T, p0, out.ctypes.data if logits else None,
+            C.byref(nxt) if choose else None))
+        return (nxt.value if choose else None), out
+
+    def set_batched_prefill(self, on: bool):
+        """generate's prompt in one batched pass (default) or per token."""
+        host_lib().q48h_model_set_batched_prefill(self.h, int(bool(on)))
 
     def kv_reset(self):
         check("q48h_kv_reset", host_lib().q48h_kv_reset(self.h))
