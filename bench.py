@@ -218,6 +218,9 @@ def main():
                     help="int8 GEMM calls timed per config-4 shape; 0 skips config 4")
     ap.add_argument("--no-sample", action="store_true",
                     help="skip the sampled-decode measurement")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the batched-prefill measurement")
+    ap.add_argument("--prefill-reps", type=int, default=3)
     ap.add_argument("--no-bf16", action="store_true",
                     help="skip the bfloat16-resident-weights decode measurement")
     ap.add_argument("--gemm-only", action="store_true",
@@ -228,6 +231,7 @@ def main():
               "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
 
+    import numpy as np
     import intllm
     import spec
 
@@ -340,10 +344,47 @@ def main():
                    "tok_s": round(1e3 / sms, 2), "ms_per_tok": round(sms, 4),
                    "positions": [s0, s0 + args.steps]}
 
+    # batched prefill: prompts of T tokens through q48h_prefill (row ops and
+    # q48_gemm projections; lm_head of the last row only), against the
+    # per-token forward that the reference's generate runs for a prompt.
+    # The golden prompt's first token joins the parity check.
+    pf = None
+    if not args.no_prefill:
+        m.kv_reset()
+        pf_next, _ = m.prefill(prompt, 0, cfg.vocab, logits=False)
+        pf = {"workload": "config 3 prompt of T tokens at positions 0..T-1, int64 "
+                               "weights, batched (q48h_prefill)",
+                   "golden_prompt_next_token_matches": pf_next == gold["tokens"][len(prompt)],
+                   "T": {}}
+        rng = np.random.default_rng(11)
+        for T in (32, 128, 512, 2048):
+            tk = [int(v) for v in rng.integers(0, cfg.vocab, size=T)]
+            m.prefill(tk, 0, cfg.vocab, logits=False)         # warm (buffers)
+            ctx.sync()
+            t0 = time.perf_counter()
+            for _ in range(args.prefill_reps):
+                m.prefill(tk, 0, cfg.vocab, logits=False)
+            pms = 1e3 * (time.perf_counter() - t0) / args.prefill_reps
+            pf["T"][str(T)] = {"ms": round(pms, 3), "tok_s": round(1e3 * T / pms, 1)}
+            log(f"batched prefill T={T}: {pms:.2f} ms ({1e3 * T / pms:.0f} tok/s)")
+        # the per-token route over the golden prompt (what generate did
+        # before batching): forward calls without logits copies
+        m.set_batched_prefill(False)
+        t0 = time.perf_counter()
+        for pos, tok in enumerate(prompt):
+            m.forward(tok, pos, cfg.vocab, logits=False, choose=pos == len(prompt) - 1)
+        seq_ms = 1e3 * (time.perf_counter() - t0)
+        m.set_batched_prefill(True)
+        pf["per_token_forward"] = {"T": len(prompt), "ms": round(seq_ms, 3),
+                                        "tok_s": round(1e3 * len(prompt) / seq_ms, 1)}
+
     # token stream vs the reference's (golden), over the tokens both have
     ref_new = gold["tokens"][len(prompt):]
     n_cmp = min(len(ref_new), len(toks))
     parity = {"tokens_compared": n_cmp, "tokens_match_reference": toks[:n_cmp] == ref_new[:n_cmp]}
+    if pf is not None:
+        parity["prefill_next_token_matches_reference"] = \
+            pf["golden_prompt_next_token_matches"]
 
     # config 5: the cache pre-filled to 2048 positions, then greedy decode
     # steps replayed from the graph (the golden stream covers 256 of them)
@@ -411,6 +452,7 @@ def main():
         "long_context": longctx,
         "bf16_resident": bf16,
         "sampled_decode": sampled,
+        "batched_prefill": pf,
         "parity": parity,
     }
     print(json.dumps(line), flush=True)
