@@ -156,8 +156,8 @@ __device__ __forceinline__ void attn_v3_head(
         for (int d = 0; d < DP2; ++d) {
             const int64_t a0 = own ? kd[2 * d] : (int64_t)kr[d].x;
             const int64_t a1 = own ? kd[2 * d + 1] : (int64_t)kr[d].y;
-            dot += (q48_u128)((q48_i128)qd[2 * d] * a0);
-            dot += (q48_u128)((q48_i128)qd[2 * d + 1] * a1);
+            dot += (q48_u128)q48_smul128(qd[2 * d], a0);
+            dot += (q48_u128)q48_smul128(qd[2 * d + 1], a1);
         }
         dot = q48_sum8_u128(dot);
         if (t < S && l8 == 0) {

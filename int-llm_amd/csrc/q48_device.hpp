@@ -5,9 +5,11 @@
 // below cites the reference lines it reproduces.  All int64 adds wrap
 // (two's complement), as the reference's -fwrapv build does.
 //
-// 128-bit values: clang's __int128 on amdgcn lowers multiplies to
-// v_mad_u64_u32 chains; division goes through q48_udiv128_64 below
-// (128 / 64 -> 128 quotient, exact, from FP64 estimates).
+// 128-bit values: signed 64 x 64 -> 128 products come from q48_smul_parts
+// (four 32 x 32 -> 64 products; clang's own expansion of a sign-extended
+// __int128 multiply issues nine quarter-rate multiplies); division goes
+// through q48_udiv128_64 below (128 / 64 -> 128 quotient, exact, from FP64
+// estimates).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -18,6 +20,46 @@ typedef unsigned __int128 q48_u128;
 
 #define Q48_ONE ((int64_t)1 << 48)
 #define Q48_HALF ((int64_t)1 << 47)
+
+// The signed product a * b mod 2^128: hi = bits 64..127, mid = bits 32..63
+// (the low 32 bits of the returned value), lo32 = bits 0..31.  Schoolbook
+// over 32-bit halves of the unsigned words (no partial sum overflows 64
+// bits), then the two's-complement correction of the high word: a negative
+// operand contributes -2^64 times the other operand's unsigned word.
+__device__ __forceinline__ void q48_smul_parts(int64_t a, int64_t b, uint64_t &hi, uint32_t &mid,
+                                               uint32_t &lo32)
+{
+    const uint64_t ua = (uint64_t)a, ub = (uint64_t)b;
+    const uint32_t al = (uint32_t)ua, ah = (uint32_t)(ua >> 32);
+    const uint32_t bl = (uint32_t)ub, bh = (uint32_t)(ub >> 32);
+    const uint64_t lo = (uint64_t)al * bl;
+    const uint64_t t = (uint64_t)ah * bl + (lo >> 32);
+    const uint64_t u = (uint64_t)al * bh + (uint32_t)t;
+    hi = (uint64_t)ah * bh + (t >> 32) + (u >> 32);
+    hi -= (a < 0 ? ub : 0) + (b < 0 ? ua : 0);
+    mid = (uint32_t)u;
+    lo32 = (uint32_t)lo;
+}
+
+// (q48_i128)a * b
+__device__ __forceinline__ q48_i128 q48_smul128(int64_t a, int64_t b)
+{
+    uint64_t hi;
+    uint32_t mid, lo32;
+    q48_smul_parts(a, b, hi, mid, lo32);
+    return (q48_i128)(((q48_u128)hi << 64) | ((uint64_t)mid << 32) | lo32);
+}
+
+// (int64_t)(((q48_i128)a * b) >> S) for 32 <= S < 64: bits S .. S + 63
+template <int S>
+__device__ __forceinline__ int64_t q48_mul_shr(int64_t a, int64_t b)
+{
+    static_assert(S >= 32 && S < 64, "shift");
+    uint64_t hi;
+    uint32_t mid, lo32;
+    q48_smul_parts(a, b, hi, mid, lo32);
+    return (int64_t)((hi << (64 - S)) | (uint64_t)(mid >> (S - 32)));
+}
 
 // Constants computed by fp_math_init (fp_math.h:833-858) on the device at
 // context creation: FP_PI, fp_cordic_gain, fp_cordic_angles[48].
@@ -166,7 +208,7 @@ __device__ __forceinline__ q48_i128 q48_divs_128_64(q48_i128 a, int64_t b)
 // fp_mul, fp_math.h:491-506
 __device__ __forceinline__ int64_t q48_mul(int64_t a, int64_t b)
 {
-    return (int64_t)(((q48_i128)a * b) >> 48);
+    return q48_mul_shr<48>(a, b);
 }
 
 // fp_div, fp_math.h:508-524
@@ -243,10 +285,10 @@ __device__ __forceinline__ int64_t q48_inv_sqrt(int64_t x)
     int64_t y = msb_n == 48 ? Q48_ONE : Q48_HALF;
     const int64_t three = (int64_t)3 << 48;
     for (int i = 0; i < 8; ++i) {
-        int64_t y2 = (int64_t)(((q48_i128)y * y) >> 48);
-        int64_t xy2 = (int64_t)(((q48_i128)xn * y2) >> 48);
+        int64_t y2 = q48_mul_shr<48>(y, y);
+        int64_t xy2 = q48_mul_shr<48>(xn, y2);
         int64_t factor = three - xy2;
-        const int64_t yn = (int64_t)(((q48_i128)y * factor) >> 49);
+        const int64_t yn = q48_mul_shr<49>(y, factor);
         if (yn <= 0) {
             y = 1;
             break;

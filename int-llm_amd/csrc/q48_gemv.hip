@@ -472,7 +472,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
             }
 #pragma unroll
             for (int b = 0; b < SB; ++b)
-                ss += (q48_u128)((q48_i128)v[b] * v[b]);
+                ss += (q48_u128)q48_smul128(v[b], v[b]);
         }
         ss = block_sum128<64 * NW>(ss, red_lo, red_hi);
         if (tid == 0)
@@ -687,7 +687,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                 h = (int64_t)((uint64_t)yres + (uint64_t)v);
                 y[rr] = h;
             }
-            q48_u128 sq = (q48_u128)((q48_i128)h * h);
+            q48_u128 sq = (q48_u128)q48_smul128(h, h);
             sq = q48_sum8_u128(sq);
             if (tid == 0) {
                 uint64_t *st = reinterpret_cast<uint64_t *>(r_out);
@@ -712,7 +712,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                 h = (int64_t)((uint64_t)yres + (uint64_t)v);
                 y[rr] = h;
             }
-            q48_u128 sq = (q48_u128)((q48_i128)h * h);
+            q48_u128 sq = (q48_u128)q48_smul128(h, h);
             sq = q48_sum8_u128(sq);
             if (tid == 0) {
                 // The partial goes out with agent-coherent (write-through)
@@ -1017,7 +1017,7 @@ __global__ __launch_bounds__(256) void k_rms_inv(int64_t *__restrict__ r_out,
             const int i = i0 + tid + 256 * b;
             if (table && i < dim)
                 out[i] = v[b];
-            ss += (q48_u128)((q48_i128)v[b] * v[b]);
+            ss += (q48_u128)q48_smul128(v[b], v[b]);
         }
     }
     ss = q48_wave_sum128(ss);
@@ -1064,7 +1064,7 @@ __global__ __launch_bounds__(256) void k_rms_stats(int64_t *__restrict__ stats,
             const int i = 8 * p + b;
             if (table && i < dim)
                 out[i] = v[b];
-            ss += (q48_u128)((q48_i128)v[b] * v[b]);
+            ss += (q48_u128)q48_smul128(v[b], v[b]);
         }
         reinterpret_cast<uint64_t *>(stats)[2 * p] = (uint64_t)ss;
         reinterpret_cast<uint64_t *>(stats)[2 * p + 1] = (uint64_t)(ss >> 64);

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(int64_t *__restrict__ out,
     q48_u128 ss = 0;
     for (int i = tid; i < dim; i += 256) {
         int64_t v = x[i];
-        ss += (q48_u128)((q48_i128)v * v);
+        ss += (q48_u128)q48_smul128(v, v);
     }
     ss = q48_wave_sum128(ss);
     if ((tid & 63) == 0) {
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_decode(
         const int64_t *kt = t == pos ? kn : kcache + (base + t) * kvd + (size_t)kh * hd;
         q48_u128 dot = 0;
         for (int d = 0; d < hd; ++d)
-            dot += (q48_u128)((q48_i128)qs[d] * kt[d]);
+            dot += (q48_u128)q48_smul128(qs[d], kt[d]);
         const int64_t s = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
         sc[t] = s;
         mx = s > mx ? s : mx;
@@ -306,8 +306,8 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
             const int64_t *qd = qs + l8 * dpl;
             for (int d = 0; d < dpl; d += 2) {
                 const int64_t a0 = kt[d], a1 = kt[d + 1];
-                dot += (q48_u128)((q48_i128)qd[d] * a0);
-                dot += (q48_u128)((q48_i128)qd[d + 1] * a1);
+                dot += (q48_u128)q48_smul128(qd[d], a0);
+                dot += (q48_u128)q48_smul128(qd[d + 1], a1);
             }
         }
         dot = q48_sum8_u128(dot);
@@ -523,8 +523,8 @@ __global__ __launch_bounds__(256) void k_attn_s1(
         for (int d = 0; d < DP2; ++d) {
             const int64_t a0 = own ? kd[2 * d] : (int64_t)kr[d].x;
             const int64_t a1 = own ? kd[2 * d + 1] : (int64_t)kr[d].y;
-            dot += (q48_u128)((q48_i128)qd[2 * d] * a0);
-            dot += (q48_u128)((q48_i128)qd[2 * d + 1] * a1);
+            dot += (q48_u128)q48_smul128(qd[2 * d], a0);
+            dot += (q48_u128)q48_smul128(qd[2 * d + 1], a1);
         }
         dot = q48_sum8_u128(dot);
         if (t < tend && l8 == 0) {
