@@ -10,11 +10,12 @@ namespace {
 
 // Sum an int64 (wrapping) across a block of NT threads; every thread gets it.
 template <int NT>
-__device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t *red)
+__device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t *red, bool reused = true)
 {
     v = q48_wave_sum64(v);
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __syncthreads();
+    if (reused)   // red may still be read by a previous reduction
+        __syncthreads();
     if (lane == 0)
         red[w] = v;
     __syncthreads();
@@ -26,11 +27,12 @@ __device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t *red)
 }
 
 template <int NT>
-__device__ __forceinline__ int64_t block_max64(int64_t v, int64_t *red)
+__device__ __forceinline__ int64_t block_max64(int64_t v, int64_t *red, bool reused = true)
 {
     v = q48_wave_max64(v);
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __syncthreads();
+    if (reused)
+        __syncthreads();
     if (lane == 0)
         red[w] = v;
     __syncthreads();
@@ -72,7 +74,7 @@ __device__ __forceinline__ void attn_v3_head(
 {
     constexpr int NT = 256, DPL = HD / 8, DP2 = DPL / 2, SL = NT / HD, NG = NT / 8, VB = 8;
     __shared__ int64_t qs[HD], ks[HD], vs[HD];
-    __shared__ int64_t red[NT / 64];
+    __shared__ int64_t red[NT / 64], red2[NT / 64];
     __shared__ int64_t part[NT];
     __shared__ int64_t sc[SMAX];
     if (d_pos)
@@ -191,14 +193,16 @@ __device__ __forceinline__ void attn_v3_head(
         vb[u] = vld(VB + u);
 
     // softmax, llama_int.c:1060-1072
-    mx = block_max64<NT>(mx, red);
+    // each reduction has its own slots, used once: no barrier before the
+    // slot writes (the one after them also orders the score stores)
+    mx = block_max64<NT>(mx, red, false);
     int64_t sum = 0;
     for (int t = tid; t < S; t += NT) {
         const int64_t e = q48_safe_exp((int64_t)((uint64_t)sc[t] - (uint64_t)mx));
         sc[t] = e;
         sum = (int64_t)((uint64_t)sum + (uint64_t)e);
     }
-    sum = block_sum64<NT>(sum, red);
+    sum = block_sum64<NT>(sum, red2, false);
     if (sum > 0)
         for (int t = tid; t < S; t += NT)
             sc[t] = q48_div(sc[t], sum);

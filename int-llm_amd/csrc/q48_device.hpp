@@ -211,10 +211,65 @@ __device__ __forceinline__ int64_t q48_mul(int64_t a, int64_t b)
     return q48_mul_shr<48>(a, b);
 }
 
+// fp_mul(r, r): r * r = u^2 with u = |r| <= 2^63 as an unsigned word;
+// u^2 = hh 2^64 + 2 lh 2^32 + ll, and w = 2 lh + (ll >> 32) stays below 2^64,
+// so bits 48..111 are (hh << 16) + (w >> 16) mod 2^64: three 32 x 32 -> 64
+// products.
+__device__ __forceinline__ int64_t q48_sqr(int64_t r)
+{
+    const uint64_t u = r < 0 ? (uint64_t)0 - (uint64_t)r : (uint64_t)r;
+    const uint32_t l = (uint32_t)u, h = (uint32_t)(u >> 32);
+    const uint64_t ll = (uint64_t)l * l, lh = (uint64_t)l * h, hh = (uint64_t)h * h;
+    const uint64_t w = (lh << 1) + (ll >> 32);
+    return (int64_t)((hh << 16) + (w >> 16));
+}
+
+// floor(mag * 2^48 / ub) for 0 < ub and mag < 16 ub (a quotient below
+// 2^52).  mag / ub from the hardware reciprocal refined by one Newton step
+// (relative error near 2^-52, so the estimate is within 2 units of the
+// quotient), then exact 128-bit remainder steps; should the estimate ever be
+// further off, the long division takes over, so the result is exact
+// whatever the FP64 unit does.  About a third of the latency of the
+// correctly rounded FP64 division plus unit remainder loops.
+__device__ __forceinline__ uint64_t q48_udiv_shl48(uint64_t mag, uint64_t ub)
+{
+    const double bd = (double)ub;
+    double r = __builtin_amdgcn_rcp(bd);
+    r = __builtin_fma(r, __builtin_fma(-bd, r, 1.0), r);
+    const double est = (double)mag * r * 281474976710656.0;   // 2^48
+    int64_t q = (int64_t)est;                                 // below 2^53
+    const q48_u128 num = (q48_u128)mag << 48;
+    q48_i128 rem = (q48_i128)(num - (q48_u128)(uint64_t)q * ub);
+    if (rem < 0) {
+        --q;
+        rem += ub;
+        if (rem < 0) {
+            --q;
+            rem += ub;
+        }
+    } else if (rem >= (q48_i128)ub) {
+        ++q;
+        rem -= ub;
+        if (rem >= (q48_i128)ub) {
+            ++q;
+            rem -= ub;
+        }
+    }
+    if (rem < 0 || rem >= (q48_i128)ub)
+        return (uint64_t)q48_udiv128_64_slow(num, ub);
+    return (uint64_t)q;
+}
+
 // fp_div, fp_math.h:508-524
 __device__ __forceinline__ int64_t q48_div(int64_t a, int64_t b)
 {
     uint64_t mag = a < 0 ? (uint64_t)0 - (uint64_t)a : (uint64_t)a;
+    const uint64_t ub = b < 0 ? (uint64_t)0 - (uint64_t)b : (uint64_t)b;
+    if (b != -1 && ub != 0 && (mag >> 4) < ub) {
+        // |num / b| = floor(mag 2^48 / |b|) < 2^52; the sign of a / b
+        const uint64_t q = q48_udiv_shl48(mag, ub);
+        return (a < 0) != (b < 0) ? (int64_t)((uint64_t)0 - q) : (int64_t)q;
+    }
     q48_i128 num = (q48_i128)((q48_u128)mag << 48);
     if (a < 0)
         num = (q48_i128)(0 - (q48_u128)num);
@@ -285,7 +340,7 @@ __device__ __forceinline__ int64_t q48_inv_sqrt(int64_t x)
     int64_t y = msb_n == 48 ? Q48_ONE : Q48_HALF;
     const int64_t three = (int64_t)3 << 48;
     for (int i = 0; i < 8; ++i) {
-        int64_t y2 = q48_mul_shr<48>(y, y);
+        int64_t y2 = q48_sqr(y);
         int64_t xy2 = q48_mul_shr<48>(xn, y2);
         int64_t factor = three - xy2;
         const int64_t yn = q48_mul_shr<49>(y, factor);
@@ -316,7 +371,7 @@ __device__ __forceinline__ int64_t q48_exp_dyadic(int64_t x, int k)
 {
     int64_t r = (int64_t)((uint64_t)Q48_ONE + (uint64_t)(x >> k));
     for (int i = 0; i < k; ++i)
-        r = q48_mul(r, r);
+        r = q48_sqr(r);
     return r;
 }
 
@@ -534,12 +589,26 @@ __device__ __forceinline__ int64_t q48_wave_sum64(int64_t x)
     return (int64_t)t;
 }
 
+// maximum across the 64 lanes of a wave (all active), every lane returns
+// it: DPP within rows of 16 lanes, then the four row maxima as scalars
 __device__ __forceinline__ int64_t q48_wave_max64(int64_t v)
 {
+    int64_t o = (int64_t)q48_dpp64<Q48_DPP_XOR1>((uint64_t)v);
+    v = o > v ? o : v;
+    o = (int64_t)q48_dpp64<Q48_DPP_XOR2>((uint64_t)v);
+    v = o > v ? o : v;
+    o = (int64_t)q48_dpp64<Q48_DPP_HALF_MIRROR>((uint64_t)v);
+    v = o > v ? o : v;
+    o = (int64_t)q48_dpp64<Q48_DPP_MIRROR>((uint64_t)v);
+    v = o > v ? o : v;
+    int64_t t = INT64_MIN;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        int64_t o = __shfl_xor(v, off, 64);
-        v = o > v ? o : v;
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32),
+                                                               16 * r);
+        const int64_t m = (int64_t)(((uint64_t)hi << 32) | lo);
+        t = m > t ? m : t;
     }
-    return v;
+    return t;
 }

@@ -116,6 +116,42 @@ def test_device_div_random_vs_oracle(ctx, oracle):
     assert np.array_equal(d, want)
 
 
+def test_device_div_quotients_at_integers(ctx, oracle):
+    """Numerators at and one unit either side of exact multiples of the
+    divisor (a 2^48 = q b): the quotient's estimate lands next to an integer,
+    where an estimate off by one is caught only by the remainder steps; and
+    softmax's e / sum, sigmoid's ONE / (ONE + e) shapes."""
+    rng = np.random.default_rng(23)
+    a, b = [], []
+    for _ in range(2048):
+        s = int(rng.integers(48, 62))
+        c = int(rng.integers(1, 1 << (62 - s)))
+        q = int(rng.integers(0, 1 << 52)) >> int(rng.integers(0, 52))
+        base = q * c << (s - 48)
+        if base >= 1 << 63:
+            continue
+        for d in (-1, 0, 1):
+            v = base + d
+            if 0 <= v < 1 << 63:
+                sg = int(rng.choice([-1, 1]))
+                a.append(sg * v)
+                b.append(int(rng.choice([-1, 1])) * (c << s))
+    one = 1 << 48
+    for _ in range(2048):
+        tot = int(rng.integers(one, 4096 * one))
+        a.append(int(rng.integers(0, one + 1)))
+        b.append(tot)
+        a.append(one)
+        b.append(one + int(rng.integers(0, 22027 * one)))
+    a = np.array(a, dtype=np.int64)
+    b = np.array(b, dtype=np.int64)
+    say("div at integer quotients", a.size)
+    d = dev_eval(ctx, intllm.FP_DIV, a, b)
+    want = np.array([oracle.q48o_fp_div(int(p), int(q)) for p, q in zip(a, b)], dtype=np.int64)
+    bad = np.nonzero(d != want)[0]
+    assert bad.size == 0, [(int(a[i]), int(b[i]), int(d[i]), int(want[i])) for i in bad[:5]]
+
+
 def gemv_dev(ctx, W, x, M, K, w_offset=0):
     dW = ctx.buffer(M * K + w_offset)
     if w_offset:
