@@ -45,11 +45,11 @@ __device__ __forceinline__ int64_t block_max64(int64_t v, int64_t *red, bool reu
 
 constexpr int ATT_LDS_MAX = 4096;   // positions whose scores fit in LDS (32 KiB)
 
-// Attention v3 of query head h, run by threads 0..255 of the block (threads
-// past 255 must not call it): RoPE of q_h and the new k, KV store at pos (by
-// the first query head of each KV head), scores, max, fp_safe_exp, sum,
-// fp_div, V (llama_int.c:997-1008, 1060-1072, 1392-1395, 1414-1416,
-// 1502-1529).
+// Attention v3 of query head h, run by threads 0..NT-1 of the block (NT =
+// 256 or 512; threads past NT - 1 must not call it): RoPE of q_h and the new
+// k, KV store at pos (by the first query head of each KV head), scores, max,
+// fp_safe_exp, sum, fp_div, V (llama_int.c:997-1008, 1060-1072, 1392-1395,
+// 1414-1416, 1502-1529).
 //  - the K rows of the first two score passes are issued before RoPE, and
 //    each later pass is issued one pass ahead (two register buffers);
 //  - the first V batches are issued before the softmax, later ones one
@@ -64,7 +64,9 @@ constexpr int ATT_LDS_MAX = 4096;   // positions whose scores fit in LDS (32 KiB
 // on other compute units in the same kernel.  PRE (batched prefill): q_h is
 // already rotated and the key and value at pos are already in the cache
 // (k_new, v_new, cos_t, sin_t unused); the rest is the same arithmetic.
-template <int HD, int SMAX, bool COH, bool PRE = false>
+// CIN: q, k_new and v_new are read with agent-coherent loads (written earlier
+// in the same kernel by other compute units, e.g. the persistent decode step).
+template <int HD, int SMAX, bool COH, bool PRE = false, bool CIN = false, int NT = 256>
 __device__ __forceinline__ void attn_v3_head(
     int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
     int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
@@ -72,7 +74,8 @@ __device__ __forceinline__ void attn_v3_head(
     const int64_t *__restrict__ sin_t, const int64_t *__restrict__ scale_p, int layer,
     const int *__restrict__ d_pos, int pos, int n_heads, int n_kv, int max_seq, int h)
 {
-    constexpr int NT = 256, DPL = HD / 8, DP2 = DPL / 2, SL = NT / HD, NG = NT / 8, VB = 8;
+    static_assert(NT == 256 || NT == 512, "attention block size");
+    constexpr int DPL = HD / 8, DP2 = DPL / 2, SL = NT / HD, NG = NT / 8, VB = 8;
     __shared__ int64_t qs[HD], ks[HD], vs[HD];
     __shared__ int64_t red[NT / 64], red2[NT / 64];
     __shared__ int64_t part[NT];
@@ -114,11 +117,17 @@ __device__ __forceinline__ void attn_v3_head(
         // RoPE then waits for them alone), every thread loading (clamped index)
         const int64_t *qh = q + (size_t)h * HD, *kn = k_new + (size_t)kh * HD;
         const int i = min(tid, half - 1), j = min(tid, HD - 1);
+        auto ld = [](const int64_t *p) {
+            if constexpr (CIN)
+                return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+                return *p;
+        };
         int64_t c = cos_t[(size_t)pos * half + i];
         int64_t sn = sin_t[(size_t)pos * half + i];
-        int64_t q0 = qh[i], q1 = qh[i + half];
-        int64_t k0 = kn[i], k1 = kn[i + half];
-        int64_t vn = v_new[(size_t)kh * HD + j];
+        int64_t q0 = ld(qh + i), q1 = ld(qh + i + half);
+        int64_t k0 = ld(kn + i), k1 = ld(kn + i + half);
+        int64_t vn = ld(v_new + (size_t)kh * HD + j);
         __builtin_amdgcn_sched_barrier(0);
 
         // K rows of passes 0 and 1: lane l8 of group g holds dims [l8 DPL, +DPL)

@@ -6,6 +6,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/intllm_hip.h"
 #include "q48_device.hpp"
 
 struct q48_ctx {
@@ -29,6 +30,11 @@ struct q48_ctx {
     int rms_blocks;
     int64_t *smp;                // device: sampling workspace (q48_sample_ws_words)
     size_t smp_words;
+    unsigned *sk_sync;           // device: k_step_fused phase counters, then its error
+                                 // word and argmax partials (one allocation)
+    int *sk_err;
+    int64_t *sk_amax;
+    int sk_grid;                 // k_step_fused blocks (0: not planned yet)
     hipGraph_t graph;            // captured decode step
     hipGraphExec_t graph_exec;
     int capturing;
@@ -127,3 +133,8 @@ int q48_launch_zero(q48_ctx *c, void *p, size_t bytes);
 int q48_launch_math_init(q48_ctx *c);
 int q48_launch_fp_eval(q48_ctx *c, int func, const int64_t *x,
                        const int64_t *y, int64_t *out0, int64_t *out1, int n);
+
+// one-launch decode step (q48_step.hip)
+int q48_step_fused_plan(q48_ctx *c, const q48_step_model *m, int *grid, size_t *lds);
+int q48_launch_step_fused(q48_ctx *c, const q48_step_model *m, int *tokens, int cap, int grid,
+                          size_t lds);

@@ -92,6 +92,9 @@ int q48h_kv_fill_synth(q48h_model *m, uint64_t seed, int npos, int threads);
  * Q48_ERANGE for a token or position out of range, like the
  * reference's NULL return. */
 int q48h_forward(q48h_model *m, int token, int pos, int64_t *logits, int *next);
+/* The logits [vocab] of the last step run on the device (forward, prefill's
+ * last row, or a decode step), copied to host memory (synchronises). */
+int q48h_read_logits(q48h_model *m, int64_t *logits);
 
 /* generate (llama_int.c:3067-3135), greedy.  step_hash (may be NULL) gets
  * FNV-1a-64 of every forward call's logits (prompt positions included);
@@ -126,6 +129,13 @@ int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_to
  * block); 3 (default) fused, the producer leaves per-block partial sums and
  * each block of the consuming GEMV finishes them. */
 void q48h_model_set_fused(q48h_model *m, int fused);
+
+/* Greedy graph-replayed decode (q48h_decode_graph) in mode 3 runs each step
+ * as one persistent launch (q48_step_fused) at the positions and shapes it
+ * serves, else the fused launches.  On by default; the bits do not depend on
+ * it.  q48h_step_onelaunch_active tells whether a step at pos would. */
+void q48h_model_set_onelaunch(q48h_model *m, int on);
+int q48h_step_onelaunch_active(q48h_model *m, int pos);
 
 /* In the fused modes, have each layer's attention launch also read that
  * layer's W_o on the idle compute units (q48_attn_decode_rope_prefetch), so
