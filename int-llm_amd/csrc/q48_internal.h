@@ -26,7 +26,7 @@ struct q48_ctx {
     size_t tmp_bytes;
     uint64_t *rms_part;          // device: per-block partial sums of squares (EPI 3)
     int *rms_count;              // device: tickets, back to 0 after use: [0] EPI 3 blocks
-                                 // finished, [256 + h] split-attention chunks of head h
+                                 // finished
     int rms_blocks;
     int64_t *smp;                // device: sampling workspace (q48_sample_ws_words)
     size_t smp_words;

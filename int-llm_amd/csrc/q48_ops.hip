@@ -431,17 +431,22 @@ __device__ __forceinline__ void argmax_scan(const int64_t *__restrict__ v, int n
 // (chunk of ATT_CH positions, head) blocks, so that a head's keys and values
 // stream through many compute units instead of one.  The reference's
 // softmax needs the global max before any exponential and the global sum
-// before any division, so:
+// before any division, so three launches over the same (chunk, head) grid:
 //  - k_attn_s1: each block rotates q_h / the new k (RoPE), scores its chunk
-//    into sc[h][t] and its chunk maximum into cmax[h][c], all with
-//    write-through stores; the last block of a head to finish (agent-scope
-//    ticket, taken after its stores completed) takes the global max, turns
-//    every score into e_t = fp_safe_exp(s_t - max), sums them (int64 wrap),
-//    stores p_t = fp_div(e_t, sum) when sum > 0, zeroes out[h] and resets
-//    the ticket (llama_int.c:1060-1072, 1502-1512);
-//  - k_attn_s2: each block adds sum_t fp_mul(p_t, v_t[d]) over its chunk
-//    into out[h][d] with 64-bit atomic adds: int64 wrap sums in any order,
-//    the bits of llama_int.c:1514-1529.
+//    into sc[h][t] and its chunk maximum into cmax[h][c]
+//    (llama_int.c:1502-1512);
+//  - k_attn_se: each block takes the global max over the chunk maxima,
+//    turns its chunk's scores into e_t = fp_safe_exp(s_t - max) (one per
+//    thread) and stores the chunk's int64 (wrapping) sum in csum[h][c]; the
+//    chunk-0 block zeroes out[h] (llama_int.c:1060-1068);
+//  - k_attn_s2: each block adds the chunk sums (wrapping: the reference's
+//    sum in any order), turns its chunk into p_t = fp_div(e_t, sum) when
+//    sum > 0 (one per thread, llama_int.c:1069-1071), then adds
+//    sum_t fp_mul(p_t, v_t[d]) over its chunk into out[h][d] with 64-bit
+//    atomic adds: int64 wrap sums in any order, the bits of
+//    llama_int.c:1514-1529.
+// Every exponential and division runs on its own thread, spread over all the
+// chunk blocks, instead of on one block per head.
 // Blocks whose chunk starts past pos exit at once (the grid covers the
 // whole cache, so a captured graph stays valid as pos grows).
 // ---------------------------------------------------------------------------
@@ -451,17 +456,15 @@ constexpr int ATT_NCMAX = 128;   // chunks per head: max_seq <= 32768
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_s1(
-    int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
-    int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
-    const int64_t *__restrict__ v_new, const int64_t *__restrict__ cos_t,
-    const int64_t *__restrict__ sin_t, const int64_t *__restrict__ scale_p,
-    int64_t *__restrict__ sc, int64_t *__restrict__ cmax, int *__restrict__ tickets, int layer,
-    const int *__restrict__ d_pos, int pos, int n_heads, int n_kv, int max_seq)
+    const int64_t *__restrict__ q, int64_t *__restrict__ kcache, int64_t *__restrict__ vcache,
+    const int64_t *__restrict__ k_new, const int64_t *__restrict__ v_new,
+    const int64_t *__restrict__ cos_t, const int64_t *__restrict__ sin_t,
+    const int64_t *__restrict__ scale_p, int64_t *__restrict__ sc, int64_t *__restrict__ cmax,
+    int layer, const int *__restrict__ d_pos, int pos, int n_heads, int n_kv, int max_seq)
 {
     constexpr int NT = 256, DPL = HD / 8, DP2 = DPL / 2, NG = NT / 8;
     __shared__ int64_t qs[HD], ks[HD], vs[HD];
     __shared__ int64_t red[NT / 64];
-    __shared__ int last_sh;
     if (d_pos)
         pos = *d_pos;
     if (pos < 0 || pos >= max_seq)
@@ -471,7 +474,6 @@ __global__ __launch_bounds__(256) void k_attn_s1(
     if (t0 >= S)
         return;   // uniform: no barrier is skipped by part of the block
     const int tend = min(t0 + ATT_CH, S);
-    const int nc = (S + ATT_CH - 1) / ATT_CH;
     const int group = n_heads / n_kv, kh = h / group;
     const size_t kvd = (size_t)n_kv * HD;
     const size_t base = (size_t)layer * max_seq;
@@ -529,7 +531,7 @@ __global__ __launch_bounds__(256) void k_attn_s1(
         dot = q48_sum8_u128(dot);
         if (t < tend && l8 == 0) {
             const int64_t sv = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
-            __hip_atomic_store(&sch[t], sv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sch[t] = sv;
             mx = sv > mx ? sv : mx;
         }
     };
@@ -545,74 +547,56 @@ __global__ __launch_bounds__(256) void k_attn_s1(
     }
     mx = block_max64<NT>(mx, red);
     if (tid == 0)
-        __hip_atomic_store(&cmax[(size_t)h * ATT_NCMAX + c], mx, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    // Every store above is write-through (agent scope); waiting for their
-    // completion before the ticket orders them before it for every block.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0)
-        last_sh = __hip_atomic_fetch_add(&tickets[h], 1, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) == nc - 1;
-    __syncthreads();
-    if (!last_sh)
-        return;
+        cmax[(size_t)h * ATT_NCMAX + c] = mx;
+}
 
-    // last block of head h: the softmax over all S positions
-    int64_t gm = INT64_MIN;
-    if (tid < nc)
-        gm = __hip_atomic_load(&cmax[(size_t)h * ATT_NCMAX + tid], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    gm = block_max64<NT>(gm, red);
-    // 8 positions per thread per round, loads first, so that the exps and
-    // divisions of a thread are independent chains the core can interleave
-    constexpr int EB = 8;
-    int64_t sum = 0;
-    for (int t0r = 0; t0r < S; t0r += NT * EB) {
-        int64_t sv[EB];
-#pragma unroll
-        for (int u = 0; u < EB; ++u)
-            sv[u] = __hip_atomic_load(&sch[min(t0r + tid + NT * u, S - 1)], __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int u = 0; u < EB; ++u) {
-            const int t = t0r + tid + NT * u;
-            if (t < S) {
-                const int64_t e = q48_safe_exp((int64_t)((uint64_t)sv[u] - (uint64_t)gm));
-                sch[t] = e;   // re-read below by this same thread
-                sum = (int64_t)((uint64_t)sum + (uint64_t)e);
-            }
-        }
+// exponentials of one chunk and their sum (see above)
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_se(int64_t *__restrict__ out,
+                                                int64_t *__restrict__ sc,
+                                                const int64_t *__restrict__ cmax,
+                                                int64_t *__restrict__ csum,
+                                                const int *__restrict__ d_pos, int pos,
+                                                int n_heads, int max_seq)
+{
+    constexpr int NT = 256;
+    static_assert(ATT_CH == NT, "one position per thread");
+    __shared__ int64_t red[NT / 64];
+    if (d_pos)
+        pos = *d_pos;
+    if (pos < 0 || pos >= max_seq)
+        return;
+    const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int S = pos + 1, t0 = c * ATT_CH;
+    if (t0 >= S)
+        return;   // uniform
+    const int nc = (S + ATT_CH - 1) / ATT_CH, t = t0 + tid;
+    int64_t *sch = sc + (size_t)h * max_seq;
+    const int64_t s = sch[min(t, S - 1)];
+    int64_t gm = tid < nc ? cmax[(size_t)h * ATT_NCMAX + tid] : INT64_MIN;
+    gm = block_max64<NT>(gm, red, false);
+    int64_t e = 0;
+    if (t < S) {
+        e = q48_safe_exp((int64_t)((uint64_t)s - (uint64_t)gm));
+        sch[t] = e;
     }
-    sum = block_sum64<NT>(sum, red);
-    if (sum > 0)
-        for (int t0r = 0; t0r < S; t0r += NT * EB) {
-            int64_t ev[EB];
-#pragma unroll
-            for (int u = 0; u < EB; ++u)
-                ev[u] = sch[min(t0r + tid + NT * u, S - 1)];
-#pragma unroll
-            for (int u = 0; u < EB; ++u) {
-                const int t = t0r + tid + NT * u;
-                if (t < S)
-                    sch[t] = q48_div(ev[u], sum);
-            }
-        }
-    if (tid < HD)
-        out[(size_t)h * HD + tid] = 0;
+    e = block_sum64<NT>(e, red);
     if (tid == 0)
-        tickets[h] = 0;
+        csum[(size_t)h * ATT_NCMAX + c] = e;
+    if (c == 0 && tid < HD)
+        out[(size_t)h * HD + tid] = 0;
 }
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_s2(int64_t *__restrict__ out,
                                                 const int64_t *__restrict__ vcache,
-                                                const int64_t *__restrict__ sc, int layer,
+                                                const int64_t *__restrict__ sc,
+                                                const int64_t *__restrict__ csum, int layer,
                                                 const int *__restrict__ d_pos, int pos,
                                                 int n_heads, int n_kv, int max_seq)
 {
     constexpr int NT = 256, SL = NT / HD, VB = 8;
-    __shared__ int64_t part[NT];
+    __shared__ int64_t part[NT], pl[ATT_CH], red[NT / 64];
     if (d_pos)
         pos = *d_pos;
     if (pos < 0 || pos >= max_seq)
@@ -627,39 +611,39 @@ __global__ __launch_bounds__(256) void k_attn_s2(int64_t *__restrict__ out,
     const int d = tid % HD, sl = tid / HD;
     const int64_t *vcol = vcache + (size_t)layer * max_seq * kvd + (size_t)kh * HD + d;
     const int64_t *ph = sc + (size_t)h * max_seq;
-    // positions t0 + sl + SL i of this thread, VB per batch, one batch ahead
+    // positions t0 + sl + SL i of this thread, VB per batch, one batch ahead;
+    // the first value batches go out before the division
     auto tpos = [&](int i) { return min(t0 + sl + SL * i, tend - 1); };
-    int64_t va[VB], vb[VB], pa[VB], pb[VB];
+    const int nc = (S + ATT_CH - 1) / ATT_CH;
+    const int64_t ev = ph[min(t0 + tid, tend - 1)];
+    int64_t cs = tid < nc ? csum[(size_t)h * ATT_NCMAX + tid] : 0;
+    int64_t va[VB], vb[VB];
 #pragma unroll
-    for (int u = 0; u < VB; ++u) {
+    for (int u = 0; u < VB; ++u)
         va[u] = vcol[(size_t)tpos(u) * kvd];
-        pa[u] = ph[tpos(u)];
-    }
 #pragma unroll
-    for (int u = 0; u < VB; ++u) {
+    for (int u = 0; u < VB; ++u)
         vb[u] = vcol[(size_t)tpos(VB + u) * kvd];
-        pb[u] = ph[tpos(VB + u)];
-    }
+    // p_t = fp_div(e_t, sum) when sum > 0, one position per thread
+    const int64_t sum = block_sum64<NT>(cs, red, false);
+    pl[tid] = sum > 0 ? q48_div(ev, sum) : ev;
+    __syncthreads();
     uint64_t acc = 0;
-    auto vmac = [&](const int64_t (&vv)[VB], const int64_t (&pp)[VB], int i0) {
+    auto vmac = [&](const int64_t (&vv)[VB], int i0) {
 #pragma unroll
         for (int u = 0; u < VB; ++u)
             if (t0 + sl + SL * (i0 + u) < tend)
-                acc += (uint64_t)q48_mul(pp[u], vv[u]);
+                acc += (uint64_t)q48_mul(pl[sl + SL * (i0 + u)], vv[u]);
     };
     for (int i0 = 0; t0 + sl + SL * i0 < tend; i0 += 2 * VB) {
-        vmac(va, pa, i0);
+        vmac(va, i0);
 #pragma unroll
-        for (int u = 0; u < VB; ++u) {
+        for (int u = 0; u < VB; ++u)
             va[u] = vcol[(size_t)tpos(i0 + 2 * VB + u) * kvd];
-            pa[u] = ph[tpos(i0 + 2 * VB + u)];
-        }
-        vmac(vb, pb, i0 + VB);
+        vmac(vb, i0 + VB);
 #pragma unroll
-        for (int u = 0; u < VB; ++u) {
+        for (int u = 0; u < VB; ++u)
             vb[u] = vcol[(size_t)tpos(i0 + 3 * VB + u) * kvd];
-            pb[u] = ph[tpos(i0 + 3 * VB + u)];
-        }
     }
     part[tid] = (int64_t)acc;
     __syncthreads();
@@ -935,19 +919,20 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
     if (rope && pos >= ATT_SPLIT_MIN && (head_dim == 32 || head_dim == 64 || head_dim == 128) &&
         (max_seq + ATT_CH - 1) / ATT_CH <= ATT_NCMAX && n_heads <= 256) {
         const size_t sc_n = (size_t)n_heads * max_seq, cm_n = (size_t)n_heads * ATT_NCMAX;
-        int rc = q48_ws_reserve(c, (sc_n + cm_n) * sizeof(int64_t));
+        int rc = q48_ws_reserve(c, (sc_n + 2 * cm_n) * sizeof(int64_t));
         if (rc)
             return rc;
-        int64_t *sc = (int64_t *)c->ws, *cm = sc + sc_n;
-        int *tk = c->rms_count + 256;
+        int64_t *sc = (int64_t *)c->ws, *cm = sc + sc_n, *cs = cm + cm_n;
         const dim3 grid((max_seq + ATT_CH - 1) / ATT_CH, n_heads);
 #define ATTS_LAUNCH(HD)                                                                       \
     do {                                                                                      \
-        hipLaunchKernelGGL((k_attn_s1<HD>), grid, dim3(256), 0, c->stream, out, q, kcache,   \
-                           vcache, k_new, v_new, c->rope_cos, c->rope_sin, scale_p, sc, cm,  \
-                           tk, layer, d_pos, pos, n_heads, n_kv, max_seq);                   \
-        hipLaunchKernelGGL((k_attn_s2<HD>), grid, dim3(256), 0, c->stream, out, vcache, sc,  \
-                           layer, d_pos, pos, n_heads, n_kv, max_seq);                       \
+        hipLaunchKernelGGL((k_attn_s1<HD>), grid, dim3(256), 0, c->stream, q, kcache, vcache, \
+                           k_new, v_new, c->rope_cos, c->rope_sin, scale_p, sc, cm, layer,    \
+                           d_pos, pos, n_heads, n_kv, max_seq);                               \
+        hipLaunchKernelGGL((k_attn_se<HD>), grid, dim3(256), 0, c->stream, out, sc, cm, cs,   \
+                           d_pos, pos, n_heads, max_seq);                                     \
+        hipLaunchKernelGGL((k_attn_s2<HD>), grid, dim3(256), 0, c->stream, out, vcache, sc,   \
+                           cs, layer, d_pos, pos, n_heads, n_kv, max_seq);                    \
     } while (0)
         if (head_dim == 64)
             ATTS_LAUNCH(64);
