@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline sweep, from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE runs scaled by the counters' reading for a copy kernel of known
 # size (profiles/k_gemv_decode_tinyllama.md); re-measure when the kernel changes
-TRAFFIC = 93507901
+TRAFFIC = 93546127
 REF_CPU_MS_PER_TOK = 501.4   # reference decode, Zen 4, 1 thread
 # int8 GEMM: MI355X dense int8 MFMA peak; one Q16.48 MAC is 63 int8 products
 # (digit pairs a + b <= 13), 2 ops each
