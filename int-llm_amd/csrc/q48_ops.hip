@@ -366,8 +366,8 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
 // HD = 32, 64 or 128; at most ATT_LDS_MAX positions.  Blocks past n_heads
 // prefetch like k_attn_v2's.
 // ---------------------------------------------------------------------------
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_v3(
+template <int HD, int NT>
+__global__ __launch_bounds__(NT) void k_attn_v3(
     int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
     int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
     const int64_t *__restrict__ v_new, const int64_t *__restrict__ cos_t,
@@ -375,7 +375,6 @@ __global__ __launch_bounds__(256) void k_attn_v3(
     const int *__restrict__ d_pos, int pos, int n_heads, int n_kv, int max_seq,
     const ulonglong2 *__restrict__ pf, size_t pf_n16)
 {
-    constexpr int NT = 256;
     if ((int)blockIdx.x >= n_heads) {
         const size_t stride = (size_t)(gridDim.x - n_heads) * NT;
         size_t i = (size_t)(blockIdx.x - n_heads) * NT + threadIdx.x;
@@ -394,9 +393,9 @@ __global__ __launch_bounds__(256) void k_attn_v3(
         asm volatile("" ::"v"(acc));
         return;
     }
-    attn_v3_head<HD, ATT_LDS_MAX, false>(out, q, kcache, vcache, k_new, v_new, cos_t, sin_t,
-                                         scale_p, layer, d_pos, pos, n_heads, n_kv, max_seq,
-                                         (int)blockIdx.x);
+    attn_v3_head<HD, ATT_LDS_MAX, false, false, false, NT>(
+        out, q, kcache, vcache, k_new, v_new, cos_t, sin_t, scale_p, layer, d_pos, pos, n_heads,
+        n_kv, max_seq, (int)blockIdx.x);
 }
 
 // This thread's share of argmax (llama_int.c:2888-2893) over v[0..n) with
@@ -451,6 +450,10 @@ __device__ __forceinline__ void argmax_scan(const int64_t *__restrict__ v, int n
 // whole cache, so a captured graph stays valid as pos grows).
 // ---------------------------------------------------------------------------
 constexpr int ATT_CH = 256;        // positions per chunk
+// k_attn_v3 block size: 512 threads score 64 positions per pass and hold 8
+// value slices, so up to 128 positions have their keys and values loaded
+// before the first score (with 256 threads a second round of loads waited)
+constexpr int ATT_V3_NT = 512;
 constexpr int ATT_SPLIT_MIN = 512; // first position served by the split kernels
 constexpr int ATT_NCMAX = 128;   // chunks per head: max_seq <= 32768
 
@@ -944,7 +947,8 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
         return (int)hipGetLastError();
     }
 #define ATT3_LAUNCH(HD)                                                                      \
-    hipLaunchKernelGGL((k_attn_v3<HD>), dim3(n_heads + pf_blocks), dim3(256), 0, c->stream,  \
+    hipLaunchKernelGGL((k_attn_v3<HD, ATT_V3_NT>), dim3(n_heads + pf_blocks), dim3(ATT_V3_NT), \
+                       0, c->stream,                                                         \
                        out, q, kcache, vcache, k_new, v_new, c->rope_cos, c->rope_sin,       \
                        scale_p, layer, d_pos, pos, n_heads, n_kv, max_seq,                   \
                        (const ulonglong2 *)prefetch, pf_n16)
