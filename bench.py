@@ -143,26 +143,60 @@ def gemm_prefill(ctx, spec, intllm, reps: int):
             "shapes": out}
 
 
-def cpu_baseline(spec, seconds: float, prompt):
-    """Single-threaded CPU decode of the same model: the reference's own
-    llama_forward (oracle/_ref, compiled from its sources) when present,
-    else the oracle port.  Bounded sample: successive decode positions
-    until `seconds` of CPU time is spent."""
-    import numpy as np
-    kind = "reference"
+def _cpu_flags():
+    model, flags = "", set()
     try:
-        lib = C.CDLL(str(ROOT / "oracle" / "_ref" / "libq48_ref.so"))
-        mk, fwd, free = lib.q48r_model_synth, lib.q48r_forward, lib.q48r_model_free
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and not model:
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
     except OSError:
+        pass
+    return model, flags
+
+
+# x86-64 micro-architecture levels (the flags /proc/cpuinfo shows for them)
+ISA_V3 = {"avx", "avx2", "bmi1", "bmi2", "f16c", "fma", "abm", "movbe", "xsave"}
+ISA_V4 = ISA_V3 | {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"}
+
+
+def cpu_baseline(spec, intllm, seconds: float, prompt, n_prompt: int = 16):
+    """Single-threaded CPU run of the same model: the reference's own
+    llama_forward (oracle/_ref, compiled from llama_int.c with the
+    reference's -O3 -fwrapv at the highest x86-64 level this CPU supports,
+    standing in for its -march=native), else the oracle port.  Bounded
+    sample: generate()'s loop over the first n_prompt prompt tokens
+    (prefill, one forward per token) and then greedy decode steps until
+    `seconds` of CPU time is spent; plus matmul_vec per config-2 shape.
+    KPIs as the reference prints them (llama_int.c:271-285)."""
+    import numpy as np
+    model_name, flags = _cpu_flags()
+    kind, isa = "reference", "x86-64"
+    lib = None
+    for lvl, need, so in (("x86-64-v4", ISA_V4, "libq48_ref_v4.so"),
+                          ("x86-64-v3", ISA_V3, "libq48_ref_v3.so"),
+                          ("x86-64", set(), "libq48_ref.so")):
+        path = ROOT / "oracle" / "_ref" / so
+        if need <= flags and path.exists():
+            lib, isa = C.CDLL(str(path)), lvl
+            break
+    if lib is not None:
+        mk, fwd, free = lib.q48r_model_synth, lib.q48r_forward, lib.q48r_model_free
+        gemv = lib.q48r_gemv
+    else:
         import oracle_lib as O
         lib = O.load()
         kind = "port"
         mk, fwd, free = lib.q48o_model_synth, lib.q48o_forward, lib.q48o_model_free
+        gemv = lib.q48o_gemv
     mk.restype = C.c_void_p
     mk.argtypes = [C.c_void_p, C.c_uint64, C.c_int]
     fwd.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
     fwd.restype = C.c_int
     free.argtypes = [C.c_void_p]
+    gemv.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+    gemv.restype = None
     import oracle_lib as O
     cfg = O.Config(*spec.TINYLLAMA)
     # the reference's setup prints to stdout: keep the JSON line alone there
@@ -177,29 +211,51 @@ def cpu_baseline(spec, seconds: float, prompt):
         os.close(saved)
         os.close(devnull)
     logits = np.empty(cfg.vocab, dtype=np.int64)
-    times = []
     t_all = time.perf_counter()
-    pos = 0
-    while pos < len(prompt) and (time.perf_counter() - t_all) < seconds:
+    t_pf = t_dc = 0.0
+    n_pf = n_dc = 0
+    tok = None
+    for pos in range(n_prompt):                        # prefill (llama_int.c:3081-3092)
         t = time.perf_counter()
-        rc = fwd(m, prompt[pos], pos, logits.ctypes.data)
-        times.append(time.perf_counter() - t)
-        assert rc == 0
+        assert fwd(m, prompt[pos], pos, logits.ctypes.data) == 0
+        t_pf += time.perf_counter() - t
+        n_pf += 1
+    tok = int(np.argmax(logits))                       # the first maximum, as argmax
+    pos = n_prompt
+    while time.perf_counter() - t_all < seconds or n_dc < 2:   # decode (:3103-3113)
+        t = time.perf_counter()
+        assert fwd(m, tok, pos, logits.ctypes.data) == 0
+        tok = int(np.argmax(logits))
+        t_dc += time.perf_counter() - t
+        n_dc += 1
         pos += 1
     free(m)
-    ms = 1e3 * sum(times) / len(times)
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(1e3 / ms, 4), "unit": "tok/s", "cores": 1, "kind": kind,
-            "ms_per_tok": round(ms, 2),
-            "sample": f"{len(times)} TinyLlama-shape forward calls (positions 0..{len(times) - 1}), "
-                      f"1 thread, {cpu_model}, nproc={os.cpu_count()}"}
+    # matmul_vec (llama_int.c:1014-1046) per config-2 shape, best of 3
+    shapes = {}
+    for (M, K) in spec.GEMV_SHAPES:
+        W, x = spec.gemv_inputs_ref(intllm.synth, M, K)
+        y = np.empty(M, dtype=np.int64)
+        best = None
+        for _ in range(3):
+            t = time.perf_counter()
+            gemv(y.ctypes.data, W.ctypes.data, x.ctypes.data, M, K)
+            dt = time.perf_counter() - t
+            best = dt if best is None else min(best, dt)
+        shapes[f"{M}x{K}"] = {"us": round(1e6 * best, 1),
+                              "GB_s": round(8.0 * (M * K + K + M) / best / 1e9, 2)}
+        del W
+    dec_ms = 1e3 * t_dc / n_dc
+    return {"value": round(1e3 / dec_ms, 4), "unit": "tok/s", "cores": 1, "kind": kind,
+            "isa": isa, "cflags": f"-O3 -fwrapv -march={isa} (reference Makefile:38 uses "
+                                  "-O3 -march=native -fwrapv)",
+            "cpu_model": model_name, "nproc": os.cpu_count(),
+            "prefill_ms_per_tok": round(1e3 * t_pf / n_pf, 2),
+            "decode_ms_per_tok": round(dec_ms, 2),
+            "tok_per_sec": round((n_pf + n_dc) / (t_pf + t_dc), 4),
+            "prefill_tokens": n_pf, "decode_tokens": n_dc,
+            "matmul_vec_1core": shapes,
+            "sample": f"generate()'s loop on the TinyLlama-shape model: {n_pf} prompt tokens "
+                      f"(positions 0..{n_pf - 1}), then {n_dc} greedy decode steps; 1 thread"}
 
 
 def main():
@@ -258,6 +314,20 @@ def main():
     log(f"model ready in {time.time() - t:.1f}s")
 
     prompt = gold["prompt"]
+    # every replayed decode step records its logits on the device and they
+    # are hashed (FNV-1a 64, as the reference's logits) against the golden
+    # per-step hashes: positions p of the golden run have step_fnv[p]
+    hashes = {"compared": 0, "matched": 0, "first_mismatch": None}
+
+    def check_hashes(label, p0, hs, ref):
+        for i, h in enumerate(hs):
+            if p0 + i < len(ref):
+                hashes["compared"] += 1
+                if h == ref[p0 + i]:
+                    hashes["matched"] += 1
+                elif hashes["first_mismatch"] is None:
+                    hashes["first_mismatch"] = f"{label} position {p0 + i}"
+
     # prefill (untimed): the prompt, one forward per token as generate() does
     nxt = None
     for pos, tok in enumerate(prompt):
@@ -265,19 +335,22 @@ def main():
     toks = [nxt]
     pos = len(prompt)
     # warm-up decode steps (also captures the decode-step graph)
-    _, steps, _ = m.decode_graph(toks[-1], pos, args.warmup)
+    _, steps, hs, _ = m.decode_graph_hashed(toks[-1], pos, args.warmup)
+    check_hashes("int64 warm-up", pos, hs, gold["step_fnv"])
     toks += steps
     pos += args.warmup
     ctx.sync()
-    # timed: K greedy decode steps replayed from the graph, argmax on device
+    # timed: K greedy decode steps replayed from the graph (argmax and the
+    # logits record on the device), from the first step's launch to the K
+    # tokens back on the host; the host hashes the records afterwards
     t0 = time.perf_counter()
-    _, steps, _ = m.decode_graph(toks[-1], pos, args.steps)
-    ctx.sync()
-    dt = time.perf_counter() - t0
+    _, steps, hs, st = m.decode_graph_hashed(toks[-1], pos, args.steps)
+    wall = time.perf_counter() - t0
+    check_hashes("int64 timed", pos, hs, gold["step_fnv"])
     toks += steps
     pos += args.steps
-    ms = 1e3 * dt / args.steps
-    log(f"decode {ms:.3f} ms/tok")
+    ms = 1e3 * st.decode_s / args.steps
+    log(f"decode {ms:.3f} ms/tok (call incl. hashing {1e3 * wall / args.steps:.3f})")
 
     p0 = len(prompt) + args.warmup
     # roofline of the dominant kernel (q48_gemv): the GEMV launches of one
@@ -298,15 +371,15 @@ def main():
     bf16 = None
     if not args.no_bf16:
         m.set_bf16(True)
-        _, steps, _ = m.decode_graph(toks[-1], pos, args.warmup)
+        _, steps, hs, _ = m.decode_graph_hashed(toks[-1], pos, args.warmup)
+        check_hashes("bf16 warm-up", pos, hs, gold["step_fnv"])
         toks += steps
         pos += args.warmup
         ctx.sync()
         b0 = pos
-        t0 = time.perf_counter()
-        _, steps, _ = m.decode_graph(toks[-1], pos, args.steps)
-        ctx.sync()
-        bms = 1e3 * (time.perf_counter() - t0) / args.steps
+        _, steps, hs, bst = m.decode_graph_hashed(toks[-1], pos, args.steps)
+        check_hashes("bf16 timed", pos, hs, gold["step_fnv"])
+        bms = 1e3 * bst.decode_s / args.steps
         toks += steps
         pos += args.steps
         m.gemv_sweep(1)
@@ -393,14 +466,14 @@ def main():
         prefill = gold_long["prefill"]
         m.kv_fill_synth(gold_long["kv_seed"], prefill, threads())
         tok0 = gold_long["start_token"]
+        long_fnv = [None] * prefill + gold_long["step_fnv"]
         # the first steps warm (they are also checked against the reference)
-        _, lw, _ = m.decode_graph(tok0, prefill, args.warmup)
+        _, lw, hs, _ = m.decode_graph_hashed(tok0, prefill, args.warmup)
+        check_hashes("config-5 warm-up", prefill, hs, long_fnv)
         ctx.sync()
-        t0 = time.perf_counter()
-        _, lt, _ = m.decode_graph(lw[-1], prefill + args.warmup, args.long_steps)
-        ctx.sync()
-        ldt = time.perf_counter() - t0
-        lms = 1e3 * ldt / args.long_steps
+        _, lt, hs, lst = m.decode_graph_hashed(lw[-1], prefill + args.warmup, args.long_steps)
+        check_hashes("config-5 timed", prefill + args.warmup, hs, long_fnv)
+        lms = 1e3 * lst.decode_s / args.long_steps
         ltoks = [tok0] + lw + lt
         ref = [tok0] + gold_long["tokens"]
         n = min(len(ref), len(ltoks))
@@ -413,12 +486,20 @@ def main():
                    "kv_bytes_per_token": kv_bytes,
                    "tokens_compared": n, "tokens_match_reference": ltoks[:n] == ref[:n]}
     m.free()
+    parity["step_logits_hashes_compared"] = hashes["compared"]
+    parity["step_logits_hashes_matched"] = hashes["matched"]
+    if hashes["first_mismatch"]:
+        parity["first_hash_mismatch"] = hashes["first_mismatch"]
+    parity["all_match"] = (parity["tokens_match_reference"] and
+                           hashes["matched"] == hashes["compared"] and
+                           (longctx is None or longctx["tokens_match_reference"]) and
+                           parity.get("prefill_next_token_matches_reference", True))
 
     shapes = None if args.no_shapes else gemv_shapes(ctx, spec, intllm, reps=64)
     gemm = gemm_prefill(ctx, spec, intllm, args.gemm_reps) if args.gemm_reps > 0 else None
     ctx.close()
 
-    cpu = None if args.no_cpu else cpu_baseline(spec, args.cpu_seconds, prompt)
+    cpu = None if args.no_cpu else cpu_baseline(spec, intllm, args.cpu_seconds, prompt)
 
     value = 1e3 / ms
     line = {
@@ -432,6 +513,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(value / (1e3 / REF_CPU_MS_PER_TOK), 1),
+        "vs_baseline_source": "published llama_int CPU decode, 501.4 ms/tok, TinyLlama-1.1B on a "
+                              "Ryzen 7 7700, 1 thread (validation/cpu/X86_64_AMD_ZEN4/results/"
+                              "2026-07-30-x86-amd-zen4-tinyllama.txt:31)",
+        "vs_cpu_same_run": (round(value / cpu["value"], 1) if cpu else None),
         "dtype": "int64",
         "data": "synthetic: random-init N(0,0.02) bf16-exact Q16.48 weights, seeded 32-token prompt",
         "config": {"workload": "config 3: TinyLlama-1.1B-shape greedy decode, batch 1, "

@@ -282,6 +282,13 @@ int q48_step_get(q48_ctx *ctx, int *token, int *pos, int *count);  /* syncs */
 /* argmax (llama_int.c:2888-2893) of v[0..n) into the state; the token is
  * also stored at d_tokens[count] while count < cap. */
 int q48_argmax_step(q48_ctx *ctx, const int64_t *v, int n, int *d_tokens, int cap);
+/* Parity hook of the replayed steps.  No reference counterpart: it keeps the
+ * logits of each step (what llama_forward returns to generate,
+ * llama_int.c:3082 and 3105) so that the host can hash every replayed step.
+ * Copies v[0..n) to rec[count * n ..] while count < cap, count being the
+ * state's number of tokens chosen so far; enqueue it before the step's
+ * q48_argmax_step or q48_sample_step. */
+int q48_record_step(q48_ctx *ctx, const int64_t *v, int n, int64_t *rec, int cap);
 
 
 /* ---- batched prefill ------------------------------------------------------ */

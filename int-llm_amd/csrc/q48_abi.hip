@@ -72,7 +72,7 @@ const char *q48_strerror(int code)
     case Q48_EHIP: return "HIP runtime error";
     case Q48_ERANGE: return "token or position out of range";
     case Q48_ESTATE: return "context state not initialised (call q48_rope_init)";
-    case Q48_ETIMEOUT: return "one-launch decode step timed out (blocks not resident)";
+    case Q48_ETIMEOUT: return "one-launch decode step or attention timed out (blocks not resident)";
     default: return "unknown error";
     }
 }
@@ -100,14 +100,19 @@ int q48_ctx_create(q48_ctx **out, int device)
         delete c;
         return Q48_EHIP;
     }
+    c->attn_one_launch = 0;
+    c->attx_per_cu[0] = c->attx_per_cu[1] = c->attx_per_cu[2] = -1;
     if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
         hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess ||
         hipMalloc(&c->d_step, 4 * sizeof(int)) != hipSuccess ||
-        hipMalloc(&c->rms_count, 512 * sizeof(int)) != hipSuccess) {
+        hipMalloc(&c->rms_count, 512 * sizeof(int)) != hipSuccess ||
+        hipMalloc(&c->attx_sync, q48_attn_sync_bytes()) != hipSuccess) {
         q48_ctx_destroy(c);
         return Q48_ENOMEM;
     }
     int rc = launch_rc(q48_launch_math_init(c));
+    if (rc == Q48_OK)
+        rc = launch_rc(q48_launch_zero(c, c->attx_sync, q48_attn_sync_bytes()));
     if (rc == Q48_OK)
         rc = launch_rc(q48_launch_step_set(c, 0, 0));
     if (rc == Q48_OK)
@@ -141,6 +146,7 @@ int q48_ctx_destroy(q48_ctx *c)
     (void)hipFree(c->smp);
     (void)hipFree(c->tmp);
     (void)hipFree(c->sk_sync);
+    (void)hipFree(c->attx_sync);
     if (c->graph_exec)
         (void)hipGraphExecDestroy(c->graph_exec);
     if (c->graph)
@@ -606,6 +612,41 @@ int q48_attn_decode_rope(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kc
 
 int q48_attn_split_min(void) { return q48_att_split_min(); }
 
+
+int q48_attn_status(q48_ctx *c)
+{
+    if (!c)
+        return Q48_EINVAL;
+    if (c->capturing)
+        return Q48_ESTATE;
+    const size_t off = q48_attn_sync_bytes() - 16 * sizeof(unsigned);
+    int e[2] = {0, 0};
+    if (hipStreamSynchronize(c->stream) != hipSuccess ||
+        hipMemcpy(&e[0], (char *)c->attx_sync + off, sizeof(int), hipMemcpyDeviceToHost) !=
+            hipSuccess ||
+        (c->scratch_sync &&
+         hipMemcpy(&e[1], (char *)c->scratch_sync + off, sizeof(int), hipMemcpyDeviceToHost) !=
+             hipSuccess))
+        return Q48_EHIP;
+    if (!e[0] && !e[1])
+        return Q48_OK;
+    // a timed-out launch left its barrier words behind: clear both regions
+    int rc = launch_rc(q48_launch_zero(c, c->attx_sync, q48_attn_sync_bytes()));
+    if (rc == Q48_OK && c->scratch_sync)
+        rc = launch_rc(q48_launch_zero(c, c->scratch_sync, q48_attn_sync_bytes()));
+    if (rc == Q48_OK)
+        rc = hip_rc(hipStreamSynchronize(c->stream));
+    return rc ? rc : Q48_ETIMEOUT;
+}
+
+int q48_set_attn_one_launch(q48_ctx *c, int on)
+{
+    if (!c)
+        return Q48_EINVAL;
+    c->attn_one_launch = on != 0;
+    return Q48_OK;
+}
+
 int q48_set_gemv_persistent(q48_ctx *c, int on)
 {
     if (!c)
@@ -914,6 +955,13 @@ int q48_argmax_step(q48_ctx *c, const int64_t *v, int n, int *d_tokens, int cap)
     if (!c || !v || n <= 0 || cap < 0 || (cap > 0 && !d_tokens))
         return Q48_EINVAL;
     return launch_rc(q48_launch_step_argmax(c, d_tokens, cap, v, n));
+}
+
+int q48_record_step(q48_ctx *c, const int64_t *v, int n, int64_t *rec, int cap)
+{
+    if (!c || !v || !rec || n <= 0 || cap <= 0)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_step_record(c, rec, cap, v, n));
 }
 
 void q48_rng_seed(uint64_t seed, uint64_t state[2])

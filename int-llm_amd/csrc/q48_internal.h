@@ -35,6 +35,11 @@ struct q48_ctx {
     int *sk_err;
     int64_t *sk_amax;
     int sk_grid;                 // k_step_fused blocks (0: not planned yet)
+    unsigned *attx_sync;         // device: k_attn_x barrier words and error word (zeroed)
+    int attn_one_launch;         // split attention as one k_attn_x launch (default on)
+    int attx_per_cu[3];          // k_attn_x<64/32/128> resident blocks per CU (-1: not asked)
+    int64_t *scratch;            // device address of the allocation-free scratch array
+    unsigned *scratch_sync;      // ... and of its barrier region
     hipGraph_t graph;            // captured decode step
     hipGraphExec_t graph_exec;
     int capturing;
@@ -101,9 +106,19 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
                        int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
                        int layer, const int *d_pos, int pos, int n_heads, int n_kv,
                        int head_dim, int max_seq, int rope,
-                       const void *prefetch, size_t prefetch_bytes);
+                       const void *prefetch, size_t prefetch_bytes,
+                       int64_t *ws_ext = nullptr, size_t ws_ext_bytes = 0,
+                       unsigned *sync_ext = nullptr);
+// bytes of the split attention's workspace; of its barrier region
+size_t q48_attn_ws_bytes(int n_heads, int max_seq, int head_dim);
+size_t q48_attn_sync_bytes();
+// the allocation-free attention's scratch on the context's device: address
+// (set up once per device by q48_ctx_create), bytes, and its barrier region
+int q48_scratch_init(q48_ctx *c);
+size_t q48_scratch_bytes();
 int q48_launch_step_set(q48_ctx *c, int token, int pos);
 int q48_launch_step_argmax(q48_ctx *c, int *tokens, int cap, const int64_t *v, int n);
+int q48_launch_step_record(q48_ctx *c, int64_t *rec, int cap, const int64_t *v, int n);
 int q48_launch_silu_mul_pairs(q48_ctx *c, int64_t *out, const int64_t *t, int n);
 int q48_launch_silu_mul(q48_ctx *c, int64_t *out, const int64_t *g,
                         const int64_t *u, int n);

@@ -7,6 +7,7 @@
 // arithmetic is integer, and every reduction is an integer sum (mod 2^64
 // or 2^128) or a max, so the parallel order cannot change a bit.
 #include "q48_internal.h"
+
 #include "q48_attn.hpp"
 
 namespace {
@@ -661,6 +662,269 @@ __global__ __launch_bounds__(256) void k_attn_s2(int64_t *__restrict__ out,
 }
 
 // ---------------------------------------------------------------------------
+// One-launch split attention (k_attn_x): the same (chunk, head) blocks as
+// k_attn_s1/se/s2, but the chunk maxima and the chunk sums are handed from
+// block to block inside the kernel: the blocks of a head meet at two
+// barriers (the global max before any exponential, the global sum before
+// any division, as the reference's softmax needs, llama_int.c:1060-1072)
+// instead of at kernel boundaries.  Per block:
+//  1. the keys of the chunk (all loads issued at once), RoPE of q_h and the
+//     new k (llama_int.c:1392-1395; the KV store at pos by the chunk's first
+//     query head of the KV head), the scores into LDS and their maximum;
+//  2. barrier 1 over the head's chunk maxima; the values of the chunk are
+//     loaded while the exponentials e_t = fp_safe_exp(s_t - max) run, one
+//     position per thread, and the chunk's int64 (wrapping) sum;
+//  3. barrier 2 over the chunk sums (the chunk-0 block zeroes out[h] before
+//     it); p_t = fp_div(e_t, sum) when sum > 0, and sum_t fp_mul(p_t,
+//     v_t[d]) over the chunk added into out[h][d] with 64-bit atomic adds
+//     (int64 wrapping sums in any order: the bits of llama_int.c:1514-1529).
+// A head with one chunk skips both barriers and stores out[h] directly.
+//
+// Barriers: a count and a generation word per head (64 bytes apart).  A
+// block reads the generation, waits for its own coherent stores, adds 1 to
+// the count; the last of the head's nc blocks sets the count back to 0 and
+// then bumps the generation, which the others poll.  Every barrier thus
+// leaves count = 0 behind, so the next launch (graph replays included)
+// starts clean; the generation only ever grows.  Every wait is bounded by
+// the wall clock: a block that waits longer than ATTX_TIMEOUT, or sees
+// another block's timeout, sets *err and leaves (the host sizes the grid
+// so that every active block is resident at once).  Data crossing blocks
+// (chunk maxima and sums, the zeroed output) goes out with agent-coherent
+// stores whose completion is awaited before the count add, and is read with
+// agent-coherent loads.
+// Blocks whose chunk starts past pos exit at once (the grid covers max_seq,
+// so a captured graph stays valid as pos grows).
+// ---------------------------------------------------------------------------
+constexpr int ATTX_NT = 256;
+constexpr int ATTX_SYNC = 16;                     // uints per head: count, generation
+constexpr int ATTX_MAX_HEADS = 256;
+constexpr uint64_t ATTX_TIMEOUT = 1ull << 24;     // wall-clock ticks (0.17 s at 100 MHz)
+
+template <int HD>
+struct AttxShape {
+    static constexpr int CH = HD == 128 ? 128 : 256;   // positions per chunk
+    static constexpr int NG = ATTX_NT / 8;             // positions per pass
+    static constexpr int NP = CH / NG;                 // passes per chunk
+    static constexpr int DP2 = HD / 16;                // 16-byte loads per lane and row
+};
+
+__device__ __forceinline__ unsigned attx_ld(const unsigned *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block-wide barrier of the n blocks of one head; false on every thread
+// when this or another block timed out.
+__device__ bool attx_barrier(unsigned *sync, unsigned n, int *err)
+{
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's coherent stores are done
+    int ok = 1;
+    if (__syncthreads_and(1) && threadIdx.x == 0) {
+        unsigned *count = sync, *gen = sync + 1;
+        const unsigned g = attx_ld(gen);
+        if (__hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            n - 1) {
+            __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            const uint64_t t0 = wall_clock64();
+            while (attx_ld(gen) == g) {
+                if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                    ok = 0;
+                    break;
+                }
+                if (wall_clock64() - t0 > ATTX_TIMEOUT) {
+                    __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = 0;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    }
+    return __syncthreads_and(ok) != 0;
+}
+
+template <int HD>
+__global__ __launch_bounds__(ATTX_NT) void k_attn_x(
+    int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
+    int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
+    const int64_t *__restrict__ v_new, const int64_t *__restrict__ cos_t,
+    const int64_t *__restrict__ sin_t, const int64_t *__restrict__ scale_p,
+    int64_t *__restrict__ cmax, int64_t *__restrict__ csum, unsigned *__restrict__ sync,
+    int *__restrict__ err, int layer, const int *__restrict__ d_pos, int pos, int n_heads,
+    int n_kv, int max_seq)
+{
+    using SH = AttxShape<HD>;
+    constexpr int NT = ATTX_NT, CH = SH::CH, NG = SH::NG, NP = SH::NP, DP2 = SH::DP2;
+    constexpr int DPL = HD / 8;
+    __shared__ int64_t qs[HD], ks[HD], vs[HD];
+    __shared__ int64_t red[NT / 64], red2[NT / 64];
+    __shared__ int64_t sc[CH];
+    __shared__ uint64_t part[NG][HD + 1];
+    if (d_pos)
+        pos = *d_pos;
+    if (pos < 0 || pos >= max_seq)
+        return;
+    const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int S = pos + 1, t0 = c * CH;
+    if (t0 >= S)
+        return;   // uniform: no barrier is skipped by part of the block
+    const int nc = (S + CH - 1) / CH;
+    const int tend = min(t0 + CH, S);
+    const int group = n_heads / n_kv, kh = h / group;
+    const size_t kvd = (size_t)n_kv * HD;
+    const size_t base = (size_t)layer * max_seq;
+    const int half = HD / 2;
+    const int g = tid >> 3, l8 = tid & 7;
+    const int64_t scale = *scale_p;
+
+    // RoPE inputs and the new v first, then every key row of the chunk
+    const int64_t *qh = q + (size_t)h * HD, *kn = k_new + (size_t)kh * HD;
+    const int i = min(tid, half - 1), j = min(tid, HD - 1);
+    int64_t cs = cos_t[(size_t)pos * half + i];
+    int64_t sn = sin_t[(size_t)pos * half + i];
+    int64_t q0 = qh[i], q1 = qh[i + half];
+    int64_t k0 = kn[i], k1 = kn[i + half];
+    int64_t vn = v_new[(size_t)kh * HD + j];
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t *kb0 = kcache + base * kvd + (size_t)kh * HD + l8 * DPL;
+    const int64_t *vb0 = vcache + base * kvd + (size_t)kh * HD + l8 * DPL;
+    auto row = [&](const int64_t *b, int t) {
+        return reinterpret_cast<const ulonglong2 *>(b + (size_t)min(t, tend - 1) * kvd);
+    };
+    ulonglong2 kr[NP][DP2];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            kr[p][d] = row(kb0, t0 + p * NG + g)[d];
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(cs), "+v"(sn), "+v"(q0), "+v"(q1), "+v"(k0), "+v"(k1), "+v"(vn));
+    qs[i] = (int64_t)((uint64_t)q48_mul(q0, cs) - (uint64_t)q48_mul(q1, sn));
+    qs[i + half] = (int64_t)((uint64_t)q48_mul(q1, cs) + (uint64_t)q48_mul(q0, sn));
+    ks[i] = (int64_t)((uint64_t)q48_mul(k0, cs) - (uint64_t)q48_mul(k1, sn));
+    ks[i + half] = (int64_t)((uint64_t)q48_mul(k1, cs) + (uint64_t)q48_mul(k0, sn));
+    vs[j] = vn;
+    __syncthreads();
+    if (h % group == 0 && c == pos / CH && tid < HD) {
+        kcache[(base + pos) * kvd + (size_t)kh * HD + tid] = ks[tid];
+        vcache[(base + pos) * kvd + (size_t)kh * HD + tid] = vs[tid];
+    }
+
+    // scores s_t = fp_mul((sum_d q_d k_t,d) >> 48, scale), llama_int.c:1502-1512;
+    // the row at pos is the block's own rotated k
+    const int64_t *qd = qs + l8 * DPL, *kd = ks + l8 * DPL;
+    int64_t mx = INT64_MIN;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int t = t0 + p * NG + g;
+        const bool own = t == pos;
+        q48_u128 dot = 0;
+#pragma unroll
+        for (int d = 0; d < DP2; ++d) {
+            const int64_t a0 = own ? kd[2 * d] : (int64_t)kr[p][d].x;
+            const int64_t a1 = own ? kd[2 * d + 1] : (int64_t)kr[p][d].y;
+            dot += (q48_u128)q48_smul128(qd[2 * d], a0);
+            dot += (q48_u128)q48_smul128(qd[2 * d + 1], a1);
+        }
+        dot = q48_sum8_u128(dot);
+        if (t < tend && l8 == 0) {
+            const int64_t sv = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
+            sc[t - t0] = sv;
+            mx = sv > mx ? sv : mx;
+        }
+    }
+    mx = block_max64<NT>(mx, red, false);
+
+    // the value rows of the chunk, in flight through the max exchange and
+    // the exponentials (the key registers are free again)
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            kr[p][d] = row(vb0, t0 + p * NG + g)[d];
+
+    unsigned *hs = sync + (size_t)h * ATTX_SYNC;
+    int64_t *cmh = cmax + (size_t)h * ATT_NCMAX, *csh = csum + (size_t)h * ATT_NCMAX;
+    if (nc > 1) {
+        if (tid == 0)
+            __hip_atomic_store(cmh + c, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!attx_barrier(hs, nc, err))
+            return;
+        int64_t m2 = tid < nc ? __hip_atomic_load(cmh + tid, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : INT64_MIN;
+        mx = block_max64<NT>(m2, red2, false);
+    }
+
+    // e_t = fp_safe_exp(s_t - max), one position per thread, and the chunk sum
+    int64_t e = 0;
+    for (int t = tid; t < tend - t0; t += NT) {
+        const int64_t ev = q48_safe_exp((int64_t)((uint64_t)sc[t] - (uint64_t)mx));
+        sc[t] = ev;
+        e = (int64_t)((uint64_t)e + (uint64_t)ev);
+    }
+    int64_t sum = block_sum64<NT>(e, red, true);
+    if (nc > 1) {
+        if (tid == 0)
+            __hip_atomic_store(csh + c, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (c == 0 && tid < HD)
+            __hip_atomic_store(out + (size_t)h * HD + tid, (int64_t)0, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        if (!attx_barrier(hs, nc, err))
+            return;
+        const int64_t s2 = tid < nc ? __hip_atomic_load(csh + tid, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0;
+        sum = block_sum64<NT>(s2, red2, true);
+    }
+    // p_t = fp_div(e_t, sum) when sum > 0 (llama_int.c:1069-1071)
+    if (sum > 0)
+        for (int t = tid; t < tend - t0; t += NT)
+            sc[t] = q48_div(sc[t], sum);
+    __syncthreads();
+
+    // o[d] += fp_mul(p_t, v_t[d]) over the chunk: lane l8 of group g holds
+    // dims [l8 DPL, +DPL) of positions t0 + g + NG p
+    uint64_t acc[DPL];
+#pragma unroll
+    for (int d = 0; d < DPL; ++d)
+        acc[d] = 0;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int t = t0 + p * NG + g;
+        if (t < tend) {
+            const int64_t pt = sc[t - t0];
+            const bool own = t == pos;
+#pragma unroll
+            for (int d = 0; d < DP2; ++d) {
+                const int64_t a0 = own ? vs[l8 * DPL + 2 * d] : (int64_t)kr[p][d].x;
+                const int64_t a1 = own ? vs[l8 * DPL + 2 * d + 1] : (int64_t)kr[p][d].y;
+                acc[2 * d] += (uint64_t)q48_mul(pt, a0);
+                acc[2 * d + 1] += (uint64_t)q48_mul(pt, a1);
+            }
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < DPL; ++d)
+        part[g][l8 * DPL + d] = acc[d];
+    __syncthreads();
+    if (tid < HD) {
+        uint64_t o = 0;
+#pragma unroll 8
+        for (int gg = 0; gg < NG; ++gg)
+            o += part[gg][tid];
+        if (nc > 1)
+            __hip_atomic_fetch_add(reinterpret_cast<uint64_t *>(out) + (size_t)h * HD + tid, o,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            out[(size_t)h * HD + tid] = (int64_t)o;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Decode-step state (graph replay): st[0] = token, st[1] = pos, st[2] =
 // number of tokens recorded.  k_step_argmax is argmax (llama_int.c:
 // 2888-2893) feeding the next step: token <- argmax, pos += 1, and the
@@ -713,6 +977,22 @@ __global__ __launch_bounds__(1024) void k_step_argmax(int *__restrict__ st,
             tokens[k] = tok;
         st[2] = k + 1;
     }
+}
+
+// Step-mode parity hook: rec[count][0..n) = v[0..n), count = st[2] (the
+// tokens chosen so far in this run of steps), while count < cap.  Enqueued
+// before the step's token choice, it keeps every step's logits so that the
+// host can hash them after a graph replay.
+__global__ __launch_bounds__(256) void k_step_record(const int *__restrict__ st,
+                                                    int64_t *__restrict__ rec, int cap,
+                                                    const int64_t *__restrict__ v, int n)
+{
+    const int k = st[2];
+    if (k < 0 || k >= cap)
+        return;
+    int64_t *dst = rec + (size_t)k * n;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256)
+        dst[i] = v[i];
 }
 
 // SwiGLU over interleaved (gate, up) pairs: out[i] = fp_mul(silu(t[2i]), t[2i+1])
@@ -894,38 +1174,106 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
 int q48_att_split_min() { return ATT_SPLIT_MIN; }
 int q48_att_lds_max() { return ATT_LDS_MAX; }
 
+// Workspace of the split attention: chunk maxima and chunk sums [n_heads]
+// [ATT_NCMAX] (k_attn_s1/se/s2 also keep the scores [n_heads][max_seq] in
+// front of them).  The barrier words of k_attn_x live apart, in a region
+// that is zero before the first launch and that every launch leaves zero:
+// [ATTX_MAX_HEADS][ATTX_SYNC] uints, then the error word.
+size_t q48_attn_ws_bytes(int n_heads, int max_seq, int head_dim)
+{
+    (void)head_dim;
+    return ((size_t)n_heads * max_seq + (size_t)2 * n_heads * ATT_NCMAX) * sizeof(int64_t);
+}
+
+size_t q48_attn_sync_bytes() { return ((size_t)ATTX_MAX_HEADS + 1) * ATTX_SYNC * sizeof(unsigned); }
+
+// k_attn_x needs every active block resident at once: blocks per head for a
+// full cache (max_seq) times the heads must fit the device's occupancy.
+static bool attx_fits(q48_ctx *c, int hd, int n_heads, int max_seq)
+{
+    const int k = hd == 64 ? 0 : hd == 32 ? 1 : 2;
+    const int ch = hd == 128 ? AttxShape<128>::CH : AttxShape<64>::CH;
+    if (c->attx_per_cu[k] < 0) {   // resident blocks per compute unit, asked once
+        const void *fn = k == 0 ? (const void *)k_attn_x<64>
+                       : k == 1 ? (const void *)k_attn_x<32> : (const void *)k_attn_x<128>;
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, ATTX_NT, 0) != hipSuccess)
+            n = 0;
+        c->attx_per_cu[k] = n;
+    }
+    const int per_cu = c->attx_per_cu[k];
+    const long need = (long)n_heads * ((max_seq + ch - 1) / ch);
+    return need <= (long)per_cu * c->cu_count && (max_seq + ch - 1) / ch <= ATT_NCMAX;
+}
+
 int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                        int64_t *vcache, const int64_t *k_new, const int64_t *v_new,
                        int layer, const int *d_pos, int pos, int n_heads, int n_kv,
                        int head_dim, int max_seq, int rope, const void *prefetch,
-                       size_t prefetch_bytes)
+                       size_t prefetch_bytes, int64_t *ws_ext, size_t ws_ext_bytes,
+                       unsigned *sync_ext)
 {
     // prefetch blocks: one per compute unit the heads leave idle
     const size_t pf_n16 = prefetch ? prefetch_bytes / 16 : 0;
     const int pf_blocks = pf_n16 ? (c->cu_count > n_heads ? c->cu_count - n_heads : 1) : 0;
     const bool lds = max_seq <= ATT_LDS_MAX;
+    // the workspace: the caller's (allocation-free entry) or the context's
+    auto ws_get = [&](size_t bytes, int64_t **p) -> int {
+        if (ws_ext) {
+            if (bytes > ws_ext_bytes)
+                return Q48_ERANGE;
+            *p = ws_ext;
+            return Q48_OK;
+        }
+        int rc = q48_ws_reserve(c, bytes);
+        *p = (int64_t *)c->ws;
+        return rc;
+    };
+    int64_t *ws = nullptr;
     if (!lds) {
-        int rc = q48_ws_reserve(c, (size_t)n_heads * max_seq * sizeof(int64_t));
+        int rc = ws_get((size_t)n_heads * max_seq * sizeof(int64_t), &ws);
         if (rc)
             return rc;
     }
-    int64_t *ws = (int64_t *)c->ws;
 #define ATT_LAUNCH(R, L)                                                                      \
     hipLaunchKernelGGL((k_attn_v2<R, L>), dim3(n_heads + pf_blocks), dim3(ATT_NT), 0,         \
                        c->stream, out, q, kcache, vcache, k_new, v_new, ws, c->rope_cos,      \
                        c->rope_sin, layer, d_pos, pos, n_heads, n_kv, head_dim, max_seq,      \
                        (const ulonglong2 *)prefetch, pf_n16)
     const int64_t *scale_p = c->rope_sin + (size_t)c->rope_max_seq * (c->rope_head_dim / 2);
-    // long caches: the split kernels (chunks of ATT_CH positions over many
-    // blocks) once the position reaches ATT_SPLIT_MIN; a captured graph
-    // keeps the kernels of the position it was captured at
+    // long caches: split kernels (chunks of positions over many blocks) once
+    // the position reaches ATT_SPLIT_MIN; a captured graph keeps the kernels
+    // of the position it was captured at
     if (rope && pos >= ATT_SPLIT_MIN && (head_dim == 32 || head_dim == 64 || head_dim == 128) &&
-        (max_seq + ATT_CH - 1) / ATT_CH <= ATT_NCMAX && n_heads <= 256) {
+        (max_seq + ATT_CH - 1) / ATT_CH <= ATT_NCMAX && n_heads <= ATTX_MAX_HEADS) {
         const size_t sc_n = (size_t)n_heads * max_seq, cm_n = (size_t)n_heads * ATT_NCMAX;
-        int rc = q48_ws_reserve(c, (sc_n + 2 * cm_n) * sizeof(int64_t));
+        unsigned *sync = ws_ext ? sync_ext : c->attx_sync;
+        if (c->attn_one_launch && sync && attx_fits(c, head_dim, n_heads, max_seq)) {
+            // chunk maxima and sums only
+            int rc = ws_get(2 * cm_n * sizeof(int64_t), &ws);
+            if (rc)
+                return rc;
+            int64_t *cm = ws, *cs = cm + cm_n;
+            int *err = reinterpret_cast<int *>(sync + (size_t)ATTX_MAX_HEADS * ATTX_SYNC);
+            const int ch = head_dim == 128 ? AttxShape<128>::CH : AttxShape<64>::CH;
+            const dim3 grid((max_seq + ch - 1) / ch, n_heads);
+#define ATTX_LAUNCH(HD)                                                                       \
+    hipLaunchKernelGGL((k_attn_x<HD>), grid, dim3(ATTX_NT), 0, c->stream, out, q, kcache,    \
+                       vcache, k_new, v_new, c->rope_cos, c->rope_sin, scale_p, cm, cs, sync, \
+                       err, layer, d_pos, pos, n_heads, n_kv, max_seq)
+            if (head_dim == 64)
+                ATTX_LAUNCH(64);
+            else if (head_dim == 32)
+                ATTX_LAUNCH(32);
+            else
+                ATTX_LAUNCH(128);
+#undef ATTX_LAUNCH
+            return (int)hipGetLastError();
+        }
+        int rc = ws_get(q48_attn_ws_bytes(n_heads, max_seq, head_dim), &ws);
         if (rc)
             return rc;
-        int64_t *sc = (int64_t *)c->ws, *cm = sc + sc_n, *cs = cm + cm_n;
+        int64_t *sc = ws, *cm = sc + sc_n, *cs = cm + cm_n;
         const dim3 grid((max_seq + ATT_CH - 1) / ATT_CH, n_heads);
 #define ATTS_LAUNCH(HD)                                                                       \
     do {                                                                                      \
@@ -981,6 +1329,14 @@ int q48_launch_step_argmax(q48_ctx *c, int *tokens, int cap, const int64_t *v, i
 {
     hipLaunchKernelGGL(k_step_argmax, dim3(1), dim3(1024), 0, c->stream, c->d_step, tokens,
                        cap, v, n);
+    return (int)hipGetLastError();
+}
+
+int q48_launch_step_record(q48_ctx *c, int64_t *rec, int cap, const int64_t *v, int n)
+{
+    const int blocks = (n + 255) / 256 < 256 ? (n + 255) / 256 : 256;
+    hipLaunchKernelGGL(k_step_record, dim3(blocks), dim3(256), 0, c->stream, c->d_step, rec, cap,
+                       v, n);
     return (int)hipGetLastError();
 }
 

@@ -150,7 +150,11 @@ int main(int argc, char **argv)
         double dc = st.decode_tokens ? 1e3 * st.decode_s / st.decode_tokens : 0;
         printf("KPI:prefill_ms_per_tok=%.3f\n", pf);
         printf("KPI:decode_ms_per_tok=%.3f\n", dc);
-        printf("KPI:tok_per_sec=%.2f\n", dc > 0 ? 1e3 / dc : 0.0);
+        /* llama_int.c:283-285: prompt and generated tokens over the whole
+         * generate() time */
+        double gen_s = st.prefill_s + st.decode_s;
+        int gen_tok = st.prefill_tokens + st.decode_tokens;
+        printf("KPI:tok_per_sec=%.2f\n", gen_s > 0 ? gen_tok / gen_s : 0.0);
     }
     free(prompt);
     free(out);

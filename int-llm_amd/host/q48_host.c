@@ -66,6 +66,10 @@ struct q48h_model {
     int batched_prefill;        /* generate's prompt through q48h_prefill (default) */
     int64_t *pf;                /* device: batched-prefill rows (grown on demand) */
     size_t pf_words;
+    int64_t *rec;               /* device: logits of recorded decode steps [rec_cap][vocab] */
+    int rec_cap;
+    int record;                 /* the decode step records its logits into rec */
+    int graph_rec;              /* the captured graph was captured with record on */
 };
 
 /* ---------------------------------------------------------------------- */
@@ -333,6 +337,7 @@ void q48h_model_free(q48h_model *m)
     q48_free(m->ctx, m->d_tokens);
     q48_free(m->ctx, m->d_rng);
     q48_free(m->ctx, m->pf);
+    q48_free(m->ctx, m->rec);
     if (m->graph_ready)
         q48_graph_drop(m->ctx);
     free(m);
@@ -445,7 +450,7 @@ static int step_kind(q48h_model *m, int pos)
     const int split = q48_attn_split_min();
     if (pos >= split)
         return 1;
-    if (m->onelaunch && m->fused == 3 && m->temperature < Q48_ONE / 100 &&
+    if (m->onelaunch && !m->record && m->fused == 3 && m->temperature < Q48_ONE / 100 &&
         split <= q48_step_fused_max_pos()) {
         q48_step_model sm;
         step_model_of(m, &sm);
@@ -1188,6 +1193,8 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
             rc = q48_step_fused_status(x);
     } else if (rc == Q48_OK) {
         rc = enqueue_forward(m, token, pos);
+        if (rc == Q48_OK && m->record)
+            rc = q48_record_step(x, m->logits, m->c.vocab, m->rec, m->rec_cap);
         if (rc == Q48_OK)
             rc = select_token_step(m);
         if (rc == Q48_OK)
@@ -1196,7 +1203,7 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
     /* attention picks its kernels by position (split from q48_attn_split_min)
      * and the one-launch step serves the positions below it: recapture when
      * the step changes kind */
-    if (rc == Q48_OK && m->graph_ready && m->graph_kind != kind) {
+    if (rc == Q48_OK && m->graph_ready && (m->graph_kind != kind || m->graph_rec != m->record)) {
         rc = q48_graph_drop(x);
         m->graph_ready = 0;
     }
@@ -1208,6 +1215,8 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
                 rc1 = q48_step_fused(x, &sm, m->d_tokens, m->c.max_seq);
             } else {
                 rc1 = enqueue_forward(m, token, pos);
+                if (rc1 == Q48_OK && m->record)
+                    rc1 = q48_record_step(x, m->logits, m->c.vocab, m->rec, m->rec_cap);
                 if (rc1 == Q48_OK)
                     rc1 = select_token_step(m);
             }
@@ -1217,6 +1226,7 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
             if (rc == Q48_OK) {
                 m->graph_ready = 1;
                 m->graph_kind = kind;
+                m->graph_rec = m->record;
             }
         }
     }
@@ -1224,8 +1234,25 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
     return rc;
 }
 
-int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
-                      q48h_stats *st)
+/* FNV-1a 64 of the recorded logits of steps [0, k), into hash[0..k). */
+static int hash_recorded(q48h_model *m, int k, uint64_t *hash)
+{
+    const size_t V = (size_t)m->c.vocab;
+    int64_t *buf = (int64_t *)malloc(V * 8);
+    if (!buf)
+        return Q48_ENOMEM;
+    int rc = Q48_OK;
+    for (int i = 0; i < k && rc == Q48_OK; ++i) {
+        rc = q48_memcpy_d2h(m->ctx, buf, m->rec + (size_t)i * V, V * 8);
+        if (rc == Q48_OK)
+            hash[i] = q48s_fnv_i64(FNV_OFF, buf, V);
+    }
+    free(buf);
+    return rc;
+}
+
+static int decode_graph_run(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
+                            uint64_t *step_hash, q48h_stats *st)
 {
     if (!m || !out_tokens || n < 0)
         return Q48_EINVAL;
@@ -1236,6 +1263,21 @@ int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_t
         n = c->max_seq - start_pos;   /* llama_forward's NULL past max_seq */
     if (n <= 0)
         return 0;
+    /* recording: one logits row per step of the longest part below */
+    m->record = step_hash != NULL;
+    if (m->record && m->rec_cap < n) {
+        if (m->graph_ready) {
+            TRY(q48_graph_drop(m->ctx));   /* it holds the old buffer's address */
+            m->graph_ready = 0;
+        }
+        q48_free(m->ctx, m->rec);
+        m->rec = NULL;
+        m->rec_cap = 0;
+        TRY(q48_malloc(m->ctx, (void **)&m->rec, (size_t)n * c->vocab * 8));
+        m->rec_cap = n;
+    }
+    /* dt: the steps on the device, from the first step's launch to the
+     * tokens back on the host (the hashing of recorded logits is not in it) */
     double t0 = now_s();
     TRY(first_step_and_capture(m, token, start_pos));
     /* a graph serves one attention kernel class: a run that crosses the
@@ -1249,20 +1291,45 @@ int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_t
     if (m->graph_kind == 2)
         TRY(q48_step_fused_status(m->ctx));
     TRY(q48_memcpy_d2h(m->ctx, out_tokens, m->d_tokens, (size_t)k * sizeof(int)));
+    double dt = now_s() - t0;
+    if (step_hash)
+        TRY(hash_recorded(m, k, step_hash));
     if (k < n) {
+        t0 = now_s();
         TRY(first_step_and_capture(m, out_tokens[k - 1], B));
         TRY(q48_graph_launch(m->ctx, n - k - 1));
         TRY(q48_memcpy_d2h(m->ctx, out_tokens + k, m->d_tokens, (size_t)(n - k) * sizeof(int)));
+        dt += now_s() - t0;
+        if (step_hash)
+            TRY(hash_recorded(m, n - k, step_hash + k));
     }
-    if (st) {
-        st->decode_s += now_s() - t0;
-        st->decode_tokens += n;
-    }
-    /* generate stops at EOS (llama_int.c:3111): report the steps up to it */
+    /* generate stops at EOS (llama_int.c:3111): the steps up to and
+     * including the one that chose it count; the device replayed the rest */
+    int ran = n;
     for (int i = 0; i < n; ++i)
-        if (out_tokens[i] == LLAMA_EOS)
-            return i + 1;
-    return n;
+        if (out_tokens[i] == LLAMA_EOS) {
+            ran = i + 1;
+            break;
+        }
+    if (st) {
+        st->decode_s += dt;
+        st->decode_tokens += ran;
+    }
+    return ran;
+}
+
+int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
+                      q48h_stats *st)
+{
+    return decode_graph_run(m, token, start_pos, n, out_tokens, NULL, st);
+}
+
+int q48h_decode_graph_hashed(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
+                             uint64_t *step_hash, q48h_stats *st)
+{
+    if (!step_hash)
+        return Q48_EINVAL;
+    return decode_graph_run(m, token, start_pos, n, out_tokens, step_hash, st);
 }
 
 /* ---------------------------------------------------------------------- */

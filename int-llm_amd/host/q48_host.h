@@ -118,7 +118,10 @@ int q48h_prefill(q48h_model *m, const int *tokens, int T, int p0, int64_t *logit
 void q48h_model_set_batched_prefill(q48h_model *m, int on);
 
 /* Greedy decode from an already filled cache: forward(token, start_pos),
- * then n - 1 more steps, stopping after EOS (long-context configuration). */
+ * then n - 1 more steps, stopping after the step that chose EOS
+ * (long-context configuration); out_tokens[i] is the token chosen by step
+ * i, and the return value counts the steps run (q48h_decode_graph's
+ * conventions). */
 int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
                      uint64_t *step_hash, q48h_stats *stats);
 
@@ -163,10 +166,24 @@ int q48h_model_set_sampling(q48h_model *m, int64_t temperature, int top_k, int64
 /* Decode of n steps replayed from a captured graph: step i runs
  * forward(token_i, start_pos + i) and its argmax (or, with sampling set,
  * its sample_token draw) becomes token_{i+1} on the device, with no host
- * round trip between steps.  out_tokens[i] receives the token of step i.  Returns the number of steps up to and including
- * the first EOS (generate stops there, llama_int.c:3111), or n. */
+ * round trip between steps.  out_tokens[i] receives the token CHOSEN by
+ * step i, so an EOS choice appears as the last counted entry (generate's
+ * token list, q48h_generate, leaves it out: llama_int.c:3111).  The device
+ * replays all n steps; the return value, and stats->decode_tokens, count
+ * the steps up to and including the first EOS choice (generate stops
+ * there), or every step.  n is clipped at max_seq (llama_forward's NULL,
+ * llama_int.c:2817-2820, ends generate's loop, :3106).
+ * q48h_decode_from has the same conventions with one forward call per step. */
 int q48h_decode_graph(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
                       q48h_stats *stats);
+
+/* q48h_decode_graph that also records every replayed step's logits on the
+ * device (q48_record_step inside the captured step) and writes their
+ * FNV-1a-64 to step_hash[i] for every replayed step i (all n after the
+ * max_seq clip, EOS or not): the per-step logits hash of the path that the
+ * decode benchmark times. */
+int q48h_decode_graph_hashed(q48h_model *m, int token, int start_pos, int n, int *out_tokens,
+                             uint64_t *step_hash, q48h_stats *stats);
 
 /* Measurement helper: enqueue `reps` times the GEMV launches of one decode
  * token (the four fused projections of every layer and the lm_head, in

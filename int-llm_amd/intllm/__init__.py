@@ -84,6 +84,7 @@ ABI_SIGNATURES = {
     "q48_step_set": [_P, _I, _I],
     "q48_step_get": [_P, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)],
     "q48_argmax_step": [_P, _P, _I, _P, _I],
+    "q48_record_step": [_P, _P, _I, _P, _I],
     "q48_graph_begin": [_P],
     "q48_graph_end": [_P],
     "q48_graph_launch": [_P, _I],
@@ -440,6 +441,8 @@ HOST_SIGNATURES = {
 
     "q48h_gemv_sweep": ([_P, _I, C.POINTER(C.c_int), C.POINTER(C.c_double)], C.c_int),
     "q48h_decode_graph": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(Stats)], C.c_int),
+    "q48h_decode_graph_hashed": ([_P, _I, _I, _I, C.POINTER(C.c_int), C.POINTER(C.c_uint64),
+                                  C.POINTER(Stats)], C.c_int),
     "q48s_fill_named": ([_P, C.c_int64, C.c_int64, C.c_uint64, C.c_char_p, C.c_int64, _I, _I],
                         None),
     "q48s_fnv_i64": ([C.c_uint64, _P, C.c_size_t], C.c_uint64),
@@ -595,6 +598,19 @@ class HostModel:
         k = check("q48h_decode_graph", host_lib().q48h_decode_graph(
             self.h, token, start_pos, n, out, C.byref(st)))
         return list(out[:k]), list(out[:n]), st
+
+    def decode_graph_hashed(self, token: int, start_pos: int, n: int):
+        """decode_graph with every replayed step's logits recorded on the
+        device and hashed: (tokens up to and including the first EOS, all
+        replayed step tokens, their logits FNVs as 16-digit hex, stats)."""
+        out = (C.c_int * max(1, n))()
+        hs = (C.c_uint64 * max(1, n))()
+        st = Stats()
+        k = check("q48h_decode_graph_hashed", host_lib().q48h_decode_graph_hashed(
+            self.h, token, start_pos, n, out, hs, C.byref(st)))
+        ms = self.cfg.max_seq if self.cfg is not None else start_pos + n
+        ran = max(0, min(n, ms - start_pos))
+        return list(out[:k]), list(out[:ran]), ["%016x" % h for h in hs[:ran]], st
 
     def gemv_sweep(self, reps: int):
         """Enqueue the decode GEMV sequence `reps` times: (launches, bytes)."""

@@ -34,6 +34,17 @@ def golden(name: str):
     return json.loads(p.read_text())
 
 
+def bf16_reference():
+    """bfloat16_to_q1648 (safetensors.h:115-152) of all 65536 bit patterns,
+    as the compiled reference computed them (tests/golden/bf16_to_q48.npz)."""
+    import numpy as np
+    meta = golden("bf16_to_q48.json")
+    with np.load(GOLD / meta["file"], allow_pickle=False) as z:
+        v = z["v"]
+    assert v.dtype == np.int64 and v.size == meta["n"] == 65536
+    return v
+
+
 @pytest.fixture(scope="session")
 def oracle():
     import oracle_lib

@@ -265,6 +265,84 @@ def gen_tiny():
         "max_new": 32, "tokens": toks, "step_fnv": hs})
 
 
+def gen_stops():
+    """generate()'s stop branches on the config-1 model (llama_int.c:3067-3135):
+    a decode that chooses EOS (id 2; not appended, :3111), a prompt whose
+    final choice is EOS (appended anyway, :3087-3090, and decoding goes on
+    from it), a run that reaches max_seq (llama_forward returns NULL,
+    :2817-2820, and decode breaks, :3106) and a prompt longer than max_seq
+    (the prefill fails: generate returns -1).  Prompts are searched with
+    the reference itself over prompt seeds SEED_TINY + i."""
+    vocab = spec.TINY[6]
+    cases = []
+
+    def run(cfg_t, prompt, max_new):
+        toks, hs, same, _, _ = run_generate(cfg_t, spec.SEED_TINY, prompt, max_new)
+        assert same, "generate() and the hashed loop disagree"
+        return toks, hs
+
+    cfg = RefCfg(*spec.TINY)
+    m = model(cfg, spec.SEED_TINY)
+    cap = 64
+    out = (C.c_int * cap)()
+    hs = (C.c_uint64 * cap)()
+    n = C.c_int()
+    eos_decode = eos_prompt = None
+    for i in range(1, 20000):
+        if eos_decode is not None and eos_prompt is not None:
+            break
+        prompt = spec.prompt(spec.SEED_TINY + i, 16, vocab)
+        p = (C.c_int * 16)(*prompt)
+        if eos_prompt is None:
+            total = R.q48r_generate(m, p, 16, 1, out, hs, C.byref(n))
+            if total == 17 and out[16] == 2:
+                eos_prompt = i
+        if eos_decode is None:
+            total = R.q48r_generate(m, p, 16, 32, out, hs, C.byref(n))
+            if 17 < total < 48:
+                eos_decode = i
+    R.q48r_model_free(m)
+    assert eos_decode is not None and eos_prompt is not None
+    for name, i, max_new in (("eos_in_decode", eos_decode, 32),
+                             ("eos_as_prompt_choice", eos_prompt, 32)):
+        prompt = spec.prompt(spec.SEED_TINY + i, 16, vocab)
+        toks, h = run(spec.TINY, prompt, max_new)
+        cases.append({"name": name, "config": list(spec.TINY), "prompt_seed": spec.SEED_TINY + i,
+                      "prompt": prompt, "max_new": max_new, "total": len(toks),
+                      "tokens": toks, "step_fnv": h})
+    short = list(spec.TINY)
+    short[7] = 24                       # max_position_embeddings
+    prompt = spec.prompt(spec.SEED_TINY, 16, vocab)
+    toks, h = run(tuple(short), prompt, 32)
+    cases.append({"name": "max_seq", "config": list(short), "prompt_seed": spec.SEED_TINY,
+                  "prompt": prompt, "max_new": 32, "total": len(toks), "tokens": toks,
+                  "step_fnv": h})
+    short[7] = 12
+    cfg = RefCfg(*short)
+    m = model(cfg, spec.SEED_TINY)
+    p = (C.c_int * 16)(*prompt)
+    total = R.q48r_generate_tokens(m, p, 16, 32, out)
+    R.q48r_model_free(m)
+    cases.append({"name": "prompt_past_max_seq", "config": list(short),
+                  "prompt_seed": spec.SEED_TINY, "prompt": prompt, "max_new": 32,
+                  "total": total})
+    write("generate_stops.json", {
+        "source": "generate (llama_int.c:3067-3135) via oracle/ref_harness.c; "
+                  "weights seed SEED_TINY", "seed": spec.SEED_TINY, "cases": cases})
+
+
+def gen_bf16():
+    """bfloat16_to_q1648 (safetensors.h:115-152) of all 65536 bit patterns,
+    as the reference computes it: the values of the normal range follow
+    from the formula; the exponent-255 clamp, shifts of 64 bits or more
+    and left-shift wrap are the reference's conventions."""
+    vals = np.array([R.q48r_bf16_to_q48(b) for b in range(65536)], dtype=np.int64)
+    np.savez_compressed(GOLD / "bf16_to_q48.npz", v=vals)
+    write("bf16_to_q48.json", {
+        "source": "bfloat16_to_q1648 (safetensors.h:115-152) via oracle/ref_harness.c",
+        "file": "bf16_to_q48.npz", "n": 65536, "fnv": fnv(vals)})
+
+
 def gen_tinyllama():
     prompt = spec.prompt(spec.SEED_TL, 32, spec.TINYLLAMA[6])
     toks, hs, _, ts, tg = run_generate(spec.TINYLLAMA, spec.SEED_TL, prompt, 128)

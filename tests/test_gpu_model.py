@@ -134,25 +134,29 @@ def test_long_context_graph_decode_bit_exact(ctx):
     """Config 5 through a graph captured at position 2048 (split attention),
     then a short-context graph decode on the same model: the step graph is
     recaptured whenever attention changes kernels, and both streams match
-    the reference's."""
+    the reference's, tokens and every replayed step's logits hash (all 256
+    config-5 steps)."""
     g = golden("longctx_decode.json")
     m = intllm.HostModel(ctx, intllm.Config(*g["config"]))
     try:
         say("longctx synth + kv fill")
         m.synth(g["seed"], threads())
         m.kv_fill_synth(g["kv_seed"], g["prefill"], threads())
-        say("longctx graph decode")
-        _, toks, _ = m.decode_graph(g["start_token"], g["prefill"], 24)
-        assert toks == g["tokens"][:24]
+        say("longctx graph decode, all", g["steps"], "steps hashed")
+        _, toks, hs, _ = m.decode_graph_hashed(g["start_token"], g["prefill"], g["steps"])
+        assert toks == g["tokens"]
+        assert hs == g["step_fnv"]
         # back to the start of the cache: the graph drops back to one-block attention
         gt = golden("tinyllama_generate.json")
         assert gt["seed"] == g["seed"]
         for pos, tok in enumerate(gt["prompt"]):
             nxt, _ = m.forward(tok, pos, spec.TINYLLAMA[6], logits=False)
         say("short graph decode after long")
-        _, toks2, _ = m.decode_graph(nxt, len(gt["prompt"]), 8)
-        ref = gt["tokens"][len(gt["prompt"]):]
+        P = len(gt["prompt"])
+        _, toks2, hs2, _ = m.decode_graph_hashed(nxt, P, 8)
+        ref = gt["tokens"][P:]
         assert [nxt] + toks2[:7] == ref[:8]
+        assert hs2 == gt["step_fnv"][P:P + 8]
     finally:
         m.free()
 
@@ -241,7 +245,8 @@ def test_tiny_graph_decode_replays(ctx):
         tok, pos, got = nxt, len(prompt), [nxt]
         for chunk in (5, 9, 10):
             say("graph decode chunk", chunk, "from pos", pos)
-            _, steps, _ = m.decode_graph(tok, pos, chunk)
+            _, steps, hs, _ = m.decode_graph_hashed(tok, pos, chunk)
+            assert hs == g["step_fnv"][pos:pos + chunk]
             got += steps
             tok, pos = steps[-1], pos + chunk
             ctx.sync()
@@ -265,9 +270,11 @@ def test_tinyllama_graph_decode_bit_exact(ctx):
         m.synth(g["seed"], threads())
         for pos, tok in enumerate(prompt):
             nxt, _ = m.forward(tok, pos, spec.TINYLLAMA[6], logits=False)
-        say("tinyllama graph decode")
-        toks, steps, st = m.decode_graph(nxt, len(prompt), g["max_new"] - 1)
-        assert [nxt] + toks[:len(ref) - len(prompt) - 1] == ref[len(prompt):]
+        say("tinyllama graph decode, every step hashed")
+        P = len(prompt)
+        toks, steps, hs, st = m.decode_graph_hashed(nxt, P, g["max_new"] - 1)
+        assert [nxt] + toks[:len(ref) - P - 1] == ref[P:]
+        assert hs == g["step_fnv"][P:]
         print(f"graph decode {1e3 * st.decode_s / max(1, st.decode_tokens):.3f} ms/tok", flush=True)
     finally:
         m.free()
@@ -290,9 +297,11 @@ def test_tinyllama_bf16_weights_bit_exact(ctx):
         prompt, ref = g["prompt"], g["tokens"]
         for pos, tok in enumerate(prompt):
             nxt, _ = m.forward(tok, pos, spec.TINYLLAMA[6], logits=False)
-        say("tinyllama bf16 graph decode")
-        toks2, _, _ = m.decode_graph(nxt, len(prompt), 32)
-        assert [nxt] + toks2[:31] == ref[len(prompt):len(prompt) + 32]
+        say("tinyllama bf16 graph decode, every step hashed")
+        P = len(prompt)
+        toks2, _, hs2, _ = m.decode_graph_hashed(nxt, P, 32)
+        assert [nxt] + toks2[:31] == ref[P:P + 32]
+        assert hs2 == g["step_fnv"][P:P + 32]
     finally:
         m.free()
 

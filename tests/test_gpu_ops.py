@@ -12,7 +12,7 @@ import pytest
 import intllm
 import oracle_lib as O
 import spec
-from conftest import golden
+from conftest import bf16_reference, golden
 
 pytestmark = pytest.mark.gpu
 ONE = spec.ONE
@@ -739,12 +739,14 @@ def test_gemv_residual_stats(ctx, oracle, M, K):
 # ---- bfloat16-resident weights ----------------------------------------------
 
 def _bf16_values(oracle, bits):
-    return np.array([oracle.q48s_bf16_to_q48(int(b)) for b in bits], dtype=np.int64)
+    """bfloat16_to_q1648 of each pattern, from the compiled reference's
+    table of all 65536 (tests/golden/bf16_to_q48.npz)."""
+    return bf16_reference()[np.asarray(bits, dtype=np.uint16).astype(np.int64)]
 
 
 def test_bf16_pack_every_pattern(ctx, oracle):
-    """Every one of the 65536 bfloat16 patterns, converted by the reference
-    rule (safetensors.h:115-152), packs back to bits that convert to the same
+    """Every one of the 65536 bfloat16 patterns, converted as the compiled
+    reference converts it (safetensors.h:115-152), packs back to bits that convert to the same
     int64; a value with more than 8 significant bits is reported inexact."""
     bits = np.arange(1 << 16, dtype=np.uint16)
     vals = _bf16_values(oracle, bits)

@@ -16,7 +16,7 @@ import numpy as np
 
 import oracle_lib as O
 import spec
-from conftest import golden
+from conftest import bf16_reference, golden
 
 ONE = spec.ONE
 SUB_ORDER = ["fp_mul", "fp_div", "fp_sqrt", "fp_sqrt_fast", "fp_inv_sqrt", "fp_exp", "fp_log",
@@ -131,6 +131,19 @@ def test_math_identities(oracle):
         # dyadic (1 + x/2^14)^(2^14): relative error ~ x^2 / 2^15
         t = v / ONE
         assert abs(oracle.q48o_fp_exp(v) / ONE / math.exp(t) - 1) < t * t / 2 ** 14 + 1e-9
+
+
+def test_bf16_conversion_equals_reference_every_pattern(oracle):
+    """The host's conversion (q48s_bf16_to_q48, used by the synthetic models
+    and as the checker of the device expansion) equals the compiled
+    reference's bfloat16_to_q1648 on all 65536 patterns: zero and subnormal
+    exponents, the exponent-255 clamp, shifts of 64 bits or more and wrapping
+    left shifts included."""
+    want = bf16_reference()
+    assert O.fnv(want) == golden("bf16_to_q48.json")["fnv"]
+    got = np.array([oracle.q48s_bf16_to_q48(b) for b in range(1 << 16)], dtype=np.int64)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [hex(int(b)) for b in bad[:8]]
 
 
 def test_bf16_conversion(oracle):
