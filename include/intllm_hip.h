@@ -181,6 +181,17 @@ int q48_attn_decode_rope(q48_ctx *ctx, int64_t *out, const int64_t *q,
  * step mode: a graph captured below this position keeps the one-block
  * kernels as replays move past it (same bits, slower). */
 int q48_attn_split_min(void);
+/* Split attention as ONE launch (on: the default), whose chunk blocks hand
+ * the softmax's global max and sum to each other at two barriers inside the
+ * kernel, or as three launches (off).  Same bits either way.  The one-launch
+ * form serves a cache whose blocks (heads x chunks of max_seq) can all be
+ * resident at once; otherwise the three launches run.  No reference
+ * counterpart: a scheduling choice of this library. */
+int q48_set_attn_one_launch(q48_ctx *ctx, int on);
+/* Synchronises; Q48_ETIMEOUT if a one-launch split attention could not
+ * finish (a block waited past its bound: blocks were not all resident; its
+ * barrier words are then cleared), else Q48_OK. */
+int q48_attn_status(q48_ctx *ctx);
 
 /* Long normed GEMVs (more than two rounds of 8-row groups: gate|up, lm_head)
  * run as persistent blocks that loop over row groups (on: the default), or

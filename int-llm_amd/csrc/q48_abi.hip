@@ -100,7 +100,7 @@ int q48_ctx_create(q48_ctx **out, int device)
         delete c;
         return Q48_EHIP;
     }
-    c->attn_one_launch = 0;
+    c->attn_one_launch = 1;
     c->attx_per_cu[0] = c->attx_per_cu[1] = c->attx_per_cu[2] = -1;
     if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
         hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess ||
@@ -619,7 +619,7 @@ int q48_attn_status(q48_ctx *c)
         return Q48_EINVAL;
     if (c->capturing)
         return Q48_ESTATE;
-    const size_t off = q48_attn_sync_bytes() - 16 * sizeof(unsigned);
+    const size_t off = q48_attn_sync_bytes() - 16 * sizeof(unsigned);   // the error word
     int e[2] = {0, 0};
     if (hipStreamSynchronize(c->stream) != hipSuccess ||
         hipMemcpy(&e[0], (char *)c->attx_sync + off, sizeof(int), hipMemcpyDeviceToHost) !=

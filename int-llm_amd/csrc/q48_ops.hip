@@ -662,265 +662,325 @@ __global__ __launch_bounds__(256) void k_attn_s2(int64_t *__restrict__ out,
 }
 
 // ---------------------------------------------------------------------------
-// One-launch split attention (k_attn_x): the same (chunk, head) blocks as
-// k_attn_s1/se/s2, but the chunk maxima and the chunk sums are handed from
-// block to block inside the kernel: the blocks of a head meet at two
-// barriers (the global max before any exponential, the global sum before
-// any division, as the reference's softmax needs, llama_int.c:1060-1072)
-// instead of at kernel boundaries.  Per block:
-//  1. the keys of the chunk (all loads issued at once), RoPE of q_h and the
-//     new k (llama_int.c:1392-1395; the KV store at pos by the chunk's first
-//     query head of the KV head), the scores into LDS and their maximum;
-//  2. barrier 1 over the head's chunk maxima; the values of the chunk are
-//     loaded while the exponentials e_t = fp_safe_exp(s_t - max) run, one
-//     position per thread, and the chunk's int64 (wrapping) sum;
-//  3. barrier 2 over the chunk sums (the chunk-0 block zeroes out[h] before
-//     it); p_t = fp_div(e_t, sum) when sum > 0, and sum_t fp_mul(p_t,
-//     v_t[d]) over the chunk added into out[h][d] with 64-bit atomic adds
-//     (int64 wrapping sums in any order: the bits of llama_int.c:1514-1529).
-// A head with one chunk skips both barriers and stores out[h] directly.
+// One-launch split attention (k_attn_g).  One block per (chunk of ATTG_CH
+// positions, KV head) serves every query head of the KV head's group
+// (llama_int.c:1506, kv_h = h / gqa_group), so each key and value row is
+// read from memory once per launch, not once per query head.  The chunk
+// blocks of a KV head hand the softmax's global max and global sum to each
+// other at two exchanges inside the kernel (the reference's softmax needs
+// the max before any exponential and the sum before any division,
+// llama_int.c:1060-1072).  Per block:
+//  1. the chunk's key and value rows and the RoPE inputs are loaded at once;
+//     RoPE of the group's q heads and of the new k (llama_int.c:1392-1395);
+//     the KV store at pos by the chunk that holds it (llama_int.c:1414-1416);
+//     keys and values go to LDS (the row at pos replaced by the block's own
+//     rotated k and new v); the score of each (query head, position), two
+//     threads per score, s_t = fp_mul((sum_d q_d k_t,d) >> 48, scale)
+//     (llama_int.c:1502-1512), and the chunk maximum per head;
+//  2. exchange 1 of the chunk maxima; e_t = fp_safe_exp(s_t - max), one per
+//     thread, and the chunk's int64 (wrapping) sum per head;
+//  3. exchange 2 of the chunk sums; p_t = fp_div(e_t, sum) when sum > 0;
+//     each thread owns one output (head, d) of the group and adds
+//     sum_t fp_mul(p_t, v_t[d]) over the chunk into out with a 64-bit atomic
+//     add (int64 wrapping sums in any order: the bits of
+//     llama_int.c:1514-1529); the chunk-0 block zeroes the group's output at
+//     its start, long before any block adds.
+// A cache of one chunk skips the exchanges and stores out directly.
 //
-// Barriers: a count and a generation word per head (64 bytes apart).  A
-// block reads the generation, waits for its own coherent stores, adds 1 to
-// the count; the last of the head's nc blocks sets the count back to 0 and
-// then bumps the generation, which the others poll.  Every barrier thus
-// leaves count = 0 behind, so the next launch (graph replays included)
-// starts clean; the generation only ever grows.  Every wait is bounded by
-// the wall clock: a block that waits longer than ATTX_TIMEOUT, or sees
-// another block's timeout, sets *err and leaves (the host sizes the grid
-// so that every active block is resident at once).  Data crossing blocks
-// (chunk maxima and sums, the zeroed output) goes out with agent-coherent
-// stores whose completion is awaited before the count add, and is read with
-// agent-coherent loads.
-// Blocks whose chunk starts past pos exit at once (the grid covers max_seq,
-// so a captured graph stays valid as pos grows).
+// Exchanges (no atomics, no separate flags).  Every published int64 goes out
+// as two 64-bit words (low half, epoch) and (high half, epoch): a 64-bit
+// store is seen whole or not at all, so a reader that finds the expected
+// epoch in a word also finds its half.  Per KV head an epoch word E is read
+// at the start; the block's values go out with epoch E + 1 and the readers
+// poll the words of all nc chunks until each carries E + 1.  After the second
+// exchange the chunk-0 block stores E + 1 into the epoch (the next launch
+// then expects E + 2, which no word of this launch carries).  A wait longer
+// than ATTG_TIMEOUT ends the block (and sets the error word, for
+// q48_attn_status); the host sizes the grid so that every active block is
+// resident at once.  Blocks whose chunk starts past pos exit at once (the
+// grid covers max_seq, so a captured graph stays valid as pos grows).
 // ---------------------------------------------------------------------------
-constexpr int ATTX_NT = 256;
-constexpr int ATTX_SYNC = 16;                     // uints per head: count, generation
-constexpr int ATTX_MAX_HEADS = 256;
-constexpr uint64_t ATTX_TIMEOUT = 1ull << 24;     // wall-clock ticks (0.17 s at 100 MHz)
+constexpr int ATTG_NT = 512;
+constexpr int ATTG_CH = 32;                       // positions per chunk
+constexpr int ATTG_NCMAX = 256;                   // chunks per KV head: max_seq <= 8192
+constexpr int ATTG_GMAX = 8;                      // query heads per KV head
+constexpr uint64_t ATTG_TIMEOUT = 1ull << 24;     // wall-clock ticks (0.17 s at 100 MHz)
+constexpr int ATTG_KVMAX = 16;                    // KV heads
+// words (uint64) of one exchange per KV head and chunk: (half, epoch) x 2 per head
+constexpr int ATTG_XW = 2 * ATTG_GMAX;
+// the exchange region: uint64 words [2 exchanges][ATTG_KVMAX][ATTG_NCMAX]
+// [ATTG_XW], then uint32 epochs [ATTG_KVMAX] 16 apart and the error word;
+// zero before the first launch, never cleared after: a word counts only
+// when it carries the current launch's epoch
+constexpr size_t ATTG_XWORDS = (size_t)2 * ATTG_KVMAX * ATTG_NCMAX * ATTG_XW;
+constexpr size_t ATTG_SYNC_BYTES = ATTG_XWORDS * 8 + ((size_t)ATTG_KVMAX * 16 + 16) * 4;
 
-template <int HD>
-struct AttxShape {
-    static constexpr int CH = HD == 128 ? 128 : 256;   // positions per chunk
-    static constexpr int NG = ATTX_NT / 8;             // positions per pass
-    static constexpr int NP = CH / NG;                 // passes per chunk
-    static constexpr int DP2 = HD / 16;                // 16-byte loads per lane and row
-};
-
-__device__ __forceinline__ unsigned attx_ld(const unsigned *p)
+__device__ __forceinline__ uint64_t attg_ld64(const uint64_t *p)
 {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Block-wide barrier of the n blocks of one head; false on every thread
-// when this or another block timed out.
-__device__ bool attx_barrier(unsigned *sync, unsigned n, int *err)
+__device__ __forceinline__ void attg_st64(uint64_t *p, uint64_t v)
 {
-    __builtin_amdgcn_s_waitcnt(0);   // this thread's coherent stores are done
-    int ok = 1;
-    if (__syncthreads_and(1) && threadIdx.x == 0) {
-        unsigned *count = sync, *gen = sync + 1;
-        const unsigned g = attx_ld(gen);
-        if (__hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            n - 1) {
-            __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
-            __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            const uint64_t t0 = wall_clock64();
-            while (attx_ld(gen) == g) {
-                if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                    ok = 0;
-                    break;
-                }
-                if (wall_clock64() - t0 > ATTX_TIMEOUT) {
-                    __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    ok = 0;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-    }
-    return __syncthreads_and(ok) != 0;
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Publish v[0..G) (thread hh < G publishes v for head hh) as epoch-tagged
+// halves into row `mine`, then gather, for every head hh < G, the values of
+// all nc chunks (rows xw + ATTG_XW c) into got[hh][c] (LDS).  Block-wide;
+// false on every thread after a timeout.
+template <int NT>
+__device__ bool attg_exchange(uint64_t *xw, int c, int nc, int G, unsigned epoch,
+                              const int64_t *v, int64_t (*got)[ATTG_NCMAX], int *err)
+{
+    const int tid = threadIdx.x;
+    if (tid < G) {
+        const uint64_t u = (uint64_t)v[tid];
+        attg_st64(xw + (size_t)ATTG_XW * c + 2 * tid, (u << 32) | epoch);
+        attg_st64(xw + (size_t)ATTG_XW * c + 2 * tid + 1, (u & 0xFFFFFFFF00000000ull) | epoch);
+    }
+    // every thread reads words (chunk, head, half) = i, i + NT, ... of nc x 2G
+    const int nw = nc * 2 * G;
+    const uint64_t t0 = wall_clock64();
+    int ok = 1;
+    for (;;) {
+        bool mine = true;
+        for (int i = tid; i < nw; i += NT) {
+            const int cc = i / (2 * G), r = i % (2 * G);
+            const uint64_t w = attg_ld64(xw + (size_t)ATTG_XW * cc + r);
+            if ((unsigned)w != epoch) {
+                mine = false;
+            } else {
+                // halves: word 2 hh carries bits 0..31 in its top, 2 hh + 1 bits 32..63
+                uint32_t *g32 = reinterpret_cast<uint32_t *>(&got[r >> 1][cc]);
+                g32[r & 1] = (uint32_t)(w >> 32);
+            }
+        }
+        if (__syncthreads_and(mine))
+            break;
+        // the give-up decision is thread 0's clock, made uniform by the OR
+        if (__syncthreads_or(tid == 0 && wall_clock64() - t0 > ATTG_TIMEOUT)) {
+            if (tid == 0)
+                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = 0;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __syncthreads();   // got[] complete (or abandoned) for every thread
+    return ok != 0;
+}
+
+// at most 128 VGPRs: two blocks (16 waves) fit a compute unit, so that the
+// grid of a 4096-position cache with 4 KV heads (512 blocks) is resident
 template <int HD>
-__global__ __launch_bounds__(ATTX_NT) void k_attn_x(
+__global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(4))) void k_attn_g(
     int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
     int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
     const int64_t *__restrict__ v_new, const int64_t *__restrict__ cos_t,
     const int64_t *__restrict__ sin_t, const int64_t *__restrict__ scale_p,
-    int64_t *__restrict__ cmax, int64_t *__restrict__ csum, unsigned *__restrict__ sync,
-    int *__restrict__ err, int layer, const int *__restrict__ d_pos, int pos, int n_heads,
-    int n_kv, int max_seq)
+    uint64_t *__restrict__ xbuf, int layer, const int *__restrict__ d_pos, int pos,
+    int n_heads, int n_kv, int max_seq)
 {
-    using SH = AttxShape<HD>;
-    constexpr int NT = ATTX_NT, CH = SH::CH, NG = SH::NG, NP = SH::NP, DP2 = SH::DP2;
-    constexpr int DPL = HD / 8;
-    __shared__ int64_t qs[HD], ks[HD], vs[HD];
-    __shared__ int64_t red[NT / 64], red2[NT / 64];
-    __shared__ int64_t sc[CH];
-    __shared__ uint64_t part[NG][HD + 1];
+    constexpr int NT = ATTG_NT, CH = ATTG_CH, GM = ATTG_GMAX;
+    constexpr int HALF = HD / 2, RS = HD + 1;
+    constexpr int RP = (GM * HALF + NT - 1) / NT;       // RoPE pairs per thread
+    constexpr int LW = CH * HD / NT;                    // row words per thread
+    constexpr int NO = (GM * HD + NT - 1) / NT;         // outputs per thread
+    constexpr int DH = HD / 2;                          // dims per score thread
+    static_assert(LW % 2 == 0 && HD % LW == 0, "16-byte row loads");
+    static_assert(GM * CH * 2 == NT, "two threads per score");
+    __shared__ int64_t qs[GM][HD];
+    __shared__ int64_t ks[HD], vs[HD];
+    __shared__ int64_t kl[CH][RS], vl[CH][RS];           // odd row stride: no bank conflicts
+    __shared__ int64_t sc[GM][CH];
+    __shared__ q48_u128 dpart[GM * CH];
+    __shared__ int64_t loc[GM];
+    __shared__ int64_t got[GM][ATTG_NCMAX];
     if (d_pos)
         pos = *d_pos;
     if (pos < 0 || pos >= max_seq)
         return;
-    const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int c = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
     const int S = pos + 1, t0 = c * CH;
     if (t0 >= S)
         return;   // uniform: no barrier is skipped by part of the block
-    const int nc = (S + CH - 1) / CH;
-    const int tend = min(t0 + CH, S);
-    const int group = n_heads / n_kv, kh = h / group;
+    const int nc = (S + CH - 1) / CH, tend = min(t0 + CH, S), nt = tend - t0;
+    const int G = n_heads / n_kv, h0 = kh * G;
     const size_t kvd = (size_t)n_kv * HD;
     const size_t base = (size_t)layer * max_seq;
-    const int half = HD / 2;
-    const int g = tid >> 3, l8 = tid & 7;
-    const int64_t scale = *scale_p;
+    uint64_t *xw1 = xbuf + (size_t)kh * ATTG_NCMAX * ATTG_XW;
+    uint64_t *xw2 = xw1 + (size_t)ATTG_KVMAX * ATTG_NCMAX * ATTG_XW;
+    unsigned *sync = reinterpret_cast<unsigned *>(xbuf + ATTG_XWORDS);
+    unsigned *ep = sync + (size_t)kh * 16;
+    int *err = reinterpret_cast<int *>(sync + (size_t)ATTG_KVMAX * 16);
 
-    // RoPE inputs and the new v first, then every key row of the chunk
-    const int64_t *qh = q + (size_t)h * HD, *kn = k_new + (size_t)kh * HD;
-    const int i = min(tid, half - 1), j = min(tid, HD - 1);
-    int64_t cs = cos_t[(size_t)pos * half + i];
-    int64_t sn = sin_t[(size_t)pos * half + i];
-    int64_t q0 = qh[i], q1 = qh[i + half];
-    int64_t k0 = kn[i], k1 = kn[i + half];
-    int64_t vn = v_new[(size_t)kh * HD + j];
-    __builtin_amdgcn_sched_barrier(0);
-    const int64_t *kb0 = kcache + base * kvd + (size_t)kh * HD + l8 * DPL;
-    const int64_t *vb0 = vcache + base * kvd + (size_t)kh * HD + l8 * DPL;
-    auto row = [&](const int64_t *b, int t) {
-        return reinterpret_cast<const ulonglong2 *>(b + (size_t)min(t, tend - 1) * kvd);
-    };
-    ulonglong2 kr[NP][DP2];
+    // loads: the epoch and the RoPE inputs first, then the chunk's rows
+    const unsigned E = nc > 1 ? __hip_atomic_load(ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : 0u;
+    int64_t cs[RP], sn[RP], q0[RP], q1[RP];
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int d = 0; d < DP2; ++d)
-            kr[p][d] = row(kb0, t0 + p * NG + g)[d];
+    for (int r = 0; r < RP; ++r) {
+        const int idx = min(tid + r * NT, G * HALF - 1);
+        const int hh = idx / HALF, i = idx % HALF;
+        cs[r] = cos_t[(size_t)pos * HALF + i];
+        sn[r] = sin_t[(size_t)pos * HALF + i];
+        q0[r] = q[(size_t)(h0 + hh) * HD + i];
+        q1[r] = q[(size_t)(h0 + hh) * HD + i + HALF];
+    }
+    const int ik = min(tid, HALF - 1), jv = min(tid, HD - 1);
+    int64_t kc0 = cos_t[(size_t)pos * HALF + ik], ks0 = sin_t[(size_t)pos * HALF + ik];
+    int64_t k0 = k_new[(size_t)kh * HD + ik], k1 = k_new[(size_t)kh * HD + ik + HALF];
+    int64_t vn = v_new[(size_t)kh * HD + jv];
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" : "+v"(cs), "+v"(sn), "+v"(q0), "+v"(q1), "+v"(k0), "+v"(k1), "+v"(vn));
-    qs[i] = (int64_t)((uint64_t)q48_mul(q0, cs) - (uint64_t)q48_mul(q1, sn));
-    qs[i + half] = (int64_t)((uint64_t)q48_mul(q1, cs) + (uint64_t)q48_mul(q0, sn));
-    ks[i] = (int64_t)((uint64_t)q48_mul(k0, cs) - (uint64_t)q48_mul(k1, sn));
-    ks[i + half] = (int64_t)((uint64_t)q48_mul(k1, cs) + (uint64_t)q48_mul(k0, sn));
-    vs[j] = vn;
+    // row words: thread tid holds LW consecutive words of row tid / (HD / LW)
+    const int rr = tid / (HD / LW), rw = (tid % (HD / LW)) * LW;
+    const int tr = min(t0 + rr, tend - 1);
+    const ulonglong2 *krow = reinterpret_cast<const ulonglong2 *>(
+        kcache + (base + tr) * kvd + (size_t)kh * HD + rw);
+    const ulonglong2 *vrow = reinterpret_cast<const ulonglong2 *>(
+        vcache + (base + tr) * kvd + (size_t)kh * HD + rw);
+    ulonglong2 kr[LW / 2], vr[LW / 2];
+#pragma unroll
+    for (int d = 0; d < LW / 2; ++d)
+        kr[d] = krow[d];
+#pragma unroll
+    for (int d = 0; d < LW / 2; ++d)
+        vr[d] = vrow[d];
+    __builtin_amdgcn_sched_barrier(0);
+    if (c == 0 && nc > 1)   // the group's output starts at zero (atomic adds below)
+#pragma unroll
+        for (int o = 0; o < NO; ++o)
+            if (tid + o * NT < G * HD)
+                __hip_atomic_store(out + (size_t)h0 * HD + tid + o * NT, (int64_t)0,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // RoPE (rope_apply, llama_int.c:997-1008): the group's q heads, the new k
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+        const int idx = tid + r * NT;
+        if (idx < G * HALF) {
+            const int hh = idx / HALF, i = idx % HALF;
+            qs[hh][i] = (int64_t)((uint64_t)q48_mul(q0[r], cs[r]) - (uint64_t)q48_mul(q1[r], sn[r]));
+            qs[hh][i + HALF] =
+                (int64_t)((uint64_t)q48_mul(q1[r], cs[r]) + (uint64_t)q48_mul(q0[r], sn[r]));
+        }
+    }
+    if (tid < HALF) {
+        ks[tid] = (int64_t)((uint64_t)q48_mul(k0, kc0) - (uint64_t)q48_mul(k1, ks0));
+        ks[tid + HALF] = (int64_t)((uint64_t)q48_mul(k1, kc0) + (uint64_t)q48_mul(k0, ks0));
+    }
+    if (tid < HD)
+        vs[tid] = vn;
+#pragma unroll
+    for (int d = 0; d < LW / 2; ++d) {
+        kl[rr][rw + 2 * d] = (int64_t)kr[d].x;
+        kl[rr][rw + 2 * d + 1] = (int64_t)kr[d].y;
+        vl[rr][rw + 2 * d] = (int64_t)vr[d].x;
+        vl[rr][rw + 2 * d + 1] = (int64_t)vr[d].y;
+    }
     __syncthreads();
-    if (h % group == 0 && c == pos / CH && tid < HD) {
+    if (pos < tend && tid < HD) {   // the row at pos: this block's rotated k, new v
+        kl[pos - t0][tid] = ks[tid];
+        vl[pos - t0][tid] = vs[tid];
         kcache[(base + pos) * kvd + (size_t)kh * HD + tid] = ks[tid];
         vcache[(base + pos) * kvd + (size_t)kh * HD + tid] = vs[tid];
     }
+    __syncthreads();
 
-    // scores s_t = fp_mul((sum_d q_d k_t,d) >> 48, scale), llama_int.c:1502-1512;
-    // the row at pos is the block's own rotated k
-    const int64_t *qd = qs + l8 * DPL, *kd = ks + l8 * DPL;
-    int64_t mx = INT64_MIN;
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        const int t = t0 + p * NG + g;
-        const bool own = t == pos;
-        q48_u128 dot = 0;
-#pragma unroll
-        for (int d = 0; d < DP2; ++d) {
-            const int64_t a0 = own ? kd[2 * d] : (int64_t)kr[p][d].x;
-            const int64_t a1 = own ? kd[2 * d + 1] : (int64_t)kr[p][d].y;
-            dot += (q48_u128)q48_smul128(qd[2 * d], a0);
-            dot += (q48_u128)q48_smul128(qd[2 * d + 1], a1);
-        }
-        dot = q48_sum8_u128(dot);
-        if (t < tend && l8 == 0) {
-            const int64_t sv = q48_mul((int64_t)((q48_i128)dot >> 48), scale);
-            sc[t - t0] = sv;
-            mx = sv > mx ? sv : mx;
-        }
+    // scores: pair p = (head hh, position t) = tid % (GM CH), dims half tid / (GM CH)
+    const int pi = tid % (GM * CH), hh = pi / CH, t = pi % CH, dh = tid / (GM * CH);
+    const bool live = hh < G && t < nt;
+    q48_u128 dot = 0;
+    if (hh < G) {
+        const int64_t *qa = qs[hh] + dh * DH, *ka = kl[t] + dh * DH;
+#pragma unroll 8
+        for (int d = 0; d < DH; ++d)
+            dot += (q48_u128)q48_smul128(qa[d], ka[d]);
     }
-    mx = block_max64<NT>(mx, red, false);
-
-    // the value rows of the chunk, in flight through the max exchange and
-    // the exponentials (the key registers are free again)
-#pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int d = 0; d < DP2; ++d)
-            kr[p][d] = row(vb0, t0 + p * NG + g)[d];
-
-    unsigned *hs = sync + (size_t)h * ATTX_SYNC;
-    int64_t *cmh = cmax + (size_t)h * ATT_NCMAX, *csh = csum + (size_t)h * ATT_NCMAX;
+    if (dh == 1)
+        dpart[pi] = dot;
+    __syncthreads();
+    if (dh == 0 && hh < G) {
+        dot += dpart[pi];
+        sc[hh][t] = live ? q48_mul((int64_t)((q48_i128)dot >> 48), *scale_p) : INT64_MIN;
+    }
+    __syncthreads();
+    if (tid < G) {
+        int64_t m = INT64_MIN;
+        for (int u = 0; u < nt; ++u)
+            m = sc[tid][u] > m ? sc[tid][u] : m;
+        loc[tid] = m;
+    }
+    __syncthreads();
     if (nc > 1) {
-        if (tid == 0)
-            __hip_atomic_store(cmh + c, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (!attx_barrier(hs, nc, err))
+        __builtin_amdgcn_s_waitcnt(0);   // chunk 0: the output zeroes are out
+        if (!attg_exchange<NT>(xw1, c, nc, G, E + 1, loc, got, err)) {
+            if (tid == 0)
+                __hip_atomic_store(ep, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
-        int64_t m2 = tid < nc ? __hip_atomic_load(cmh + tid, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT)
-                              : INT64_MIN;
-        mx = block_max64<NT>(m2, red2, false);
+        }
+        if (tid < G) {
+            int64_t m = INT64_MIN;
+            for (int u = 0; u < nc; ++u)
+                m = got[tid][u] > m ? got[tid][u] : m;
+            loc[tid] = m;
+        }
+        __syncthreads();
     }
 
-    // e_t = fp_safe_exp(s_t - max), one position per thread, and the chunk sum
-    int64_t e = 0;
-    for (int t = tid; t < tend - t0; t += NT) {
-        const int64_t ev = q48_safe_exp((int64_t)((uint64_t)sc[t] - (uint64_t)mx));
-        sc[t] = ev;
-        e = (int64_t)((uint64_t)e + (uint64_t)ev);
+    // e_t = fp_safe_exp(s_t - max), one per thread, and the chunk sums
+    if (dh == 0 && hh < G)
+        sc[hh][t] = live ? q48_safe_exp((int64_t)((uint64_t)sc[hh][t] - (uint64_t)loc[hh])) : 0;
+    __syncthreads();
+    if (tid < G) {
+        uint64_t sm = 0;
+        for (int u = 0; u < nt; ++u)
+            sm += (uint64_t)sc[tid][u];
+        loc[tid] = (int64_t)sm;
     }
-    int64_t sum = block_sum64<NT>(e, red, true);
+    __syncthreads();
     if (nc > 1) {
-        if (tid == 0)
-            __hip_atomic_store(csh + c, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (c == 0 && tid < HD)
-            __hip_atomic_store(out + (size_t)h * HD + tid, (int64_t)0, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        if (!attx_barrier(hs, nc, err))
+        if (!attg_exchange<NT>(xw2, c, nc, G, E + 1, loc, got, err)) {
+            if (tid == 0)
+                __hip_atomic_store(ep, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
-        const int64_t s2 = tid < nc ? __hip_atomic_load(csh + tid, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT)
-                                    : 0;
-        sum = block_sum64<NT>(s2, red2, true);
+        }
+        if (tid < G) {
+            uint64_t sm = 0;
+            for (int u = 0; u < nc; ++u)
+                sm += (uint64_t)got[tid][u];
+            loc[tid] = (int64_t)sm;
+        }
+        if (c == 0 && tid == 0)   // every block of the head is past exchange 2
+            __hip_atomic_store(ep, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
     }
     // p_t = fp_div(e_t, sum) when sum > 0 (llama_int.c:1069-1071)
-    if (sum > 0)
-        for (int t = tid; t < tend - t0; t += NT)
-            sc[t] = q48_div(sc[t], sum);
+    if (dh == 0 && live) {
+        const int64_t sum = loc[hh];
+        if (sum > 0)
+            sc[hh][t] = q48_div(sc[hh][t], sum);
+    }
     __syncthreads();
 
-    // o[d] += fp_mul(p_t, v_t[d]) over the chunk: lane l8 of group g holds
-    // dims [l8 DPL, +DPL) of positions t0 + g + NG p
-    uint64_t acc[DPL];
+    // o[h][d] += sum_t fp_mul(p_t, v_t[d]) over the chunk: thread owns the
+    // outputs tid + NT o of the group's [G][HD]
 #pragma unroll
-    for (int d = 0; d < DPL; ++d)
-        acc[d] = 0;
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        const int t = t0 + p * NG + g;
-        if (t < tend) {
-            const int64_t pt = sc[t - t0];
-            const bool own = t == pos;
-#pragma unroll
-            for (int d = 0; d < DP2; ++d) {
-                const int64_t a0 = own ? vs[l8 * DPL + 2 * d] : (int64_t)kr[p][d].x;
-                const int64_t a1 = own ? vs[l8 * DPL + 2 * d + 1] : (int64_t)kr[p][d].y;
-                acc[2 * d] += (uint64_t)q48_mul(pt, a0);
-                acc[2 * d + 1] += (uint64_t)q48_mul(pt, a1);
-            }
+    for (int o = 0; o < NO; ++o) {
+        const int oi = tid + o * NT;
+        if (oi < G * HD) {
+            const int oh = oi / HD, d = oi % HD;
+            uint64_t acc = 0;
+            for (int u = 0; u < nt; ++u)
+                acc += (uint64_t)q48_mul(sc[oh][u], vl[u][d]);
+            int64_t *dst = out + (size_t)h0 * HD + oi;
+            if (nc > 1)
+                __hip_atomic_fetch_add(reinterpret_cast<uint64_t *>(dst), acc, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            else
+                *dst = (int64_t)acc;
         }
-    }
-#pragma unroll
-    for (int d = 0; d < DPL; ++d)
-        part[g][l8 * DPL + d] = acc[d];
-    __syncthreads();
-    if (tid < HD) {
-        uint64_t o = 0;
-#pragma unroll 8
-        for (int gg = 0; gg < NG; ++gg)
-            o += part[gg][tid];
-        if (nc > 1)
-            __hip_atomic_fetch_add(reinterpret_cast<uint64_t *>(out) + (size_t)h * HD + tid, o,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-            out[(size_t)h * HD + tid] = (int64_t)o;
     }
 }
 
@@ -1174,36 +1234,37 @@ int q48_launch_attn(q48_ctx *c, int64_t *out, const int64_t *q,
 int q48_att_split_min() { return ATT_SPLIT_MIN; }
 int q48_att_lds_max() { return ATT_LDS_MAX; }
 
-// Workspace of the split attention: chunk maxima and chunk sums [n_heads]
-// [ATT_NCMAX] (k_attn_s1/se/s2 also keep the scores [n_heads][max_seq] in
-// front of them).  The barrier words of k_attn_x live apart, in a region
-// that is zero before the first launch and that every launch leaves zero:
-// [ATTX_MAX_HEADS][ATTX_SYNC] uints, then the error word.
+// Workspace of the split attention: k_attn_s1/se/s2's scores [n_heads]
+// [max_seq], chunk maxima and sums [n_heads][ATT_NCMAX].  k_attn_g's
+// exchange words, epochs and error word live apart, in a region that is zero
+// before the first launch (ATTG_SYNC_BYTES).
 size_t q48_attn_ws_bytes(int n_heads, int max_seq, int head_dim)
 {
     (void)head_dim;
     return ((size_t)n_heads * max_seq + (size_t)2 * n_heads * ATT_NCMAX) * sizeof(int64_t);
 }
 
-size_t q48_attn_sync_bytes() { return ((size_t)ATTX_MAX_HEADS + 1) * ATTX_SYNC * sizeof(unsigned); }
+size_t q48_attn_sync_bytes() { return ATTG_SYNC_BYTES; }
 
-// k_attn_x needs every active block resident at once: blocks per head for a
-// full cache (max_seq) times the heads must fit the device's occupancy.
-static bool attx_fits(q48_ctx *c, int hd, int n_heads, int max_seq)
+// k_attn_g needs every active block resident at once: the chunks of a full
+// cache (max_seq) times the KV heads must fit the device's occupancy.
+static bool attg_fits(q48_ctx *c, int hd, int n_heads, int n_kv, int max_seq)
 {
     const int k = hd == 64 ? 0 : hd == 32 ? 1 : 2;
-    const int ch = hd == 128 ? AttxShape<128>::CH : AttxShape<64>::CH;
+    if (n_heads % n_kv || n_heads / n_kv > ATTG_GMAX || n_kv > ATTG_KVMAX)
+        return false;
+    if ((max_seq + ATTG_CH - 1) / ATTG_CH > ATTG_NCMAX)
+        return false;
     if (c->attx_per_cu[k] < 0) {   // resident blocks per compute unit, asked once
-        const void *fn = k == 0 ? (const void *)k_attn_x<64>
-                       : k == 1 ? (const void *)k_attn_x<32> : (const void *)k_attn_x<128>;
+        const void *fn = k == 0 ? (const void *)k_attn_g<64>
+                       : k == 1 ? (const void *)k_attn_g<32> : (const void *)k_attn_g<128>;
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, ATTX_NT, 0) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, ATTG_NT, 0) != hipSuccess)
             n = 0;
         c->attx_per_cu[k] = n;
     }
-    const int per_cu = c->attx_per_cu[k];
-    const long need = (long)n_heads * ((max_seq + ch - 1) / ch);
-    return need <= (long)per_cu * c->cu_count && (max_seq + ch - 1) / ch <= ATT_NCMAX;
+    const long need = (long)n_kv * ((max_seq + ATTG_CH - 1) / ATTG_CH);
+    return need <= (long)c->attx_per_cu[k] * c->cu_count;
 }
 
 int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
@@ -1245,29 +1306,23 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
     // the position reaches ATT_SPLIT_MIN; a captured graph keeps the kernels
     // of the position it was captured at
     if (rope && pos >= ATT_SPLIT_MIN && (head_dim == 32 || head_dim == 64 || head_dim == 128) &&
-        (max_seq + ATT_CH - 1) / ATT_CH <= ATT_NCMAX && n_heads <= ATTX_MAX_HEADS) {
+        (max_seq + ATT_CH - 1) / ATT_CH <= ATT_NCMAX && n_heads <= 256) {
         const size_t sc_n = (size_t)n_heads * max_seq, cm_n = (size_t)n_heads * ATT_NCMAX;
         unsigned *sync = ws_ext ? sync_ext : c->attx_sync;
-        if (c->attn_one_launch && sync && attx_fits(c, head_dim, n_heads, max_seq)) {
-            // chunk maxima and sums only
-            int rc = ws_get(2 * cm_n * sizeof(int64_t), &ws);
-            if (rc)
-                return rc;
-            int64_t *cm = ws, *cs = cm + cm_n;
-            int *err = reinterpret_cast<int *>(sync + (size_t)ATTX_MAX_HEADS * ATTX_SYNC);
-            const int ch = head_dim == 128 ? AttxShape<128>::CH : AttxShape<64>::CH;
-            const dim3 grid((max_seq + ch - 1) / ch, n_heads);
-#define ATTX_LAUNCH(HD)                                                                       \
-    hipLaunchKernelGGL((k_attn_x<HD>), grid, dim3(ATTX_NT), 0, c->stream, out, q, kcache,    \
-                       vcache, k_new, v_new, c->rope_cos, c->rope_sin, scale_p, cm, cs, sync, \
-                       err, layer, d_pos, pos, n_heads, n_kv, max_seq)
+        if (c->attn_one_launch && sync && attg_fits(c, head_dim, n_heads, n_kv, max_seq)) {
+            const dim3 grid((max_seq + ATTG_CH - 1) / ATTG_CH, n_kv);
+#define ATTG_LAUNCH(HD)                                                                       \
+    hipLaunchKernelGGL((k_attn_g<HD>), grid, dim3(ATTG_NT), 0, c->stream, out, q, kcache,    \
+                       vcache, k_new, v_new, c->rope_cos, c->rope_sin, scale_p,               \
+                       reinterpret_cast<uint64_t *>(sync), layer, d_pos, pos, n_heads, n_kv,  \
+                       max_seq)
             if (head_dim == 64)
-                ATTX_LAUNCH(64);
+                ATTG_LAUNCH(64);
             else if (head_dim == 32)
-                ATTX_LAUNCH(32);
+                ATTG_LAUNCH(32);
             else
-                ATTX_LAUNCH(128);
-#undef ATTX_LAUNCH
+                ATTG_LAUNCH(128);
+#undef ATTG_LAUNCH
             return (int)hipGetLastError();
         }
         int rc = ws_get(q48_attn_ws_bytes(n_heads, max_seq, head_dim), &ws);

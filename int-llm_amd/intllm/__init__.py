@@ -69,6 +69,8 @@ ABI_SIGNATURES = {
     "q48_rmsnorm_gemv_swiglu": [_P, _P, _P, _P, _P, _I, _I],
     "q48_attn_decode_rope": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
     "q48_attn_split_min": [],
+    "q48_set_attn_one_launch": [_P, _I],
+    "q48_attn_status": [_P],
     "q48_attn_decode_rope_prefetch": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _SZ],
     "q48_rms_inv": [_P, _P, _P, _I],
     "q48_embed_rms": [_P, _P, _P, _I, _I, _P],
@@ -250,6 +252,12 @@ class Context:
     def gemv_residual_stats_bf16(self, acc, W, x, M, K, stats):
         return check("q48_gemv_residual_stats_bf16",
                      hip_lib().q48_gemv_residual_stats_bf16(self.h, acc, W, x, M, K, stats))
+
+    def set_attn_one_launch(self, on: bool):
+        return check("q48_set_attn_one_launch", hip_lib().q48_set_attn_one_launch(self.h, int(on)))
+
+    def attn_status(self):
+        return check("q48_attn_status", hip_lib().q48_attn_status(self.h))
 
     def set_gemv_persistent(self, on: bool):
         return check("q48_set_gemv_persistent", hip_lib().q48_set_gemv_persistent(self.h, int(on)))

@@ -452,14 +452,28 @@ def test_rmsnorm_gemv_swiglu_fused(ctx, oracle, ffn, K):
         b.free()
 
 
+@pytest.mark.parametrize("one_launch", [True, False], ids=["one_launch", "three_launches"])
 @pytest.mark.parametrize("nh,nkv,hd,max_seq,positions", [
     (8, 2, 32, 64, [0, 1, 63]),
     (32, 4, 64, 300, [0, 7, 299]),
     # from position 512 on, the split (chunked) kernels: chunk edges 767/768
     (32, 4, 64, 1300, [511, 512, 767, 768, 1299]),
     (8, 2, 32, 600, [513, 599]),
+    # head_dim 128: chunks of 128 positions
+    (16, 4, 128, 700, [512, 639, 640, 699]),
+    # the largest one-launch grid of the TinyLlama heads: 16 chunks x 32 heads
+    (32, 4, 64, 4096, [2047, 2048, 4095]),
 ])
-def test_attention_rope_fused(ctx, oracle, nh, nkv, hd, max_seq, positions):
+def test_attention_rope_fused(ctx, oracle, nh, nkv, hd, max_seq, positions, one_launch):
+    ctx.set_attn_one_launch(one_launch)
+    try:
+        _attention_rope_case(ctx, oracle, nh, nkv, hd, max_seq, positions)
+        assert ctx.attn_status() == 0
+    finally:
+        ctx.set_attn_one_launch(True)
+
+
+def _attention_rope_case(ctx, oracle, nh, nkv, hd, max_seq, positions):
     rng = np.random.default_rng(nh + hd + max_seq)
     kvd = nkv * hd
     kc = (rng.standard_normal(2 * max_seq * kvd) * ONE).astype(np.int64)
@@ -484,7 +498,7 @@ def test_attention_rope_fused(ctx, oracle, nh, nkv, hd, max_seq, positions):
         oracle.q48o_attn_decode(out.ctypes.data, qr.ctypes.data, kc.ctypes.data, vc.ctypes.data,
                                 kr.ctypes.data, vn.ctypes.data, 1, pos, nh, nkv, hd, max_seq)
         dq, dkn, dvn, do = ctx.to_device(q), ctx.to_device(kn), ctx.to_device(vn), ctx.buffer(nh * hd)
-        say("attention+rope", nh, nkv, hd, "pos", pos)
+        say("attention+rope", nh, nkv, hd, "max_seq", max_seq, "pos", pos)
         ctx.attn_decode_rope(do.ptr, dq.ptr, dk.ptr, dv.ptr, dkn.ptr, dvn.ptr, 1, pos, nh, nkv, hd,
                              max_seq)
         assert np.array_equal(do.download(), out), pos
