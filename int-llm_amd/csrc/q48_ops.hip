@@ -771,10 +771,11 @@ __device__ bool attg_exchange(uint64_t *xw, int c, int nc, int G, unsigned epoch
     return ok != 0;
 }
 
-// at most 128 VGPRs: two blocks (16 waves) fit a compute unit, so that the
-// grid of a 4096-position cache with 4 KV heads (512 blocks) is resident
+// head_dim 32/64: at most 128 VGPRs, so that two blocks (16 waves) fit a
+// compute unit and the grid of a 4096-position cache with 4 KV heads (512
+// blocks) is resident; head_dim 128: its LDS rows allow one block per unit
 template <int HD>
-__global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(4))) void k_attn_g(
+__global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 128 ? 2 : 4))) void k_attn_g(
     int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
     int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
     const int64_t *__restrict__ v_new, const int64_t *__restrict__ cos_t,
