@@ -36,6 +36,7 @@ extern "C" {
 #define Q48_ERANGE     (-4)   /* token or position out of range               */
 #define Q48_ESTATE     (-5)   /* op needs state not yet set up (rope tables)  */
 #define Q48_ETIMEOUT   (-6)   /* a one-launch decode step could not finish     */
+#define Q48_ETOOBIG    (-7)   /* size exceeds the allocation-free scratch      */
 
 typedef struct q48_ctx q48_ctx;
 
@@ -188,6 +189,21 @@ int q48_attn_split_min(void);
  * resident at once; otherwise the three launches run.  No reference
  * counterpart: a scheduling choice of this library. */
 int q48_set_attn_one_launch(q48_ctx *ctx, int on);
+/* q48_attn_decode_rope without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  q48_attn_decode_rope grows the context's workspace with
+ * hipMalloc when a longer cache needs it; this entry takes the split
+ * attention's workspace from a fixed per-device array of 4 MiB (its usable
+ * part is q48_attn_noalloc_max_bytes()) and returns Q48_ETOOBIG, launching
+ * nothing, when the call would need more.  Same arguments, same bits.  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (from two contexts or two streams) race. */
+int q48_attn_decode_rope_noalloc(q48_ctx *ctx, int64_t *out, const int64_t *q,
+                                 int64_t *kcache, int64_t *vcache, const int64_t *k_new,
+                                 const int64_t *v_new, int layer, int pos, int n_heads,
+                                 int n_kv, int head_dim, int max_seq);
+size_t q48_attn_noalloc_max_bytes(void);
 /* Synchronises; Q48_ETIMEOUT if a one-launch split attention could not
  * finish (a block waited past its bound: blocks were not all resident; its
  * barrier words are then cleared), else Q48_OK. */

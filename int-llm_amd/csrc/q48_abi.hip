@@ -73,6 +73,7 @@ const char *q48_strerror(int code)
     case Q48_ERANGE: return "token or position out of range";
     case Q48_ESTATE: return "context state not initialised (call q48_rope_init)";
     case Q48_ETIMEOUT: return "one-launch decode step or attention timed out (blocks not resident)";
+    case Q48_ETOOBIG: return "size exceeds the allocation-free scratch";
     default: return "unknown error";
     }
 }
@@ -113,6 +114,8 @@ int q48_ctx_create(q48_ctx **out, int device)
     int rc = launch_rc(q48_launch_math_init(c));
     if (rc == Q48_OK)
         rc = launch_rc(q48_launch_zero(c, c->attx_sync, q48_attn_sync_bytes()));
+    if (rc == Q48_OK)   // the allocation-free entry point's scratch on this device
+        rc = q48_scratch_init(c);
     if (rc == Q48_OK)
         rc = launch_rc(q48_launch_step_set(c, 0, 0));
     if (rc == Q48_OK)

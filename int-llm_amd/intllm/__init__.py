@@ -21,6 +21,7 @@ HIP_LIB = LIB_DIR / "libintllm_hip.so"
 HOST_LIB = LIB_DIR / "libq48host.so"
 
 Q48_OK, Q48_EINVAL, Q48_ENOMEM, Q48_EHIP, Q48_ERANGE, Q48_ESTATE = 0, -1, -2, -3, -4, -5
+Q48_ETIMEOUT, Q48_ETOOBIG = -6, -7
 
 # fp_eval function ids (include/intllm_hip.h, q48_fp_eval)
 FP_MUL, FP_DIV, FP_SQRT, FP_SQRT_FAST, FP_INV_SQRT, FP_EXP, FP_LOG, FP_SINCOS, \
