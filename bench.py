@@ -440,6 +440,17 @@ def main():
             pms = 1e3 * (time.perf_counter() - t0) / args.prefill_reps
             pf["T"][str(T)] = {"ms": round(pms, 3), "tok_s": round(1e3 * T / pms, 1)}
             log(f"batched prefill T={T}: {pms:.2f} ms ({1e3 * T / pms:.0f} tok/s)")
+            if T >= 512:
+                # the same prefill with attention on the VALU kernel
+                ctx.set_pf_attn_mfma(False)
+                m.prefill(tk, 0, cfg.vocab, logits=False)
+                ctx.sync()
+                t0 = time.perf_counter()
+                m.prefill(tk, 0, cfg.vocab, logits=False)
+                vms = 1e3 * (time.perf_counter() - t0)
+                ctx.set_pf_attn_mfma(True)
+                pf["T"][str(T)]["valu_attention_ms"] = round(vms, 3)
+                log(f"batched prefill T={T}, VALU attention: {vms:.2f} ms")
         # the per-token route over the golden prompt (what generate did
         # before batching): forward calls without logits copies
         m.set_batched_prefill(False)

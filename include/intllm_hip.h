@@ -189,6 +189,12 @@ int q48_attn_split_min(void);
  * resident at once; otherwise the three launches run.  No reference
  * counterpart: a scheduling choice of this library. */
 int q48_set_attn_one_launch(q48_ctx *ctx, int on);
+/* Batched-prefill attention (q48_attn_prefill) with the q.k and p.v products
+ * on the int8 matrix cores (on: the default, for head_dim 32, 64 or 128 and
+ * up to 16320 cache rows) or on the VALU, one block per (head, query row)
+ * (off; up to 4096 cache rows).  Same bits either way.  No reference
+ * counterpart: a kernel choice of this library. */
+int q48_set_pf_attn_mfma(q48_ctx *ctx, int on);
 /* q48_attn_decode_rope without any device allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under hipGraph capture, tight serving loops, harnesses that forbid
@@ -337,7 +343,9 @@ int q48_rope_store_rows(q48_ctx *ctx, int64_t *QKV, int64_t *kcache, int64_t *vc
                         int p0, int T, int n_heads, int n_kv, int head_dim, int max_seq);
 /* Exact causal attention (llama_int.c:1433, 1502-1529) of the rotated q of
  * every row over cache positions 0 .. p0 + t (stored by
- * q48_rope_store_rows); out[T][n_heads * head_dim].  p0 + T at most 4096. */
+ * q48_rope_store_rows); out[T][n_heads * head_dim].  p0 + T at most 16320
+ * (head_dim 32, 64, 128; 4096 on the VALU kernel, see q48_set_pf_attn_mfma).
+ * Uses up to 16 * 8 bytes per (head, query row, cache row) of workspace. */
 int q48_attn_prefill(q48_ctx *ctx, int64_t *out, const int64_t *QKV, int64_t *kcache,
                      int64_t *vcache, int layer, int p0, int T, int n_heads, int n_kv,
                      int head_dim, int max_seq);

@@ -102,6 +102,7 @@ int q48_ctx_create(q48_ctx **out, int device)
         return Q48_EHIP;
     }
     c->attn_one_launch = 1;
+    c->pf_attn_mfma = 1;
     c->attx_per_cu[0] = c->attx_per_cu[1] = c->attx_per_cu[2] = -1;
     if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
         hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess ||
@@ -650,6 +651,14 @@ int q48_set_attn_one_launch(q48_ctx *c, int on)
     return Q48_OK;
 }
 
+int q48_set_pf_attn_mfma(q48_ctx *c, int on)
+{
+    if (!c)
+        return Q48_EINVAL;
+    c->pf_attn_mfma = on != 0;
+    return Q48_OK;
+}
+
 int q48_set_gemv_persistent(q48_ctx *c, int on)
 {
     if (!c)
@@ -731,7 +740,12 @@ int q48_attn_prefill(q48_ctx *c, int64_t *out, const int64_t *QKV, int64_t *kcac
         return Q48_EINVAL;
     if (!c->rope_cos || head_dim != c->rope_head_dim || max_seq > c->rope_max_seq)
         return Q48_ESTATE;
-    if (p0 < 0 || p0 + T > max_seq || p0 + T > q48_att_lds_max())
+    if (p0 < 0 || p0 + T > max_seq)
+        return Q48_ERANGE;
+    if (c->pf_attn_mfma && q48_pf_attn_mfma_ok(p0, T, head_dim))
+        return launch_rc(q48_launch_pf_attn_mfma(c, out, QKV, kcache, vcache, layer, p0, T,
+                                                 n_heads, n_kv, head_dim, max_seq));
+    if (p0 + T > q48_att_lds_max())
         return Q48_ERANGE;
     return launch_rc(q48_launch_pf_attn(c, out, QKV, kcache, vcache, layer, p0, T, n_heads, n_kv,
                                         head_dim, max_seq));

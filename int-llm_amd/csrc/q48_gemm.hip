@@ -22,15 +22,11 @@
 // planes in LDS (double-buffered) and every wave issues 63 MFMAs; the global
 // loads run two steps ahead and the byte split of the next step is
 // interleaved with the MFMAs of the current one.
-#include "q48_internal.h"
+#include "q48_digits.hpp"
 #include "../../include/intllm_hip.h"
 
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-constexpr uint64_t kDig = 0x0080808080808080ull;
 constexpr int MT = 64;             // tokens per block
 constexpr int MN = 64;             // rows per block
 constexpr int MK = 32;             // k per step: one MFMA depth
@@ -46,21 +42,6 @@ constexpr int CH = MK / 16;        // 16-byte k chunks per row and limb
 constexpr int SLICE = CH * 512;    // one 32-row slice of one limb
 constexpr int PLANE = 2 * SLICE;   // 64 rows of one limb
 constexpr int STAGE = 8 * PLANE;   // one operand: 32 KiB
-
-// 4 x 4 byte transpose: out_j = [a_j, b_j, c_j, d_j] (v_perm_b32 selects
-// bytes 0-3 from its second operand and 4-7 from its first).
-__device__ __forceinline__ void tr4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
-                                    uint32_t (&o)[4])
-{
-    const uint32_t t0 = __builtin_amdgcn_perm(b, a, 0x06020400u);   // a0 b0 a2 b2
-    const uint32_t t1 = __builtin_amdgcn_perm(b, a, 0x07030501u);   // a1 b1 a3 b3
-    const uint32_t t2 = __builtin_amdgcn_perm(d, c, 0x06020400u);   // c0 d0 c2 d2
-    const uint32_t t3 = __builtin_amdgcn_perm(d, c, 0x07030501u);   // c1 d1 c3 d3
-    o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-    o[1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-    o[2] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-    o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-}
 
 // Piece p (0 .. 64 CH - 1) of a tile: row r, elements [k8, k8 + 8) of the
 // step, and its byte offset in a plane.  Lanes 2i, 2i + 1 take one 16-byte

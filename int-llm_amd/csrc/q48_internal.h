@@ -37,6 +37,7 @@ struct q48_ctx {
     int sk_grid;                 // k_step_fused blocks (0: not planned yet)
     unsigned *attx_sync;         // device: k_attn_x barrier words and error word (zeroed)
     int attn_one_launch;         // split attention as one k_attn_x launch (default on)
+    int pf_attn_mfma;            // batched-prefill attention on the matrix cores (default on)
     int attx_per_cu[3];          // k_attn_x<64/32/128> resident blocks per CU (-1: not asked)
     int64_t *scratch;            // device address of the allocation-free scratch array
     unsigned *scratch_sync;      // ... and of its barrier region
@@ -134,6 +135,14 @@ int q48_launch_pf_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *X, const int6
 int q48_launch_pf_rope_store(q48_ctx *c, int64_t *QKV, int64_t *kcache, int64_t *vcache,
                              int layer, int p0, int T, int n_heads, int n_kv, int hd,
                              int max_seq);
+// the same attention with both products on the int8 matrix cores
+// (q48_pfattn.hip): head_dim 32, 64 or 128 and at most
+// q48_pf_attn_mfma_max_pos() cache rows
+bool q48_pf_attn_mfma_ok(int p0, int T, int hd);
+int q48_pf_attn_mfma_max_pos();
+int q48_launch_pf_attn_mfma(q48_ctx *c, int64_t *out, const int64_t *QKV, int64_t *kcache,
+                            int64_t *vcache, int layer, int p0, int T, int n_heads, int n_kv,
+                            int hd, int max_seq);
 int q48_launch_pf_attn(q48_ctx *c, int64_t *out, const int64_t *QKV, int64_t *kcache,
                        int64_t *vcache, int layer, int p0, int T, int n_heads, int n_kv, int hd,
                        int max_seq);

@@ -71,6 +71,8 @@ ABI_SIGNATURES = {
     "q48_attn_decode_rope": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
     "q48_attn_split_min": [],
     "q48_set_attn_one_launch": [_P, _I],
+    "q48_set_pf_attn_mfma": [_P, _I],
+    "q48_attn_prefill": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I],
     "q48_attn_status": [_P],
     "q48_attn_decode_rope_prefetch": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _SZ],
     "q48_rms_inv": [_P, _P, _P, _I],
@@ -259,6 +261,15 @@ class Context:
 
     def attn_status(self):
         return check("q48_attn_status", hip_lib().q48_attn_status(self.h))
+
+    def set_pf_attn_mfma(self, on: bool):
+        return check("q48_set_pf_attn_mfma", hip_lib().q48_set_pf_attn_mfma(self.h, int(on)))
+
+    def attn_prefill(self, out, qkv, kc, vc, layer, p0, T, nh, nkv, hd, max_seq):
+        """Causal attention of T rotated [q | k | v] rows at positions p0 .. p0 + T - 1
+        over the cache rows stored before (q48_rope_store_rows)."""
+        return check("q48_attn_prefill", hip_lib().q48_attn_prefill(
+            self.h, out, qkv, kc, vc, layer, p0, T, nh, nkv, hd, max_seq))
 
     def set_gemv_persistent(self, on: bool):
         return check("q48_set_gemv_persistent", hip_lib().q48_set_gemv_persistent(self.h, int(on)))
