@@ -66,6 +66,27 @@ int64_t q48s_bf16_to_q48(uint16_t bits)
     return sign ? -r : r;
 }
 
+/* Exact IEEE half -> Q16.48: normal values (1024 + m) * 2^(e - 25), subnormal
+ * m * 2^-24, scaled by 2^48 (shifts of e + 23 and 24); +-0 -> 0; e = 31 (inf /
+ * nan) -> +-32000.  Follows safetensors.h:74-111, sign applied last; the left
+ * shift and the negation wrap (e = 30 reaches bit 63). */
+int64_t q48s_f16_to_q48(uint16_t bits)
+{
+    int sign = bits >> 15;
+    int e = (bits >> 10) & 0x1f;
+    int m = bits & 0x3ff;
+    uint64_t r;
+    if (e == 0 && m == 0)
+        return 0;
+    if (e == 0x1f)
+        r = (uint64_t)32000 << 48;
+    else if (e == 0)
+        r = (uint64_t)m << 24;
+    else
+        r = (uint64_t)(1024 + m) << (e + 23);
+    return (int64_t)(sign ? (uint64_t)0 - r : r);
+}
+
 uint16_t q48s_q48_to_bf16(int64_t v)
 {
     if (v == 0)

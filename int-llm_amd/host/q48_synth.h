@@ -47,6 +47,9 @@ uint64_t q48s_tensor_seed(uint64_t base_seed, const char *name);
 /* bf16 bits -> exact Q16.48 (restates safetensors.h:115-152). */
 int64_t q48s_bf16_to_q48(uint16_t bits);
 
+/* IEEE half bits -> exact Q16.48 (restates safetensors.h:74-111). */
+int64_t q48s_f16_to_q48(uint16_t bits);
+
 /* Q16.48 -> bf16 bits, round to nearest, ties to even. */
 uint16_t q48s_q48_to_bf16(int64_t v);
 

@@ -44,6 +44,7 @@ void q48r_fp_consts(int64_t *pi, int64_t *gain, int64_t *angles48)
     memcpy(angles48, fp_cordic_angles, sizeof fp_cordic_angles);
 }
 int64_t q48r_bf16_to_q48(uint16_t b) { return bfloat16_to_q1648(b); }
+int64_t q48r_f16_to_q48(uint16_t b) { return float16_to_q1648(b); }
 
 /* ---- tensor ops ---------------------------------------------------------- */
 void q48r_gemv(int64_t *y, const int64_t *W, const int64_t *x, int M, int K)

@@ -66,6 +66,7 @@ def ref():
         "q48s_tokens": ([P, I, U, I, I], None),
         "q48s_fnv_i64": ([U, P, C.c_size_t], U),
         "q48r_bf16_to_q48": ([C.c_uint16], C.c_int64),
+        "q48r_f16_to_q48": ([C.c_uint16], C.c_int64),
         "q48r_rng_seed": ([U, P], None),
         "q48r_rng_next": ([P], U),
         "q48r_sample": ([P, I, C.c_int64, I, C.c_int64, P], I),
@@ -341,6 +342,17 @@ def gen_bf16():
     write("bf16_to_q48.json", {
         "source": "bfloat16_to_q1648 (safetensors.h:115-152) via oracle/ref_harness.c",
         "file": "bf16_to_q48.npz", "n": 65536, "fnv": fnv(vals)})
+
+
+def gen_f16():
+    """float16_to_q1648 (safetensors.h:74-111) of all 65536 bit patterns, as
+    the reference computes them (subnormals, the exponent-31 clamp and the
+    wrapping shift at exponent 30 included)."""
+    vals = np.array([R.q48r_f16_to_q48(b) for b in range(65536)], dtype=np.int64)
+    np.savez_compressed(GOLD / "f16_to_q48.npz", v=vals)
+    write("f16_to_q48.json", {
+        "source": "float16_to_q1648 (safetensors.h:74-111) via oracle/ref_harness.c",
+        "file": "f16_to_q48.npz", "n": 65536, "fnv": fnv(vals)})
 
 
 def gen_tinyllama():

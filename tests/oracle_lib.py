@@ -58,6 +58,7 @@ _SIG = {
     "q48s_tensor_seed": ([U, C.c_char_p], U),
     "q48s_fnv_i64": ([U, P, C.c_size_t], U),
     "q48s_bf16_to_q48": ([C.c_uint16], I64), "q48s_q48_to_bf16": ([I64], C.c_uint16),
+    "q48s_f16_to_q48": ([C.c_uint16], I64),
 }
 
 _lib = None

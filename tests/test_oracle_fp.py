@@ -16,7 +16,7 @@ import numpy as np
 
 import oracle_lib as O
 import spec
-from conftest import bf16_reference, golden
+from conftest import GOLD, bf16_reference, golden
 
 ONE = spec.ONE
 SUB_ORDER = ["fp_mul", "fp_div", "fp_sqrt", "fp_sqrt_fast", "fp_inv_sqrt", "fp_exp", "fp_log",
@@ -144,6 +144,28 @@ def test_bf16_conversion_equals_reference_every_pattern(oracle):
     got = np.array([oracle.q48s_bf16_to_q48(b) for b in range(1 << 16)], dtype=np.int64)
     bad = np.nonzero(got != want)[0]
     assert bad.size == 0, [hex(int(b)) for b in bad[:8]]
+
+
+def test_f16_conversion_equals_reference_every_pattern(oracle):
+    """The host's half-precision conversion (q48s_f16_to_q48) equals the
+    compiled reference's float16_to_q1648 (safetensors.h:74-111) on all 65536
+    patterns (tests/golden/f16_to_q48.npz), and the normal and subnormal
+    ranges follow the closed form (1024 + m) 2^(e + 23), m 2^24 (wrapping at
+    exponent 30, where the value reaches bit 63)."""
+    import numpy as np
+    meta = golden("f16_to_q48.json")
+    with np.load(GOLD / meta["file"], allow_pickle=False) as z:
+        want = z["v"]
+    assert want.dtype == np.int64 and want.size == 65536 and O.fnv(want) == meta["fnv"]
+    got = np.array([oracle.q48s_f16_to_q48(b) for b in range(1 << 16)], dtype=np.int64)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [hex(int(b)) for b in bad[:8]]
+    for bits in range(0, 1 << 16, 5):
+        e, m, sgn = (bits >> 10) & 0x1F, bits & 0x3FF, bits >> 15
+        if e == 0x1F:
+            continue
+        v = (1024 + m) << (e + 23) if e else m << 24
+        assert int(want[bits]) == spec.wrap64(-v if sgn else v), hex(bits)
 
 
 def test_bf16_conversion(oracle):
