@@ -134,3 +134,69 @@ def test_refbind_generate_config1_on_device():
         lib.lq48_detach()
     finally:
         rm.free()
+
+
+@needs_so
+@pytest.mark.gpu
+def test_tinyllama_mgw_full_size_both_loaders(ctx):
+    """Config 3 at full size through a .mgw: the 8.8 GB file (201 tensors,
+    mgw_export's layout) loaded by the reference's own mgw_load
+    (llama_int.c:2344-2560) and run by its generate() with llama_forward on
+    the device, and loaded by the C host's q48h_model_load_mgw and run by
+    q48h_generate: both give the reference's 32 + 16 tokens and every
+    step's logits hash.  Write and load rates are printed."""
+    import shutil
+    import time
+    g = golden("tinyllama_generate.json")
+    cfg = intllm.Config(*g["config"])
+    prompt, new = g["prompt"], 16
+    want_toks = g["tokens"][:len(prompt) + new]
+    want_hs = g["step_fnv"][:len(prompt) + new - 1]
+    lib = _lib()
+    with tempfile.TemporaryDirectory() as d:
+        if shutil.disk_usage(d).free < (12 << 30):
+            pytest.skip(f"{d} has under 12 GiB free for the 8.8 GB .mgw")
+        path = os.path.join(d, "tinyllama.mgw")
+        print("[case] tinyllama mgw write", flush=True)
+        t = time.time()
+        rc = intllm.host_lib().q48h_mgw_write_synth(path.encode(), C.byref(cfg), g["seed"],
+                                                     max(1, min(16, os.cpu_count() or 1)))
+        assert rc == 0
+        size = os.path.getsize(path)
+        print(f"[case] wrote {size / 1e9:.2f} GB in {time.time() - t:.1f} s", flush=True)
+        assert size > 8.5e9
+
+        print("[case] reference mgw_load + attach + generate", flush=True)
+        t = time.time()
+        m = lib.lq48_model_load_mgw(path.encode())
+        assert m
+        t_load = time.time() - t
+        try:
+            t = time.time()
+            assert lib.lq48_attach(m, 0) == 0
+            t_up = time.time() - t
+            out = (C.c_int * (len(prompt) + new))()
+            hs = (C.c_uint64 * (len(prompt) + new))()
+            n = C.c_int()
+            p = (C.c_int * len(prompt))(*prompt)
+            total = lib.lq48_generate(m, p, len(prompt), new, out, hs, len(hs), C.byref(n))
+            lib.lq48_detach()
+        finally:
+            lib.lq48_model_free(m)
+        print(f"[case] reference mgw_load {size / t_load / 1e9:.2f} GB/s, upload "
+              f"{size / t_up / 1e9:.2f} GB/s", flush=True)
+        assert total == len(want_toks)
+        assert list(out[:total]) == want_toks
+        assert ["%016x" % h for h in hs[:n.value]] == want_hs
+
+        print("[case] host q48h_model_load_mgw + generate", flush=True)
+        t = time.time()
+        hm = intllm.HostModel(ctx, mgw=path)
+        t_host = time.time() - t
+        try:
+            toks, hh, _ = hm.generate(prompt, new)
+        finally:
+            hm.free()
+        print(f"[case] host load + upload {size / t_host / 1e9:.2f} GB/s", flush=True)
+        assert toks == want_toks
+        assert ["%016x" % h for h in hh] == want_hs
