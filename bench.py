@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import hashlib
 import json
 import os
 import sys
@@ -35,8 +36,13 @@ sys.path.insert(0, str(ROOT / "tests"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline sweep, from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE runs scaled by the counters' reading for a copy kernel of known
-# size (profiles/k_gemv_decode_tinyllama.md); re-measure when the kernel changes
-TRAFFIC = 93546127
+# size (profiles/k_gemv_decode_tinyllama.md).  The figure holds for the GEMV
+# sources it was measured on: TRAFFIC_SOURCES hash to TRAFFIC_SHA256 (the first
+# 16 hex digits of the sha256 of their bytes, in this order); with any other
+# sources the bench line reports traffic null until the counters are re-run.
+TRAFFIC = 93544995
+TRAFFIC_SOURCES = ("int-llm_amd/csrc/q48_gemv.hip", "int-llm_amd/csrc/q48_gemv_tiles.hpp")
+TRAFFIC_SHA256 = "058a876df0dcedbb"
 REF_CPU_MS_PER_TOK = 501.4   # reference decode, Zen 4, 1 thread
 # int8 GEMM: MI355X dense int8 MFMA peak; one Q16.48 MAC is 63 int8 products
 # (digit pairs a + b <= 13), 2 ops each
@@ -97,6 +103,19 @@ def gemv_shapes(ctx, spec, intllm, reps: int):
         log("gemv", M, K, out[f"{M}x{K}"])
     pool.free()
     return out
+
+
+def sources_sha256() -> str:
+    h = hashlib.sha256()
+    for f in TRAFFIC_SOURCES:
+        h.update((ROOT / f).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def traffic_bytes():
+    """The PMC-measured HBM bytes per GEMV launch, or None when the GEMV
+    sources differ from the ones the counters were read on."""
+    return TRAFFIC if sources_sha256() == TRAFFIC_SHA256 else None
 
 
 def gemm_prefill(ctx, spec, intllm, reps: int):
@@ -538,7 +557,8 @@ def main():
                      "kernel": "k_gemv_v5 / k_gemv_p6 (q48_gemv family: the 89 fused GEMV "
                                "launches of a decode token, back to back)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(),
+                     "traffic_sources_sha256": sources_sha256(),
                      "avg_launch_us": round(avg_us, 3),
                      "algorithmic_bytes_per_launch": round(bytes_per_launch),
                      "launches_timed": launches},
