@@ -38,11 +38,12 @@ HBM_PEAK_GBS = 8000.0
 # and WRITE_SIZE runs scaled by the counters' reading for a copy kernel of known
 # size (profiles/k_gemv_decode_tinyllama.md).  The figure holds for the GEMV
 # sources it was measured on: TRAFFIC_SOURCES hash to TRAFFIC_SHA256 (the first
-# 16 hex digits of the sha256 of their bytes, in this order); with any other
-# sources the bench line reports traffic null until the counters are re-run.
+# 16 hex digits of the sha256 of their code, in this order, with comments and
+# whitespace removed); with any other code the bench line reports traffic null
+# until the counters are re-run.
 TRAFFIC = 93544995
 TRAFFIC_SOURCES = ("int-llm_amd/csrc/q48_gemv.hip", "int-llm_amd/csrc/q48_gemv_tiles.hpp")
-TRAFFIC_SHA256 = "058a876df0dcedbb"
+TRAFFIC_SHA256 = "89cfc0315ba12a95"
 REF_CPU_MS_PER_TOK = 501.4   # reference decode, Zen 4, 1 thread
 # int8 GEMM: MI355X dense int8 MFMA peak; one Q16.48 MAC is 63 int8 products
 # (digit pairs a + b <= 13), 2 ops each
@@ -106,9 +107,15 @@ def gemv_shapes(ctx, spec, intllm, reps: int):
 
 
 def sources_sha256() -> str:
+    """sha256 (16 hex digits) of the TRAFFIC_SOURCES' code: // and /* */
+    comments and all whitespace removed, so comment edits keep the hash."""
+    import re
     h = hashlib.sha256()
     for f in TRAFFIC_SOURCES:
-        h.update((ROOT / f).read_bytes())
+        src = (ROOT / f).read_text()
+        src = re.sub(r"/\*.*?\*/", " ", src, flags=re.S)
+        src = re.sub(r"//[^\n]*", " ", src)
+        h.update(re.sub(r"\s+", "", src).encode())
     return h.hexdigest()[:16]
 
 

@@ -35,7 +35,7 @@ extern "C" {
 #define Q48_EHIP       (-3)   /* HIP runtime / launch error                    */
 #define Q48_ERANGE     (-4)   /* token or position out of range               */
 #define Q48_ESTATE     (-5)   /* op needs state not yet set up (rope tables)  */
-#define Q48_ETIMEOUT   (-6)   /* a one-launch decode step could not finish     */
+#define Q48_ETIMEOUT   (-6)   /* a one-launch split attention could not finish */
 #define Q48_ETOOBIG    (-7)   /* size exceeds the allocation-free scratch      */
 
 typedef struct q48_ctx q48_ctx;
@@ -377,49 +377,6 @@ int q48_graph_begin(q48_ctx *ctx);
 int q48_graph_end(q48_ctx *ctx);
 int q48_graph_launch(q48_ctx *ctx, int times);
 int q48_graph_drop(q48_ctx *ctx);
-
-/* ---- one-launch decode step ------------------------------------------------ */
-/* No reference counterpart as one launch: llama_forward (llama_int.c:
- * 2807-2886) followed by argmax (2888-2893), the greedy step of generate
- * (3101-3113), run as ONE persistent kernel instead of 2 + 5 L launches.
- * Resident blocks walk the step's phases in order (embedding, per layer the
- * normed q|k|v GEMV, attention, the O GEMV + residual, the normed gate|up GEMV
- * + SwiGLU, the down GEMV + residual, then the normed lm_head and argmax),
- * each block issuing its first weight loads before it waits for the phase
- * it reads.  Same bits as the multi-launch step.  In step mode terms: it
- * reads token and pos from the device step state and writes the greedy
- * token back (pos += 1, token appended to d_tokens[count] while count < cap),
- * like q48_argmax_step; it may be captured into the context graph.
- * The model is described by plain pointers and element offsets into one
- * int64 weight slab `w` (embedding, norm weights, and with wfmt 0 the
- * matrices) and `wmat` (the matrices: the same slab for wfmt 0, or bfloat16
- * bits at the same element offsets for wfmt 1, see q48_bf16_pack).
- * Served shapes: dim 2048, ffn 5632, head_dim 64 (TinyLlama-1.1B), positions
- * below q48_step_fused_max_pos() and below max_seq; q48_rope_init done. */
-typedef struct {
-    const void *wmat;
-    int wfmt;                     /* 0: int64 Q16.48 matrices, 1: bfloat16 bits */
-    const int64_t *w;
-    size_t off_embed, off_norm, off_lm, off_layers, layer_elems;
-    /* per-layer element offsets: attn_norm, ffn_norm, [q;k;v], o, [gate;up], down */
-    size_t lo_an, lo_fn, lo_qkv, lo_wo, lo_gu, lo_wd;
-    /* activations (16-byte aligned): hidden [dim], q|k|v [dim + 2 kvd],
-     * attention output [dim], FFN hidden [ffn], logits [vocab], and the norm
-     * partial sums s_attn, s_ffn [dim / 4] */
-    int64_t *hidden, *qkv, *attn, *h_ffn, *logits, *s_attn, *s_ffn;
-    int64_t *kcache, *vcache;     /* [L][max_seq][n_kv][head_dim] */
-    int n_layers, dim, n_heads, n_kv_heads, head_dim, ffn, vocab, max_seq;
-} q48_step_model;
-
-/* 1 when q48_step_fused serves this model on this device, else 0. */
-int q48_step_fused_supported(q48_ctx *ctx, const q48_step_model *m);
-int q48_step_fused_max_pos(void);
-int q48_step_fused(q48_ctx *ctx, const q48_step_model *m, int *d_tokens, int cap);
-/* Synchronise, then Q48_OK, or Q48_ETIMEOUT when a step's blocks could not
- * all run (its results are void; the step state is left as it was), or
- * Q48_ERANGE when a step saw a state token or position it does not serve.
- * Clears the condition. */
-int q48_step_fused_status(q48_ctx *ctx);
 
 /* ---- kernel timing (diagnostic) -------------------------------------------- */
 

@@ -149,7 +149,6 @@ int q48_ctx_destroy(q48_ctx *c)
     (void)hipFree(c->rms_part);
     (void)hipFree(c->smp);
     (void)hipFree(c->tmp);
-    (void)hipFree(c->sk_sync);
     (void)hipFree(c->attx_sync);
     if (c->graph_exec)
         (void)hipGraphExecDestroy(c->graph_exec);
@@ -1061,110 +1060,6 @@ int q48_sample_step(q48_ctx *c, const int64_t *logits, int vocab, int64_t temper
         return rc;
     return launch_rc(q48_launch_sample(c, c->smp, logits, vocab, temperature, top_k, top_p, rng,
                                        nullptr, d_tokens, cap));
-}
-
-// ---- one-launch decode step ------------------------------------------------
-namespace {
-
-// counters: 3 + 5 L phases of 32 x 16 uints (a phase counter and up to 31
-// arrival-group counters, 64 bytes apart)
-constexpr int kSkMaxLayers = 200, kSkMaxGrid = 31 * 64, kSkPhase = 32 * 16;
-constexpr size_t kSkCountBytes = (size_t)(3 + 5 * kSkMaxLayers) * kSkPhase * sizeof(unsigned);
-constexpr size_t kSkBytes = kSkCountBytes + 256 + (size_t)2 * kSkMaxGrid * sizeof(int64_t);
-
-bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
-
-// shape, pointer and alignment checks; grid and LDS of the launch
-int step_fused_check(q48_ctx *c, const q48_step_model *m, int *grid, size_t *lds)
-{
-    if (!c || !m || !m->wmat || !m->w || !m->hidden || !m->qkv || !m->attn || !m->h_ffn ||
-        !m->logits || !m->s_attn || !m->s_ffn || !m->kcache || !m->vcache)
-        return Q48_EINVAL;
-    if (m->n_layers > kSkMaxLayers || m->max_seq <= 0)
-        return Q48_EINVAL;
-    const int es = m->wfmt == 1 ? 2 : 8;
-    const size_t offs[] = {m->off_lm, m->off_layers, m->layer_elems, m->lo_qkv,
-                           m->lo_wo,  m->lo_gu,      m->lo_wd};
-    for (size_t o : offs)
-        if ((o * es) % 16)
-            return Q48_EINVAL;
-    if (!al16(m->wmat) || !al16(m->w) || ((m->lo_an | m->lo_fn | m->off_norm | m->off_layers |
-                                           m->layer_elems) & 1))
-        return Q48_EINVAL;
-    if (!al16(m->hidden) || !al16(m->qkv) || !al16(m->attn) || !al16(m->h_ffn) ||
-        !al16(m->s_attn) || !al16(m->s_ffn))
-        return Q48_EINVAL;
-    int rc = q48_step_fused_plan(c, m, grid, lds);
-    if (rc)
-        return rc;
-    return *grid <= kSkMaxGrid ? Q48_OK : Q48_EINVAL;
-}
-
-} // namespace
-
-int q48_step_fused_supported(q48_ctx *c, const q48_step_model *m)
-{
-    int grid = 0;
-    size_t lds = 0;
-    return step_fused_check(c, m, &grid, &lds) == Q48_OK;
-}
-
-int q48_step_fused(q48_ctx *c, const q48_step_model *m, int *d_tokens, int cap)
-{
-    if (!c || cap < 0 || (cap > 0 && !d_tokens))
-        return Q48_EINVAL;
-    int grid = 0;
-    size_t lds = 0;
-    int rc = step_fused_check(c, m, &grid, &lds);
-    if (rc)
-        return rc;
-    if (!c->rope_cos || c->rope_head_dim != m->head_dim || c->rope_max_seq < m->max_seq)
-        return Q48_ESTATE;
-    if (!c->sk_sync) {
-        if (c->capturing)
-            return Q48_ESTATE;   // allocate with one eager step first
-        if (hipMalloc(&c->sk_sync, kSkBytes) != hipSuccess) {
-            c->sk_sync = nullptr;
-            return Q48_ENOMEM;
-        }
-        c->sk_err = reinterpret_cast<int *>(reinterpret_cast<char *>(c->sk_sync) + kSkCountBytes);
-        c->sk_amax = reinterpret_cast<int64_t *>(reinterpret_cast<char *>(c->sk_sync) +
-                                                 kSkCountBytes + 256);
-        rc = launch_rc(q48_launch_zero(c, c->sk_sync, kSkBytes));
-        if (rc == Q48_OK)
-            rc = hip_rc(hipStreamSynchronize(c->stream));
-        if (rc) {
-            (void)hipFree(c->sk_sync);
-            c->sk_sync = nullptr;
-            return rc;
-        }
-    }
-    c->sk_grid = grid;
-    return launch_rc(q48_launch_step_fused(c, m, d_tokens, cap, grid, lds));
-}
-
-int q48_step_fused_status(q48_ctx *c)
-{
-    if (!c)
-        return Q48_EINVAL;
-    if (c->capturing)
-        return Q48_ESTATE;
-    if (hipStreamSynchronize(c->stream) != hipSuccess)
-        return Q48_EHIP;
-    if (!c->sk_sync)
-        return Q48_OK;
-    int err = 0;
-    if (hipMemcpy(&err, c->sk_err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
-        return Q48_EHIP;
-    if (err == 0)
-        return Q48_OK;
-    // a step that stopped early leaves its counters set: clear everything
-    int rc = launch_rc(q48_launch_zero(c, c->sk_sync, kSkBytes));
-    if (rc == Q48_OK)
-        rc = hip_rc(hipStreamSynchronize(c->stream));
-    if (rc)
-        return rc;
-    return err == 2 ? Q48_ERANGE : Q48_ETIMEOUT;
 }
 
 int q48_graph_begin(q48_ctx *c)

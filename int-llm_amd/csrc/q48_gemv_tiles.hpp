@@ -1,7 +1,6 @@
 // q48_gemv_tiles.hpp — the tile arithmetic of the decode GEMVs (k_gemv_v5,
-// k_gemv_p6) and of the persistent decode step (k_step_fused): carry-free
-// limb products of staged x against int64 or bfloat16 weight tiles, the
-// rmsnorm scalar r, and 128-bit block sums.  Included by the HIP sources of
+// k_gemv_p6): carry-free limb products of staged x against int64 or bfloat16
+// weight tiles, the rmsnorm scalar r, and 128-bit block sums.  Included by the HIP sources of
 // libintllm_hip only.
 #pragma once
 

@@ -30,11 +30,6 @@ struct q48_ctx {
     int rms_blocks;
     int64_t *smp;                // device: sampling workspace (q48_sample_ws_words)
     size_t smp_words;
-    unsigned *sk_sync;           // device: k_step_fused phase counters, then its error
-                                 // word and argmax partials (one allocation)
-    int *sk_err;
-    int64_t *sk_amax;
-    int sk_grid;                 // k_step_fused blocks (0: not planned yet)
     unsigned *attx_sync;         // device: k_attn_x barrier words and error word (zeroed)
     int attn_one_launch;         // split attention as one k_attn_x launch (default on)
     int pf_attn_mfma;            // batched-prefill attention on the matrix cores (default on)
@@ -158,7 +153,3 @@ int q48_launch_math_init(q48_ctx *c);
 int q48_launch_fp_eval(q48_ctx *c, int func, const int64_t *x,
                        const int64_t *y, int64_t *out0, int64_t *out1, int n);
 
-// one-launch decode step (q48_step.hip)
-int q48_step_fused_plan(q48_ctx *c, const q48_step_model *m, int *grid, size_t *lds);
-int q48_launch_step_fused(q48_ctx *c, const q48_step_model *m, int *tokens, int cap, int grid,
-                          size_t lds);

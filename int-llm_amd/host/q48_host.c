@@ -57,8 +57,6 @@ struct q48h_model {
                                    consumer block finishes them */
     int graph_ready;            /* the context graph holds this model's decode step */
     int graph_kind;             /* ... of this kind (step_kind) */
-    int onelaunch;              /* greedy graph decode through q48_step_fused where it
-                                   serves the model (default off: measured slower) */
     int prefetch;               /* attention warms the cache with W_o (fused modes) */
     uint16_t *wb;               /* device: bfloat16 bits of the projection matrices and
                                    lm_head, at the element offsets of w (else NULL) */
@@ -219,7 +217,6 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
     m->fused = 3;
     m->prefetch = 1;
     m->batched_prefill = 1;
-    m->onelaunch = 0;
     if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->kc, kvn * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->vc, kvn * 8)) ||
@@ -395,74 +392,13 @@ void q48h_model_set_fused(q48h_model *m, int fused)
     }
 }
 
-void q48h_model_set_onelaunch(q48h_model *m, int on)
-{
-    if (m && m->onelaunch != (on != 0)) {
-        m->onelaunch = on != 0;
-        drop_graph(m);
-    }
-}
-
-/* the model as q48_step_fused reads it */
-static void step_model_of(const q48h_model *m, q48_step_model *sm)
-{
-    const q48h_config *c = &m->c;
-    memset(sm, 0, sizeof *sm);
-    sm->wfmt = m->bf16 ? 1 : 0;
-    sm->wmat = m->bf16 ? (const void *)m->wb : (const void *)m->w;
-    sm->w = m->w;
-    sm->off_embed = m->off_embed;
-    sm->off_norm = m->off_norm;
-    sm->off_lm = m->off_lm;
-    sm->off_layers = m->off_layers;
-    sm->layer_elems = m->layer_elems;
-    sm->lo_an = m->lo_an;
-    sm->lo_fn = m->lo_fn;
-    sm->lo_qkv = m->lo_qkv;
-    sm->lo_wo = m->lo_wo;
-    sm->lo_gu = m->lo_gu;
-    sm->lo_wd = m->lo_wd;
-    sm->hidden = m->hidden;
-    sm->qkv = m->qkv;
-    sm->attn = m->attn;
-    sm->h_ffn = m->h_ffn;
-    sm->logits = m->logits;
-    sm->s_attn = m->s_attn;
-    sm->s_ffn = m->s_ffn;
-    sm->kcache = m->kc;
-    sm->vcache = m->vc;
-    sm->n_layers = c->n_layers;
-    sm->dim = c->dim;
-    sm->n_heads = c->n_heads;
-    sm->n_kv_heads = c->n_kv_heads;
-    sm->head_dim = c->head_dim;
-    sm->ffn = c->ffn;
-    sm->vocab = c->vocab;
-    sm->max_seq = c->max_seq;
-}
-
 /* How a graph-replayed decode step at pos runs: 0 the fused launches with
  * single-block attention, 1 the same with split attention (from
- * q48_attn_split_min), 2 one q48_step_fused launch (greedy, mode 3, a served
- * shape, positions below both limits). */
+ * q48_attn_split_min). */
 static int step_kind(q48h_model *m, int pos)
 {
-    const int split = q48_attn_split_min();
-    if (pos >= split)
-        return 1;
-    if (m->onelaunch && !m->record && m->fused == 3 && m->temperature < Q48_ONE / 100 &&
-        split <= q48_step_fused_max_pos()) {
-        q48_step_model sm;
-        step_model_of(m, &sm);
-        if (q48_step_fused_supported(m->ctx, &sm))
-            return 2;
-    }
-    return 0;
-}
-
-int q48h_step_onelaunch_active(q48h_model *m, int pos)
-{
-    return m && step_kind(m, pos) == 2;
+    (void)m;
+    return pos >= q48_attn_split_min() ? 1 : 0;
 }
 
 void q48h_model_set_prefetch(q48h_model *m, int on)
@@ -1183,15 +1119,9 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
 {
     q48_ctx *x = m->ctx;
     const int kind = step_kind(m, pos);
-    q48_step_model sm;
-    step_model_of(m, &sm);
     TRY(q48_step_mode(x, 1));
     int rc = q48_step_set(x, token, pos);
-    if (rc == Q48_OK && kind == 2) {
-        rc = q48_step_fused(x, &sm, m->d_tokens, m->c.max_seq);
-        if (rc == Q48_OK)
-            rc = q48_step_fused_status(x);
-    } else if (rc == Q48_OK) {
+    if (rc == Q48_OK) {
         rc = enqueue_forward(m, token, pos);
         if (rc == Q48_OK && m->record)
             rc = q48_record_step(x, m->logits, m->c.vocab, m->rec, m->rec_cap);
@@ -1200,9 +1130,8 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
         if (rc == Q48_OK)
             rc = q48_sync(x);
     }
-    /* attention picks its kernels by position (split from q48_attn_split_min)
-     * and the one-launch step serves the positions below it: recapture when
-     * the step changes kind */
+    /* attention picks its kernels by position (split from q48_attn_split_min):
+     * recapture when the step changes kind */
     if (rc == Q48_OK && m->graph_ready && (m->graph_kind != kind || m->graph_rec != m->record)) {
         rc = q48_graph_drop(x);
         m->graph_ready = 0;
@@ -1210,16 +1139,11 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
     if (rc == Q48_OK && !m->graph_ready) {
         rc = q48_graph_begin(x);
         if (rc == Q48_OK) {
-            int rc1;
-            if (kind == 2) {
-                rc1 = q48_step_fused(x, &sm, m->d_tokens, m->c.max_seq);
-            } else {
-                rc1 = enqueue_forward(m, token, pos);
-                if (rc1 == Q48_OK && m->record)
-                    rc1 = q48_record_step(x, m->logits, m->c.vocab, m->rec, m->rec_cap);
-                if (rc1 == Q48_OK)
-                    rc1 = select_token_step(m);
-            }
+            int rc1 = enqueue_forward(m, token, pos);
+            if (rc1 == Q48_OK && m->record)
+                rc1 = q48_record_step(x, m->logits, m->c.vocab, m->rec, m->rec_cap);
+            if (rc1 == Q48_OK)
+                rc1 = select_token_step(m);
             rc = q48_graph_end(x);
             if (rc1)
                 rc = rc1;
@@ -1288,8 +1212,6 @@ static int decode_graph_run(q48h_model *m, int token, int start_pos, int n, int 
     if (start_pos < B && start_pos + n > B)
         k = B - start_pos;
     TRY(q48_graph_launch(m->ctx, k - 1));
-    if (m->graph_kind == 2)
-        TRY(q48_step_fused_status(m->ctx));
     TRY(q48_memcpy_d2h(m->ctx, out_tokens, m->d_tokens, (size_t)k * sizeof(int)));
     double dt = now_s() - t0;
     if (step_hash)

@@ -133,13 +133,6 @@ int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_to
  * each block of the consuming GEMV finishes them. */
 void q48h_model_set_fused(q48h_model *m, int fused);
 
-/* Greedy graph-replayed decode (q48h_decode_graph) in mode 3 runs each step
- * as one persistent launch (q48_step_fused) at the positions and shapes it
- * serves, else the fused launches.  On by default; the bits do not depend on
- * it.  q48h_step_onelaunch_active tells whether a step at pos would. */
-void q48h_model_set_onelaunch(q48h_model *m, int on);
-int q48h_step_onelaunch_active(q48h_model *m, int pos);
-
 /* In the fused modes, have each layer's attention launch also read that
  * layer's W_o on the idle compute units (q48_attn_decode_rope_prefetch), so
  * the O projection finds it in the device-side cache.  On by default; the

@@ -451,9 +451,7 @@ HOST_SIGNATURES = {
                           C.POINTER(Stats)], C.c_int),
     "q48h_model_set_fused": ([_P, _I], None),
     "q48h_model_set_prefetch": ([_P, _I], None),
-    "q48h_model_set_onelaunch": ([_P, _I], None),
     "q48h_read_logits": ([_P, _P], C.c_int),
-    "q48h_step_onelaunch_active": ([_P, _I], C.c_int),
     "q48h_model_set_bf16": ([_P, _I], C.c_int),
     "q48h_model_set_sampling": ([_P, C.c_int64, _I, C.c_int64, C.c_uint64], C.c_int),
     "q48h_model_set_batched_prefill": ([_P, _I], None),
@@ -579,19 +577,11 @@ class HostModel:
         host_lib().q48h_model_set_prefetch(self.h, int(bool(on)))
 
 
-    def set_onelaunch(self, on: bool):
-        """Greedy graph decode as one persistent launch per step where served."""
-        host_lib().q48h_model_set_onelaunch(self.h, int(bool(on)))
-
     def read_logits(self) -> np.ndarray:
         """The logits of the last step run on the device."""
         out = np.empty(self.cfg.vocab, dtype=np.int64)
         check("q48h_read_logits", host_lib().q48h_read_logits(self.h, out.ctypes.data))
         return out
-
-    def onelaunch_active(self, pos: int) -> bool:
-        """True when a graph-replayed step at pos runs as one launch."""
-        return bool(host_lib().q48h_step_onelaunch_active(self.h, int(pos)))
 
     def set_bf16(self, on: bool):
         """Read the projection matrices and lm_head as bfloat16 bits (mode 3)."""
