@@ -783,16 +783,14 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
         TRY(q48_rmsnorm_gemv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an,
                              dim + 2 * kvd, dim));
     }
-    /* the attention's spare blocks warm the cache with W_o, read next (in
-     * the format the next GEMV reads) */
+    /* with bfloat16-resident weights the attention's spare blocks warm the
+     * cache with W_o, read next (1.4751 against 1.4779 ms per TinyLlama-shape
+     * token).  int64 weights are read with non-temporal loads, and warming
+     * them measured slower (1.8436 against 1.8234). */
     if (m->prefetch && bb)
         TRY(q48_attn_decode_rope_prefetch(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
                                           c->n_kv_heads, hd, c->max_seq, bb + m->lo_wo,
                                           (size_t)dim * dim * 2));
-    else if (m->prefetch)
-        TRY(q48_attn_decode_rope_prefetch(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
-                                          c->n_kv_heads, hd, c->max_seq, b + m->lo_wo,
-                                          (size_t)dim * dim * 8));
     else
         TRY(q48_attn_decode_rope(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
                                  c->n_kv_heads, hd, c->max_seq));

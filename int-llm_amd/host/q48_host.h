@@ -133,10 +133,11 @@ int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_to
  * each block of the consuming GEMV finishes them. */
 void q48h_model_set_fused(q48h_model *m, int fused);
 
-/* In the fused modes, have each layer's attention launch also read that
- * layer's W_o on the idle compute units (q48_attn_decode_rope_prefetch), so
- * the O projection finds it in the device-side cache.  On by default; the
- * bits do not depend on it. */
+/* In the fused modes with bfloat16-resident weights, have each layer's
+ * attention launch also read that layer's W_o on the idle compute units
+ * (q48_attn_decode_rope_prefetch), so the O projection finds it in the
+ * device-side cache.  On by default; int64 weights are never warmed (the
+ * GEMVs read them with non-temporal loads).  The bits do not depend on it. */
 void q48h_model_set_prefetch(q48h_model *m, int on);
 
 /* Mode 3 with the projection matrices and lm_head read as bfloat16 bits
