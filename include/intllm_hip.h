@@ -231,6 +231,35 @@ int q48_attn_decode_rope_prefetch(q48_ctx *ctx, int64_t *out, const int64_t *q,
                                   int n_kv, int head_dim, int max_seq, const void *prefetch,
                                   size_t prefetch_bytes);
 
+/* The decode layer's first half split the other way: the projection's
+ * epilogue does RoPE and the KV store, so that attention starts from the
+ * cache.  q48_norm_gemv_rope_kv: qkv = W . rmsnorm(x, norm_w) (statistics as
+ * partial sums, see Q48_STATS_WORDS; rmsnorm and matmul_vec,
+ * llama_int.c:1048-1058, 1014-1046, 1384-1389) with W the q, k and v
+ * projections stacked ([(n_heads + 2 n_kv) head_dim][K]), then rope_apply on
+ * the q and k heads (llama_int.c:997-1008, 1392-1395) and k, v stored in the
+ * caches at pos (llama_int.c:1414-1416).  qkv receives every row, q and k
+ * rotated.  Needs q48_rope_init(head_dim, >= max_seq), head_dim 32, 64 or
+ * 128.  In step mode pos is read from the device-side state. */
+int q48_norm_gemv_rope_kv(q48_ctx *ctx, int64_t *qkv, const int64_t *W, const int64_t *x,
+                          const int64_t *norm_w, const int64_t *stats, int64_t *kcache,
+                          int64_t *vcache, int layer, int pos, int n_heads, int n_kv,
+                          int head_dim, int max_seq, int K);
+/* q48_norm_gemv_rope_kv on bfloat16 weights (the bfloat16 section's rules). */
+int q48_norm_gemv_rope_kv_bf16(q48_ctx *ctx, int64_t *qkv, const uint16_t *W,
+                               const int64_t *x, const int64_t *norm_w, const int64_t *stats,
+                               int64_t *kcache, int64_t *vcache, int layer, int pos,
+                               int n_heads, int n_kv, int head_dim, int max_seq, int K);
+/* Attention of one token over the cache (llama_int.c:1060-1072, 1502-1529)
+ * after q48_norm_gemv_rope_kv: q rotated, the key and value at pos already
+ * in the caches.  max_seq <= 4096; prefetch (16-byte aligned, may be NULL)
+ * as in q48_attn_decode_rope_prefetch.  Same bits as q48_attn_decode_rope on
+ * the unrotated inputs. */
+int q48_attn_decode_cached(q48_ctx *ctx, int64_t *out, const int64_t *q, int64_t *kcache,
+                           int64_t *vcache, int layer, int pos, int n_heads, int n_kv,
+                           int head_dim, int max_seq, const void *prefetch,
+                           size_t prefetch_bytes);
+
 /* The same fusions with the rmsnorm statistics computed once per vector:
  * r = fp_inv_sqrt((int64)((sum x^2 >> 48) / dim) + 2814749767), the scalar
  * of rmsnorm (llama_int.c:1049-1055), lives in device memory (*r) and the

@@ -1206,3 +1206,88 @@ int q48_gemv_residual_stats_bf16(q48_ctx *c, int64_t *acc, const uint16_t *W, co
                       gemv_bytes_bf16(M, K, M));
 }
 
+
+// ---- projection with RoPE + KV store, attention over the cache ---------------
+
+namespace {
+// Shape and state checks shared by the two q48_norm_gemv_rope_kv forms.
+int rope_kv_args(q48_ctx *c, int64_t *kcache, int64_t *vcache, int layer, int pos, int n_heads,
+                 int n_kv, int head_dim, int max_seq, int K, q48_ropekv *rk, int *M)
+{
+    if (!kcache || !vcache || !heads_ok(n_heads, n_kv, head_dim) || layer < 0 ||
+        max_seq <= 0 || K <= 0 || K > kMaxDim ||
+        (long long)(n_heads + 2LL * n_kv) * head_dim > kMaxDim)
+        return Q48_EINVAL;
+    if (!c->rope_cos || head_dim != c->rope_head_dim || max_seq > c->rope_max_seq)
+        return Q48_ESTATE;
+    if (pos < 0 || pos >= max_seq)
+        return Q48_ERANGE;
+    *rk = q48_ropekv{kcache, vcache, c->rope_cos, c->rope_sin,
+                     c->step_mode ? c->d_step + 1 : nullptr, pos, layer, max_seq, n_heads,
+                     n_kv, head_dim};
+    *M = (n_heads + 2 * n_kv) * head_dim;
+    return Q48_OK;
+}
+} // namespace
+
+int q48_norm_gemv_rope_kv(q48_ctx *c, int64_t *qkv, const int64_t *W, const int64_t *x,
+                          const int64_t *norm_w, const int64_t *stats, int64_t *kcache,
+                          int64_t *vcache, int layer, int pos, int n_heads, int n_kv,
+                          int head_dim, int max_seq, int K)
+{
+    if (!c || bad_ptrs(qkv, W, x) || !norm_w || !stats || !q48_gemv_v2_ok(W, K))
+        return Q48_EINVAL;
+    q48_ropekv rk;
+    int M;
+    int rc = rope_kv_args(c, kcache, vcache, layer, pos, n_heads, n_kv, head_dim, max_seq, K,
+                          &rk, &M);
+    if (rc)
+        return rc;
+    int prc;
+    q48_ctx::ProfRec *pr = prof_begin(c, gemv_bytes(M, K, M), &prc);
+    if (prc)
+        return prc;
+    return prof_end(c, pr,
+                    launch_rc(q48_launch_gemv_rope_kv(c, qkv, W, x, norm_w, stats, &rk, M, K)));
+}
+
+int q48_norm_gemv_rope_kv_bf16(q48_ctx *c, int64_t *qkv, const uint16_t *W, const int64_t *x,
+                               const int64_t *norm_w, const int64_t *stats, int64_t *kcache,
+                               int64_t *vcache, int layer, int pos, int n_heads, int n_kv,
+                               int head_dim, int max_seq, int K)
+{
+    if (!c || !norm_w || !stats || bad_bf16(qkv, W, x, norm_w, stats, K))
+        return Q48_EINVAL;
+    q48_ropekv rk;
+    int M;
+    int rc = rope_kv_args(c, kcache, vcache, layer, pos, n_heads, n_kv, head_dim, max_seq, K,
+                          &rk, &M);
+    if (rc)
+        return rc;
+    int prc;
+    q48_ctx::ProfRec *pr = prof_begin(c, gemv_bytes_bf16(M, K, M), &prc);
+    if (prc)
+        return prc;
+    const int lrc = q48_launch_gemv_rope_kv_bf16(c, qkv, W, x, norm_w, stats, &rk, M, K);
+    return prof_end(c, pr, lrc < 0 ? Q48_EINVAL : launch_rc(lrc));
+}
+
+int q48_attn_decode_cached(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
+                           int64_t *vcache, int layer, int pos, int n_heads, int n_kv,
+                           int head_dim, int max_seq, const void *prefetch,
+                           size_t prefetch_bytes)
+{
+    if (!c || !out || !q || !kcache || !vcache || !heads_ok(n_heads, n_kv, head_dim) ||
+        layer < 0 || max_seq <= 0 || max_seq > q48_att_lds_max() ||
+        (prefetch && ((uintptr_t)prefetch & 15)))
+        return Q48_EINVAL;
+    // the score scale lives after the sine table
+    if (!c->rope_cos || head_dim != c->rope_head_dim || max_seq > c->rope_max_seq)
+        return Q48_ESTATE;
+    if (pos < 0 || pos >= max_seq)
+        return Q48_ERANGE;
+    const int *dp = c->step_mode ? c->d_step + 1 : nullptr;
+    return launch_rc(q48_launch_attn_cached(c, out, q, kcache, vcache, layer, dp, pos, n_heads,
+                                            n_kv, head_dim, max_seq, prefetch,
+                                            prefetch ? prefetch_bytes : 0));
+}

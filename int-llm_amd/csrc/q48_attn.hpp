@@ -66,7 +66,13 @@ constexpr int ATT_LDS_MAX = 4096;   // positions whose scores fit in LDS (32 KiB
 // (k_new, v_new, cos_t, sin_t unused); the rest is the same arithmetic.
 // CIN: q, k_new and v_new are read with agent-coherent loads (written earlier
 // in the same kernel by other compute units, e.g. the persistent decode step).
-template <int HD, int SMAX, bool COH, bool PRE = false, bool CIN = false, int NT = 256>
+// ROT (decode over the cache): like PRE (q_h rotated, k and v at pos already
+// stored by the projection's epilogue), and q and the K rows of the first
+// two passes (rows up to 2 NT / 8 - 1, clamped to max_seq - 1: in bounds
+// whatever the position) go out before the device-resident position is
+// read, so that its round trip overlaps theirs.
+template <int HD, int SMAX, bool COH, bool PRE = false, bool CIN = false, int NT = 256,
+          bool ROT = false>
 __device__ __forceinline__ void attn_v3_head(
     int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
     int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
@@ -80,15 +86,18 @@ __device__ __forceinline__ void attn_v3_head(
     __shared__ int64_t red[NT / 64], red2[NT / 64];
     __shared__ int64_t part[NT];
     __shared__ int64_t sc[SMAX];
-    if (d_pos)
-        pos = *d_pos;
-    if (pos < 0 || pos >= max_seq)
-        return;   // uniform over the block: no barrier is skipped by part of it
+    if (!ROT) {
+        if (d_pos)
+            pos = *d_pos;
+        if (pos < 0 || pos >= max_seq)
+            return;   // uniform over the block: no barrier is skipped by part of it
+    }
     const int tid = threadIdx.x;
     const int group = n_heads / n_kv, kh = h / group;
     const size_t kvd = (size_t)n_kv * HD;
     const size_t base = (size_t)layer * max_seq;
-    const int S = pos + 1, half = HD / 2;
+    int S = pos + 1;
+    const int half = HD / 2;
     const int g = tid >> 3, l8 = tid & 7;
     const int64_t scale = *scale_p;
 
@@ -97,7 +106,29 @@ __device__ __forceinline__ void attn_v3_head(
         return reinterpret_cast<const ulonglong2 *>(kb0 + (size_t)min(t, S - 1) * kvd);
     };
     ulonglong2 ka[DP2], kb[DP2];
-    if constexpr (PRE) {
+    if constexpr (ROT) {
+        const int j = min(tid, HD - 1);
+        const int64_t qv = q[(size_t)h * HD + j];
+        const auto *r0 = reinterpret_cast<const ulonglong2 *>(kb0 + (size_t)min(g, max_seq - 1) * kvd);
+        const auto *r1 =
+            reinterpret_cast<const ulonglong2 *>(kb0 + (size_t)min(g + NG, max_seq - 1) * kvd);
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            ka[d] = r0[d];
+#pragma unroll
+        for (int d = 0; d < DP2; ++d)
+            kb[d] = r1[d];
+        // a scalar load (constant address space): no vector-memory wait,
+        // which would cover the K rows, is needed for it
+        typedef const __attribute__((address_space(4))) int cint;
+        if (d_pos)
+            pos = *(cint *)d_pos;
+        if (pos < 0 || pos >= max_seq)
+            return;   // uniform over the block: no barrier is skipped by part of it
+        S = pos + 1;
+        qs[j] = qv;
+        __syncthreads();
+    } else if constexpr (PRE) {
         const int j = min(tid, HD - 1);
         const int64_t qv = q[(size_t)h * HD + j];
         const int64_t kv = kcache[(base + pos) * kvd + (size_t)kh * HD + j];
@@ -161,7 +192,7 @@ __device__ __forceinline__ void attn_v3_head(
     const int64_t *qd = qs + l8 * DPL, *kd = ks + l8 * DPL;
     int64_t mx = INT64_MIN;
     auto score = [&](const ulonglong2 (&kr)[DP2], int t) {
-        const bool own = t == pos;
+        const bool own = !ROT && t == pos;
         q48_u128 dot = 0;
 #pragma unroll
         for (int d = 0; d < DP2; ++d) {
@@ -224,7 +255,7 @@ __device__ __forceinline__ void attn_v3_head(
         for (int u = 0; u < VB; ++u) {
             const int t = sl + SL * (i0 + u);
             if (t < S)
-                acc += (uint64_t)q48_mul(sc[t], t == pos ? vs[d] : vv[u]);
+                acc += (uint64_t)q48_mul(sc[t], !ROT && t == pos ? vs[d] : vv[u]);
         }
     };
     for (int i0 = 0; sl + SL * i0 < S; i0 += 2 * VB) {

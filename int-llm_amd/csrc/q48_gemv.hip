@@ -226,7 +226,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                                                     int64_t *__restrict__ r_out,
                                                     uint64_t *__restrict__ rms_part,
                                                     int *__restrict__ rms_count,
-                                                    int M, int K, int seg)
+                                                    int M, int K, int seg, const q48_ropekv rk)
 {
     extern __shared__ __align__(16) uint32_t xs[];   // 3 limbs per staged x
     __shared__ uint64_t red_lo[NW], red_hi[NW];
@@ -244,10 +244,27 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     const int k0 = wave * seg;
     const int kn = max(0, min(seg, K - k0));
 
-    // row of group g (EPI 2: gate rows 4b+g, then up rows ffn+4b+g-4)
+    // row of group g (EPI 2: gate rows 4b+g, then up rows ffn+4b+g-4; EPI 5:
+    // the RoPE pairs i = j0 + (g & 3) and i + hd / 2 of head hh, hd / 8
+    // blocks per head)
     const int pr = blockIdx.x * 4 + (g & 3);
-    const int row = EPI == 2 ? (g < 4 ? pr : ffn + pr) : row0 + g;
+    int hh = 0, j0 = 0;
+    if (EPI == 5) {
+        const int bph = rk.hd >> 3;
+        hh = blockIdx.x / bph;
+        j0 = 4 * (blockIdx.x - hh * bph);
+    }
+    const int row = EPI == 2   ? (g < 4 ? pr : ffn + pr)
+                    : EPI == 5 ? hh * rk.hd + j0 + (g & 3) + (g < 4 ? 0 : rk.hd >> 1)
+                               : row0 + g;
     const bool live = EPI == 2 ? pr < ffn : row < M;
+    // EPI 5: the position, read first (a scalar load through the constant
+    // address space, so that no vector-memory wait has to cover it)
+    int p5 = 0;
+    if constexpr (EPI == 5) {
+        typedef const __attribute__((address_space(4))) int cint;
+        p5 = rk.d_pos ? *(cint *)rk.d_pos : rk.pos;
+    }
     // rows past the end read row 0 (in bounds, never accumulated)
     constexpr int ES = WFmt<WT>::ES, SEGC = WFmt<WT>::TE * NTF;
     const ulonglong2 *w2 = reinterpret_cast<const ulonglong2 *>(
@@ -350,6 +367,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         wa[u] = ld_wtile<WT>(&wt[min(u, tlast) * tstep]);
     // nothing that waits on a load may be scheduled above this point
     __builtin_amdgcn_sched_barrier(0);
+
+    // EPI 5: this block's four cos / sin pairs at the position, issued
+    // behind the first weight tiles and used only by the epilogue; every
+    // lane loads (lane & 3's pair, clamped row) so that the loads stay here
+    int64_t c5 = 0, s5 = 0;
+    if constexpr (EPI == 5) {
+        const int pc = min(max(p5, 0), rk.max_seq - 1), half = rk.hd >> 1;
+        const size_t at = (size_t)pc * half + j0 + (lane & 3);
+        c5 = rk.cos_t[at];
+        s5 = rk.sin_t[at];
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     if (PRO == 3) {
         // every wave adds the partials (cheap; it keeps their loads first in
@@ -588,6 +617,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     if (EPI == 0) {
         if (rr < M)
             y[rr] = v;
+    } else if (EPI == 5) {
+        // threads 0-3 hold dims i = j0 + tid of head hh, 4-7 dims i + hd / 2;
+        // RoPE of the q and k heads (rope_apply, llama_int.c:997-1008), then
+        // k and v to the caches at pos (llama_int.c:1414-1416)
+        const int half = rk.hd >> 1, d = j0 + (tid & 3) + (tid < 4 ? 0 : half);
+        const int64_t o = __shfl_xor(v, 4, 64);
+        int64_t r5 = v;
+        if (hh < rk.n_heads + rk.n_kv)
+            r5 = tid < 4 ? (int64_t)((uint64_t)q48_mul(v, c5) - (uint64_t)q48_mul(o, s5))
+                         : (int64_t)((uint64_t)q48_mul(v, c5) + (uint64_t)q48_mul(o, s5));
+        const int rw = hh * rk.hd + d;
+        if (rw < M)
+            y[rw] = r5;
+        if (hh >= rk.n_heads && rw < M && p5 >= 0 && p5 < rk.max_seq) {
+            const bool isk = hh < rk.n_heads + rk.n_kv;
+            const int kh = hh - rk.n_heads - (isk ? 0 : rk.n_kv);
+            int64_t *cache = isk ? rk.kc : rk.vc;
+            cache[((size_t)rk.layer * rk.max_seq + p5) * ((size_t)rk.n_kv * rk.hd) +
+                  (size_t)kh * rk.hd + d] = r5;
+        }
     } else if (EPI == 1) {
         if (rr < M)
             y[rr] = (int64_t)((uint64_t)yres + (uint64_t)v);
@@ -933,8 +982,10 @@ static int p6_grid(const q48_ctx *c, int groups)
 
 template <int PRO, int EPI>
 static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
-                     const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M, int K)
+                     const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M, int K,
+                     const q48_ropekv *rk = nullptr)
 {
+    const q48_ropekv rkv = rk ? *rk : q48_ropekv{};
     constexpr int NW = 8;
     // segment: K / NW rounded up to a multiple of 16 elements
     const int seg = ((K + NW - 1) / NW + 15) / 16 * 16;
@@ -963,15 +1014,15 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
     if (al && K == NW * seg && seg == 16 * 16)
         hipLaunchKernelGGL((k_gemv_v5<NW, 4, PRO, EPI, 16>), dim3(blocks), dim3(64 * NW), lds,
                            c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
-                           M, K, seg);
+                           M, K, seg, rkv);
     else if (al && K == NW * seg && seg == 16 * 44)
         hipLaunchKernelGGL((k_gemv_v5<NW, 6, PRO, EPI, 44>), dim3(blocks), dim3(64 * NW), lds,
                            c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
-                           M, K, seg);
+                           M, K, seg, rkv);
     else
         hipLaunchKernelGGL((k_gemv_v5<NW, 16, PRO, EPI, 0>), dim3(blocks), dim3(64 * NW), lds,
                            c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
-                           M, K, seg);
+                           M, K, seg, rkv);
     return (int)hipGetLastError();
 }
 
@@ -982,8 +1033,9 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
 template <int PRO, int EPI, int NTF>
 static int launch_b16_ntf(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
                           const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
-                          int K)
+                          int K, const q48_ropekv *rk = nullptr)
 {
+    const q48_ropekv rkv = rk ? *rk : q48_ropekv{};
     // the window: every tile of the segment in flight when it divides no
     // other way (11 tiles for K = 5632), else 4
     constexpr int NW = 8, UNR = NTF < 4 ? NTF : NTF % 4 == 0 ? 4 : NTF;
@@ -1000,25 +1052,27 @@ static int launch_b16_ntf(q48_ctx *c, int64_t *y, const uint16_t *W, const int64
     }
     hipLaunchKernelGGL((k_gemv_v5<NW, UNR, PRO, EPI, NTF, 1>), dim3(blocks), dim3(64 * NW), lds,
                        c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count, M,
-                       K, seg);
+                       K, seg, rkv);
     return (int)hipGetLastError();
 }
 
 template <int PRO, int EPI>
 static int launch_b16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
-                      const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M, int K)
+                      const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M, int K,
+                      const q48_ropekv *rk = nullptr)
 {
+    const q48_ropekv rkv = rk ? *rk : q48_ropekv{};
     switch (K) {
     case 512:
-        return launch_b16_ntf<PRO, EPI, 1>(c, y, W, x, norm_w, r_in, r_out, M, K);
+        return launch_b16_ntf<PRO, EPI, 1>(c, y, W, x, norm_w, r_in, r_out, M, K, rk);
     case 1024:
-        return launch_b16_ntf<PRO, EPI, 2>(c, y, W, x, norm_w, r_in, r_out, M, K);
+        return launch_b16_ntf<PRO, EPI, 2>(c, y, W, x, norm_w, r_in, r_out, M, K, rk);
     case 2048:
-        return launch_b16_ntf<PRO, EPI, 4>(c, y, W, x, norm_w, r_in, r_out, M, K);
+        return launch_b16_ntf<PRO, EPI, 4>(c, y, W, x, norm_w, r_in, r_out, M, K, rk);
     case 5632:
         // all 11 tiles in flight: registers allow it without the norm prologue
         if constexpr (PRO == 0)
-            return launch_b16_ntf<PRO, EPI, 11>(c, y, W, x, norm_w, r_in, r_out, M, K);
+            return launch_b16_ntf<PRO, EPI, 11>(c, y, W, x, norm_w, r_in, r_out, M, K, rk);
         [[fallthrough]];
     default: {
         // other K (a multiple of 512): batches of 4 tiles in a loop (an
@@ -1029,7 +1083,7 @@ static int launch_b16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *
         const int blocks = EPI == 2 ? (M / 2 + 3) / 4 : (M + V4_RB - 1) / V4_RB;
         hipLaunchKernelGGL((k_gemv_v5<NW, 4, PRO, EPI, 0, 1>), dim3(blocks), dim3(64 * NW), lds,
                            c->stream, y, W, x, norm_w, r_in, r_out, c->rms_part, c->rms_count,
-                           M, K, seg);
+                           M, K, seg, rkv);
         return (int)hipGetLastError();
     }
     }
@@ -1200,6 +1254,20 @@ int q48_launch_gemv_fused_bf16(q48_ctx *c, int64_t *y, const uint16_t *W, const 
     if (epi == 4)
         return launch_b16<0, 4>(c, y, W, x, nullptr, nullptr, r_out, M, K);
     return launch_b16<0, 0>(c, y, W, x, nullptr, nullptr, nullptr, M, K);
+}
+
+int q48_launch_gemv_rope_kv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                            const int64_t *norm_w, const int64_t *stats,
+                            const q48_ropekv *rk, int M, int K)
+{
+    return launch_v4<3, 5>(c, y, W, x, norm_w, stats, nullptr, M, K, rk);
+}
+
+int q48_launch_gemv_rope_kv_bf16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
+                                 const int64_t *norm_w, const int64_t *stats,
+                                 const q48_ropekv *rk, int M, int K)
+{
+    return launch_b16<3, 5>(c, y, W, x, norm_w, stats, nullptr, M, K, rk);
 }
 
 // int64 -> bfloat16 bits where exact: b is the candidate with 8 significant

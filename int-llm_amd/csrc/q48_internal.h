@@ -67,6 +67,24 @@ bool q48_gemv_bf16_ok(int K);
 int q48_launch_gemv_fused_bf16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
                                const int64_t *norm_w, const int64_t *r_in, int64_t *r_out, int M,
                                int K, int pro, int epi);
+// Operands of the q|k|v projection's RoPE + KV-store epilogue (epi 5): the
+// projection's rows are (n_heads + 2 n_kv) heads of hd, q then k then v.
+struct q48_ropekv {
+    int64_t *kc, *vc;               // caches [L][max_seq][n_kv][hd]
+    const int64_t *cos_t, *sin_t;   // RoPE tables [rope_max_seq][hd / 2]
+    const int *d_pos;               // device position (graph replay), or null: pos
+    int pos, layer, max_seq, n_heads, n_kv, hd;
+};
+// rmsnorm (r from the partial sums at stats) + q|k|v projection + RoPE of
+// the q and k heads + k and v stored at pos; y gets every row (q and k
+// rotated).  The int64 form needs q48_gemv_v2_ok, the bfloat16 one
+// q48_gemv_bf16_ok.
+int q48_launch_gemv_rope_kv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
+                            const int64_t *norm_w, const int64_t *stats,
+                            const q48_ropekv *rk, int M, int K);
+int q48_launch_gemv_rope_kv_bf16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *x,
+                                 const int64_t *norm_w, const int64_t *stats,
+                                 const q48_ropekv *rk, int M, int K);
 // out[i] = the bfloat16 bits of in[i] where exact; *inexact = 1 otherwise
 int q48_launch_bf16_pack(q48_ctx *c, uint16_t *out, const int64_t *in, size_t n, int *inexact);
 int q48_launch_rms_inv(q48_ctx *c, int64_t *r_out, int64_t *out, const int64_t *x,
@@ -105,6 +123,14 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
                        const void *prefetch, size_t prefetch_bytes,
                        int64_t *ws_ext = nullptr, size_t ws_ext_bytes = 0,
                        unsigned *sync_ext = nullptr);
+// Decode attention over the cache (k_attn_v3's ROT form): q rotated, k and v
+// at pos already stored (q48_launch_gemv_rope_kv); head_dim 32, 64 or 128,
+// max_seq <= q48_att_lds_max().  Spare blocks warm the cache with
+// `prefetch` as in q48_launch_attn_v2.
+int q48_launch_attn_cached(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
+                           int64_t *vcache, int layer, const int *d_pos, int pos, int n_heads,
+                           int n_kv, int head_dim, int max_seq, const void *prefetch,
+                           size_t prefetch_bytes);
 // bytes of the split attention's workspace; of its barrier region
 size_t q48_attn_ws_bytes(int n_heads, int max_seq, int head_dim);
 size_t q48_attn_sync_bytes();

@@ -365,9 +365,10 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
 // Attention v3: k_attn_v2's computation with its memory round trips cut
 // (attn_v3_head, q48_attn.hpp).  One block of 256 threads per query head;
 // HD = 32, 64 or 128; at most ATT_LDS_MAX positions.  Blocks past n_heads
-// prefetch like k_attn_v2's.
+// prefetch like k_attn_v2's.  ROT: q rotated, k and v at pos already in the
+// cache (q48_launch_gemv_rope_kv); k_new, v_new and the RoPE tables unused.
 // ---------------------------------------------------------------------------
-template <int HD, int NT>
+template <int HD, int NT, bool ROT = false>
 __global__ __launch_bounds__(NT) void k_attn_v3(
     int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
     int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(NT) void k_attn_v3(
         asm volatile("" ::"v"(acc));
         return;
     }
-    attn_v3_head<HD, ATT_LDS_MAX, false, false, false, NT>(
+    attn_v3_head<HD, ATT_LDS_MAX, false, false, false, NT, ROT>(
         out, q, kcache, vcache, k_new, v_new, cos_t, sin_t, scale_p, layer, d_pos, pos, n_heads,
         n_kv, max_seq, (int)blockIdx.x);
 }
@@ -1372,6 +1373,33 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
         ATT_LAUNCH(0, 0);
 #undef ATT_LAUNCH
 #undef ATT3_LAUNCH
+    return (int)hipGetLastError();
+}
+
+int q48_launch_attn_cached(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
+                           int64_t *vcache, int layer, const int *d_pos, int pos, int n_heads,
+                           int n_kv, int head_dim, int max_seq, const void *prefetch,
+                           size_t prefetch_bytes)
+{
+    // prefetch blocks: one per compute unit the heads leave idle (as
+    // q48_launch_attn_v2)
+    const size_t pf_n16 = prefetch ? prefetch_bytes / 16 : 0;
+    const int pf_blocks = pf_n16 ? (c->cu_count > n_heads ? c->cu_count - n_heads : 1) : 0;
+    const int64_t *scale_p = c->rope_sin + (size_t)c->rope_max_seq * (c->rope_head_dim / 2);
+#define ATTC_LAUNCH(HD)                                                                       \
+    hipLaunchKernelGGL((k_attn_v3<HD, ATT_V3_NT, true>), dim3(n_heads + pf_blocks),           \
+                       dim3(ATT_V3_NT), 0, c->stream, out, q, kcache, vcache, nullptr, nullptr, \
+                       nullptr, nullptr, scale_p, layer, d_pos, pos, n_heads, n_kv, max_seq,  \
+                       (const ulonglong2 *)prefetch, pf_n16)
+    if (head_dim == 64)
+        ATTC_LAUNCH(64);
+    else if (head_dim == 32)
+        ATTC_LAUNCH(32);
+    else if (head_dim == 128)
+        ATTC_LAUNCH(128);
+    else
+        return (int)hipErrorInvalidValue;
+#undef ATTC_LAUNCH
     return (int)hipGetLastError();
 }
 

@@ -58,6 +58,9 @@ struct q48h_model {
     int graph_ready;            /* the context graph holds this model's decode step */
     int graph_kind;             /* ... of this kind (step_kind) */
     int prefetch;               /* attention warms the cache with W_o (fused modes) */
+    int rope_gemv;              /* mode 3 below the split position: RoPE and the KV
+                                   store in the q|k|v projection, attention from the
+                                   cache (q48_norm_gemv_rope_kv, q48_attn_decode_cached) */
     uint16_t *wb;               /* device: bfloat16 bits of the projection matrices and
                                    lm_head, at the element offsets of w (else NULL) */
     int bf16;                   /* mode 3 reads the matrices from wb */
@@ -216,6 +219,7 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
 
     m->fused = 3;
     m->prefetch = 1;
+    m->rope_gemv = 1;
     m->batched_prefill = 1;
     if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->kc, kvn * 8)) ||
@@ -399,6 +403,17 @@ static int step_kind(q48h_model *m, int pos)
 {
     (void)m;
     return pos >= q48_attn_split_min() ? 1 : 0;
+}
+
+void q48h_model_set_rope_gemv(q48h_model *m, int on)
+{
+    if (m && m->rope_gemv != (on != 0)) {
+        m->rope_gemv = on != 0;
+        if (m->graph_ready) {
+            q48_graph_drop(m->ctx);
+            m->graph_ready = 0;
+        }
+    }
 }
 
 void q48h_model_set_prefetch(q48h_model *m, int on)
@@ -754,9 +769,21 @@ int q48h_kv_fill_synth(q48h_model *m, uint64_t seed, int npos, int threads)
 
 #define TRY(x) do { int rc_ = (x); if (rc_) return rc_; } while (0)
 
+/* Whether mode 3 runs RoPE and the KV store in the q|k|v projection and
+ * attention from the cache (single-block attention: below the split
+ * position, head_dim 32, 64 or 128, at most 4096 cached positions). */
+static int rope_in_gemv(const q48h_model *m)
+{
+    const q48h_config *c = &m->c;
+    return m->rope_gemv && m->fused == 3 &&
+           (c->head_dim == 32 || c->head_dim == 64 || c->head_dim == 128) &&
+           c->max_seq <= 4096 && c->dim % 2 == 0 && c->dim <= 12288;
+}
+
 /* transformer_layer_forward, llama_int.c:1326-1569 (exact-cache path),
  * fused: 5 launches.  rmsnorm+q|k|v, RoPE+KV store+attention, o+residual,
- * rmsnorm+gate|up+SwiGLU, down+residual. */
+ * rmsnorm+gate|up+SwiGLU, down+residual; below the split position (mode 3)
+ * rmsnorm+q|k|v+RoPE+KV store, attention from the cache, and the rest. */
 static int layer_forward_fused(q48h_model *m, int l, int pos)
 {
     const q48h_config *c = &m->c;
@@ -766,7 +793,17 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
     int64_t *q = m->qkv, *k = m->qkv + dim, *v = m->qkv + dim + kvd;
 
     const uint16_t *bb = m->bf16 ? m->wb + m->off_layers + (size_t)l * m->layer_elems : NULL;
-    if (m->fused == 3 && bb) {
+    const int cached = rope_in_gemv(m) && pos < q48_attn_split_min();
+    if (cached) {
+        if (bb)
+            TRY(q48_norm_gemv_rope_kv_bf16(x, m->qkv, bb + m->lo_qkv, m->hidden, b + m->lo_an,
+                                           m->s_attn, m->kc, m->vc, l, pos, c->n_heads,
+                                           c->n_kv_heads, hd, c->max_seq, dim));
+        else
+            TRY(q48_norm_gemv_rope_kv(x, m->qkv, b + m->lo_qkv, m->hidden, b + m->lo_an,
+                                      m->s_attn, m->kc, m->vc, l, pos, c->n_heads,
+                                      c->n_kv_heads, hd, c->max_seq, dim));
+    } else if (m->fused == 3 && bb) {
         TRY(q48_norm_gemv_stats_bf16(x, m->qkv, bb + m->lo_qkv, m->hidden, b + m->lo_an,
                                      m->s_attn, dim + 2 * kvd, dim));
     } else if (m->fused == 3) {
@@ -787,7 +824,12 @@ static int layer_forward_fused(q48h_model *m, int l, int pos)
      * cache with W_o, read next (1.4751 against 1.4779 ms per TinyLlama-shape
      * token).  int64 weights are read with non-temporal loads, and warming
      * them measured slower (1.8436 against 1.8234). */
-    if (m->prefetch && bb)
+    if (cached)
+        TRY(q48_attn_decode_cached(x, m->attn, q, m->kc, m->vc, l, pos, c->n_heads,
+                                   c->n_kv_heads, hd, c->max_seq,
+                                   m->prefetch && bb ? bb + m->lo_wo : NULL,
+                                   m->prefetch && bb ? (size_t)dim * dim * 2 : 0));
+    else if (m->prefetch && bb)
         TRY(q48_attn_decode_rope_prefetch(x, m->attn, q, m->kc, m->vc, k, v, l, pos, c->n_heads,
                                           c->n_kv_heads, hd, c->max_seq, bb + m->lo_wo,
                                           (size_t)dim * dim * 2));
@@ -1266,15 +1308,30 @@ int q48h_gemv_sweep(q48h_model *m, int reps, int *launches, double *bytes)
     int n = 0;
     double b = 0;
     const int wb16 = m->fused == 3 && m->bf16;
+    const int rq = rope_in_gemv(m);
     const double wbytes = wb16 ? 2.0 : 8.0;
 #define GB(M, K, out) (b += wbytes * (double)(M) * (K) + 8.0 * ((double)(K) + (out)), ++n)
     for (int r = 0; r < reps; ++r) {
         for (int l = 0; l < c->n_layers; ++l) {
             const int64_t *w = m->w + m->off_layers + (size_t)l * m->layer_elems;
             const uint16_t *bw = wb16 ? m->wb + m->off_layers + (size_t)l * m->layer_elems : NULL;
+            /* the q|k|v form short-context decode runs; its k and v go to
+             * the last cache row, which a decode step writes before it
+             * reads it */
+            if (wb16 && rq)
+                TRY(q48_norm_gemv_rope_kv_bf16(x, m->qkv, bw + m->lo_qkv, m->hidden,
+                                               w + m->lo_an, m->s_attn, m->kc, m->vc, l,
+                                               c->max_seq - 1, c->n_heads, c->n_kv_heads,
+                                               c->head_dim, c->max_seq, dim));
+            else if (m->fused == 3 && rq)
+                TRY(q48_norm_gemv_rope_kv(x, m->qkv, w + m->lo_qkv, m->hidden, w + m->lo_an,
+                                          m->s_attn, m->kc, m->vc, l, c->max_seq - 1,
+                                          c->n_heads, c->n_kv_heads, c->head_dim, c->max_seq,
+                                          dim));
             if (wb16) {
-                TRY(q48_norm_gemv_stats_bf16(x, m->qkv, bw + m->lo_qkv, m->hidden, w + m->lo_an,
-                                             m->s_attn, dim + 2 * kvd, dim));
+                if (!rq)
+                    TRY(q48_norm_gemv_stats_bf16(x, m->qkv, bw + m->lo_qkv, m->hidden,
+                                                 w + m->lo_an, m->s_attn, dim + 2 * kvd, dim));
                 TRY(q48_gemv_residual_stats_bf16(x, m->hidden, bw + m->lo_wo, m->attn, dim, dim,
                                                  m->s_ffn));
                 TRY(q48_norm_gemv_swiglu_stats_bf16(x, m->h_ffn, bw + m->lo_gu, m->hidden,
@@ -1282,8 +1339,9 @@ int q48h_gemv_sweep(q48h_model *m, int reps, int *launches, double *bytes)
                 TRY(q48_gemv_residual_stats_bf16(x, m->hidden, bw + m->lo_wd, m->h_ffn, dim, ffn,
                                                  m->s_attn));
             } else if (m->fused == 3) {
-                TRY(q48_norm_gemv_stats(x, m->qkv, w + m->lo_qkv, m->hidden, w + m->lo_an,
-                                        m->s_attn, dim + 2 * kvd, dim));
+                if (!rq)
+                    TRY(q48_norm_gemv_stats(x, m->qkv, w + m->lo_qkv, m->hidden, w + m->lo_an,
+                                            m->s_attn, dim + 2 * kvd, dim));
                 TRY(q48_gemv_residual_stats(x, m->hidden, w + m->lo_wo, m->attn, dim, dim,
                                             m->s_ffn));
                 TRY(q48_norm_gemv_swiglu_stats(x, m->h_ffn, w + m->lo_gu, m->hidden,

@@ -140,6 +140,14 @@ void q48h_model_set_fused(q48h_model *m, int fused);
  * GEMVs read them with non-temporal loads).  The bits do not depend on it. */
 void q48h_model_set_prefetch(q48h_model *m, int on);
 
+/* In mode 3 below the split position (q48_attn_split_min), run RoPE and the
+ * KV store in the q|k|v projection's epilogue and attention from the cache
+ * (q48_norm_gemv_rope_kv, q48_attn_decode_cached) instead of RoPE and the
+ * store inside attention (q48_attn_decode_rope).  On by default where the
+ * shapes allow it (head_dim 32, 64 or 128, max_seq <= 4096); the bits do not
+ * depend on it. */
+void q48h_model_set_rope_gemv(q48h_model *m, int on);
+
 /* Mode 3 with the projection matrices and lm_head read as bfloat16 bits
  * (the reference's .mgwc representation, llama_int.c:1906-1929): on packs a
  * device copy of them (2 bytes per weight, kept until the weights change)

@@ -75,6 +75,9 @@ ABI_SIGNATURES = {
     "q48_attn_prefill": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I],
     "q48_attn_status": [_P],
     "q48_attn_decode_rope_prefetch": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _SZ],
+    "q48_norm_gemv_rope_kv": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I],
+    "q48_norm_gemv_rope_kv_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I],
+    "q48_attn_decode_cached": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _SZ],
     "q48_rms_inv": [_P, _P, _P, _I],
     "q48_embed_rms": [_P, _P, _P, _I, _I, _P],
     "q48_norm_gemv": [_P, _P, _P, _P, _P, _P, _I, _I],
@@ -342,6 +345,21 @@ class Context:
         return check("q48_attn_decode_rope_prefetch", hip_lib().q48_attn_decode_rope_prefetch(
             self.h, out, q, kc, vc, kn, vn, layer, pos, nh, nkv, hd, max_seq, prefetch, nbytes))
 
+    def norm_gemv_rope_kv(self, qkv, W, x, norm_w, stats, kc, vc, layer, pos, nh, nkv, hd,
+                          max_seq, K):
+        return check("q48_norm_gemv_rope_kv", hip_lib().q48_norm_gemv_rope_kv(
+            self.h, qkv, W, x, norm_w, stats, kc, vc, layer, pos, nh, nkv, hd, max_seq, K))
+
+    def norm_gemv_rope_kv_bf16(self, qkv, W, x, norm_w, stats, kc, vc, layer, pos, nh, nkv,
+                               hd, max_seq, K):
+        return check("q48_norm_gemv_rope_kv_bf16", hip_lib().q48_norm_gemv_rope_kv_bf16(
+            self.h, qkv, W, x, norm_w, stats, kc, vc, layer, pos, nh, nkv, hd, max_seq, K))
+
+    def attn_decode_cached(self, out, q, kc, vc, layer, pos, nh, nkv, hd, max_seq,
+                           prefetch=None, nbytes=0):
+        return check("q48_attn_decode_cached", hip_lib().q48_attn_decode_cached(
+            self.h, out, q, kc, vc, layer, pos, nh, nkv, hd, max_seq, prefetch, nbytes))
+
     def rms_inv(self, r_out, x, dim):
         return check("q48_rms_inv", hip_lib().q48_rms_inv(self.h, r_out, x, dim))
 
@@ -451,6 +469,7 @@ HOST_SIGNATURES = {
                           C.POINTER(Stats)], C.c_int),
     "q48h_model_set_fused": ([_P, _I], None),
     "q48h_model_set_prefetch": ([_P, _I], None),
+    "q48h_model_set_rope_gemv": ([_P, _I], None),
     "q48h_read_logits": ([_P, _P], C.c_int),
     "q48h_model_set_bf16": ([_P, _I], C.c_int),
     "q48h_model_set_sampling": ([_P, C.c_int64, _I, C.c_int64, C.c_uint64], C.c_int),
@@ -575,6 +594,11 @@ class HostModel:
     def set_prefetch(self, on: bool):
         """Warm the device cache with each layer's W_o during its attention."""
         host_lib().q48h_model_set_prefetch(self.h, int(bool(on)))
+
+    def set_rope_gemv(self, on: bool):
+        """RoPE and the KV store in the q|k|v projection, attention from the
+        cache (short context, mode 3); off: RoPE inside attention."""
+        host_lib().q48h_model_set_rope_gemv(self.h, int(bool(on)))
 
 
     def read_logits(self) -> np.ndarray:
