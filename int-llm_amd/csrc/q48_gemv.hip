@@ -246,13 +246,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
 
     // row of group g (EPI 2: gate rows 4b+g, then up rows ffn+4b+g-4; EPI 5:
     // the RoPE pairs i = j0 + (g & 3) and i + hd / 2 of head hh, hd / 8
-    // blocks per head)
+    // blocks per head; hd a power of two, so shifts)
     const int pr = blockIdx.x * 4 + (g & 3);
     int hh = 0, j0 = 0;
     if (EPI == 5) {
-        const int bph = rk.hd >> 3;
-        hh = blockIdx.x / bph;
-        j0 = 4 * (blockIdx.x - hh * bph);
+        const int sh = 28 - __builtin_clz((unsigned)rk.hd);   // log2(hd / 8)
+        hh = (int)blockIdx.x >> sh;
+        j0 = 4 * ((int)blockIdx.x & ((1 << sh) - 1));
     }
     const int row = EPI == 2   ? (g < 4 ? pr : ffn + pr)
                     : EPI == 5 ? hh * rk.hd + j0 + (g & 3) + (g < 4 ? 0 : rk.hd >> 1)
@@ -621,8 +621,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         // threads 0-3 hold dims i = j0 + tid of head hh, 4-7 dims i + hd / 2;
         // RoPE of the q and k heads (rope_apply, llama_int.c:997-1008), then
         // k and v to the caches at pos (llama_int.c:1414-1416)
+        // (the partner row tid ^ 4 summed here too: no cross-lane step)
         const int half = rk.hd >> 1, d = j0 + (tid & 3) + (tid < 4 ? 0 : half);
-        const int64_t o = __shfl_xor(v, 4, 64);
+        q48_u128 T2 = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+            T2 += ((q48_u128)part[w][tid ^ 4][1] << 64) | part[w][tid ^ 4][0];
+        const int64_t o = (int64_t)((q48_i128)T2 >> 48);
         int64_t r5 = v;
         if (hh < rk.n_heads + rk.n_kv)
             r5 = tid < 4 ? (int64_t)((uint64_t)q48_mul(v, c5) - (uint64_t)q48_mul(o, s5))
