@@ -51,13 +51,13 @@ constexpr int ATT_LDS_MAX = 4096;   // positions whose scores fit in LDS (32 KiB
 // fp_safe_exp, sum, fp_div, V (llama_int.c:997-1008, 1060-1072, 1392-1395,
 // 1414-1416, 1502-1529).
 //  - the K rows of the first two score passes are issued before RoPE, and
-//    each later pass is issued one pass ahead (two register buffers);
+//    each later pass is issued one pass ahead (two register buffers), only
+//    where it exists;
 //  - the first V batches are issued before the softmax, later ones one
-//    batch ahead, so the V pass rarely waits;
+//    batch ahead where they exist, so the V pass rarely waits;
 //  - the score scale fp_inv_sqrt(fp_from_int(hd)) is read, not recomputed
 //    (k_rope_init stores it after the sine table).
-// Loads past the last position are clamped to it (in bounds, unused), so
-// every wait is for a known, static number of younger loads.  Rows at pos
+// Loads past the last position are clamped to it (in bounds, unused).  Rows at pos
 // are read from the cache and replaced by the block's own rotated k and v.
 // HD = 32, 64 or 128; at most SMAX positions (scores in LDS).  COH: the
 // output goes out with agent-coherent (write-through) stores, for a consumer
@@ -209,14 +209,21 @@ __device__ __forceinline__ void attn_v3_head(
         }
     };
     for (int t0 = 0; t0 < S; t0 += 2 * NG) {
+        // the next passes' rows, where there is a next pass (a block-uniform
+        // test: unneeded reloads would hold the compute unit's load return
+        // path, and the wave, until they landed)
         score(ka, t0 + g);
+        if (t0 + 2 * NG < S) {
 #pragma unroll
-        for (int d = 0; d < DP2; ++d)
-            ka[d] = krow(t0 + 2 * NG + g)[d];
+            for (int d = 0; d < DP2; ++d)
+                ka[d] = krow(t0 + 2 * NG + g)[d];
+        }
         score(kb, t0 + NG + g);
+        if (t0 + 3 * NG < S) {
 #pragma unroll
-        for (int d = 0; d < DP2; ++d)
-            kb[d] = krow(t0 + 3 * NG + g)[d];
+            for (int d = 0; d < DP2; ++d)
+                kb[d] = krow(t0 + 3 * NG + g)[d];
+        }
     }
 
     // V batches 0 and 1 go out before the softmax: thread (d, sl) takes
@@ -259,14 +266,19 @@ __device__ __forceinline__ void attn_v3_head(
         }
     };
     for (int i0 = 0; sl + SL * i0 < S; i0 += 2 * VB) {
+        // the next batches where some position of them exists (as above)
         vmac(va, i0);
+        if (SL * (i0 + 2 * VB) < S) {
 #pragma unroll
-        for (int u = 0; u < VB; ++u)
-            va[u] = vld(i0 + 2 * VB + u);
+            for (int u = 0; u < VB; ++u)
+                va[u] = vld(i0 + 2 * VB + u);
+        }
         vmac(vb, i0 + VB);
+        if (SL * (i0 + 3 * VB) < S) {
 #pragma unroll
-        for (int u = 0; u < VB; ++u)
-            vb[u] = vld(i0 + 3 * VB + u);
+            for (int u = 0; u < VB; ++u)
+                vb[u] = vld(i0 + 3 * VB + u);
+        }
     }
     part[tid] = (int64_t)acc;
     __syncthreads();

@@ -540,15 +540,20 @@ __global__ __launch_bounds__(256) void k_attn_s1(
             mx = sv > mx ? sv : mx;
         }
     };
+    // the next passes' rows only where there is a next pass (block-uniform)
     for (int tt = t0; tt < tend; tt += 2 * NG) {
         score(ka, tt + g);
+        if (tt + 2 * NG < tend) {
 #pragma unroll
-        for (int d = 0; d < DP2; ++d)
-            ka[d] = krow(tt + 2 * NG + g)[d];
+            for (int d = 0; d < DP2; ++d)
+                ka[d] = krow(tt + 2 * NG + g)[d];
+        }
         score(kb, tt + NG + g);
+        if (tt + 3 * NG < tend) {
 #pragma unroll
-        for (int d = 0; d < DP2; ++d)
-            kb[d] = krow(tt + 3 * NG + g)[d];
+            for (int d = 0; d < DP2; ++d)
+                kb[d] = krow(tt + 3 * NG + g)[d];
+        }
     }
     mx = block_max64<NT>(mx, red);
     if (tid == 0)
@@ -640,15 +645,20 @@ __global__ __launch_bounds__(256) void k_attn_s2(int64_t *__restrict__ out,
             if (t0 + sl + SL * (i0 + u) < tend)
                 acc += (uint64_t)q48_mul(pl[sl + SL * (i0 + u)], vv[u]);
     };
+    // the next batches only where some position of them exists (block-uniform)
     for (int i0 = 0; t0 + sl + SL * i0 < tend; i0 += 2 * VB) {
         vmac(va, i0);
+        if (t0 + SL * (i0 + 2 * VB) < tend) {
 #pragma unroll
-        for (int u = 0; u < VB; ++u)
-            va[u] = vcol[(size_t)tpos(i0 + 2 * VB + u) * kvd];
+            for (int u = 0; u < VB; ++u)
+                va[u] = vcol[(size_t)tpos(i0 + 2 * VB + u) * kvd];
+        }
         vmac(vb, i0 + VB);
+        if (t0 + SL * (i0 + 3 * VB) < tend) {
 #pragma unroll
-        for (int u = 0; u < VB; ++u)
-            vb[u] = vcol[(size_t)tpos(i0 + 3 * VB + u) * kvd];
+            for (int u = 0; u < VB; ++u)
+                vb[u] = vcol[(size_t)tpos(i0 + 3 * VB + u) * kvd];
+        }
     }
     part[tid] = (int64_t)acc;
     __syncthreads();
