@@ -370,20 +370,26 @@ __device__ __forceinline__ int64_t q48_inv_sqrt(int64_t x)
 __device__ __forceinline__ int64_t q48_exp_dyadic(int64_t x, int k)
 {
     int64_t r = (int64_t)((uint64_t)Q48_ONE + (uint64_t)(x >> k));
+#pragma unroll
     for (int i = 0; i < k; ++i)
         r = q48_sqr(r);
     return r;
 }
 
-// fp_exp, fp_math.h:724-732
+// fp_exp, fp_math.h:724-732, as one path for every lane: the squarings of
+// |x| (the reference's -x, wrapping), then the reciprocal unless x > 0.  At
+// x = 0 the reference squares 0 and gets ONE; here ONE / ONE, also ONE.  With
+// the reference's two branches a wave whose lanes hold both signs (a softmax
+// row around its maximum, SiLU arguments) would run the 14 squarings twice.
 __device__ __forceinline__ int64_t q48_exp(int64_t x)
 {
-    if (x >= 0)
-        return q48_exp_dyadic(x, 14);
-    int64_t pos = q48_exp_dyadic((int64_t)(0 - (uint64_t)x), 14);
-    if (pos == 0)
+    const uint64_t m = x >= 0 ? (uint64_t)x : (uint64_t)0 - (uint64_t)x;
+    const int64_t r = q48_exp_dyadic((int64_t)m, 14);
+    if (x > 0)
+        return r;
+    if (r == 0)
         return 0;
-    return q48_div(Q48_ONE, pos);
+    return q48_div(Q48_ONE, r);
 }
 
 // fp_safe_exp, fp_math.h:739-744
