@@ -339,7 +339,17 @@ __device__ __forceinline__ int64_t q48_inv_sqrt(int64_t x)
     int msb_n = 63 - __builtin_clzll((uint64_t)xn);
     int64_t y = msb_n == 48 ? Q48_ONE : Q48_HALF;
     const int64_t three = (int64_t)3 << 48;
-    for (int i = 0; i < 8; ++i) {
+    // The first step in closed form: from ONE (xn in [2^48, 2^49)) the
+    // square is ONE and xn * ONE >> 48 is xn, so yn = (3 ONE - xn) >> 1; from
+    // HALF (xn in [2^49, 2^50)) the square is ONE / 4, so yn = (3 ONE -
+    // (xn >> 2)) >> 2.  Both factors are positive and yn > 0.
+    const int64_t y1 = msb_n == 48 ? (three - xn) >> 1 : (three - (xn >> 2)) >> 2;
+    int i = 8;   // index of the next step (8: the first step was a fixed point)
+    if (y1 != y) {
+        y = y1;
+        i = 1;
+    }
+    for (; i < 8; ++i) {
         int64_t y2 = q48_sqr(y);
         int64_t xy2 = q48_mul_shr<48>(xn, y2);
         int64_t factor = three - xy2;
