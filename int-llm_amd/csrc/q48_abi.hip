@@ -103,7 +103,8 @@ int q48_ctx_create(q48_ctx **out, int device)
     }
     c->attn_one_launch = 1;
     c->pf_attn_mfma = 1;
-    c->attx_per_cu[0] = c->attx_per_cu[1] = c->attx_per_cu[2] = -1;
+    c->attx_per_cu[0] = c->attx_per_cu[1] = c->attx_per_cu[2] = c->attx_per_cu[3] = -1;
+    c->attn_g_mfma = 1;
     if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
         hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess ||
         hipMalloc(&c->d_step, 4 * sizeof(int)) != hipSuccess ||
@@ -647,6 +648,14 @@ int q48_set_attn_one_launch(q48_ctx *c, int on)
     if (!c)
         return Q48_EINVAL;
     c->attn_one_launch = on != 0;
+    return Q48_OK;
+}
+
+int q48_set_attn_g_mfma(q48_ctx *c, int on)
+{
+    if (!c)
+        return Q48_EINVAL;
+    c->attn_g_mfma = on != 0;
     return Q48_OK;
 }
 

@@ -75,6 +75,16 @@ __device__ __forceinline__ q48_u128 digits_total(const v4i (&q)[14], int i)
     return tot;
 }
 
+// v ^ (the same value on lane l ^ m), 128 bits as four 32-bit shuffles
+__device__ __forceinline__ q48_u128 shfl_xor128(q48_u128 v, int m)
+{
+    q48_u128 r = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        r |= (q48_u128)(uint32_t)__shfl_xor((int)(uint32_t)(v >> (32 * k)), m) << (32 * k);
+    return r;
+}
+
 // v_mad_u32_u24: a * b + c over the low 24 bits of a and b (full rate)
 __device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c)
 {

@@ -33,7 +33,9 @@ struct q48_ctx {
     unsigned *attx_sync;         // device: k_attn_x barrier words and error word (zeroed)
     int attn_one_launch;         // split attention as one k_attn_x launch (default on)
     int pf_attn_mfma;            // batched-prefill attention on the matrix cores (default on)
-    int attx_per_cu[3];          // k_attn_x<64/32/128> resident blocks per CU (-1: not asked)
+    int attx_per_cu[4];          // k_attn_g<64/32/128>, <64, matrix scores> resident blocks
+                                 // per CU (-1: not asked)
+    int attn_g_mfma;             // k_attn_g's scores on the matrix cores (head_dim 64; default on)
     int64_t *scratch;            // device address of the allocation-free scratch array
     unsigned *scratch_sync;      // ... and of its barrier region
     hipGraph_t graph;            // captured decode step

@@ -9,6 +9,7 @@
 #include "q48_internal.h"
 
 #include "q48_attn.hpp"
+#include "q48_digits.hpp"
 
 namespace {
 
@@ -784,8 +785,15 @@ __device__ bool attg_exchange(uint64_t *xw, int c, int nc, int G, unsigned epoch
 
 // head_dim 32/64: at most 128 VGPRs, so that two blocks (16 waves) fit a
 // compute unit and the grid of a 4096-position cache with 4 KV heads (512
-// blocks) is resident; head_dim 128: its LDS rows allow one block per unit
-template <int HD>
+// blocks) is resident; head_dim 128: its LDS rows allow one block per unit.
+// MF (head_dim 64): the scores on the int8 matrix cores.  The chunk's key
+// rows and the group's rotated q heads become digit planes in LDS (the key
+// planes share their LDS with the exchange buffer, which is used only after
+// the scores); waves 0 and 1 each run the 63 digit-pair
+// v_mfma_i32_16x16x64_i8 of one 16-position tile (query heads as rows,
+// padded to 16 with zero digits), and the correction sums C sum_d q_d and
+// C sum_d k_d - hd C^2 complete the exact int128 dot (q48_digits.hpp).
+template <int HD, bool MF = false>
 __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 128 ? 2 : 4))) void k_attn_g(
     int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
     int64_t *__restrict__ vcache, const int64_t *__restrict__ k_new,
@@ -802,13 +810,22 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
     constexpr int DH = HD / 2;                          // dims per score thread
     static_assert(LW % 2 == 0 && HD % LW == 0, "16-byte row loads");
     static_assert(GM * CH * 2 == NT, "two threads per score");
+    static_assert(!MF || (HD == 64 && LW == 4 && CH == 32 && GM == 8), "matrix-core scores");
+    constexpr int KDW = HD / 4 + 4;                     // digit-plane row: 16 words + 4 pad
     __shared__ int64_t qs[GM][HD];
     __shared__ int64_t ks[HD], vs[HD];
     __shared__ int64_t kl[CH][RS], vl[CH][RS];           // odd row stride: no bank conflicts
     __shared__ int64_t sc[GM][CH];
-    __shared__ q48_u128 dpart[GM * CH];
+    __shared__ q48_u128 dpart[MF ? 1 : GM * CH];
     __shared__ int64_t loc[GM];
-    __shared__ int64_t got[GM][ATTG_NCMAX];
+    // the exchange buffer, and before it the key digit planes (MF)
+    __shared__ union __align__(16) {
+        int64_t got[GM][ATTG_NCMAX];
+        uint32_t kd[MF ? 8 : 1][CH][KDW];
+    } gk;
+    int64_t (*got)[ATTG_NCMAX] = gk.got;
+    __shared__ __align__(16) uint32_t qd[MF ? 8 : 1][GM][KDW];   // q digit planes (MF)
+    __shared__ uint64_t ck[MF ? CH : 1][2], cq[MF ? GM : 1][2];   // correction sums (MF)
     if (d_pos)
         pos = *d_pos;
     if (pos < 0 || pos >= max_seq)
@@ -903,21 +920,113 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
     // scores: pair p = (head hh, position t) = tid % (GM CH), dims half tid / (GM CH)
     const int pi = tid % (GM * CH), hh = pi / CH, t = pi % CH, dh = tid / (GM * CH);
     const bool live = hh < G && t < nt;
-    q48_u128 dot = 0;
-    if (hh < G) {
-        const int64_t *qa = qs[hh] + dh * DH, *ka = kl[t] + dh * DH;
+    if constexpr (MF) {
+        // digit planes: the key words this thread loaded (row rr, dims rw..rw+3,
+        // read back from LDS: the row at pos may have been replaced) and, on
+        // threads below 128, four dims of one q head (zero digits past G)
+        {
+            uint64_t v4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v4[e] = (uint64_t)kl[rr][rw + e];
+            uint32_t wd[8];
+            digits4(v4, wd);
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+                gk.kd[a][rr][rw / 4] = wd[a];
+            q48_u128 sm = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                sm += (q48_u128)(q48_i128)(int64_t)v4[e];
+            // the 16 threads of row rr are lanes 16k .. 16k + 15
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1)
+                sm += shfl_xor128(sm, m);
+            if ((tid & 15) == 0) {
+                const q48_u128 cc = sm * kDig - (q48_u128)HD * kDig * kDig;
+                ck[rr][0] = (uint64_t)cc;
+                ck[rr][1] = (uint64_t)(cc >> 64);
+            }
+        }
+        if (tid < GM * 16) {
+            const int qh = tid >> 4, dq = 4 * (tid & 15);
+            uint64_t v4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v4[e] = qh < G ? (uint64_t)qs[qh][dq + e] : kDig;
+            uint32_t wd[8];
+            digits4(v4, wd);
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+                qd[a][qh][dq / 4] = wd[a];
+            q48_u128 sm = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                sm += (q48_u128)(q48_i128)(int64_t)v4[e];
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1)
+                sm += shfl_xor128(sm, m);
+            if ((tid & 15) == 0) {
+                const q48_u128 cc = sm * kDig;
+                cq[qh][0] = (uint64_t)cc;
+                cq[qh][1] = (uint64_t)(cc >> 64);
+            }
+        }
+        __syncthreads();
+        // waves 0 and 1: tile w = positions 16 w .. 16 w + 15.  Lane l holds
+        // A row (q head) l % 16 and B column (position) l % 16, dims 16 (l / 16)
+        // .. + 15; the result rows 4 (l / 16) + i at column l % 16.
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        if (wv < 2) {
+            const int ln = tid & 63, col = ln & 15, kq = ln >> 4, tt = 16 * wv + col;
+            v4i A[8];
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+                A[a] = col < GM ? *reinterpret_cast<const v4i *>(&qd[a][col][4 * kq])
+                                : (v4i){0, 0, 0, 0};
+            v4i acc[14];
+#pragma unroll
+            for (int d = 0; d < 14; ++d)
+                acc[d] = (v4i){0, 0, 0, 0};
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const v4i B = *reinterpret_cast<const v4i *>(&gk.kd[b][tt][4 * kq]);
+#pragma unroll
+                for (int a = 0; a < 8; ++a)
+                    if (a + b <= 13)
+                        acc[a + b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[a], B, acc[a + b],
+                                                                          0, 0, 0);
+            }
+            const q48_u128 ckj = ((q48_u128)ck[tt][1] << 64) | ck[tt][0];
+            const int64_t scale = *scale_p;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int qh = 4 * kq + i;
+                if (qh < G) {
+                    const q48_u128 tot = digits_total(acc, i) + ckj +
+                                         (((q48_u128)cq[qh][1] << 64) | cq[qh][0]);
+                    sc[qh][tt] = tt < nt ? q48_mul((int64_t)(tot >> 48), scale) : INT64_MIN;
+                }
+            }
+        }
+        __syncthreads();
+    } else {
+        q48_u128 dot = 0;
+        if (hh < G) {
+            const int64_t *qa = qs[hh] + dh * DH, *ka = kl[t] + dh * DH;
 #pragma unroll 8
-        for (int d = 0; d < DH; ++d)
-            dot += (q48_u128)q48_smul128(qa[d], ka[d]);
+            for (int d = 0; d < DH; ++d)
+                dot += (q48_u128)q48_smul128(qa[d], ka[d]);
+        }
+        if (dh == 1)
+            dpart[pi] = dot;
+        __syncthreads();
+        if (dh == 0 && hh < G) {
+            dot += dpart[pi];
+            sc[hh][t] = live ? q48_mul((int64_t)((q48_i128)dot >> 48), *scale_p) : INT64_MIN;
+        }
+        __syncthreads();
     }
-    if (dh == 1)
-        dpart[pi] = dot;
-    __syncthreads();
-    if (dh == 0 && hh < G) {
-        dot += dpart[pi];
-        sc[hh][t] = live ? q48_mul((int64_t)((q48_i128)dot >> 48), *scale_p) : INT64_MIN;
-    }
-    __syncthreads();
     if (tid < G) {
         int64_t m = INT64_MIN;
         for (int u = 0; u < nt; ++u)
@@ -1262,14 +1371,16 @@ size_t q48_attn_sync_bytes() { return ATTG_SYNC_BYTES; }
 // cache (max_seq) times the KV heads must fit the device's occupancy.
 static bool attg_fits(q48_ctx *c, int hd, int n_heads, int n_kv, int max_seq)
 {
-    const int k = hd == 64 ? 0 : hd == 32 ? 1 : 2;
+    const int k = hd == 64 ? (c->attn_g_mfma ? 3 : 0) : hd == 32 ? 1 : 2;
     if (n_heads % n_kv || n_heads / n_kv > ATTG_GMAX || n_kv > ATTG_KVMAX)
         return false;
     if ((max_seq + ATTG_CH - 1) / ATTG_CH > ATTG_NCMAX)
         return false;
     if (c->attx_per_cu[k] < 0) {   // resident blocks per compute unit, asked once
-        const void *fn = k == 0 ? (const void *)k_attn_g<64>
-                       : k == 1 ? (const void *)k_attn_g<32> : (const void *)k_attn_g<128>;
+        const void *fn = k == 0   ? (const void *)k_attn_g<64>
+                         : k == 3 ? (const void *)k_attn_g<64, true>
+                         : k == 1 ? (const void *)k_attn_g<32>
+                                  : (const void *)k_attn_g<128>;
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, ATTG_NT, 0) != hipSuccess)
             n = 0;
@@ -1323,17 +1434,19 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
         unsigned *sync = ws_ext ? sync_ext : c->attx_sync;
         if (c->attn_one_launch && sync && attg_fits(c, head_dim, n_heads, n_kv, max_seq)) {
             const dim3 grid((max_seq + ATTG_CH - 1) / ATTG_CH, n_kv);
-#define ATTG_LAUNCH(HD)                                                                       \
-    hipLaunchKernelGGL((k_attn_g<HD>), grid, dim3(ATTG_NT), 0, c->stream, out, q, kcache,    \
+#define ATTG_LAUNCH(HD, MFS)                                                                  \
+    hipLaunchKernelGGL((k_attn_g<HD, MFS>), grid, dim3(ATTG_NT), 0, c->stream, out, q, kcache, \
                        vcache, k_new, v_new, c->rope_cos, c->rope_sin, scale_p,               \
                        reinterpret_cast<uint64_t *>(sync), layer, d_pos, pos, n_heads, n_kv,  \
                        max_seq)
-            if (head_dim == 64)
-                ATTG_LAUNCH(64);
+            if (head_dim == 64 && c->attn_g_mfma)
+                ATTG_LAUNCH(64, true);
+            else if (head_dim == 64)
+                ATTG_LAUNCH(64, false);
             else if (head_dim == 32)
-                ATTG_LAUNCH(32);
+                ATTG_LAUNCH(32, false);
             else
-                ATTG_LAUNCH(128);
+                ATTG_LAUNCH(128, false);
 #undef ATTG_LAUNCH
             return (int)hipGetLastError();
         }

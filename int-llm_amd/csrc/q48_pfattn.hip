@@ -63,15 +63,6 @@ __device__ __forceinline__ uint64_t group_sum64(uint64_t v)
     return v;
 }
 
-__device__ __forceinline__ q48_u128 shfl_xor128(q48_u128 v, int m)
-{
-    q48_u128 r = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        r |= (q48_u128)(uint32_t)__shfl_xor((int)(uint32_t)(v >> (32 * k)), m) << (32 * k);
-    return r;
-}
-
 __device__ __forceinline__ q48_u128 ld128(const uint64_t *p)
 {
     return ((q48_u128)p[1] << 64) | p[0];

@@ -72,6 +72,7 @@ ABI_SIGNATURES = {
     "q48_attn_split_min": [],
     "q48_set_attn_one_launch": [_P, _I],
     "q48_set_pf_attn_mfma": [_P, _I],
+    "q48_set_attn_g_mfma": [_P, _I],
     "q48_attn_prefill": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I],
     "q48_attn_status": [_P],
     "q48_attn_decode_rope_prefetch": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _SZ],
@@ -267,6 +268,9 @@ class Context:
 
     def set_pf_attn_mfma(self, on: bool):
         return check("q48_set_pf_attn_mfma", hip_lib().q48_set_pf_attn_mfma(self.h, int(on)))
+
+    def set_attn_g_mfma(self, on: bool):
+        return check("q48_set_attn_g_mfma", hip_lib().q48_set_attn_g_mfma(self.h, int(on)))
 
     def attn_prefill(self, out, qkv, kc, vc, layer, p0, T, nh, nkv, hd, max_seq):
         """Causal attention of T rotated [q | k | v] rows at positions p0 .. p0 + T - 1

@@ -452,25 +452,32 @@ def test_rmsnorm_gemv_swiglu_fused(ctx, oracle, ffn, K):
         b.free()
 
 
-@pytest.mark.parametrize("one_launch", [True, False], ids=["one_launch", "three_launches"])
+@pytest.mark.parametrize("one_launch", [(True, True), (True, False), (False, True)],
+                         ids=["one_launch", "one_launch_valu_scores", "three_launches"])
 @pytest.mark.parametrize("nh,nkv,hd,max_seq,positions", [
     (8, 2, 32, 64, [0, 1, 63]),
     (32, 4, 64, 300, [0, 7, 299]),
     # from position 512 on, the split (chunked) kernels: chunk edges 767/768
     (32, 4, 64, 1300, [511, 512, 767, 768, 1299]),
     (8, 2, 32, 600, [513, 599]),
+    # a group of 3 query heads: rows 3..15 of the matrix-core scores are padding
+    (12, 4, 64, 600, [520, 599]),
     # head_dim 128: chunks of 128 positions
     (16, 4, 128, 700, [512, 639, 640, 699]),
     # the largest one-launch grid of the TinyLlama heads: 16 chunks x 32 heads
     (32, 4, 64, 4096, [2047, 2048, 4095]),
 ])
 def test_attention_rope_fused(ctx, oracle, nh, nkv, hd, max_seq, positions, one_launch):
-    ctx.set_attn_one_launch(one_launch)
+    """one_launch = (one-launch split form, its scores on the matrix cores
+    for head_dim 64): every form against the oracle."""
+    ctx.set_attn_one_launch(one_launch[0])
+    ctx.set_attn_g_mfma(one_launch[1])
     try:
         _attention_rope_case(ctx, oracle, nh, nkv, hd, max_seq, positions)
         assert ctx.attn_status() == 0
     finally:
         ctx.set_attn_one_launch(True)
+        ctx.set_attn_g_mfma(True)
 
 
 def _attention_rope_case(ctx, oracle, nh, nkv, hd, max_seq, positions):
