@@ -75,6 +75,20 @@ __device__ __forceinline__ q48_u128 digits_total(const v4i (&q)[14], int i)
     return tot;
 }
 
+// sum over the lanes of a group of N = 2, 4, 8 or 16 (lane % N varies)
+template <int N>
+__device__ __forceinline__ uint64_t group_sum64(uint64_t v)
+{
+    v += q48_dpp64<Q48_DPP_XOR1>(v);
+    if (N >= 4)
+        v += q48_dpp64<Q48_DPP_XOR2>(v);
+    if (N >= 8)
+        v += q48_dpp64<Q48_DPP_HALF_MIRROR>(v);
+    if (N >= 16)
+        v += q48_dpp64<Q48_DPP_MIRROR>(v);
+    return v;
+}
+
 // v ^ (the same value on lane l ^ m), 128 bits as four 32-bit shuffles
 __device__ __forceinline__ q48_u128 shfl_xor128(q48_u128 v, int m)
 {
@@ -83,6 +97,43 @@ __device__ __forceinline__ q48_u128 shfl_xor128(q48_u128 v, int m)
     for (int k = 0; k < 4; ++k)
         r |= (q48_u128)(uint32_t)__shfl_xor((int)(uint32_t)(v >> (32 * k)), m) << (32 * k);
     return r;
+}
+
+// sum_e v[e] over the four words of each of the 16 lanes of a row group
+// (lane % 16 varies), on every lane: 64 int64 in exact 128-bit arithmetic,
+// as the 64-bit sums of their signed high and unsigned low 32-bit halves
+// (in-row DPP adds, no cross-lane round trip through LDS)
+__device__ __forceinline__ q48_u128 row16_sum4(const uint64_t (&v)[4])
+{
+    uint64_t lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        lo += (uint32_t)v[e];
+        hi += (uint64_t)((int64_t)v[e] >> 32);
+    }
+    lo = group_sum64<16>(lo);
+    hi = group_sum64<16>(hi);
+    return (q48_u128)((q48_i128)(int64_t)hi << 32) + lo;
+}
+
+// sum_d 256^d a[d] (int128) of 14 digit-product sums
+__device__ __forceinline__ q48_u128 digits_total14(const int (&a)[14])
+{
+    int64_t part[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        int64_t s = 0;
+#pragma unroll
+        for (int d = 4 * g + 3; d >= 4 * g; --d)
+            if (d < 14)
+                s = s * 256 + (int64_t)a[d];
+        part[g] = s;
+    }
+    q48_u128 tot = (q48_u128)(q48_i128)part[3];
+#pragma unroll
+    for (int g = 2; g >= 0; --g)
+        tot = (tot << 32) + (q48_u128)(q48_i128)part[g];
+    return tot;
 }
 
 // v_mad_u32_u24: a * b + c over the low 24 bits of a and b (full rate)

@@ -791,8 +791,9 @@ __device__ bool attg_exchange(uint64_t *xw, int c, int nc, int G, unsigned epoch
 // planes share their LDS with the exchange buffer, which is used only after
 // the scores); waves 0 and 1 each run the 63 digit-pair
 // v_mfma_i32_16x16x64_i8 of one 16-position tile (query heads as rows,
-// padded to 16 with zero digits), and the correction sums C sum_d q_d and
-// C sum_d k_d - hd C^2 complete the exact int128 dot (q48_digits.hpp).
+// padded to 16 with zero digits), and the corrections C sum_d q_d and
+// C sum_d S(k_d) (a ones row of the same tile) complete the exact int128
+// dot (q48_digits.hpp).
 template <int HD, bool MF = false>
 __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 128 ? 2 : 4))) void k_attn_g(
     int64_t *__restrict__ out, const int64_t *__restrict__ q, int64_t *__restrict__ kcache,
@@ -826,6 +827,11 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
     int64_t (*got)[ATTG_NCMAX] = gk.got;
     __shared__ __align__(16) uint32_t qd[MF ? 8 : 1][GM][KDW];   // q digit planes (MF)
     __shared__ uint64_t ck[MF ? CH : 1][2], cq[MF ? GM : 1][2];   // correction sums (MF)
+    // the digit sums of the matrix-core scores, [14][head][position], in
+    // the key rows' LDS (MF)
+    int(*accs)[GM][CH] = reinterpret_cast<int(*)[GM][CH]>(&kl[0][0]);
+    static_assert(!MF || 14 * GM * CH * 4 <= (int)sizeof(int64_t) * CH * RS, "digit sums fit");
+    static_assert(!MF || GM <= 8, "row 8 of the score tile is the ones row");
     if (d_pos)
         pos = *d_pos;
     if (pos < 0 || pos >= max_seq)
@@ -934,19 +940,6 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
 #pragma unroll
             for (int a = 0; a < 8; ++a)
                 gk.kd[a][rr][rw / 4] = wd[a];
-            q48_u128 sm = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                sm += (q48_u128)(q48_i128)(int64_t)v4[e];
-            // the 16 threads of row rr are lanes 16k .. 16k + 15
-#pragma unroll
-            for (int m = 1; m < 16; m <<= 1)
-                sm += shfl_xor128(sm, m);
-            if ((tid & 15) == 0) {
-                const q48_u128 cc = sm * kDig - (q48_u128)HD * kDig * kDig;
-                ck[rr][0] = (uint64_t)cc;
-                ck[rr][1] = (uint64_t)(cc >> 64);
-            }
         }
         if (tid < GM * 16) {
             const int qh = tid >> 4, dq = 4 * (tid & 15);
@@ -959,23 +952,15 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
 #pragma unroll
             for (int a = 0; a < 8; ++a)
                 qd[a][qh][dq / 4] = wd[a];
-            q48_u128 sm = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                sm += (q48_u128)(q48_i128)(int64_t)v4[e];
-#pragma unroll
-            for (int m = 1; m < 16; m <<= 1)
-                sm += shfl_xor128(sm, m);
-            if ((tid & 15) == 0) {
-                const q48_u128 cc = sm * kDig;
-                cq[qh][0] = (uint64_t)cc;
-                cq[qh][1] = (uint64_t)(cc >> 64);
-            }
         }
         __syncthreads();
         // waves 0 and 1: tile w = positions 16 w .. 16 w + 15.  Lane l holds
         // A row (q head) l % 16 and B column (position) l % 16, dims 16 (l / 16)
-        // .. + 15; the result rows 4 (l / 16) + i at column l % 16.
+        // .. + 15; the result rows 4 (l / 16) + i at column l % 16.  A row 8
+        // (never a head: at most 8 per group) is ones in digit 0, so that its
+        // result is sum_d S(k_t,d), and the correction C sum_d q_d + C sum_d
+        // k_d - hd C^2 is C sum_d q_d + C sum_d S(k_t,d).  Waves 2 and 3 sum
+        // the q heads meanwhile.
         const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         if (wv < 2) {
             const int ln = tid & 63, col = ln & 15, kq = ln >> 4, tt = 16 * wv + col;
@@ -983,7 +968,8 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
 #pragma unroll
             for (int a = 0; a < 8; ++a)
                 A[a] = col < GM ? *reinterpret_cast<const v4i *>(&qd[a][col][4 * kq])
-                                : (v4i){0, 0, 0, 0};
+                       : col == 8 && a == 0 ? (v4i){0x01010101, 0x01010101, 0x01010101, 0x01010101}
+                                            : (v4i){0, 0, 0, 0};
             v4i acc[14];
 #pragma unroll
             for (int d = 0; d < 14; ++d)
@@ -997,16 +983,49 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
                         acc[a + b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[a], B, acc[a + b],
                                                                           0, 0, 0);
             }
-            const q48_u128 ckj = ((q48_u128)ck[tt][1] << 64) | ck[tt][0];
-            const int64_t scale = *scale_p;
+            // the raw sums to LDS (the key rows' space: kl is read only by the
+            // digit split above), [d][head][position]; row 8's lanes the key
+            // correction
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int qh = 4 * kq + i;
-                if (qh < G) {
-                    const q48_u128 tot = digits_total(acc, i) + ckj +
-                                         (((q48_u128)cq[qh][1] << 64) | cq[qh][0]);
-                    sc[qh][tt] = tt < nt ? q48_mul((int64_t)(tot >> 48), scale) : INT64_MIN;
-                }
+                if (qh < G)
+#pragma unroll
+                    for (int d = 0; d < 14; ++d)
+                        accs[d][qh][tt] = acc[d][i];
+            }
+            if (kq == 2) {
+                const q48_u128 cc = digits_total(acc, 0) * kDig;
+                ck[tt][0] = (uint64_t)cc;
+                ck[tt][1] = (uint64_t)(cc >> 64);
+            }
+        } else if (wv < 4) {
+            // C sum_d q_d of head (tid - 128) / 16: 16 threads, 4 dims each
+            const int qh = (tid - 128) >> 4, dq = 4 * (tid & 15);
+            uint64_t v4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v4[e] = qh < G ? (uint64_t)qs[qh][dq + e] : 0;
+            const q48_u128 sm = row16_sum4(v4);
+            if ((tid & 15) == 0) {
+                const q48_u128 cc = sm * kDig;
+                cq[qh][0] = (uint64_t)cc;
+                cq[qh][1] = (uint64_t)(cc >> 64);
+            }
+        }
+        __syncthreads();
+        // one score per thread: the digit sums, the corrections, the scale
+        if (tid < GM * CH) {
+            const int qh = tid / CH, tt = tid % CH;
+            if (qh < G) {
+                int a14[14];
+#pragma unroll
+                for (int d = 0; d < 14; ++d)
+                    a14[d] = accs[d][qh][tt];
+                const q48_u128 tot = digits_total14(a14) +
+                                     (((q48_u128)ck[tt][1] << 64) | ck[tt][0]) +
+                                     (((q48_u128)cq[qh][1] << 64) | cq[qh][0]);
+                sc[qh][tt] = tt < nt ? q48_mul((int64_t)(tot >> 48), *scale_p) : INT64_MIN;
             }
         }
         __syncthreads();

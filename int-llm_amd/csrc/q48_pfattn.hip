@@ -49,20 +49,6 @@ __device__ __forceinline__ int64_t row16_max64(int64_t v)
     return o > v ? o : v;
 }
 
-// sum over the lanes of a group of N = 2, 4, 8 or 16 (lane % N varies)
-template <int N>
-__device__ __forceinline__ uint64_t group_sum64(uint64_t v)
-{
-    v += q48_dpp64<Q48_DPP_XOR1>(v);
-    if (N >= 4)
-        v += q48_dpp64<Q48_DPP_XOR2>(v);
-    if (N >= 8)
-        v += q48_dpp64<Q48_DPP_HALF_MIRROR>(v);
-    if (N >= 16)
-        v += q48_dpp64<Q48_DPP_MIRROR>(v);
-    return v;
-}
-
 __device__ __forceinline__ q48_u128 ld128(const uint64_t *p)
 {
     return ((q48_u128)p[1] << 64) | p[0];
