@@ -288,7 +288,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     uint64_t plo[PC], phi[PC];
     const int np = (K + 7) >> 3;
     const uint64_t *st = reinterpret_cast<const uint64_t *>(r_in);
-    if (PRO == 3 && NTF > 0) {
+    if (PRO == 3 && NTF > 0 && wave == 0) {
 #pragma unroll
         for (int c = 0; c < PC; ++c) {
             const int i = min(lane + c * 64, np - 1);
@@ -381,25 +381,25 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     }
 
     if (PRO == 3) {
-        // every wave adds the partials (cheap; it keeps their loads first in
-        // every wave), wave 0 alone derives r and the others meet it at the
-        // barrier: the chain of 64 x 64-bit products inside rms_inv_of is
-        // issue-bound, and run by every wave it would contend for the SIMDs
-        q48_u128 ss = 0;
-        if constexpr (NTF > 0) {
-#pragma unroll
-            for (int c = 0; c < PC; ++c) {
-                // masked, not branched: a branch would sink the load and wait
-                const uint64_t m = lane + c * 64 < np ? ~0ull : 0ull;
-                ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
-            }
-        } else {
-            for (int i = lane; i < np; i += 64)
-                ss += ((q48_u128)st[2 * i + 1] << 64) | st[2 * i];
-        }
-        ss = q48_wave_sum128(ss);
-        q48_keep128(ss);
+        // wave 0 alone loads and adds the producer's partials and derives r;
+        // the others meet it at the barrier.  Loaded by every wave, the
+        // partials (4 KB per wave) would queue ahead of each wave's x and
+        // weight loads in the CU's load path, and the chain of 64 x 64-bit
+        // products inside rms_inv_of would contend for the SIMDs
         if (wave == 0) {
+            q48_u128 ss = 0;
+            if constexpr (NTF > 0) {
+#pragma unroll
+                for (int c = 0; c < PC; ++c) {
+                    // masked, not branched: a branch would sink the load and wait
+                    const uint64_t m = lane + c * 64 < np ? ~0ull : 0ull;
+                    ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
+                }
+            } else {
+                for (int i = lane; i < np; i += 64)
+                    ss += ((q48_u128)st[2 * i + 1] << 64) | st[2 * i];
+            }
+            ss = q48_wave_sum128(ss);
             const int64_t rv = rms_inv_of(ss, K);
             if (lane == 0)
                 r_sh = rv;
@@ -712,7 +712,7 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
     uint64_t plo[PC], phi[PC];
     const int np = (K + 7) >> 3;
     const uint64_t *st = reinterpret_cast<const uint64_t *>(r_in);
-    if (PRO == 3) {
+    if (PRO == 3 && wave == 0) {
 #pragma unroll
         for (int c = 0; c < PC; ++c) {
             const int i = min(lane + c * 64, np - 1);
@@ -746,16 +746,15 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
 
     int64_t r = 0;
     if (PRO == 3) {
-        // wave 0 derives r for the block (as in k_gemv_v5)
-        q48_u128 ss = 0;
-#pragma unroll
-        for (int c = 0; c < PC; ++c) {
-            const uint64_t m = lane + c * 64 < np ? ~0ull : 0ull;
-            ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
-        }
-        ss = q48_wave_sum128(ss);
-        q48_keep128(ss);
+        // wave 0 alone loads the partials and derives r (as in k_gemv_v5)
         if (wave == 0) {
+            q48_u128 ss = 0;
+#pragma unroll
+            for (int c = 0; c < PC; ++c) {
+                const uint64_t m = lane + c * 64 < np ? ~0ull : 0ull;
+                ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
+            }
+            ss = q48_wave_sum128(ss);
             const int64_t rv = rms_inv_of(ss, K);
             if (lane == 0)
                 r_sh = rv;

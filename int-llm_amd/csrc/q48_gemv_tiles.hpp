@@ -27,14 +27,6 @@ __device__ __forceinline__ int64_t rms_inv_of(q48_u128 ss, int dim)
     return q48_inv_sqrt(ms);
 }
 
-// Marks a value as used here, in every wave, so that the compiler computes
-// it (and waits for its loads) at this point instead of sinking the work
-// into the one branch that reads it.
-__device__ __forceinline__ void q48_keep128(q48_u128 v)
-{
-    asm volatile("" ::"v"((uint64_t)v), "v"((uint64_t)(v >> 64)));
-}
-
 // 128-bit sum over the block (NT threads); result valid in thread 0.
 template <int NT>
 __device__ __forceinline__ q48_u128 block_sum128(q48_u128 v, uint64_t *red_lo, uint64_t *red_hi)
