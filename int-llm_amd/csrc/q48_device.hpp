@@ -349,6 +349,41 @@ __device__ __forceinline__ int64_t q48_inv_sqrt(int64_t x)
         y = y1;
         i = 1;
     }
+    // Steps 1..7 on exact doubles, straight-line.  y, y2 = floor(y^2 /
+    // 2^48), xy2 = floor(xn y2 / 2^48), the factor and the next y are
+    // integers below 2^53 while y < 2^49 (xn < 2^50), and each truncated
+    // product a b / 2^s (|a b| <= 2^(s + 52)) is exact:
+    //   with bs = b 2^-s (exact), P = a bs = RN(a b) 2^-s has ulp(P) <= 1,
+    //   so a b 2^-s lies in [f - 1, f + 1) for f = floor(P), and
+    //   fma(a, bs, -f) = (a b - f 2^s) 2^-s exactly (a multiple of 2^-s in
+    //   [-1, 1)): floor(a b / 2^s) = f + floor(fma(a, bs, -f)).
+    // No compare or branch: the chain stays on the vector unit.  A fixed
+    // point stays fixed, and so does 1 (the reference's value once a step
+    // gives y <= 0), so running every remaining step gives the reference's
+    // y.  Should y ever reach 2^49 the integer steps below run instead.
+    if (i < 8) {
+        const double xs = (double)xn * 0x1p-48;                 // exact
+        const double tq = 844424930131968.0 * 0x1p-49;          // 3 * 2^48 * 2^-49
+        double yd = (double)y, mx = yd;
+#pragma unroll
+        for (int j = 0; j < 7; ++j) {
+            const double ys = yd * 0x1p-48;
+            double P = yd * ys, f = __builtin_floor(P);
+            const double y2 = f + __builtin_floor(__fma_rn(yd, ys, -f));
+            P = y2 * xs;
+            f = __builtin_floor(P);
+            const double xy2 = f + __builtin_floor(__fma_rn(y2, xs, -f));
+            const double fs = __fma_rn(xy2, -0x1p-49, tq);     // (3 * 2^48 - xy2) 2^-49
+            P = yd * fs;
+            f = __builtin_floor(P);
+            yd = __builtin_fmax(f + __builtin_floor(__fma_rn(yd, fs, -f)), 1.0);
+            mx = __builtin_fmax(mx, yd);
+        }
+        if (mx < 562949953421312.0) {   // 2^49
+            y = (int64_t)yd;
+            i = 8;
+        }
+    }
     for (; i < 8; ++i) {
         int64_t y2 = q48_sqr(y);
         int64_t xy2 = q48_mul_shr<48>(xn, y2);

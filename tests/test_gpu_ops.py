@@ -116,6 +116,29 @@ def test_device_div_random_vs_oracle(ctx, oracle):
     assert np.array_equal(d, want)
 
 
+def test_device_inv_sqrt_vs_oracle(ctx, oracle):
+    """fp_inv_sqrt on the device (Newton steps on exact FP64 products) equals
+    the oracle: every magnitude 2^0 .. 2^62 log-uniformly, the rmsnorm range
+    around ONE, and one unit either side of each power of two, where the
+    normalised argument crosses 2^48, 2^49 and 2^50."""
+    rng = np.random.default_rng(29)
+    n = 65536
+    e = rng.integers(0, 63, size=n)
+    x = [max(1, int(rng.integers(0, 1 << 62)) >> (62 - int(k))) for k in e]
+    x += [int(v) for v in rng.integers(1 << 46, 1 << 51, size=16384)]
+    for k in range(63):
+        for d in (-1, 0, 1):
+            v = (1 << k) + d
+            if 0 < v < 1 << 63:
+                x.append(v)
+    x += [spec.INT64_MAX, spec.INT64_MAX - 1, 0, -1, spec.INT64_MIN]
+    x = np.array(x, dtype=np.int64)
+    say("inv_sqrt", x.size)
+    got = dev_eval(ctx, intllm.FP_INV_SQRT, x)
+    want = np.array([oracle.q48o_fp_inv_sqrt(int(v)) for v in x], dtype=np.int64)
+    assert np.array_equal(got, want)
+
+
 def test_device_div_quotients_at_integers(ctx, oracle):
     """Numerators at and one unit either side of exact multiples of the
     divisor (a 2^48 = q b): the quotient's estimate lands next to an integer,
