@@ -437,6 +437,35 @@ __device__ __forceinline__ int64_t q48_exp(int64_t x)
     return q48_div(Q48_ONE, r);
 }
 
+// fp_exp for |x| <= 10 ONE, the range fp_safe_exp leaves (fp_math.h:739-744):
+// the same squarings, the first 11 on exact doubles.  r0 = ONE + (|x| >> 14)
+// and r_k = floor(r_{k-1}^2 / 2^48) <= e^(10 2^(k - 14)) ONE, so r_0 .. r_11
+// stay below 3.5 ONE < 2^50 and each square is below 2^100: with rs = r 2^-48
+// (exact), f = floor(r rs) and fma(r, rs, -f) = (r^2 - f 2^48) 2^-48 exactly
+// (a multiple of 2^-48 in [-1, 1)), floor(r^2 / 2^48) = f + floor(fma(r, rs,
+// -f)).  Full-rate FP64 instead of three quarter-rate 32 x 32 -> 64 products
+// per square; the last three squares (up to e^10 ONE < 2^63) stay integer.
+__device__ __forceinline__ int64_t q48_exp_small(int64_t x)
+{
+    const uint64_t m = x >= 0 ? (uint64_t)x : (uint64_t)0 - (uint64_t)x;
+    double rd = (double)(int64_t)((uint64_t)Q48_ONE + (m >> 14));
+#pragma unroll
+    for (int k = 0; k < 11; ++k) {
+        const double rs = rd * 0x1p-48;
+        const double f = __builtin_floor(rd * rs);
+        rd = f + __builtin_floor(__fma_rn(rd, rs, -f));
+    }
+    int64_t r = (int64_t)rd;
+    r = q48_sqr(r);
+    r = q48_sqr(r);
+    r = q48_sqr(r);
+    if (x > 0)
+        return r;
+    if (r == 0)
+        return 0;
+    return q48_div(Q48_ONE, r);
+}
+
 // fp_safe_exp, fp_math.h:739-744
 __device__ __forceinline__ int64_t q48_safe_exp(int64_t x)
 {
@@ -445,7 +474,7 @@ __device__ __forceinline__ int64_t q48_safe_exp(int64_t x)
         x = max_x;
     if (x < -max_x)
         return 0;
-    return q48_exp(x);
+    return q48_exp_small(x);
 }
 
 // fp_log, fp_math.h:752-773

@@ -139,6 +139,28 @@ def test_device_inv_sqrt_vs_oracle(ctx, oracle):
     assert np.array_equal(got, want)
 
 
+def test_device_safe_exp_sigmoid_silu_vs_oracle(ctx, oracle):
+    """fp_safe_exp (squarings partly on exact FP64), fp_sigmoid and fp_silu
+    on the device equal the oracle: uniform over [-11, 11] ONE, small
+    magnitudes, and a few units either side of 0 and of the +-10 ONE clamps."""
+    rng = np.random.default_rng(31)
+    one, ten = 1 << 48, 10 << 48
+    x = [int(v) for v in rng.integers(-11 * one, 11 * one, size=32768)]
+    x += [int(v) >> int(s) for v, s in zip(rng.integers(-ten, ten, size=8192),
+                                           rng.integers(0, 48, size=8192))]
+    for c in (0, ten, -ten, one, -one):
+        x += [c + d for d in range(-40, 41)]
+    x += [spec.INT64_MAX, spec.INT64_MIN]
+    x = np.array(x, dtype=np.int64)
+    say("safe_exp / sigmoid / silu", x.size)
+    for fn, ref in ((intllm.FP_SAFE_EXP, oracle.q48o_fp_safe_exp),
+                    (intllm.FP_SIGMOID, oracle.q48o_fp_sigmoid),
+                    (intllm.FP_SILU, oracle.q48o_fp_silu)):
+        got = dev_eval(ctx, fn, x)
+        want = np.array([ref(int(v)) for v in x], dtype=np.int64)
+        assert np.array_equal(got, want), fn
+
+
 def test_device_div_quotients_at_integers(ctx, oracle):
     """Numerators at and one unit either side of exact multiples of the
     divisor (a 2^48 = q b): the quotient's estimate lands next to an integer,
