@@ -41,9 +41,9 @@ HBM_PEAK_GBS = 8000.0
 # 16 hex digits of the sha256 of their code, in this order, with comments and
 # whitespace removed); with any other code the bench line reports traffic null
 # until the counters are re-run.
-TRAFFIC = 93620837
+TRAFFIC = 93625687
 TRAFFIC_SOURCES = ("int-llm_amd/csrc/q48_gemv.hip", "int-llm_amd/csrc/q48_gemv_tiles.hpp")
-TRAFFIC_SHA256 = "b99c07e7529c78e6"
+TRAFFIC_SHA256 = "dd46f743a878b331"
 REF_CPU_MS_PER_TOK = 501.4   # reference decode, Zen 4, 1 thread
 # int8 GEMM: MI355X dense int8 MFMA peak; one Q16.48 MAC is 63 int8 products
 # (digit pairs a + b <= 13), 2 ops each
@@ -561,8 +561,8 @@ def main():
                    "layers": 22, "dim": 2048, "heads": 32, "kv_heads": 4, "ffn": 5632,
                    "vocab": 32000, "prompt_tokens": len(prompt), "positions": [p0, p0 + args.steps]},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_gemv_v5 / k_gemv_p6 (q48_gemv family: the 89 fused GEMV "
-                               "launches of a decode token, back to back)",
+                     "kernel": "k_gemv_r1 / k_gemv_v5 / k_gemv_p6 (q48_gemv family: the 89 "
+                               "fused GEMV launches of a decode token, back to back)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(),
                      "traffic_sources_sha256": sources_sha256(),

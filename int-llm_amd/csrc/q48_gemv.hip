@@ -655,6 +655,178 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
 }
 
 // ---------------------------------------------------------------------------
+// k_gemv_r1: the normed q|k|v projection with the RoPE and KV-store epilogue
+// (prologue 3, epilogue 5 of k_gemv_v5) as one block per compute unit.  With
+// 8-row blocks the 2560 rows of TinyLlama's q|k|v make 320 blocks on 256
+// compute units: 64 of them share a unit with another block, start their
+// norm statistics behind its loads and finish 1-2 us after the rest.  Here
+// each wave streams one whole row (lane l holds elements 2 l + 128 t and
+// 2 l + 128 t + 1 of tile t), RW = M / (compute units) waves per block, RW / 2
+// RoPE pairs (rows i and i + hd / 2 of a head) per block.  Every block stages
+// the whole normed x (all waves read all of it); the arithmetic is k_gemv_v5's
+// (same limbs, same carry-free sums, same correction, same epilogue), so the
+// bits are the same.  K = 128 NT, int64 weights; UNR tiles of the row in
+// flight (8 for TinyLlama: the prologue and the block-wide staging take about
+// 3 us, a window of 4 drained before them).
+// ---------------------------------------------------------------------------
+template <int RW, int NT, int UNR>
+__global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
+                                                     const int64_t *__restrict__ W,
+                                                     const int64_t *__restrict__ x,
+                                                     const int64_t *__restrict__ norm_w,
+                                                     const int64_t *__restrict__ r_in, int M,
+                                                     const q48_ropekv rk)
+{
+    static_assert(RW % 2 == 0 && NT % UNR == 0, "row pairs, whole windows");
+    constexpr int K = 128 * NT;
+    constexpr int NP = K / 2;                           // element pairs of x
+    constexpr int XB = (NP + 64 * RW - 1) / (64 * RW);  // x pairs per thread
+    constexpr int PC = (K / 8 + 63) / 64;               // partial sums per lane (wave 0)
+    extern __shared__ __align__(16) uint32_t xs[];      // 3 limbs per element, all of K
+    __shared__ uint64_t xsum_w[RW];
+    __shared__ int64_t vrow[RW];
+    __shared__ int64_t r_sh;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // the row of this wave: pair p of the projection (hd / 2 pairs per head),
+    // its first row (even waves) or its partner hd / 2 rows on (odd waves)
+    const int half = rk.hd >> 1, sh = 31 - __builtin_clz((unsigned)half);
+    const int p = (RW / 2) * (int)blockIdx.x + (wave >> 1);
+    const int hh = p >> sh, j = p & (half - 1);
+    const int row = hh * rk.hd + j + ((wave & 1) ? half : 0);
+    const bool live = row < M;
+    // the position, read first through the constant address space (a scalar
+    // load: no vector-memory wait covers it)
+    typedef const __attribute__((address_space(4))) int cint;
+    const int p5 = rk.d_pos ? *(cint *)rk.d_pos : rk.pos;
+
+    // issue order: wave 0's partial sums, then every thread's x and norm
+    // weight pairs, then the wave's first UNR weight tiles
+    const uint64_t *st = reinterpret_cast<const uint64_t *>(r_in);
+    uint64_t plo[PC], phi[PC];
+    if (wave == 0) {
+#pragma unroll
+        for (int c = 0; c < PC; ++c) {
+            const int i = min(lane + c * 64, K / 8 - 1);
+            const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(st + 2 * i);
+            plo[c] = v.x;
+            phi[c] = v.y;
+        }
+    }
+    int64_t xv[2 * XB], nw[2 * XB];
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+        const int pi = min(tid + 64 * RW * b, NP - 1);
+        const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(x + 2 * pi);
+        const ulonglong2 w = *reinterpret_cast<const ulonglong2 *>(norm_w + 2 * pi);
+        xv[2 * b] = (int64_t)v.x;
+        xv[2 * b + 1] = (int64_t)v.y;
+        nw[2 * b] = (int64_t)w.x;
+        nw[2 * b + 1] = (int64_t)w.y;
+    }
+    // every wave's x loads ahead of any wave's weight loads in the compute
+    // unit's load path (measured: 5-10 us per token with the 8-tile window)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const ulonglong2 *w2 = reinterpret_cast<const ulonglong2 *>(W + (size_t)(live ? row : 0) * K) + lane;
+    ulonglong2 wa[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+        wa[u] = ld_wtile<0>(&w2[64 * u]);
+    __builtin_amdgcn_sched_barrier(0);
+    // the wave's cos / sin pair at the position (scalar loads)
+    typedef const __attribute__((address_space(4))) int64_t cint64;
+    const int pc = min(max(p5, 0), rk.max_seq - 1);
+    const int64_t c5 = *(cint64 *)(rk.cos_t + (size_t)pc * half + j);
+    const int64_t s5 = *(cint64 *)(rk.sin_t + (size_t)pc * half + j);
+
+    // r from the producer's partial sums, on wave 0 alone (as k_gemv_v5)
+    if (wave == 0) {
+        q48_u128 ss = 0;
+#pragma unroll
+        for (int c = 0; c < PC; ++c) {
+            const uint64_t m = lane + c * 64 < K / 8 ? ~0ull : 0ull;
+            ss += ((q48_u128)(phi[c] & m) << 64) | (plo[c] & m);
+        }
+        ss = q48_wave_sum128(ss);
+        const int64_t rv = rms_inv_of(ss, K);
+        if (lane == 0)
+            r_sh = rv;
+    }
+    __syncthreads();
+    const int64_t r = r_sh;
+
+    // stage fp_mul(fp_mul(x, r), w) as limbs (offset binary, as k_gemv_v5)
+    uint64_t xsum = 0;
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+        const int pi = tid + 64 * RW * b;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            int64_t v = q48_mul(q48_mul(xv[2 * b + e], r), nw[2 * b + e]);
+            v = pi < NP ? v : 0;
+            xsum += (uint64_t)v;
+            if (pi < NP) {
+                const int k = 2 * pi + e;
+                const uint64_t X = (uint64_t)v ^ 0x8000000000000000ull;
+                xs[3 * k] = (uint32_t)X & 0x3FFFFFu;
+                xs[3 * k + 1] = (uint32_t)(X >> 22) & 0x1FFFFFu;
+                xs[3 * k + 2] = (uint32_t)(X >> 43);
+            }
+        }
+    }
+    xsum = (uint64_t)q48_wave_sum64((int64_t)xsum);
+    if (lane == 0)
+        xsum_w[wave] = xsum;
+    __syncthreads();
+    uint64_t xtot = 0;
+#pragma unroll
+    for (int w = 0; w < RW; ++w)
+        xtot += xsum_w[w];
+
+    // the row: a rotating window of UNR tiles in flight
+    Acc6 A = {0, 0, 0, 0, 0, 0, 0};
+    const uint32_t *xl = xs + 6 * lane;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const uint32_t *q = xl + 384 * t;
+        const ulonglong2 w = wa[t % UNR];
+        mac6(A, q[0], q[1], q[2], w.x);
+        mac6(A, q[3], q[4], q[5], w.y);
+        if (t + UNR < NT)
+            wa[t % UNR] = ld_wtile<0>(&w2[64 * (t + UNR)]);
+    }
+    q48_u128 S = q48_wave_sum128(acc6_value(A));
+    S -= (q48_u128)xtot << 63;
+    const int64_t v = (int64_t)((q48_i128)S >> 48);
+    if (lane == 0)
+        vrow[wave] = v;
+    __syncthreads();
+
+    // RoPE of the q and k rows (rope_apply, llama_int.c:997-1008), then k
+    // and v to the caches at pos (llama_int.c:1414-1416): lane 0 of each wave
+    if (lane != 0 || !live)
+        return;
+    const int64_t o = vrow[wave ^ 1];
+    int64_t r5 = v;
+    if (hh < rk.n_heads + rk.n_kv)
+        r5 = (wave & 1) == 0 ? (int64_t)((uint64_t)q48_mul(v, c5) - (uint64_t)q48_mul(o, s5))
+                             : (int64_t)((uint64_t)q48_mul(v, c5) + (uint64_t)q48_mul(o, s5));
+    y[row] = r5;
+    if (hh >= rk.n_heads && p5 >= 0 && p5 < rk.max_seq) {
+        const bool isk = hh < rk.n_heads + rk.n_kv;
+        const int kh = hh - rk.n_heads - (isk ? 0 : rk.n_kv);
+        int64_t *cache = isk ? rk.kc : rk.vc;
+        const int d = j + ((wave & 1) ? half : 0);
+        cache[((size_t)rk.layer * rk.max_seq + p5) * ((size_t)rk.n_kv * rk.hd) +
+              (size_t)kh * rk.hd + d] = r5;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // k_gemv_p6: the persistent form of k_gemv_v5 for the long projections whose
 // blocks would otherwise repeat a costly prologue in lockstep rounds (the
 // normed gate|up with SwiGLU, the normed lm_head).  Block b takes the row
@@ -1012,6 +1184,16 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
             hipLaunchKernelGGL((k_gemv_p6<NW, 4, PRO, EPI, 16>), dim3(p6_grid(c, blocks)),
                                dim3(64 * NW), lds,
                                c->stream, y, W, x, norm_w, r_in, M, K, seg);
+            return (int)hipGetLastError();
+        }
+    }
+    // the q|k|v projection with RoPE at 10 rows per compute unit (TinyLlama
+    // on 256 units): one block per unit, one row per wave
+    if constexpr (PRO == 3 && EPI == 5) {
+        if (al && K == 2048 && c->cu_count > 0 && M == 10 * c->cu_count) {
+            hipLaunchKernelGGL((k_gemv_r1<10, 16, 8>), dim3(c->cu_count), dim3(64 * 10),
+                               (size_t)3 * K * sizeof(uint32_t), c->stream, y, W, x, norm_w, r_in,
+                               M, rkv);
             return (int)hipGetLastError();
         }
     }
