@@ -836,7 +836,7 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
         pos = *d_pos;
     if (pos < 0 || pos >= max_seq)
         return;
-    const int c = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
+    const int c = blockIdx.y, kh = blockIdx.x, tid = threadIdx.x;
     const int S = pos + 1, t0 = c * CH;
     if (t0 >= S)
         return;   // uniform: no barrier is skipped by part of the block
@@ -1452,7 +1452,11 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
         const size_t sc_n = (size_t)n_heads * max_seq, cm_n = (size_t)n_heads * ATT_NCMAX;
         unsigned *sync = ws_ext ? sync_ext : c->attx_sync;
         if (c->attn_one_launch && sync && attg_fits(c, head_dim, n_heads, n_kv, max_seq)) {
-            const dim3 grid((max_seq + ATTG_CH - 1) / ATTG_CH, n_kv);
+            // KV head fastest: the blocks of the live chunks are dispatched
+            // first and take one compute unit each (with chunk fastest, half of
+            // them shared a unit with another live block and ran slower, and
+            // both in-kernel exchanges waited for them)
+            const dim3 grid(n_kv, (max_seq + ATTG_CH - 1) / ATTG_CH);
 #define ATTG_LAUNCH(HD, MFS)                                                                  \
     hipLaunchKernelGGL((k_attn_g<HD, MFS>), grid, dim3(ATTG_NT), 0, c->stream, out, q, kcache, \
                        vcache, k_new, v_new, c->rope_cos, c->rope_sin, scale_p,               \
