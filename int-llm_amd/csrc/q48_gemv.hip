@@ -667,9 +667,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
 // (same limbs, same carry-free sums, same correction, same epilogue), so the
 // bits are the same.  K = 128 NT, int64 weights; UNR tiles of the row in
 // flight (8 for TinyLlama: the prologue and the block-wide staging take about
-// 3 us, a window of 4 drained before them).
+// 3 us, a window of 4 drained before them).  ROPE false: the plain q|k|v
+// projection (epilogue 0, attention above 512 positions rotates itself),
+// row RW b + w in wave w of block b.
 // ---------------------------------------------------------------------------
-template <int RW, int NT, int UNR>
+template <int RW, int NT, int UNR, bool ROPE = true>
 __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
                                                      const int64_t *__restrict__ W,
                                                      const int64_t *__restrict__ x,
@@ -691,15 +693,15 @@ __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // the row of this wave: pair p of the projection (hd / 2 pairs per head),
     // its first row (even waves) or its partner hd / 2 rows on (odd waves)
-    const int half = rk.hd >> 1, sh = 31 - __builtin_clz((unsigned)half);
+    const int half = ROPE ? rk.hd >> 1 : 1, sh = 31 - __builtin_clz((unsigned)half);
     const int p = (RW / 2) * (int)blockIdx.x + (wave >> 1);
     const int hh = p >> sh, j = p & (half - 1);
-    const int row = hh * rk.hd + j + ((wave & 1) ? half : 0);
+    const int row = ROPE ? hh * rk.hd + j + ((wave & 1) ? half : 0) : RW * (int)blockIdx.x + wave;
     const bool live = row < M;
     // the position, read first through the constant address space (a scalar
     // load: no vector-memory wait covers it)
     typedef const __attribute__((address_space(4))) int cint;
-    const int p5 = rk.d_pos ? *(cint *)rk.d_pos : rk.pos;
+    const int p5 = !ROPE ? 0 : rk.d_pos ? *(cint *)rk.d_pos : rk.pos;
 
     // issue order: wave 0's partial sums, then every thread's x and norm
     // weight pairs, then the wave's first UNR weight tiles
@@ -739,9 +741,12 @@ __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
     __builtin_amdgcn_sched_barrier(0);
     // the wave's cos / sin pair at the position (scalar loads)
     typedef const __attribute__((address_space(4))) int64_t cint64;
-    const int pc = min(max(p5, 0), rk.max_seq - 1);
-    const int64_t c5 = *(cint64 *)(rk.cos_t + (size_t)pc * half + j);
-    const int64_t s5 = *(cint64 *)(rk.sin_t + (size_t)pc * half + j);
+    int64_t c5 = 0, s5 = 0;
+    if constexpr (ROPE) {
+        const int pc = min(max(p5, 0), rk.max_seq - 1);
+        c5 = *(cint64 *)(rk.cos_t + (size_t)pc * half + j);
+        s5 = *(cint64 *)(rk.sin_t + (size_t)pc * half + j);
+    }
 
     // r from the producer's partial sums, on wave 0 alone (as k_gemv_v5)
     if (wave == 0) {
@@ -802,6 +807,11 @@ __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
     q48_u128 S = q48_wave_sum128(acc6_value(A));
     S -= (q48_u128)xtot << 63;
     const int64_t v = (int64_t)((q48_i128)S >> 48);
+    if constexpr (!ROPE) {
+        if (lane == 0 && live)
+            y[row] = v;
+        return;
+    }
     if (lane == 0)
         vrow[wave] = v;
     __syncthreads();
@@ -1187,11 +1197,12 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
             return (int)hipGetLastError();
         }
     }
-    // the q|k|v projection with RoPE at 10 rows per compute unit (TinyLlama
-    // on 256 units): one block per unit, one row per wave
-    if constexpr (PRO == 3 && EPI == 5) {
+    // the normed q|k|v projection (with or without RoPE) at 10 rows per
+    // compute unit (TinyLlama on 256 units): one block per unit, one row per
+    // wave
+    if constexpr (PRO == 3 && (EPI == 5 || EPI == 0)) {
         if (al && K == 2048 && c->cu_count > 0 && M == 10 * c->cu_count) {
-            hipLaunchKernelGGL((k_gemv_r1<10, 16, 8>), dim3(c->cu_count), dim3(64 * 10),
+            hipLaunchKernelGGL((k_gemv_r1<10, 16, 8, EPI == 5>), dim3(c->cu_count), dim3(64 * 10),
                                (size_t)3 * K * sizeof(uint32_t), c->stream, y, W, x, norm_w, r_in,
                                M, rkv);
             return (int)hipGetLastError();
