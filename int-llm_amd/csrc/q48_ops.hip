@@ -751,7 +751,10 @@ __device__ bool attg_exchange(uint64_t *xw, int c, int nc, int G, unsigned epoch
         attg_st64(xw + (size_t)ATTG_XW * c + 2 * tid, (u << 32) | epoch);
         attg_st64(xw + (size_t)ATTG_XW * c + 2 * tid + 1, (u & 0xFFFFFFFF00000000ull) | epoch);
     }
-    // every thread reads words (chunk, head, half) = i, i + NT, ... of nc x 2G
+    // every thread reads words (chunk, head, half) = i, i + NT, ... of nc x 2G;
+    // each wave polls until all of its words carry the epoch (a wave vote, no
+    // block barrier per round: a round is one load latency), then one
+    // barrier joins the waves
     const int nw = nc * 2 * G;
     const uint64_t t0 = wall_clock64();
     int ok = 1;
@@ -768,19 +771,22 @@ __device__ bool attg_exchange(uint64_t *xw, int c, int nc, int G, unsigned epoch
                 g32[r & 1] = (uint32_t)(w >> 32);
             }
         }
-        if (__syncthreads_and(mine))
+        if (__all(mine))
             break;
-        // the give-up decision is thread 0's clock, made uniform by the OR
-        if (__syncthreads_or(tid == 0 && wall_clock64() - t0 > ATTG_TIMEOUT)) {
-            if (tid == 0)
-                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the give-up decision: the wave's clock (a scalar read, uniform)
+        if (wall_clock64() - t0 > ATTG_TIMEOUT) {
             ok = 0;
             break;
         }
-        __builtin_amdgcn_s_sleep(1);
     }
-    __syncthreads();   // got[] complete (or abandoned) for every thread
-    return ok != 0;
+    // got[] complete (or abandoned) for every thread; a wave that gave up
+    // fails the block
+    if (__syncthreads_or(!ok)) {
+        if (tid == 0)
+            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+    }
+    return true;
 }
 
 // head_dim 32/64: at most 128 VGPRs, so that two blocks (16 waves) fit a
