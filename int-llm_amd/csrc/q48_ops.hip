@@ -737,6 +737,32 @@ __device__ __forceinline__ void attg_st64(uint64_t *p, uint64_t v)
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Maximum and wrapping sum over each 32-lane half of a wave (all lanes
+// active; every lane returns its half's result): DPP within rows of 16, then
+// the other row of the half.
+__device__ __forceinline__ int64_t attg_max32(int64_t v)
+{
+    int64_t o = (int64_t)q48_dpp64<Q48_DPP_XOR1>((uint64_t)v);
+    v = o > v ? o : v;
+    o = (int64_t)q48_dpp64<Q48_DPP_XOR2>((uint64_t)v);
+    v = o > v ? o : v;
+    o = (int64_t)q48_dpp64<Q48_DPP_HALF_MIRROR>((uint64_t)v);
+    v = o > v ? o : v;
+    o = (int64_t)q48_dpp64<Q48_DPP_MIRROR>((uint64_t)v);
+    v = o > v ? o : v;
+    o = (int64_t)__shfl_xor((long long)v, 16, 64);
+    return o > v ? o : v;
+}
+
+__device__ __forceinline__ uint64_t attg_sum32(uint64_t v)
+{
+    v += q48_dpp64<Q48_DPP_XOR1>(v);
+    v += q48_dpp64<Q48_DPP_XOR2>(v);
+    v += q48_dpp64<Q48_DPP_HALF_MIRROR>(v);
+    v += q48_dpp64<Q48_DPP_MIRROR>(v);
+    return v + (uint64_t)__shfl_xor((long long)v, 16, 64);
+}
+
 // Publish v[0..G) (thread hh < G publishes v for head hh) as epoch-tagged
 // halves into row `mine`, then gather, for every head hh < G, the values of
 // all nc chunks (rows xw + ATTG_XW c) into got[hh][c] (LDS).  Block-wide;
@@ -817,6 +843,7 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
     constexpr int DH = HD / 2;                          // dims per score thread
     static_assert(LW % 2 == 0 && HD % LW == 0, "16-byte row loads");
     static_assert(GM * CH * 2 == NT, "two threads per score");
+    static_assert(CH == 32 && NT == 64 * GM, "32 lanes per head in a chunk, a wave per head");
     static_assert(!MF || (HD == 64 && LW == 4 && CH == 32 && GM == 8), "matrix-core scores");
     constexpr int KDW = HD / 4 + 4;                     // digit-plane row: 16 words + 4 pad
     __shared__ int64_t qs[GM][HD];
@@ -1052,11 +1079,12 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
         }
         __syncthreads();
     }
-    if (tid < G) {
-        int64_t m = INT64_MIN;
-        for (int u = 0; u < nt; ++u)
-            m = sc[tid][u] > m ? sc[tid][u] : m;
-        loc[tid] = m;
+    // the chunk's maximum per head: 32 lanes per head (waves 0 .. GM / 2 - 1)
+    if (tid < 32 * GM) {
+        const int hq = tid >> 5, u = tid & 31;
+        const int64_t m = attg_max32(hq < G && u < nt ? sc[hq][u] : INT64_MIN);
+        if (u == 0 && hq < G)
+            loc[hq] = m;
     }
     __syncthreads();
     if (nc > 1) {
@@ -1066,11 +1094,15 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
                 __hip_atomic_store(ep, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
         }
-        if (tid < G) {
+        {
+            // the maximum over the chunks: wave hq for head hq
+            const int hq = tid >> 6, l = tid & 63;
             int64_t m = INT64_MIN;
-            for (int u = 0; u < nc; ++u)
-                m = got[tid][u] > m ? got[tid][u] : m;
-            loc[tid] = m;
+            for (int u = l; u < nc; u += 64)
+                m = got[hq][u] > m ? got[hq][u] : m;
+            m = q48_wave_max64(m);
+            if (l == 0 && hq < G)
+                loc[hq] = m;
         }
         __syncthreads();
     }
@@ -1079,11 +1111,11 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
     if (dh == 0 && hh < G)
         sc[hh][t] = live ? q48_safe_exp((int64_t)((uint64_t)sc[hh][t] - (uint64_t)loc[hh])) : 0;
     __syncthreads();
-    if (tid < G) {
-        uint64_t sm = 0;
-        for (int u = 0; u < nt; ++u)
-            sm += (uint64_t)sc[tid][u];
-        loc[tid] = (int64_t)sm;
+    if (tid < 32 * GM) {
+        const int hq = tid >> 5, u = tid & 31;
+        const uint64_t sm = attg_sum32(hq < G && u < nt ? (uint64_t)sc[hq][u] : 0);
+        if (u == 0 && hq < G)
+            loc[hq] = (int64_t)sm;
     }
     __syncthreads();
     if (nc > 1) {
@@ -1092,11 +1124,14 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
                 __hip_atomic_store(ep, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
         }
-        if (tid < G) {
+        {
+            const int hq = tid >> 6, l = tid & 63;
             uint64_t sm = 0;
-            for (int u = 0; u < nc; ++u)
-                sm += (uint64_t)got[tid][u];
-            loc[tid] = (int64_t)sm;
+            for (int u = l; u < nc; u += 64)
+                sm += (uint64_t)got[hq][u];
+            sm = (uint64_t)q48_wave_sum64((int64_t)sm);
+            if (l == 0 && hq < G)
+                loc[hq] = (int64_t)sm;
         }
         if (c == 0 && tid == 0)   // every block of the head is past exchange 2
             __hip_atomic_store(ep, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
