@@ -669,18 +669,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
 // flight (8 for TinyLlama: the prologue and the block-wide staging take about
 // 3 us, a window of 4 drained before them).  ROPE false: the plain q|k|v
 // projection (epilogue 0, attention above 512 positions rotates itself),
-// row RW b + w in wave w of block b.
+// row RW b + w in wave w of block b.  WT 1: bfloat16-resident weights, 512
+// per 1 KB tile (8 per lane), by k_gemv_v5's fast form with its wave check
+// and exact recomputation.
 // ---------------------------------------------------------------------------
-template <int RW, int NT, int UNR, bool ROPE = true>
+template <int RW, int NT, int UNR, bool ROPE = true, int WT = 0>
 __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
-                                                     const int64_t *__restrict__ W,
+                                                     const void *__restrict__ Wv,
                                                      const int64_t *__restrict__ x,
                                                      const int64_t *__restrict__ norm_w,
                                                      const int64_t *__restrict__ r_in, int M,
                                                      const q48_ropekv rk)
 {
     static_assert(RW % 2 == 0 && NT % UNR == 0, "row pairs, whole windows");
-    constexpr int K = 128 * NT;
+    constexpr int TE = WFmt<WT>::TE * 8;                // elements per 1 KB tile
+    constexpr int K = TE * NT;
     constexpr int NP = K / 2;                           // element pairs of x
     constexpr int XB = (NP + 64 * RW - 1) / (64 * RW);  // x pairs per thread
     constexpr int PC = (K / 8 + 63) / 64;               // partial sums per lane (wave 0)
@@ -733,11 +736,13 @@ __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    const ulonglong2 *w2 = reinterpret_cast<const ulonglong2 *>(W + (size_t)(live ? row : 0) * K) + lane;
+    const ulonglong2 *w2 = reinterpret_cast<const ulonglong2 *>(
+                               static_cast<const char *>(Wv) +
+                               (size_t)(live ? row : 0) * K * WFmt<WT>::ES) + lane;
     ulonglong2 wa[UNR];
 #pragma unroll
     for (int u = 0; u < UNR; ++u)
-        wa[u] = ld_wtile<0>(&w2[64 * u]);
+        wa[u] = ld_wtile<WT>(&w2[64 * u]);
     __builtin_amdgcn_sched_barrier(0);
     // the wave's cos / sin pair at the position (scalar loads)
     typedef const __attribute__((address_space(4))) int64_t cint64;
@@ -779,7 +784,8 @@ __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
                 const uint64_t X = (uint64_t)v ^ 0x8000000000000000ull;
                 xs[3 * k] = (uint32_t)X & 0x3FFFFFu;
                 xs[3 * k + 1] = (uint32_t)(X >> 22) & 0x1FFFFFu;
-                xs[3 * k + 2] = (uint32_t)(X >> 43);
+                // bfloat16 weights: the signed top limb (b16_tile_fast)
+                xs[3 * k + 2] = WT == 1 ? (uint32_t)(v >> 43) : (uint32_t)(X >> 43);
             }
         }
     }
@@ -792,20 +798,46 @@ __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
     for (int w = 0; w < RW; ++w)
         xtot += xsum_w[w];
 
-    // the row: a rotating window of UNR tiles in flight
+    // the row: a rotating window of UNR tiles in flight; lane l's elements
+    // of tile t start at TE t + (TE / 64) l
     Acc6 A = {0, 0, 0, 0, 0, 0, 0};
-    const uint32_t *xl = xs + 6 * lane;
+    Acc3 F = {0, 0, 0, 0, 0, 0};
+    q48_u16x2 chk = {0, 0};
+    const uint32_t *xl = xs + 3 * (TE / 64) * lane;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const uint32_t *q = xl + 384 * t;
+        const uint32_t *q = xl + 3 * TE * t;
         const ulonglong2 w = wa[t % UNR];
-        mac6(A, q[0], q[1], q[2], w.x);
-        mac6(A, q[3], q[4], q[5], w.y);
+        if constexpr (WT == 0) {
+            mac6(A, q[0], q[1], q[2], w.x);
+            mac6(A, q[3], q[4], q[5], w.y);
+        } else {
+            b16_tile_fast(F, chk, q, 0, 0, w);
+        }
         if (t + UNR < NT)
-            wa[t % UNR] = ld_wtile<0>(&w2[64 * (t + UNR)]);
+            wa[t % UNR] = ld_wtile<WT>(&w2[64 * (t + UNR)]);
     }
-    q48_u128 S = q48_wave_sum128(acc6_value(A));
-    S -= (q48_u128)xtot << 63;
+    // bfloat16: a pattern outside the fast window anywhere in the wave's row
+    // sends the wave through the general expansion (rare)
+    bool fast = false;
+    q48_u128 Sl;
+    if constexpr (WT == 1) {
+        b16_pin(F);
+        fast = b16_wave_ok(chk);
+        if (fast) {
+            Sl = acc3_value(F);
+        } else {
+#pragma unroll 1
+            for (int t = 0; t < NT; ++t)
+                mac_tile<1>(A, xl + 3 * TE * t, 0, 0, w2[64 * t]);
+            Sl = acc6_value(A);
+        }
+    } else {
+        Sl = acc6_value(A);
+    }
+    q48_u128 S = q48_wave_sum128(Sl);
+    if (!fast)
+        S -= (q48_u128)xtot << 63;
     const int64_t v = (int64_t)((q48_i128)S >> 48);
     if constexpr (!ROPE) {
         if (lane == 0 && live)
@@ -1202,9 +1234,9 @@ static int launch_v4(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,
     // wave
     if constexpr (PRO == 3 && (EPI == 5 || EPI == 0)) {
         if (al && K == 2048 && c->cu_count > 0 && M == 10 * c->cu_count) {
-            hipLaunchKernelGGL((k_gemv_r1<10, 16, 8, EPI == 5>), dim3(c->cu_count), dim3(64 * 10),
-                               (size_t)3 * K * sizeof(uint32_t), c->stream, y, W, x, norm_w, r_in,
-                               M, rkv);
+            hipLaunchKernelGGL((k_gemv_r1<10, 16, 8, EPI == 5, 0>), dim3(c->cu_count),
+                               dim3(64 * 10), (size_t)3 * K * sizeof(uint32_t), c->stream, y,
+                               (const void *)W, x, norm_w, r_in, M, rkv);
             return (int)hipGetLastError();
         }
     }
@@ -1259,6 +1291,18 @@ static int launch_b16(q48_ctx *c, int64_t *y, const uint16_t *W, const int64_t *
                       const q48_ropekv *rk = nullptr)
 {
     const q48_ropekv rkv = rk ? *rk : q48_ropekv{};
+    // the normed q|k|v projection at 10 rows per compute unit: one block per
+    // unit, one row per wave (as for int64 weights)
+    if constexpr (PRO == 3 && (EPI == 5 || EPI == 0)) {
+        const bool al = ((uintptr_t)x & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 &&
+                        ((uintptr_t)r_in & 15) == 0 && ((uintptr_t)W & 15) == 0;
+        if (al && K == 2048 && c->cu_count > 0 && M == 10 * c->cu_count) {
+            hipLaunchKernelGGL((k_gemv_r1<10, 4, 4, EPI == 5, 1>), dim3(c->cu_count),
+                               dim3(64 * 10), (size_t)3 * K * sizeof(uint32_t), c->stream, y,
+                               (const void *)W, x, norm_w, r_in, M, rkv);
+            return (int)hipGetLastError();
+        }
+    }
     switch (K) {
     case 512:
         return launch_b16_ntf<PRO, EPI, 1>(c, y, W, x, norm_w, r_in, r_out, M, K, rk);
