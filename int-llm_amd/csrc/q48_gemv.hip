@@ -490,21 +490,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                     tile(t0 + u, wa[u]);
         }
     }
-    // bfloat16: a pattern outside the fast window anywhere in the wave's
-    // tiles sends the wave through the general expansion (rare)
-    bool fast = false;
+    // bfloat16: the fast sums plus, when a pattern outside the fast window
+    // is anywhere in the wave's tiles (rare), their residuals
     q48_u128 S;
     if constexpr (WT == 1) {
         b16_pin(F);
-        fast = b16_wave_ok(chk);
-        if (fast) {
-            S = acc3_value(F);
-        } else {
-#pragma unroll 1
-            for (int t = 0; t < nt; ++t)
-                mac_tile<1>(A, xw, l8, t, w2[t * 8]);
-            S = acc6_value(A);
-        }
+        S = acc3_value(F);
+        if (!b16_wave_ok(chk))
+            b16_fix_tiles(
+                S, nt, [&](int t) { return w2[t * 8]; },
+                [&](int t) { return xw + 3 * (64 * t + 8 * l8); });
     } else {
         // the kn % 16 elements (even) of the segment's end, one pair per lane
         if (2 * l8 < (kn & 15)) {
@@ -517,7 +512,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     }
     S = q48_sum8_u128(S);
     if (l8 == 0) {
-        if (!fast)
+        if constexpr (WT == 0)
             S -= (q48_u128)xsum << 63;
         part[wave][g][0] = (uint64_t)S;
         part[wave][g][1] = (uint64_t)(S >> 64);
@@ -817,26 +812,21 @@ __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
         if (t + UNR < NT)
             wa[t % UNR] = ld_wtile<WT>(&w2[64 * (t + UNR)]);
     }
-    // bfloat16: a pattern outside the fast window anywhere in the wave's row
-    // sends the wave through the general expansion (rare)
-    bool fast = false;
+    // bfloat16: the fast sums plus, when a pattern outside the fast window
+    // is anywhere in the wave's row (rare), their residuals
     q48_u128 Sl;
     if constexpr (WT == 1) {
         b16_pin(F);
-        fast = b16_wave_ok(chk);
-        if (fast) {
-            Sl = acc3_value(F);
-        } else {
-#pragma unroll 1
-            for (int t = 0; t < NT; ++t)
-                mac_tile<1>(A, xl + 3 * TE * t, 0, 0, w2[64 * t]);
-            Sl = acc6_value(A);
-        }
+        Sl = acc3_value(F);
+        if (!b16_wave_ok(chk))
+            b16_fix_tiles(
+                Sl, NT, [&](int t) { return w2[64 * t]; },
+                [&](int t) { return xl + 3 * TE * t; });
     } else {
         Sl = acc6_value(A);
     }
     q48_u128 S = q48_wave_sum128(Sl);
-    if (!fast)
+    if constexpr (WT == 0)
         S -= (q48_u128)xtot << 63;
     const int64_t v = (int64_t)((q48_i128)S >> 48);
     if constexpr (!ROPE) {
@@ -1020,28 +1010,23 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
             else
                 wa[t % UNR] = ld_wtile<WT>(&w2n[(t + UNR - NTF) * 8]);
         }
-        // bfloat16 outside the fast window: this group again, general form
-        // (the next group's tiles stay in the window)
-        bool fast = false;
+        // bfloat16 outside the fast window: the residuals of this group's
+        // tiles (the next group's tiles stay in the window)
         q48_u128 S;
         if constexpr (WT == 1) {
             b16_pin(F);
-            fast = b16_wave_ok(chk);
-            if (fast) {
-                S = acc3_value(F);
-            } else {
-#pragma unroll 1
-                for (int t = 0; t < NTF; ++t)
-                    mac_tile<1>(A, xw, l8, t, w2[t * 8]);
-                S = acc6_value(A);
-            }
+            S = acc3_value(F);
+            if (!b16_wave_ok(chk))
+                b16_fix_tiles(
+                    S, NTF, [&](int t) { return w2[t * 8]; },
+                    [&](int t) { return xw + 3 * (64 * t + 8 * l8); });
         } else {
             S = acc6_value(A);
         }
         w2 = w2n;
         S = q48_sum8_u128(S);
         if (l8 == 0) {
-            if (!fast)
+            if constexpr (WT == 0)
                 S -= (q48_u128)xsum << 63;
             part[i & 1][wave][g][0] = (uint64_t)S;
             part[i & 1][wave][g][1] = (uint64_t)(S >> 64);

@@ -101,32 +101,15 @@ template <int WT> struct WFmt;
 template <> struct WFmt<0> { static constexpr int ES = 8, TE = 16; };
 template <> struct WFmt<1> { static constexpr int ES = 2, TE = 64; };
 
-// One 128-byte tile t of this lane's row against the staged x limbs (3 per
-// element at xw[3 j]).  For the bfloat16 weights this is the general form,
-// every pattern expanded by q48_bf16; the staged top limb is signed there
-// (see b16_tile_fast) and is moved back to offset binary for mac6.
+// One 128-byte tile t of this lane's row of int64 weights against the staged
+// x limbs (3 per element at xw[3 j]).
 template <int WT>
 __device__ __forceinline__ void mac_tile(Acc6 &A, const uint32_t *xw, int l8, int t, ulonglong2 w)
 {
-    if constexpr (WT == 0) {
-        const uint32_t *p = xw + 6 * l8 + 48 * t;
-        mac6(A, p[0], p[1], p[2], w.x);
-        mac6(A, p[3], p[4], p[5], w.y);
-    } else {
-        // one tile at a time: without the barrier the scheduler hoists the
-        // limb reads and expansions of every tile and runs out of registers
-        __builtin_amdgcn_sched_barrier(0);
-        const uint32_t *p = xw + 3 * (64 * t + 8 * l8);
-        const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)(w.x >> 32), (uint32_t)w.y,
-                               (uint32_t)(w.y >> 32)};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            mac6(A, p[3 * e], p[3 * e + 1], p[3 * e + 2] + 0x100000u,
-                 (uint64_t)q48_bf16((u[e >> 1] >> (16 * (e & 1))) & 0xffffu));
-            if (e & 1)
-                __builtin_amdgcn_sched_barrier(0);
-        }
-    }
+    static_assert(WT == 0, "the bfloat16 tiles use b16_tile_fast and b16_tile_fix");
+    const uint32_t *p = xw + 6 * l8 + 48 * t;
+    mac6(A, p[0], p[1], p[2], w.x);
+    mac6(A, p[3], p[4], p[5], w.y);
 }
 
 // Fast form of the bfloat16 tiles.  A pattern with exponent e in [103, 126]
@@ -140,13 +123,23 @@ __device__ __forceinline__ void mac_tile(Acc6 &A, const uint32_t *xw, int l8, in
 // subnormal, |w| < 2^-24, |w| >= 1, inf, NaN) is caught by a range check
 // folded into a running packed 16-bit maximum: 2 b mod 2^16 drops the sign,
 // and 2 b - (103 << 8) wraps to at least 24 << 8 outside the window.  A
-// wave whose check fails recomputes its tiles with mac_tile<1>.
+// wave whose check fails adds the residuals of b16_tile_fix.
 struct Acc3 {
     int64_t f0, f1, f2, g0, g1, g2;   // even / odd weights of a pair
 };
 constexpr uint32_t B16_EXP = 31u << 23;                 // 2^31 in the f32 exponent
 constexpr unsigned short B16_DLO = (unsigned short)(0x10000 - (103 << 8));
 constexpr unsigned B16_DMAX = (24u << 8) - 1;           // largest in-window value
+
+// v_cvt_i32_f32 of the bits fb: the fast form's t.  Written out so that its
+// value outside the window (saturated, or 0 for NaN, as the ISA defines it)
+// is the same in the fast sums and in b16_tile_fix.
+__device__ __forceinline__ int32_t b16_t(uint32_t fb)
+{
+    int32_t t;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(t) : "v"(fb));
+    return t;
+}
 
 __device__ __forceinline__ void b16_tile_fast(Acc3 &F, q48_u16x2 &chk, const uint32_t *xw,
                                               int l8, int t, ulonglong2 w)
@@ -167,14 +160,76 @@ __device__ __forceinline__ void b16_tile_fast(Acc3 &F, q48_u16x2 &chk, const uin
         const q48_u16x2 d = __builtin_bit_cast(q48_u16x2, u[h]) * (q48_u16x2)(2) +
                             (q48_u16x2)(B16_DLO);
         chk = __builtin_elementwise_max(chk, d);
-        const int32_t ta = (int32_t)__builtin_bit_cast(float, (u[h] << 16) + B16_EXP);
-        const int32_t tb = (int32_t)__builtin_bit_cast(float, (u[h] & 0xffff0000u) + B16_EXP);
+        const int32_t ta = b16_t((u[h] << 16) + B16_EXP);
+        const int32_t tb = b16_t((u[h] & 0xffff0000u) + B16_EXP);
         F.f0 += (int64_t)ta * q[6 * h];
         F.f1 += (int64_t)ta * q[6 * h + 1];
         F.f2 += (int64_t)ta * q[6 * h + 2];
         F.g0 += (int64_t)tb * q[6 * h + 3];
         F.g1 += (int64_t)tb * q[6 * h + 4];
         F.g2 += (int64_t)tb * q[6 * h + 5];
+    }
+}
+
+// The exact residual of one tile's patterns outside the fast window, added
+// to S.  The fast sums hold t 2^17 x for every weight, t = b16_t of the
+// shifted pattern, and stay exact outside the window too (|t| <= 2^31 keeps
+// every product below 2^53); adding w x - t 2^17 x for exactly those
+// weights, w = q48_bf16(b) and x rebuilt from its limbs, gives sum w x mod
+// 2^128.  Per weight under a per-lane test: the wave runs a body only when
+// one of its lanes holds such a pattern there.
+__device__ __forceinline__ void b16_tile_fix(q48_u128 &S, const uint32_t *p, ulonglong2 w)
+{
+    const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)(w.x >> 32), (uint32_t)w.y,
+                           (uint32_t)(w.y >> 32)};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t b = (u[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        const uint32_t ex = (b >> 7) & 0xffu;
+        if (ex < 103u || ex > 126u) {
+            const uint32_t fb = (e & 1) ? (u[e >> 1] & 0xffff0000u) + B16_EXP
+                                        : (u[e >> 1] << 16) + B16_EXP;
+            const int64_t x = (int64_t)((uint64_t)p[3 * e] + ((uint64_t)p[3 * e + 1] << 22) +
+                                        ((uint64_t)(int64_t)(int32_t)p[3 * e + 2] << 43));
+            S += (q48_u128)q48_smul128(q48_bf16(b), x) -
+                 ((q48_u128)q48_smul128(b16_t(fb), x) << 17);
+        }
+    }
+}
+
+// true on every lane when some lane of the wave holds a pattern of the tile
+// w outside the fast window (the range check of b16_tile_fast)
+__device__ __forceinline__ bool b16_tile_out(ulonglong2 w)
+{
+    const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)(w.x >> 32), (uint32_t)w.y,
+                           (uint32_t)(w.y >> 32)};
+    q48_u16x2 m = (q48_u16x2)(0);
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+        m = __builtin_elementwise_max(m, __builtin_bit_cast(q48_u16x2, u[h]) * (q48_u16x2)(2) +
+                                             (q48_u16x2)(B16_DLO));
+    const unsigned mx = m.x > m.y ? m.x : m.y;
+    return __builtin_amdgcn_ballot_w64(mx > B16_DMAX) != 0;
+}
+
+// The residual pass of a wave whose range check failed: its nt tiles again,
+// ld(t) the lane's 16 bytes of tile t and px(t) their staged limbs, read 8
+// tiles at a time (one round of load latency per 8) and fixed only where a
+// lane holds a pattern outside the window.
+template <class Ld, class Px>
+__device__ __forceinline__ void b16_fix_tiles(q48_u128 &S, int nt, Ld ld, Px px)
+{
+    constexpr int B = 8;
+#pragma unroll 1
+    for (int t0 = 0; t0 < nt; t0 += B) {
+        ulonglong2 wb[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+            wb[u] = ld(t0 + u < nt ? t0 + u : nt - 1);
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+            if (t0 + u < nt && b16_tile_out(wb[u]))
+                b16_tile_fix(S, px(t0 + u), wb[u]);
     }
 }
 
