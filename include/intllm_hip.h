@@ -406,7 +406,10 @@ int q48_sample_step(q48_ctx *ctx, const int64_t *logits, int vocab, int64_t temp
  * capture). */
 int q48_sample_reserve(q48_ctx *ctx, int vocab);
 
-/* Capture the ops enqueued between begin and end into the context's graph. */
+/* Capture the ops enqueued between begin and end into the context's graph.
+ * begin (which replaces any previous graph) and drop wait for the stream
+ * before destroying the executable graph, so in-flight launches of it finish
+ * first. */
 int q48_graph_begin(q48_ctx *ctx);
 int q48_graph_end(q48_ctx *ctx);
 int q48_graph_launch(q48_ctx *ctx, int times);

@@ -1076,6 +1076,8 @@ int q48_graph_begin(q48_ctx *c)
     if (!c || c->capturing)
         return Q48_EINVAL;
     if (c->graph_exec) {
+        // launches of the old graph may still be in flight on the stream
+        (void)hipStreamSynchronize(c->stream);
         (void)hipGraphExecDestroy(c->graph_exec);
         c->graph_exec = nullptr;
     }
@@ -1121,8 +1123,11 @@ int q48_graph_drop(q48_ctx *c)
 {
     if (!c || c->capturing)
         return Q48_EINVAL;
-    if (c->graph_exec)
+    if (c->graph_exec) {
+        // launches of the graph may still be in flight on the stream
+        (void)hipStreamSynchronize(c->stream);
         (void)hipGraphExecDestroy(c->graph_exec);
+    }
     if (c->graph)
         (void)hipGraphDestroy(c->graph);
     c->graph_exec = nullptr;
