@@ -926,3 +926,41 @@ def test_bf16_gemv_forms_equal_int64(ctx, oracle, M, K, persistent, mode):
         ctx.set_gemv_persistent(True)
     for b in (dW, dWb, dx, dnw, ds, ya, yb):
         b.free()
+
+
+def test_graph_drop_and_replace_while_in_flight(ctx):
+    """q48_graph_drop, and q48_graph_begin replacing a graph, right after
+    q48_graph_launch with no synchronisation between: the launches in flight
+    finish before the executable graph is destroyed, and the captured GEMV's
+    output equals the eager one's."""
+    rng = np.random.default_rng(11)
+    M, K = 2048, 2048
+    W = rng.integers(-(1 << 46), 1 << 46, M * K, dtype=np.int64)
+    x = rng.integers(-(1 << 50), 1 << 50, K, dtype=np.int64)
+    dW, dx = ctx.buffer(M * K), ctx.to_device(x)
+    dW.upload(W)
+    ya, yb = ctx.buffer(M), ctx.buffer(M)
+    L = intllm.hip_lib()
+    try:
+        ctx.gemv(ya.ptr, dW.ptr, dx.ptr, M, K)
+        want = ya.download()
+        def capture():
+            assert L.q48_graph_begin(ctx.h) == 0
+            ctx.gemv(yb.ptr, dW.ptr, dx.ptr, M, K)
+            assert L.q48_graph_end(ctx.h) == 0
+
+        say("graph drop while in flight")
+        capture()
+        assert L.q48_graph_launch(ctx.h, 16) == 0
+        assert L.q48_graph_drop(ctx.h) == 0
+        assert np.array_equal(yb.download(), want), "drop"
+        say("graph replaced while in flight")
+        capture()
+        assert L.q48_graph_launch(ctx.h, 16) == 0
+        capture()                                   # replaces the graph in flight
+        assert L.q48_graph_launch(ctx.h, 1) == 0
+        assert np.array_equal(yb.download(), want), "replace"
+        assert L.q48_graph_drop(ctx.h) == 0
+    finally:
+        for b in (dW, dx, ya, yb):
+            b.free()
