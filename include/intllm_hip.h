@@ -215,10 +215,20 @@ int q48_attn_decode_rope_noalloc(q48_ctx *ctx, int64_t *out, const int64_t *q,
                                  const int64_t *v_new, int layer, int pos, int n_heads,
                                  int n_kv, int head_dim, int max_seq);
 size_t q48_attn_noalloc_max_bytes(void);
-/* Synchronises; Q48_ETIMEOUT if a one-launch split attention could not
- * finish (a block waited past its bound: blocks were not all resident; its
- * barrier words are then cleared), else Q48_OK. */
+/* Synchronises; Q48_ETIMEOUT if a one-launch split attention launched since
+ * the last call could not finish (a block waited past its bound: blocks were
+ * not all resident; its output is then wrong and its exchange words are
+ * cleared, so the next launch starts clean), else Q48_OK.  The reference's
+ * llama_forward cannot fail this way; its callers treat a failed forward
+ * (NULL) as the end of generation (llama_int.c:3083-3086, 3106), and
+ * q48h_forward / q48h_generate / q48h_decode_* return this code. */
 int q48_attn_status(q48_ctx *ctx);
+/* The one-launch split attention's wait bound in wall-clock ticks (a
+ * negative value restores the default, 2^24 ticks); 0 makes every chunk
+ * block give up at its first exchange without waiting, so that the timeout
+ * path can be tested while every block still exits normally.  No reference
+ * counterpart.  Changes q48_graph_stamp. */
+int q48_set_attn_wait(q48_ctx *ctx, int64_t ticks);
 
 /* Long normed GEMVs (more than two rounds of 8-row groups: gate|up, lm_head)
  * run as persistent blocks that loop over row groups (on: the default), or
@@ -406,14 +416,34 @@ int q48_sample_step(q48_ctx *ctx, const int64_t *logits, int vocab, int64_t temp
  * capture). */
 int q48_sample_reserve(q48_ctx *ctx, int vocab);
 
-/* Capture the ops enqueued between begin and end into the context's graph.
- * begin (which replaces any previous graph) and drop wait for the stream
- * before destroying the executable graph, so in-flight launches of it finish
- * first. */
+/* Graph capture of stream-ordered ops (no reference counterpart: the
+ * reference calls llama_forward once per token, llama_int.c:3103-3113; a
+ * captured decode step replays that call's kernels with the token and
+ * position read from the device step state).
+ *
+ * The context graph: begin captures into it (replacing any previous one),
+ * end instantiates it, launch replays it, drop destroys it.  Destroying waits
+ * for the stream first, so in-flight launches finish. */
 int q48_graph_begin(q48_ctx *ctx);
 int q48_graph_end(q48_ctx *ctx);
 int q48_graph_launch(q48_ctx *ctx, int times);
 int q48_graph_drop(q48_ctx *ctx);
+/* Graphs the caller holds, any number at once: q48_graph_capture starts a
+ * capture that q48_graph_instantiate ends into a new handle (uploaded to the
+ * device before it returns); q48_graph_replay launches it `times` times;
+ * q48_graph_destroy waits for the stream and frees it.  Workspaces the
+ * context replaces while any graph is alive are freed only after the last
+ * graph is destroyed, so a graph never replays against freed memory.
+ * q48_graph_stamp changes whenever a context setting that selects the
+ * kernels or kernel arguments a capture records changes (the q48_set_*
+ * switches, q48_rope_init with new parameters): a caller that caches graphs
+ * keys them on it. */
+typedef struct q48_graph q48_graph;
+int q48_graph_capture(q48_ctx *ctx);
+int q48_graph_instantiate(q48_ctx *ctx, q48_graph **out);
+int q48_graph_replay(q48_ctx *ctx, q48_graph *graph, int times);
+int q48_graph_destroy(q48_ctx *ctx, q48_graph *graph);
+uint64_t q48_graph_stamp(const q48_ctx *ctx);
 
 /* ---- kernel timing (diagnostic) -------------------------------------------- */
 

@@ -20,15 +20,50 @@ constexpr int kMaxHeadDim = 256;
 
 } // namespace
 
+int q48_release(q48_ctx *c, void *p)
+{
+    if (!p)
+        return Q48_OK;
+    // earlier kernels may still read it
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q48_EHIP;
+    if (c->n_graphs <= 0)
+        return hip_rc(hipFree(p));
+    // an instantiated graph may hold this address: keep the buffer until the
+    // last graph is destroyed (the graph keeps working on it)
+    if (c->n_retired == c->cap_retired) {
+        const int cap = c->cap_retired ? 2 * c->cap_retired : 8;
+        void **r = (void **)realloc(c->retired, (size_t)cap * sizeof(void *));
+        if (!r)
+            return Q48_ENOMEM;
+        c->retired = r;
+        c->cap_retired = cap;
+    }
+    c->retired[c->n_retired++] = p;
+    return Q48_OK;
+}
+
+namespace {
+void graph_destroy(q48_ctx *c, q48_graph *g);
+
+void free_retired(q48_ctx *c)
+{
+    for (int i = 0; i < c->n_retired; ++i)
+        (void)hipFree(c->retired[i]);
+    c->n_retired = 0;
+}
+} // namespace
+
 int q48_ws_reserve(q48_ctx *c, size_t bytes)
 {
     if (bytes <= c->ws_bytes)
         return Q48_OK;
+    if (c->capturing)
+        return Q48_ESTATE;   // workspaces reach their size outside a capture
     if (c->ws) {
-        // earlier kernels may still read the old workspace
-        if (hipStreamSynchronize(c->stream) != hipSuccess)
-            return Q48_EHIP;
-        (void)hipFree(c->ws);
+        int rc = q48_release(c, c->ws);
+        if (rc)
+            return rc;
         c->ws = nullptr;
         c->ws_bytes = 0;
     }
@@ -48,9 +83,9 @@ int q48_rms_reserve(q48_ctx *c, int blocks)
     if (c->capturing)
         return Q48_ESTATE;
     if (c->rms_part) {
-        if (hipStreamSynchronize(c->stream) != hipSuccess)
-            return Q48_EHIP;
-        (void)hipFree(c->rms_part);
+        int rc = q48_release(c, c->rms_part);
+        if (rc)
+            return rc;
         c->rms_part = nullptr;
         c->rms_blocks = 0;
     }
@@ -105,6 +140,7 @@ int q48_ctx_create(q48_ctx **out, int device)
     c->pf_attn_mfma = 1;
     c->attx_per_cu[0] = c->attx_per_cu[1] = c->attx_per_cu[2] = c->attx_per_cu[3] = -1;
     c->attn_g_mfma = 1;
+    c->attg_wait = q48_attg_default_wait();
     if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
         hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess ||
         hipMalloc(&c->d_step, 4 * sizeof(int)) != hipSuccess ||
@@ -151,10 +187,10 @@ int q48_ctx_destroy(q48_ctx *c)
     (void)hipFree(c->smp);
     (void)hipFree(c->tmp);
     (void)hipFree(c->attx_sync);
-    if (c->graph_exec)
-        (void)hipGraphExecDestroy(c->graph_exec);
-    if (c->graph)
-        (void)hipGraphDestroy(c->graph);
+    graph_destroy(c, c->cur);
+    c->cur = nullptr;
+    free_retired(c);   // handles the caller never destroyed keep nothing alive
+    free(c->retired);
     for (int i = 0; i < c->prof_cap; ++i) {
         if (c->prof[i].a)
             (void)hipEventDestroy(c->prof[i].a);
@@ -399,12 +435,16 @@ int q48_rope_init(q48_ctx *c, int head_dim, int max_seq, int theta)
     if (c->rope_cos && c->rope_head_dim == head_dim && c->rope_max_seq == max_seq &&
         c->rope_theta == theta)
         return Q48_OK;
-    if (hipStreamSynchronize(c->stream) != hipSuccess)
-        return Q48_EHIP;
-    (void)hipFree(c->rope_cos);
-    (void)hipFree(c->rope_sin);
+    if (c->capturing)
+        return Q48_ESTATE;
+    int rrc = q48_release(c, c->rope_cos);
+    if (rrc == Q48_OK)
+        rrc = q48_release(c, c->rope_sin);
+    if (rrc)
+        return rrc;
     c->rope_cos = c->rope_sin = nullptr;
     c->rope_head_dim = c->rope_max_seq = c->rope_theta = 0;
+    ++c->stamp;   // captured kernels hold the old tables' addresses
     size_t n = (size_t)max_seq * (head_dim / 2) * sizeof(int64_t);
     // the sine table carries one more value: the attention score scale
     if (hipMalloc(&c->rope_cos, n) != hipSuccess ||
@@ -524,9 +564,9 @@ int tmp_reserve(q48_ctx *c, size_t bytes)
     if (c->capturing)
         return Q48_ESTATE;
     if (c->tmp) {
-        if (hipStreamSynchronize(c->stream) != hipSuccess)
-            return Q48_EHIP;
-        (void)hipFree(c->tmp);
+        int rc = q48_release(c, c->tmp);
+        if (rc)
+            return rc;
         c->tmp = nullptr;
         c->tmp_bytes = 0;
     }
@@ -623,30 +663,53 @@ int q48_attn_status(q48_ctx *c)
         return Q48_EINVAL;
     if (c->capturing)
         return Q48_ESTATE;
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return Q48_EHIP;
+    if (!c->attg_unchecked)
+        return Q48_OK;   // no k_attn_g launch since the words were last read
     const size_t off = q48_attn_sync_bytes() - 16 * sizeof(unsigned);   // the error word
     int e[2] = {0, 0};
-    if (hipStreamSynchronize(c->stream) != hipSuccess ||
-        hipMemcpy(&e[0], (char *)c->attx_sync + off, sizeof(int), hipMemcpyDeviceToHost) !=
+    if (hipMemcpy(&e[0], (char *)c->attx_sync + off, sizeof(int), hipMemcpyDeviceToHost) !=
             hipSuccess ||
         (c->scratch_sync &&
          hipMemcpy(&e[1], (char *)c->scratch_sync + off, sizeof(int), hipMemcpyDeviceToHost) !=
              hipSuccess))
         return Q48_EHIP;
+    c->attg_unchecked = 0;
     if (!e[0] && !e[1])
         return Q48_OK;
-    // a timed-out launch left its barrier words behind: clear both regions
+    // a timed-out launch left its exchange words behind: clear both regions
     int rc = launch_rc(q48_launch_zero(c, c->attx_sync, q48_attn_sync_bytes()));
     if (rc == Q48_OK && c->scratch_sync)
         rc = launch_rc(q48_launch_zero(c, c->scratch_sync, q48_attn_sync_bytes()));
     if (rc == Q48_OK)
         rc = hip_rc(hipStreamSynchronize(c->stream));
+    if (rc == Q48_OK) {
+        c->attg_count = 0;
+        if (c->scratch_sync)
+            *q48_scratch_attg_count(c->device) = 0;
+    }
     return rc ? rc : Q48_ETIMEOUT;
+}
+
+int q48_set_attn_wait(q48_ctx *c, int64_t ticks)
+{
+    if (!c)
+        return Q48_EINVAL;
+    const uint64_t w = ticks < 0 ? q48_attg_default_wait() : (uint64_t)ticks;
+    if (w != c->attg_wait) {
+        c->attg_wait = w;
+        ++c->stamp;   // a kernel argument of captured launches
+    }
+    return Q48_OK;
 }
 
 int q48_set_attn_one_launch(q48_ctx *c, int on)
 {
     if (!c)
         return Q48_EINVAL;
+    if (c->attn_one_launch != (on != 0))
+        ++c->stamp;
     c->attn_one_launch = on != 0;
     return Q48_OK;
 }
@@ -655,6 +718,8 @@ int q48_set_attn_g_mfma(q48_ctx *c, int on)
 {
     if (!c)
         return Q48_EINVAL;
+    if (c->attn_g_mfma != (on != 0))
+        ++c->stamp;
     c->attn_g_mfma = on != 0;
     return Q48_OK;
 }
@@ -671,6 +736,8 @@ int q48_set_gemv_persistent(q48_ctx *c, int on)
 {
     if (!c)
         return Q48_EINVAL;
+    if (c->gemv_persistent != (on != 0))
+        ++c->stamp;
     c->gemv_persistent = on != 0;
     return Q48_OK;
 }
@@ -1016,9 +1083,9 @@ int q48_sample_reserve(q48_ctx *c, int vocab)
     if (c->capturing)
         return Q48_ESTATE;
     if (c->smp) {
-        if (hipStreamSynchronize(c->stream) != hipSuccess)
-            return Q48_EHIP;
-        (void)hipFree(c->smp);
+        int rc = q48_release(c, c->smp);
+        if (rc)
+            return rc;
         c->smp = nullptr;
         c->smp_words = 0;
     }
@@ -1071,23 +1138,94 @@ int q48_sample_step(q48_ctx *c, const int64_t *logits, int vocab, int64_t temper
                                        nullptr, d_tokens, cap));
 }
 
+namespace {
+void graph_destroy(q48_ctx *c, q48_graph *g)
+{
+    if (!g)
+        return;
+    // launches of the graph may still be in flight on the stream
+    (void)hipStreamSynchronize(c->stream);
+    if (g->x)
+        (void)hipGraphExecDestroy(g->x);
+    if (g->g)
+        (void)hipGraphDestroy(g->g);
+    delete g;
+    if (--c->n_graphs == 0)
+        free_retired(c);
+}
+
+// End the capture in progress into a new executable graph.
+int graph_finish(q48_ctx *c, q48_graph **out)
+{
+    c->capturing = 0;
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture(c->stream, &g) != hipSuccess || !g)
+        return Q48_EHIP;
+    q48_graph *h = new (std::nothrow) q48_graph();
+    if (!h) {
+        (void)hipGraphDestroy(g);
+        return Q48_ENOMEM;
+    }
+    h->g = g;
+    h->attg[0] = c->capture_attg[0];
+    h->attg[1] = c->capture_attg[1];
+    if (hipGraphInstantiate(&h->x, g, nullptr, nullptr, 0) != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        delete h;
+        return Q48_EHIP;
+    }
+    // the executable graph's device-side setup now, not inside the first launch
+    if (hipGraphUpload(h->x, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess) {
+        (void)hipGraphExecDestroy(h->x);
+        (void)hipGraphDestroy(g);
+        delete h;
+        return Q48_EHIP;
+    }
+    ++c->n_graphs;
+    *out = h;
+    return Q48_OK;
+}
+
+int graph_replay(q48_ctx *c, q48_graph *g, int times)
+{
+    // one replay at a time, each counted on the exchange regions its
+    // k_attn_g launches use
+    for (int i = 0; i < times; ++i) {
+        if (g->attg[0]) {
+            int rc = q48_attg_account(c, c->attx_sync, g->attg[0]);
+            if (rc)
+                return rc;
+        }
+        if (g->attg[1]) {
+            int rc = q48_attg_account(c, c->scratch_sync, g->attg[1]);
+            if (rc)
+                return rc;
+        }
+        if (hipGraphLaunch(g->x, c->stream) != hipSuccess)
+            return Q48_EHIP;
+    }
+    return Q48_OK;
+}
+} // namespace
+
 int q48_graph_begin(q48_ctx *c)
 {
     if (!c || c->capturing)
         return Q48_EINVAL;
-    if (c->graph_exec) {
-        // launches of the old graph may still be in flight on the stream
-        (void)hipStreamSynchronize(c->stream);
-        (void)hipGraphExecDestroy(c->graph_exec);
-        c->graph_exec = nullptr;
-    }
-    if (c->graph) {
-        (void)hipGraphDestroy(c->graph);
-        c->graph = nullptr;
-    }
+    graph_destroy(c, c->cur);
+    c->cur = nullptr;
+    return q48_graph_capture(c);
+}
+
+int q48_graph_capture(q48_ctx *c)
+{
+    if (!c || c->capturing)
+        return Q48_EINVAL;
     if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
         return Q48_EHIP;
     c->capturing = 1;
+    c->capture_attg[0] = c->capture_attg[1] = 0;
     return Q48_OK;
 }
 
@@ -1095,45 +1233,55 @@ int q48_graph_end(q48_ctx *c)
 {
     if (!c || !c->capturing)
         return Q48_EINVAL;
-    c->capturing = 0;
-    hipGraph_t g = nullptr;
-    if (hipStreamEndCapture(c->stream, &g) != hipSuccess || !g)
-        return Q48_EHIP;
-    c->graph = g;
-    if (hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0) != hipSuccess) {
-        c->graph_exec = nullptr;
-        return Q48_EHIP;
-    }
-    return Q48_OK;
+    graph_destroy(c, c->cur);
+    c->cur = nullptr;
+    return graph_finish(c, &c->cur);
+}
+
+int q48_graph_instantiate(q48_ctx *c, q48_graph **out)
+{
+    if (!c || !c->capturing || !out)
+        return Q48_EINVAL;
+    *out = nullptr;
+    return graph_finish(c, out);
 }
 
 int q48_graph_launch(q48_ctx *c, int times)
 {
     if (!c || times < 0 || c->capturing)
         return Q48_EINVAL;
-    if (!c->graph_exec)
+    if (!c->cur)
         return Q48_ESTATE;
-    for (int i = 0; i < times; ++i)
-        if (hipGraphLaunch(c->graph_exec, c->stream) != hipSuccess)
-            return Q48_EHIP;
-    return Q48_OK;
+    return graph_replay(c, c->cur, times);
+}
+
+int q48_graph_replay(q48_ctx *c, q48_graph *g, int times)
+{
+    if (!c || !g || times < 0 || c->capturing)
+        return Q48_EINVAL;
+    return graph_replay(c, g, times);
 }
 
 int q48_graph_drop(q48_ctx *c)
 {
     if (!c || c->capturing)
         return Q48_EINVAL;
-    if (c->graph_exec) {
-        // launches of the graph may still be in flight on the stream
-        (void)hipStreamSynchronize(c->stream);
-        (void)hipGraphExecDestroy(c->graph_exec);
-    }
-    if (c->graph)
-        (void)hipGraphDestroy(c->graph);
-    c->graph_exec = nullptr;
-    c->graph = nullptr;
+    graph_destroy(c, c->cur);
+    c->cur = nullptr;
     return Q48_OK;
 }
+
+int q48_graph_destroy(q48_ctx *c, q48_graph *g)
+{
+    if (!c || c->capturing)
+        return Q48_EINVAL;
+    if (g == c->cur)
+        c->cur = nullptr;
+    graph_destroy(c, g);
+    return Q48_OK;
+}
+
+uint64_t q48_graph_stamp(const q48_ctx *c) { return c ? c->stamp : 0; }
 
 } // extern "C"
 

@@ -30,17 +30,28 @@ struct q48_ctx {
     int rms_blocks;
     int64_t *smp;                // device: sampling workspace (q48_sample_ws_words)
     size_t smp_words;
-    unsigned *attx_sync;         // device: k_attn_x barrier words and error word (zeroed)
-    int attn_one_launch;         // split attention as one k_attn_x launch (default on)
+    unsigned *attx_sync;         // device: k_attn_g's exchange region (epoch-tagged words,
+                                 // per-KV-head epochs, error word); zeroed at creation
+    int attn_one_launch;         // split attention as one k_attn_g launch (default on)
     int pf_attn_mfma;            // batched-prefill attention on the matrix cores (default on)
     int attx_per_cu[4];          // k_attn_g<64/32/128>, <64, matrix scores> resident blocks
                                  // per CU (-1: not asked)
     int attn_g_mfma;             // k_attn_g's scores on the matrix cores (head_dim 64; default on)
+    uint64_t attg_wait;          // k_attn_g's wait bound in wall-clock ticks (0: give up at once)
+    uint64_t attg_count;         // k_attn_g launches on attx_sync since it was last zeroed
+    int attg_unchecked;          // k_attn_g ran since q48_attn_status last read the error words
     int64_t *scratch;            // device address of the allocation-free scratch array
-    unsigned *scratch_sync;      // ... and of its barrier region
-    hipGraph_t graph;            // captured decode step
-    hipGraphExec_t graph_exec;
+    unsigned *scratch_sync;      // ... and of its exchange region
+    q48_graph *cur;              // the context graph (q48_graph_begin / end / launch / drop)
     int capturing;
+    uint64_t capture_attg[2];    // k_attn_g launches recorded by the capture in progress,
+                                 // on attx_sync and on the scratch's region
+    int n_graphs;                // instantiated graphs alive (handles and the context graph)
+    uint64_t stamp;              // changes with every setting that selects captured kernels
+    // buffers replaced while graphs were alive: a graph may hold their
+    // addresses, so they are freed only once no graph is left
+    void **retired;
+    int n_retired, cap_retired;
     // GEMV launch timing (q48_prof_*): event pairs in use, then a free pool
     int prof_on;
     struct ProfRec { hipEvent_t a, b; double bytes; };
@@ -49,8 +60,27 @@ struct q48_ctx {
     hipEvent_t span_a, span_b;   // q48_timer_start / q48_timer_stop
 };
 
+// An executable graph and the k_attn_g launches one replay makes on each
+// exchange region ([0] the context's, [1] the allocation-free scratch's).
+struct q48_graph {
+    hipGraph_t g;
+    hipGraphExec_t x;
+    uint64_t attg[2];
+};
+
 // Grow the context workspace to at least `bytes` (stream-synchronising).
 int q48_ws_reserve(q48_ctx *c, size_t bytes);
+// Give back a device buffer the context owns (stream-synchronising): freed
+// now, or kept until the last graph is destroyed when graphs are alive.
+int q48_release(q48_ctx *c, void *p);
+// Count n k_attn_g launches on the exchange region `sync` before they are
+// enqueued, zeroing the region first when its 32-bit epochs could come back
+// to a value a stale word still carries (stream-synchronising then).
+int q48_attg_account(q48_ctx *c, const unsigned *sync, uint64_t n);
+// k_attn_g's default wait bound (wall-clock ticks).
+uint64_t q48_attg_default_wait();
+// Launches counted on this device's scratch exchange region.
+uint64_t *q48_scratch_attg_count(int device);
 
 // ---- launchers (return hipError_t as int; shapes already validated) ----
 int q48_launch_gemv(q48_ctx *c, int64_t *y, const int64_t *W, const int64_t *x,

@@ -18,17 +18,27 @@ constexpr int kMaxHeadDim = 256;
 } // namespace
 
 // ---- the allocation-free entry point's scratch ------------------------------
-// The device memory of q48_attn_decode_rope_noalloc: the split attention's
-// chunk maxima and sums (or, where k_attn_x does not serve, the scores in
-// front of them) in the first q48_scratch_bytes() bytes, then
-// k_attn_x's barrier words and error word.  One copy per device (a
-// file-scope device array), zero at load; the barrier words are zero again
-// after every launch.  Host code never uses the array's name as a device
-// address: q48_scratch_init looks its address up once per device.
+// The device memory of q48_attn_decode_rope_noalloc: the three-launch split
+// attention's scores, chunk maxima and chunk sums (where the one-launch
+// k_attn_g does not serve) in the first q48_scratch_bytes() bytes, then
+// k_attn_g's exchange region: epoch-tagged exchange words, per-KV-head
+// epochs and the error word.  One copy per device (a file-scope device
+// array), zero at load; the exchange region is zeroed once per device here,
+// and again only by q48_attn_status after a timeout or by q48_attg_account
+// before the epochs could wrap.  Host code never uses the array's name as a
+// device address: q48_scratch_init looks its address up once per device.
 constexpr size_t Q48_SCRATCH_BYTES = (size_t)4 << 20;   // the stated maximum: 4 MiB
 static __device__ __align__(256) int64_t scratch[Q48_SCRATCH_BYTES / sizeof(int64_t)];
 
 size_t q48_scratch_bytes() { return Q48_SCRATCH_BYTES - q48_attn_sync_bytes(); }
+
+// k_attn_g launches on each device's scratch exchange region (every context
+// on the device shares the array)
+uint64_t *q48_scratch_attg_count(int device)
+{
+    static uint64_t count[64];
+    return device >= 0 && device < 64 ? &count[device] : nullptr;
+}
 
 int q48_scratch_init(q48_ctx *c)
 {

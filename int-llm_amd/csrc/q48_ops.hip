@@ -707,8 +707,9 @@ __global__ __launch_bounds__(256) void k_attn_s2(int64_t *__restrict__ out,
 // poll the words of all nc chunks until each carries E + 1.  After the second
 // exchange the chunk-0 block stores E + 1 into the epoch (the next launch
 // then expects E + 2, which no word of this launch carries).  A wait longer
-// than ATTG_TIMEOUT ends the block (and sets the error word, for
-// q48_attn_status); the host sizes the grid so that every active block is
+// than the wait bound `tmo` (ATTG_TIMEOUT unless the host sets another; 0
+// gives up at once, without polling) ends the block and sets the error word,
+// for q48_attn_status; the host sizes the grid so that every active block is
 // resident at once.  Blocks whose chunk starts past pos exit at once (the
 // grid covers max_seq, so a captured graph stays valid as pos grows).
 // ---------------------------------------------------------------------------
@@ -769,7 +770,8 @@ __device__ __forceinline__ uint64_t attg_sum32(uint64_t v)
 // false on every thread after a timeout.
 template <int NT>
 __device__ bool attg_exchange(uint64_t *xw, int c, int nc, int G, unsigned epoch,
-                              const int64_t *v, int64_t (*got)[ATTG_NCMAX], int *err)
+                              const int64_t *v, int64_t (*got)[ATTG_NCMAX], int *err,
+                              uint64_t tmo)
 {
     const int tid = threadIdx.x;
     if (tid < G) {
@@ -783,8 +785,8 @@ __device__ bool attg_exchange(uint64_t *xw, int c, int nc, int G, unsigned epoch
     // barrier joins the waves
     const int nw = nc * 2 * G;
     const uint64_t t0 = wall_clock64();
-    int ok = 1;
-    for (;;) {
+    int ok = tmo != 0;
+    while (ok) {
         bool mine = true;
         for (int i = tid; i < nw; i += NT) {
             const int cc = i / (2 * G), r = i % (2 * G);
@@ -800,7 +802,7 @@ __device__ bool attg_exchange(uint64_t *xw, int c, int nc, int G, unsigned epoch
         if (__all(mine))
             break;
         // the give-up decision: the wave's clock (a scalar read, uniform)
-        if (wall_clock64() - t0 > ATTG_TIMEOUT) {
+        if (wall_clock64() - t0 > tmo) {
             ok = 0;
             break;
         }
@@ -833,7 +835,7 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
     const int64_t *__restrict__ v_new, const int64_t *__restrict__ cos_t,
     const int64_t *__restrict__ sin_t, const int64_t *__restrict__ scale_p,
     uint64_t *__restrict__ xbuf, int layer, const int *__restrict__ d_pos, int pos,
-    int n_heads, int n_kv, int max_seq)
+    int n_heads, int n_kv, int max_seq, uint64_t tmo)
 {
     constexpr int NT = ATTG_NT, CH = ATTG_CH, GM = ATTG_GMAX;
     constexpr int HALF = HD / 2, RS = HD + 1;
@@ -1089,7 +1091,7 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
     __syncthreads();
     if (nc > 1) {
         __builtin_amdgcn_s_waitcnt(0);   // chunk 0: the output zeroes are out
-        if (!attg_exchange<NT>(xw1, c, nc, G, E + 1, loc, got, err)) {
+        if (!attg_exchange<NT>(xw1, c, nc, G, E + 1, loc, got, err, tmo)) {
             if (tid == 0)
                 __hip_atomic_store(ep, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
@@ -1119,7 +1121,7 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
     }
     __syncthreads();
     if (nc > 1) {
-        if (!attg_exchange<NT>(xw2, c, nc, G, E + 1, loc, got, err)) {
+        if (!attg_exchange<NT>(xw2, c, nc, G, E + 1, loc, got, err, tmo)) {
             if (tid == 0)
                 __hip_atomic_store(ep, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
@@ -1427,6 +1429,30 @@ size_t q48_attn_ws_bytes(int n_heads, int max_seq, int head_dim)
 
 size_t q48_attn_sync_bytes() { return ATTG_SYNC_BYTES; }
 
+uint64_t q48_attg_default_wait() { return ATTG_TIMEOUT; }
+
+// Each launch with more than one chunk advances its KV heads' 32-bit epochs
+// by one, and a chunk word counts when it carries the launch's epoch.  A word
+// not rewritten since an earlier launch with the same epoch value (2^32
+// launches before) would be taken for this launch's: so the region is zeroed,
+// with the stream idle, before its count of launches reaches 2^31.
+int q48_attg_account(q48_ctx *c, const unsigned *sync, uint64_t n)
+{
+    constexpr uint64_t kLimit = (uint64_t)1 << 31;
+    uint64_t *count = sync == c->attx_sync ? &c->attg_count : q48_scratch_attg_count(c->device);
+    if (!count)
+        return Q48_EINVAL;
+    if (*count + n >= kLimit) {
+        if (hipStreamSynchronize(c->stream) != hipSuccess ||
+            q48_launch_zero(c, const_cast<unsigned *>(sync), ATTG_SYNC_BYTES) != (int)hipSuccess ||
+            hipStreamSynchronize(c->stream) != hipSuccess)
+            return Q48_EHIP;
+        *count = 0;
+    }
+    *count += n;
+    return Q48_OK;
+}
+
 // k_attn_g needs every active block resident at once: the chunks of a full
 // cache (max_seq) times the KV heads must fit the device's occupancy.
 static bool attg_fits(q48_ctx *c, int hd, int n_heads, int n_kv, int max_seq)
@@ -1498,11 +1524,21 @@ int q48_launch_attn_v2(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcac
             // them shared a unit with another live block and ran slower, and
             // both in-kernel exchanges waited for them)
             const dim3 grid(n_kv, (max_seq + ATTG_CH - 1) / ATTG_CH);
+            // count the launch on its exchange region (a captured one counts
+            // at every replay of its graph)
+            if (c->capturing) {
+                ++c->capture_attg[sync == c->attx_sync ? 0 : 1];
+            } else {
+                int arc = q48_attg_account(c, sync, 1);
+                if (arc)
+                    return arc;
+            }
+            c->attg_unchecked = 1;
 #define ATTG_LAUNCH(HD, MFS)                                                                  \
     hipLaunchKernelGGL((k_attn_g<HD, MFS>), grid, dim3(ATTG_NT), 0, c->stream, out, q, kcache, \
                        vcache, k_new, v_new, c->rope_cos, c->rope_sin, scale_p,               \
                        reinterpret_cast<uint64_t *>(sync), layer, d_pos, pos, n_heads, n_kv,  \
-                       max_seq)
+                       max_seq, c->attg_wait)
             if (head_dim == 64 && c->attn_g_mfma)
                 ATTG_LAUNCH(64, true);
             else if (head_dim == 64)

@@ -29,6 +29,7 @@
 #define FNV_OFF 1469598103934665603ULL
 
 #define ALIGN_ELEMS 32   /* 256 bytes */
+#define GRAPH_SLOTS 8
 
 static size_t align_up(size_t n) { return (n + ALIGN_ELEMS - 1) / ALIGN_ELEMS * ALIGN_ELEMS; }
 
@@ -55,8 +56,6 @@ struct q48h_model {
                                    once by the producer (last block); 3 (default):
                                    fused, the producer leaves partial sums and every
                                    consumer block finishes them */
-    int graph_ready;            /* the context graph holds this model's decode step */
-    int graph_kind;             /* ... of this kind (step_kind) */
     int prefetch;               /* attention warms the cache with W_o (fused modes) */
     int rope_gemv;              /* mode 3 below the split position: RoPE and the KV
                                    store in the q|k|v projection, attention from the
@@ -70,7 +69,23 @@ struct q48h_model {
     int64_t *rec;               /* device: logits of recorded decode steps [rec_cap][vocab] */
     int rec_cap;
     int record;                 /* the decode step records its logits into rec */
-    int graph_rec;              /* the captured graph was captured with record on */
+    /* Captured decode steps, one per combination of the settings baked into
+     * the kernels and their arguments.  A graph lives until the model is
+     * freed (or, with every slot taken, until it is the least recently
+     * used): switching settings between runs replays another slot rather
+     * than destroying and re-capturing. */
+    struct graph_slot {
+        q48_graph *g;
+        unsigned long long used;   /* 0: empty, else the run count at last use */
+        struct graph_key {
+            int kind, record, rec_cap, bf16, fused, rope_gemv, prefetch, top_k;
+            int64_t temperature, top_p;
+            const void *rec, *wb;
+            uint64_t stamp;
+        } k;
+    } gslot[GRAPH_SLOTS];
+    unsigned long long runs;
+    q48_graph *g_run;           /* the graph of the run in progress */
 };
 
 /* ---------------------------------------------------------------------- */
@@ -262,12 +277,15 @@ int q48h_model_create(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg)
     return model_alloc(out, ctx, cfg, 0);
 }
 
-static void drop_graph(q48h_model *m)
+static void graphs_free(q48h_model *m)
 {
-    if (m->graph_ready) {
-        q48_graph_drop(m->ctx);
-        m->graph_ready = 0;
-    }
+    for (int i = 0; i < GRAPH_SLOTS; ++i)
+        if (m->gslot[i].used) {
+            q48_graph_destroy(m->ctx, m->gslot[i].g);
+            m->gslot[i].g = NULL;
+            m->gslot[i].used = 0;
+        }
+    m->g_run = NULL;
 }
 
 /* Forget the bfloat16 copy of the weights (they are about to change). */
@@ -277,10 +295,7 @@ static void drop_bf16(q48h_model *m)
         q48_free(m->ctx, m->wb);
         m->wb = NULL;
     }
-    if (m->bf16) {
-        m->bf16 = 0;
-        drop_graph(m);
-    }
+    m->bf16 = 0;
 }
 
 int q48h_model_set_bf16(q48h_model *m, int on)
@@ -319,10 +334,7 @@ int q48h_model_set_bf16(q48h_model *m, int on)
             return rc ? rc : Q48_EINVAL;
         }
     }
-    if (m->bf16 != on) {
-        m->bf16 = on;
-        drop_graph(m);
-    }
+    m->bf16 = on;
     return Q48_OK;
 }
 
@@ -330,6 +342,7 @@ void q48h_model_free(q48h_model *m)
 {
     if (!m)
         return;
+    graphs_free(m);   /* before the buffers their kernels read */
     q48_free(m->ctx, m->wb);
     q48_free(m->ctx, m->w);
     q48_free(m->ctx, m->kc);
@@ -339,8 +352,6 @@ void q48h_model_free(q48h_model *m)
     q48_free(m->ctx, m->d_rng);
     q48_free(m->ctx, m->pf);
     q48_free(m->ctx, m->rec);
-    if (m->graph_ready)
-        q48_graph_drop(m->ctx);
     free(m);
 }
 
@@ -361,7 +372,6 @@ int q48h_model_set_sampling(q48h_model *m, int64_t temperature, int top_k, int64
     m->temperature = temperature;
     m->top_k = top_k;
     m->top_p = top_p;
-    drop_graph(m);   /* the parameters are arguments of the captured kernels */
     return Q48_OK;
 }
 
@@ -387,13 +397,8 @@ void q48h_model_set_fused(q48h_model *m, int fused)
 {
     if (fused < 0 || fused > 3)
         fused = 3;
-    if (m && m->fused != fused) {
+    if (m)
         m->fused = fused;
-        if (m->graph_ready) {
-            q48_graph_drop(m->ctx);
-            m->graph_ready = 0;
-        }
-    }
 }
 
 /* How a graph-replayed decode step at pos runs: 0 the fused launches with
@@ -407,24 +412,14 @@ static int step_kind(q48h_model *m, int pos)
 
 void q48h_model_set_rope_gemv(q48h_model *m, int on)
 {
-    if (m && m->rope_gemv != (on != 0)) {
+    if (m)
         m->rope_gemv = on != 0;
-        if (m->graph_ready) {
-            q48_graph_drop(m->ctx);
-            m->graph_ready = 0;
-        }
-    }
 }
 
 void q48h_model_set_prefetch(q48h_model *m, int on)
 {
-    if (m && m->prefetch != (on != 0)) {
+    if (m)
         m->prefetch = on != 0;
-        if (m->graph_ready) {
-            q48_graph_drop(m->ctx);
-            m->graph_ready = 0;
-        }
-    }
 }
 
 const q48h_config *q48h_model_config(const q48h_model *m) { return &m->c; }
@@ -942,9 +937,11 @@ int q48h_forward(q48h_model *m, int token, int pos, int64_t *logits, int *next)
         TRY(select_token(m, next));
     if (logits)
         TRY(q48_memcpy_d2h(m->ctx, logits, m->logits, (size_t)c->vocab * 8));
-    if (!next && !logits)
-        TRY(q48_sync(m->ctx));
-    return Q48_OK;
+    /* a split attention that gave up left wrong logits: the forward fails,
+     * as the reference's llama_forward returning NULL (llama_int.c:3083-3086,
+     * 3106); synchronises (nothing is read back unless one-launch split
+     * attention ran) */
+    return q48_attn_status(m->ctx);
 }
 
 static double now_s(void)
@@ -984,7 +981,7 @@ int q48h_prefill(q48h_model *m, const int *tokens, int T, int p0, int64_t *logit
         }
         if (next)
             TRY(select_token(m, next));
-        return q48_sync(x);
+        return q48_attn_status(x);
     }
     /* rows: H, XN, QKV, ATT, D, GU, HF, logits (all T, or the last), ids */
     const size_t nlog = logits_all ? (size_t)T * V : (size_t)V;
@@ -1158,7 +1155,6 @@ int q48h_decode_from(q48h_model *m, int token, int start_pos, int n, int *out_to
 static int first_step_and_capture(q48h_model *m, int token, int pos)
 {
     q48_ctx *x = m->ctx;
-    const int kind = step_kind(m, pos);
     TRY(q48_step_mode(x, 1));
     int rc = q48_step_set(x, token, pos);
     if (rc == Q48_OK) {
@@ -1170,29 +1166,70 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
         if (rc == Q48_OK)
             rc = q48_sync(x);
     }
-    /* attention picks its kernels by position (split from q48_attn_split_min):
-     * recapture when the step changes kind */
-    if (rc == Q48_OK && m->graph_ready && (m->graph_kind != kind || m->graph_rec != m->record)) {
-        rc = q48_graph_drop(x);
-        m->graph_ready = 0;
+    /* the graph of this step's settings: cached, or captured now */
+    struct graph_key k;
+    memset(&k, 0, sizeof k);   /* the key is compared byte for byte */
+    k.kind = step_kind(m, pos);
+    k.record = m->record;
+    k.rec = m->record ? (const void *)m->rec : NULL;
+    k.rec_cap = m->record ? m->rec_cap : 0;
+    k.bf16 = m->bf16;
+    k.wb = m->bf16 ? (const void *)m->wb : NULL;
+    k.fused = m->fused;
+    k.rope_gemv = m->rope_gemv;
+    k.prefetch = m->prefetch;
+    if (m->temperature >= Q48_ONE / 100) {   /* sampling: its parameters are kernel arguments */
+        k.temperature = m->temperature;
+        k.top_k = m->top_k;
+        k.top_p = m->top_p;
     }
-    if (rc == Q48_OK && !m->graph_ready) {
-        rc = q48_graph_begin(x);
+    k.stamp = q48_graph_stamp(x);
+    m->g_run = NULL;
+    int slot = -1;
+    for (int i = 0; i < GRAPH_SLOTS && slot < 0; ++i)
+        if (m->gslot[i].used && !memcmp(&m->gslot[i].k, &k, sizeof k))
+            slot = i;
+    if (rc == Q48_OK && slot < 0) {
+        /* an empty slot, else the least recently used one */
+        slot = 0;
+        for (int i = 0; i < GRAPH_SLOTS; ++i) {
+            if (!m->gslot[i].used) {
+                slot = i;
+                break;
+            }
+            if (m->gslot[i].used < m->gslot[slot].used)
+                slot = i;
+        }
+        if (m->gslot[slot].used) {
+            q48_graph_destroy(x, m->gslot[slot].g);
+            m->gslot[slot].g = NULL;
+            m->gslot[slot].used = 0;
+        }
+        rc = q48_graph_capture(x);
         if (rc == Q48_OK) {
             int rc1 = enqueue_forward(m, token, pos);
             if (rc1 == Q48_OK && m->record)
                 rc1 = q48_record_step(x, m->logits, m->c.vocab, m->rec, m->rec_cap);
             if (rc1 == Q48_OK)
                 rc1 = select_token_step(m);
-            rc = q48_graph_end(x);
+            q48_graph *g = NULL;
+            rc = q48_graph_instantiate(x, &g);
+            if (rc == Q48_OK && rc1) {
+                q48_graph_destroy(x, g);
+                g = NULL;
+            }
             if (rc1)
                 rc = rc1;
             if (rc == Q48_OK) {
-                m->graph_ready = 1;
-                m->graph_kind = kind;
-                m->graph_rec = m->record;
+                m->gslot[slot].g = g;
+                m->gslot[slot].k = k;
+                m->gslot[slot].used = 1;
             }
         }
+    }
+    if (rc == Q48_OK) {
+        m->gslot[slot].used = ++m->runs;
+        m->g_run = m->gslot[slot].g;
     }
     q48_step_mode(x, 0);
     return rc;
@@ -1230,15 +1267,14 @@ static int decode_graph_run(q48h_model *m, int token, int start_pos, int n, int 
     /* recording: one logits row per step of the longest part below */
     m->record = step_hash != NULL;
     if (m->record && m->rec_cap < n) {
-        if (m->graph_ready) {
-            TRY(q48_graph_drop(m->ctx));   /* it holds the old buffer's address */
-            m->graph_ready = 0;
-        }
+        /* graphs that record into the old buffer are keyed on its address
+         * and capacity: they are never replayed against the new one */
+        int cap = n > 512 ? n : (c->max_seq < 512 ? c->max_seq : 512);
         q48_free(m->ctx, m->rec);
         m->rec = NULL;
         m->rec_cap = 0;
-        TRY(q48_malloc(m->ctx, (void **)&m->rec, (size_t)n * c->vocab * 8));
-        m->rec_cap = n;
+        TRY(q48_malloc(m->ctx, (void **)&m->rec, (size_t)cap * c->vocab * 8));
+        m->rec_cap = cap;
     }
     /* dt: the steps on the device, from the first step's launch to the
      * tokens back on the host (the hashing of recorded logits is not in it) */
@@ -1251,7 +1287,7 @@ static int decode_graph_run(q48h_model *m, int token, int start_pos, int n, int 
     int k = n;
     if (start_pos < B && start_pos + n > B)
         k = B - start_pos;
-    TRY(q48_graph_launch(m->ctx, k - 1));
+    TRY(q48_graph_replay(m->ctx, m->g_run, k - 1));
     TRY(q48_memcpy_d2h(m->ctx, out_tokens, m->d_tokens, (size_t)k * sizeof(int)));
     double dt = now_s() - t0;
     if (step_hash)
@@ -1259,12 +1295,15 @@ static int decode_graph_run(q48h_model *m, int token, int start_pos, int n, int 
     if (k < n) {
         t0 = now_s();
         TRY(first_step_and_capture(m, out_tokens[k - 1], B));
-        TRY(q48_graph_launch(m->ctx, n - k - 1));
+        TRY(q48_graph_replay(m->ctx, m->g_run, n - k - 1));
         TRY(q48_memcpy_d2h(m->ctx, out_tokens + k, m->d_tokens, (size_t)(n - k) * sizeof(int)));
         dt += now_s() - t0;
         if (step_hash)
             TRY(hash_recorded(m, n - k, step_hash + k));
     }
+    /* a split attention that gave up: the run's outputs are wrong (the
+     * reference's generate stops on a failed forward, llama_int.c:3106) */
+    TRY(q48_attn_status(m->ctx));
     /* generate stops at EOS (llama_int.c:3111): the steps up to and
      * including the one that chose it count; the device replayed the rest */
     int ran = n;

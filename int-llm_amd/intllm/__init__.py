@@ -98,6 +98,11 @@ ABI_SIGNATURES = {
     "q48_graph_end": [_P],
     "q48_graph_launch": [_P, _I],
     "q48_graph_drop": [_P],
+    "q48_graph_capture": [_P],
+    "q48_graph_instantiate": [_P, C.POINTER(C.c_void_p)],
+    "q48_graph_replay": [_P, _P, _I],
+    "q48_graph_destroy": [_P, _P],
+    "q48_set_attn_wait": [_P, C.c_int64],
     "q48_prof_enable": [_P, _I],
     "q48_timer_start": [_P],
     "q48_timer_stop": [_P, C.POINTER(C.c_double)],
@@ -141,6 +146,8 @@ def hip_lib() -> C.CDLL:
         lib.q48_strerror.restype = C.c_char_p
         lib.q48_rng_seed.argtypes = [C.c_uint64, C.POINTER(C.c_uint64)]
         lib.q48_rng_seed.restype = None
+        lib.q48_graph_stamp.argtypes = [_P]
+        lib.q48_graph_stamp.restype = C.c_uint64
         _hip = lib
     return _hip
 
@@ -264,7 +271,18 @@ class Context:
         return check("q48_set_attn_one_launch", hip_lib().q48_set_attn_one_launch(self.h, int(on)))
 
     def attn_status(self):
-        return check("q48_attn_status", hip_lib().q48_attn_status(self.h))
+        """0, or Q48_ETIMEOUT (returned, not raised) when a one-launch split
+        attention gave up since the last call."""
+        rc = hip_lib().q48_attn_status(self.h)
+        return rc if rc == Q48_ETIMEOUT else check("q48_attn_status", rc)
+
+    def set_attn_wait(self, ticks: int):
+        """k_attn_g's wait bound in wall-clock ticks; -1 restores the default,
+        0 gives up at the first exchange (the timeout path, for tests)."""
+        return check("q48_set_attn_wait", hip_lib().q48_set_attn_wait(self.h, int(ticks)))
+
+    def graph_stamp(self) -> int:
+        return int(hip_lib().q48_graph_stamp(self.h))
 
     def set_pf_attn_mfma(self, on: bool):
         return check("q48_set_pf_attn_mfma", hip_lib().q48_set_pf_attn_mfma(self.h, int(on)))

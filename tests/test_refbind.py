@@ -44,6 +44,8 @@ def _lib():
     lib.lq48_forward.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p]
     lib.lq48_generate.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                   C.c_void_p, C.c_int, C.POINTER(C.c_int)]
+    lib.lq48_set_fused.argtypes = [C.c_int]
+    lib.lq48_set_attn_wait.argtypes = [C.c_int64]
     return lib
 
 
@@ -84,7 +86,8 @@ def test_refbind_links_library_and_exports():
     assert "libintllm_hip.so" in out
     lib = _lib()
     for name in ("lq48_attach", "lq48_detach", "lq48_generate", "lq48_forward",
-                 "lq48_model_load_mgw", "lq48_model_free", "llama_int_main"):
+                 "lq48_model_load_mgw", "lq48_model_free", "lq48_set_fused",
+                 "lq48_set_attn_wait", "llama_int_main"):
         assert hasattr(lib, name)
 
 
@@ -115,24 +118,68 @@ def test_refbind_cpu_route_unchanged():
 
 @needs_so
 @pytest.mark.gpu
-def test_refbind_generate_config1_on_device():
+@pytest.mark.parametrize("fused", [1, 0], ids=["fused-graph", "call-per-step"])
+def test_refbind_generate_config1_on_device(fused):
     """Config 1 through the reference's own generate() with llama_forward
-    on the device: the 48 golden tokens and all 47 logits hashes."""
+    on the device, by both routes (five fused launches per layer replayed
+    from a graph, and one library call per step of
+    transformer_layer_forward): the 48 golden tokens and all 47 logits
+    hashes, twice in a row (the second run replays the captured graph from
+    its first forward on)."""
     g = golden("tiny_generate.json")
     lib = _lib()
     rm = RefModel(lib, spec.TINY, g["seed"])
     try:
         assert lib.lq48_attach(rm.m, 0) == 0
-        total, toks, hs = rm.generate(g["prompt"], g["max_new"])
-        assert total == len(g["tokens"])
-        assert toks == g["tokens"]
-        assert hs == g["step_fnv"]
+        assert lib.lq48_set_fused(fused) == 0
+        for rep in range(2):
+            print("[case] refbind generate, fused", fused, "run", rep, flush=True)
+            total, toks, hs = rm.generate(g["prompt"], g["max_new"])
+            assert total == len(g["tokens"])
+            assert toks == g["tokens"]
+            assert hs == g["step_fnv"]
         # out-of-range calls return NULL (-1) as llama_forward does
         lg = np.empty(512, dtype=np.int64)
         assert lib.lq48_forward(rm.m, 512, 0, lg.ctypes.data) == -1
         assert lib.lq48_forward(rm.m, 3, 2048, lg.ctypes.data) == -1
         lib.lq48_detach()
     finally:
+        rm.free()
+
+
+@needs_so
+@pytest.mark.gpu
+def test_refbind_forward_fails_on_attention_timeout():
+    """A split attention that gives up (the context told to give up at
+    once, so every block exits normally) makes the routed llama_forward
+    return NULL, as the reference's callers expect of a failed forward
+    (llama_int.c:3083-3086, 3106); with the default bound the same forward
+    gives the oracle's logits (both caches zero but for the row written)."""
+    lib = _lib()
+    rm = RefModel(lib, spec.TINY, 11)
+    om = O.Model(spec.TINY, 11)
+    try:
+        assert lib.lq48_attach(rm.m, 0) == 0
+        pos = 600   # past the split position: the one-launch split attention
+        lg = np.empty(512, dtype=np.int64)
+        rc, want = om.forward(5, pos)
+        assert rc == 0
+        for fused in (1, 0):
+            assert lib.lq48_set_fused(fused) == 0
+            print("[case] refbind give-up forward, fused", fused, flush=True)
+            assert lib.lq48_set_attn_wait(0) == 0
+            got = lib.lq48_forward(rm.m, 5, pos, lg.ctypes.data)
+            # the call-per-step route's attention (RoPE applied before it)
+            # is not the one-launch split kernel and never waits
+            assert got == (-1 if fused else 0)
+            if not fused:
+                assert np.array_equal(lg, want)
+            assert lib.lq48_set_attn_wait(-1) == 0
+            assert lib.lq48_forward(rm.m, 5, pos, lg.ctypes.data) == 0
+            assert np.array_equal(lg, want)
+        lib.lq48_detach()
+    finally:
+        om.free()
         rm.free()
 
 
