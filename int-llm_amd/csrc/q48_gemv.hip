@@ -496,10 +496,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     if constexpr (WT == 1) {
         b16_pin(F);
         S = acc3_value(F);
-        if (!b16_wave_ok(chk))
-            b16_fix_tiles(
-                S, nt, [&](int t) { return w2[t * 8]; },
-                [&](int t) { return xw + 3 * (64 * t + 8 * l8); });
+        if (!b16_wave_ok(chk)) {
+            // every tile of the segment is still in the window's registers
+            // when the window holds the whole segment; else read again
+            // (up to 4 tiles: holding 11 spills registers)
+            if constexpr (NTF > 0 && NTF == UNR && NTF <= 4)
+                b16_fix_regs(S, wa, [&](int t) { return xw + 3 * (64 * t + 8 * l8); });
+            else
+                b16_fix_tiles(
+                    S, nt, [&](int t) { return w2[t * 8]; },
+                    [&](int t) { return xw + 3 * (64 * t + 8 * l8); });
+        }
     } else {
         // the kn % 16 elements (even) of the segment's end, one pair per lane
         if (2 * l8 < (kn & 15)) {
@@ -818,10 +825,15 @@ __global__ __launch_bounds__(64 * RW) void k_gemv_r1(int64_t *__restrict__ y,
     if constexpr (WT == 1) {
         b16_pin(F);
         Sl = acc3_value(F);
-        if (!b16_wave_ok(chk))
-            b16_fix_tiles(
-                Sl, NT, [&](int t) { return w2[64 * t]; },
-                [&](int t) { return xl + 3 * TE * t; });
+        if (!b16_wave_ok(chk)) {
+            // the window holds the whole row when UNR == NT: no second read
+            if constexpr (NT == UNR)
+                b16_fix_regs(Sl, wa, [&](int t) { return xl + 3 * TE * t; });
+            else
+                b16_fix_tiles(
+                    Sl, NT, [&](int t) { return w2[64 * t]; },
+                    [&](int t) { return xl + 3 * TE * t; });
+        }
     } else {
         Sl = acc6_value(A);
     }
@@ -999,12 +1011,17 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
         Acc6 A = {0, 0, 0, 0, 0, 0, 0};
         Acc3 F = {0, 0, 0, 0, 0, 0};
         q48_u16x2 chk = {0, 0};
+        // bfloat16: this group's tiles, kept after the window moves on to
+        // the next group's (for the residual pass, without a second read)
+        ulonglong2 wc[WT == 1 ? NTF : 1];
 #pragma unroll
         for (int t = 0; t < NTF; ++t) {
-            if constexpr (WT == 0)
+            if constexpr (WT == 0) {
                 mac_tile<0>(A, xw, l8, t, wa[t % UNR]);
-            else
+            } else {
                 b16_tile_fast(F, chk, xw, l8, t, wa[t % UNR]);
+                wc[t] = wa[t % UNR];
+            }
             if (t + UNR < NTF)
                 wa[t % UNR] = ld_wtile<WT>(&w2[(t + UNR) * 8]);
             else
@@ -1017,9 +1034,7 @@ k_gemv_p6(int64_t *__restrict__ y, const void *__restrict__ Wv,
             b16_pin(F);
             S = acc3_value(F);
             if (!b16_wave_ok(chk))
-                b16_fix_tiles(
-                    S, NTF, [&](int t) { return w2[t * 8]; },
-                    [&](int t) { return xw + 3 * (64 * t + 8 * l8); });
+                b16_fix_regs(S, wc, [&](int t) { return xw + 3 * (64 * t + 8 * l8); });
         } else {
             S = acc6_value(A);
         }

@@ -233,6 +233,18 @@ __device__ __forceinline__ void b16_fix_tiles(q48_u128 &S, int nt, Ld ld, Px px)
     }
 }
 
+// The same residual pass over tiles still held in registers (w[0 .. N)):
+// no second read of the weights, so a wave with a pattern outside the window
+// costs its fix alone, not a memory round trip.
+template <int N, class Px>
+__device__ __forceinline__ void b16_fix_regs(q48_u128 &S, const ulonglong2 (&w)[N], Px px)
+{
+#pragma unroll
+    for (int t = 0; t < N; ++t)
+        if (b16_tile_out(w[t]))
+            b16_tile_fix(S, px(t), w[t]);
+}
+
 // Pins the fast sums in registers before the wave's range check: otherwise
 // the compiler sinks the fast multiply-adds below the check and keeps every
 // tile's staged limbs live across it.
