@@ -569,7 +569,7 @@ def main():
         parity["prefill_next_token_matches_reference"] = \
             pf["golden_prompt_next_token_matches"]
 
-    # a one-launch split attention (positions from 512) that gave up reports
+    # a one-launch split attention (positions from q48_attn_split_min()) that gave up reports
     # Q48_ETIMEOUT instead of logits: the leg is recorded as failed and the
     # parity check fails, rather than the run ending without a line
     timeouts = []

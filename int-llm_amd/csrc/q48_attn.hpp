@@ -52,7 +52,8 @@ constexpr int ATT_LDS_MAX = 4096;   // positions whose scores fit in LDS (32 KiB
 // 1414-1416, 1502-1529).
 //  - the K rows of the first two score passes are issued before RoPE, and
 //    each later pass is issued one pass ahead (two register buffers), only
-//    where it exists;
+//    where it exists; a pass or V batch with no position below S is neither
+//    scored nor used;
 //  - the first V batches are issued before the softmax, later ones one
 //    batch ahead where they exist, so the V pass rarely waits;
 //  - the score scale fp_inv_sqrt(fp_from_int(hd)) is read, not recomputed
@@ -218,7 +219,8 @@ __device__ __forceinline__ void attn_v3_head(
             for (int d = 0; d < DP2; ++d)
                 ka[d] = krow(t0 + 2 * NG + g)[d];
         }
-        score(kb, t0 + NG + g);
+        if (t0 + NG < S)
+            score(kb, t0 + NG + g);
         if (t0 + 3 * NG < S) {
 #pragma unroll
             for (int d = 0; d < DP2; ++d)
@@ -273,7 +275,8 @@ __device__ __forceinline__ void attn_v3_head(
             for (int u = 0; u < VB; ++u)
                 va[u] = vld(i0 + 2 * VB + u);
         }
-        vmac(vb, i0 + VB);
+        if (SL * (i0 + VB) < S)
+            vmac(vb, i0 + VB);
         if (SL * (i0 + 3 * VB) < S) {
 #pragma unroll
             for (int u = 0; u < VB; ++u)

@@ -457,7 +457,12 @@ constexpr int ATT_CH = 256;        // positions per chunk
 // value slices, so up to 128 positions have their keys and values loaded
 // before the first score (with 256 threads a second round of loads waited)
 constexpr int ATT_V3_NT = 512;
-constexpr int ATT_SPLIT_MIN = 512; // first position served by the split kernels
+// first position served by the split kernels: from 256 positions on the
+// one-launch split form (about 13.4 us per launch at TinyLlama's heads,
+// whatever the position up to 2048) is faster than one block per head
+// (14.9 us at 256, 22.5 us at 511: its fifth key pass and value batch go out
+// after the first are consumed)
+constexpr int ATT_SPLIT_MIN = 256;
 constexpr int ATT_NCMAX = 128;   // chunks per head: max_seq <= 32768
 
 template <int HD>

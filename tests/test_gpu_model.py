@@ -200,20 +200,21 @@ def test_tiny_generate_other_paths_bit_exact(ctx, mode):
 
 
 def test_graph_decode_across_split_position(ctx, oracle):
-    """A graph-replayed run that crosses position 512, where attention changes
-    kernels (one block per head below it, split attention from it on): the
-    run is replayed from two captured graphs and equals the eager per-token
-    decode and the oracle's decode."""
+    """A graph-replayed run that crosses q48_attn_split_min() (256), where
+    attention changes kernels (one block per head below it, split attention
+    from it on): the run is replayed from two captured graphs and equals the
+    eager per-token decode and the oracle's decode."""
     g = golden("tiny_generate.json")
     cfg = intllm.Config(*g["config"])
-    start, n, tok0 = 500, 24, 7
+    split = intllm.hip_lib().q48_attn_split_min()
+    start, n, tok0 = split - 12, 24, 7
     m = intllm.HostModel(ctx, cfg)
     try:
         m.synth(g["seed"], threads())
         m.kv_fill_synth(spec.SEED_KV, start, threads())
-        say("graph decode across 512")
+        say("graph decode across", split)
         _, steps, _ = m.decode_graph(tok0, start, n)
-        say("eager decode across 512")
+        say("eager decode across", split)
         eager, _, _ = m.decode_from(tok0, start, n, hashes=False)
     finally:
         m.free()

@@ -355,7 +355,7 @@ def test_rope_errors(ctx):
 
 @pytest.mark.parametrize("nh,nkv,hd,max_seq,positions", [
     (8, 2, 32, 64, [0, 1, 5, 63]),
-    (32, 4, 64, 600, [0, 300, 599]),
+    (32, 4, 64, 600, [0, 130, 200, 257, 300, 599]),
     (4, 4, 64, 40, [0, 39]),
     (6, 1, 128, 300, [257]),
 ])
@@ -502,8 +502,9 @@ def test_rmsnorm_gemv_swiglu_fused(ctx, oracle, ffn, K):
 @pytest.mark.parametrize("nh,nkv,hd,max_seq,positions", [
     (8, 2, 32, 64, [0, 1, 63]),
     (32, 4, 64, 300, [0, 7, 299]),
-    # from position 512 on, the split (chunked) kernels: chunk edges 767/768
-    (32, 4, 64, 1300, [511, 512, 767, 768, 1299]),
+    # from q48_attn_split_min() (256) on, the split (chunked) kernels; chunk
+    # edges 767/768 of the three-launch form
+    (32, 4, 64, 1300, [255, 256, 511, 512, 767, 768, 1299]),
     (8, 2, 32, 600, [513, 599]),
     # a group of 3 query heads: rows 3..15 of the matrix-core scores are padding
     (12, 4, 64, 600, [520, 599]),

@@ -48,7 +48,8 @@ def _oracle_case(oracle, rng, nh, nkv, hd, K, max_seq, pos, W, x, nw, kc, vc, la
 
 @pytest.mark.parametrize("nh,nkv,hd,K,max_seq,positions", [
     # TinyLlama heads (the v5 pipeline with 16 tiles per wave)
-    (32, 4, 64, 2048, 600, [0, 1, 37, 127, 128, 129, 300, 511]),
+    (32, 4, 64, 2048, 600, [0, 1, 37, 63, 64, 127, 128, 129, 191, 192, 255, 256, 257, 300,
+                            383, 447, 511]),
     (8, 2, 32, 256, 200, [0, 5, 199]),
     (16, 4, 128, 1024, 300, [0, 130, 299]),
     # K off the unrolled pipeline (the batched-loop kernel)

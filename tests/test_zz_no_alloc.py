@@ -94,7 +94,7 @@ def test_noalloc_attention_equals_allocating_entry(ctx):
     _case(ctx, lib, rng, 32, 4, 64, 4096, 2100)
     _case(ctx, lib, rng, 8, 2, 64, 1024, 700)
     # below the split position: one block per head, no scratch
-    _case(ctx, lib, rng, 8, 2, 64, 1024, 300)
+    _case(ctx, lib, rng, 8, 2, 64, 1024, lib.q48_attn_split_min() - 56)
 
 
 def test_noalloc_first_on_fresh_context(ctx):
@@ -132,8 +132,8 @@ def test_noalloc_split_fallback_rejects_oversize(ctx):
                                               hd, max_seq)
         assert rc == intllm.Q48_ETOOBIG
         # below the split position the same call needs no workspace
-        rc = lib.q48_attn_decode_rope_noalloc(ctx.h, *[b.ptr for b in bufs], 0, 300, nh, nkv,
-                                              hd, max_seq)
+        rc = lib.q48_attn_decode_rope_noalloc(ctx.h, *[b.ptr for b in bufs], 0,
+                                              lib.q48_attn_split_min() - 56, nh, nkv, hd, max_seq)
         assert rc == 0, intllm.strerror(rc)
         ctx.sync()
         for b in bufs:
