@@ -195,7 +195,7 @@ int q48_set_attn_one_launch(q48_ctx *ctx, int on);
  * (off; up to 4096 cache rows).  Same bits either way.  No reference
  * counterpart: a kernel choice of this library. */
 int q48_set_pf_attn_mfma(q48_ctx *ctx, int on);
-/* Decode attention from position 512 (the one-launch split form, head_dim
+/* Decode attention from q48_attn_split_min() (the one-launch split form, head_dim
  * 64) with its q.k scores on the int8 matrix cores (on: the default) or on
  * the VALU (off).  Same bits either way.  No reference counterpart: a kernel
  * choice of this library. */
