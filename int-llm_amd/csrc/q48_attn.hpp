@@ -252,37 +252,54 @@ __device__ __forceinline__ void attn_v3_head(
         sum = (int64_t)((uint64_t)sum + (uint64_t)e);
     }
     sum = block_sum64<NT>(sum, red2, false);
-    if (sum > 0)
-        for (int t = tid; t < S; t += NT)
+    // the weights are never negative (exponentials over a positive sum, or
+    // the exponentials themselves); checked, and the values take the product
+    // for non-negative weights (q48_pv_mac) unless one is
+    int neg = 0;
+    for (int t = tid; t < S; t += NT) {
+        if (sum > 0)
             sc[t] = q48_div(sc[t], sum);
-    __syncthreads();
-
-    // o[d] = sum_t fp_mul(p_t, v_t[d]), llama_int.c:1514-1529
-    uint64_t acc = 0;
-    auto vmac = [&](const int64_t (&vv)[VB], int i0) {
-#pragma unroll
-        for (int u = 0; u < VB; ++u) {
-            const int t = sl + SL * (i0 + u);
-            if (t < S)
-                acc += (uint64_t)q48_mul(sc[t], !ROT && t == pos ? vs[d] : vv[u]);
-        }
-    };
-    for (int i0 = 0; sl + SL * i0 < S; i0 += 2 * VB) {
-        // the next batches where some position of them exists (as above)
-        vmac(va, i0);
-        if (SL * (i0 + 2 * VB) < S) {
-#pragma unroll
-            for (int u = 0; u < VB; ++u)
-                va[u] = vld(i0 + 2 * VB + u);
-        }
-        if (SL * (i0 + VB) < S)
-            vmac(vb, i0 + VB);
-        if (SL * (i0 + 3 * VB) < S) {
-#pragma unroll
-            for (int u = 0; u < VB; ++u)
-                vb[u] = vld(i0 + 3 * VB + u);
-        }
+        neg |= sc[t] < 0;
     }
+    neg = __syncthreads_or(neg);
+
+    // o[d] = sum_t fp_mul(p_t, v_t[d]), llama_int.c:1514-1529; one copy of
+    // the loop per product form, chosen once for the block
+    auto values = [&](auto nonneg) -> uint64_t {
+        uint64_t acc = 0;
+        q48_pv_acc pa = {0, 0};
+        auto vmac = [&](const int64_t(&vv)[VB], int i0) {
+#pragma unroll
+            for (int u = 0; u < VB; ++u) {
+                const int t = sl + SL * (i0 + u);
+                if (t < S) {
+                    const int64_t v = !ROT && t == pos ? vs[d] : vv[u];
+                    if constexpr (decltype(nonneg)::value)
+                        q48_pv_mac(pa, sc[t], v);
+                    else
+                        acc += (uint64_t)q48_mul(sc[t], v);
+                }
+            }
+        };
+        for (int i0 = 0; sl + SL * i0 < S; i0 += 2 * VB) {
+            // the next batches where some position of them exists (as above)
+            vmac(va, i0);
+            if (SL * (i0 + 2 * VB) < S) {
+#pragma unroll
+                for (int u = 0; u < VB; ++u)
+                    va[u] = vld(i0 + 2 * VB + u);
+            }
+            if (SL * (i0 + VB) < S)
+                vmac(vb, i0 + VB);
+            if (SL * (i0 + 3 * VB) < S) {
+#pragma unroll
+                for (int u = 0; u < VB; ++u)
+                    vb[u] = vld(i0 + 3 * VB + u);
+            }
+        }
+        return acc + (uint64_t)q48_pv_total(pa);
+    };
+    const uint64_t acc = neg ? values(std::false_type{}) : values(std::true_type{});
     part[tid] = (int64_t)acc;
     __syncthreads();
     if (sl == 0) {

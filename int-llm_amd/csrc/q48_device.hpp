@@ -211,6 +211,35 @@ __device__ __forceinline__ int64_t q48_mul(int64_t a, int64_t b)
     return q48_mul_shr<48>(a, b);
 }
 
+// sum_t fp_mul(p_t, v_t) (mod 2^64) for 0 <= p_t < 2^63 (softmax weights),
+// as two words: with p = ph 2^32 + pl and v = vh 2^32 + vl (vh signed),
+//   p v = pl vl + (pl vh_u + ph vl) 2^32 + (ph vh - pl [vh < 0]) 2^64
+// (vh_u: vh's bits unsigned), and with mid + cy 2^64 = pl vh_u + hi(pl vl)
+// + ph vl, floor(p v / 2^48) = (mid >> 16) + (ph vh + cy 2^32 - pl [vh < 0])
+// 2^16.  So a1 sums mid >> 16, a2 the second factor, and the sum is a1 +
+// (a2 << 16): three 32 x 32 products per term instead of a signed
+// 64 x 64 -> 128 product.
+struct q48_pv_acc {
+    uint64_t a1, a2;
+};
+
+__device__ __forceinline__ void q48_pv_mac(q48_pv_acc &acc, int64_t p, int64_t v)
+{
+    const uint32_t pl = (uint32_t)(uint64_t)p, ph = (uint32_t)((uint64_t)p >> 32);
+    const uint32_t vl = (uint32_t)(uint64_t)v, vh = (uint32_t)((uint64_t)v >> 32);
+    const uint64_t b = (uint64_t)pl * vh + __umulhi(pl, vl);   // < 2^64
+    uint64_t mid;
+    const bool cy = __builtin_add_overflow(b, (uint64_t)ph * vl, &mid);
+    acc.a1 += mid >> 16;
+    acc.a2 += (uint64_t)((int64_t)(int32_t)ph * (int64_t)(int32_t)vh) + ((uint64_t)cy << 32) -
+              ((int32_t)vh < 0 ? (uint64_t)pl : 0);
+}
+
+__device__ __forceinline__ int64_t q48_pv_total(const q48_pv_acc &acc)
+{
+    return (int64_t)(acc.a1 + (acc.a2 << 16));
+}
+
 // fp_mul(r, r): r * r = u^2 with u = |r| <= 2^63 as an unsigned word;
 // u^2 = hh 2^64 + 2 lh 2^32 + ll, and w = 2 lh + (ll >> 32) stays below 2^64,
 // so bits 48..111 are (hh << 16) + (w >> 16) mod 2^64: three 32 x 32 -> 64

@@ -1144,13 +1144,18 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
             __hip_atomic_store(ep, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
     }
-    // p_t = fp_div(e_t, sum) when sum > 0 (llama_int.c:1069-1071)
+    // p_t = fp_div(e_t, sum) when sum > 0 (llama_int.c:1069-1071).  The
+    // weights are never negative (exponentials over a positive sum, or the
+    // exponentials themselves); the block checks it, and the values take
+    // the product for non-negative weights (q48_pv_mac) unless one is
+    int neg = 0;
     if (dh == 0 && live) {
         const int64_t sum = loc[hh];
         if (sum > 0)
             sc[hh][t] = q48_div(sc[hh][t], sum);
+        neg = sc[hh][t] < 0;
     }
-    __syncthreads();
+    neg = __syncthreads_or(neg);
 
     // o[h][d] += sum_t fp_mul(p_t, v_t[d]) over the chunk: thread owns the
     // outputs tid + NT o of the group's [G][HD]
@@ -1160,8 +1165,15 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
         if (oi < G * HD) {
             const int oh = oi / HD, d = oi % HD;
             uint64_t acc = 0;
-            for (int u = 0; u < nt; ++u)
-                acc += (uint64_t)q48_mul(sc[oh][u], vl[u][d]);
+            if (!neg) {
+                q48_pv_acc pa = {0, 0};
+                for (int u = 0; u < nt; ++u)
+                    q48_pv_mac(pa, sc[oh][u], vl[u][d]);
+                acc = (uint64_t)q48_pv_total(pa);
+            } else {
+                for (int u = 0; u < nt; ++u)
+                    acc += (uint64_t)q48_mul(sc[oh][u], vl[u][d]);
+            }
             int64_t *dst = out + (size_t)h0 * HD + oi;
             if (nc > 1)
                 __hip_atomic_fetch_add(reinterpret_cast<uint64_t *>(dst), acc, __ATOMIC_RELAXED,

@@ -526,11 +526,30 @@ def test_attention_rope_fused(ctx, oracle, nh, nkv, hd, max_seq, positions, one_
         ctx.set_attn_g_mfma(True)
 
 
-def _attention_rope_case(ctx, oracle, nh, nkv, hd, max_seq, positions):
+@pytest.mark.parametrize("full_keys", [False, True], ids=["normal_keys", "full_range_keys"])
+def test_attention_full_range_values(ctx, oracle, full_keys):
+    """Values spread over the whole int64 range (and, in one case, keys too,
+    so that scores wrap and the softmax weights take their extremes): the
+    single-block and split kernels' value products against the oracle."""
+    _attention_rope_case(ctx, oracle, 32, 4, 64, 1400, [40, 200, 300, 1300],
+                         full_values=True, full_keys=full_keys)
+    assert ctx.attn_status() == 0
+
+
+def _attention_rope_case(ctx, oracle, nh, nkv, hd, max_seq, positions, full_values=False,
+                         full_keys=False):
     rng = np.random.default_rng(nh + hd + max_seq)
     kvd = nkv * hd
     kc = (rng.standard_normal(2 * max_seq * kvd) * ONE).astype(np.int64)
     vc = (rng.standard_normal(2 * max_seq * kvd) * ONE).astype(np.int64)
+    if full_keys:
+        kc = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=kc.size, dtype=np.int64,
+                          endpoint=True)
+    if full_values:
+        vc = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=vc.size, dtype=np.int64,
+                          endpoint=True)
+        vc[::97] = spec.INT64_MIN
+        vc[1::89] = spec.INT64_MAX
     cos_t = np.empty(max_seq * hd // 2, dtype=np.int64)
     sin_t = np.empty(max_seq * hd // 2, dtype=np.int64)
     oracle.q48o_rope_tables(cos_t.ctypes.data, sin_t.ctypes.data, hd, max_seq, 10000)
