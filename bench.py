@@ -292,7 +292,9 @@ def refbind_decode(spec, intllm, gold, new_tokens: int):
     the reference's own mgw_load.  Each forward is one graph replay of the
     fused launches plus the synchronous logits copy llama_forward's
     contract needs.  Decode tok/s = K / (t(generate with K + 1 new tokens)
-    - t(generate with 1 new token)), the same prompt both times."""
+    - t(generate with 1 new token)), the same prompt both times, without
+    hashing; a third, untimed run hashes every logits vector on the host
+    (FNV-1a over 256 KB, about 0.25 ms each) for the parity check."""
     import tempfile
     so = ROOT / "int-llm_amd" / "refbind" / "_out" / "libllama_int_q48.so"
     if not so.exists():
@@ -325,18 +327,21 @@ def refbind_decode(spec, intllm, gold, new_tokens: int):
             out["setup_s"] = round(time.perf_counter() - t, 2)
             p = (C.c_int * len(prompt))(*prompt)
 
-            def gen(k):
+            def gen(k, hashed=False):
                 buf = (C.c_int * (len(prompt) + k))()
                 hs = (C.c_uint64 * (len(prompt) + k))()
                 n = C.c_int()
                 t0 = time.perf_counter()
-                total = lib.lq48_generate(m, p, len(prompt), k, buf, hs, len(hs), C.byref(n))
+                total = lib.lq48_generate(m, p, len(prompt), k, buf, hs,
+                                          len(hs) if hashed else 0, C.byref(n))
                 dt = time.perf_counter() - t0
-                return dt, list(buf[:max(total, 0)]), ["%016x" % h for h in hs[:n.value]]
+                return (dt, list(buf[:max(total, 0)]),
+                        ["%016x" % h for h in hs[:min(n.value, len(hs))]] if hashed else [])
 
             gen(2)                                  # warm: captures both graphs' first kind
             t1, _, _ = gen(1)
-            t2, toks, hs = gen(1 + new_tokens)
+            t2, toks, _ = gen(1 + new_tokens)
+            _, toks_h, hs = gen(1 + new_tokens, hashed=True)
             lib.lq48_detach()
             lib.lq48_model_free(m)
     finally:
@@ -349,7 +354,7 @@ def refbind_decode(spec, intllm, gold, new_tokens: int):
                             "llama_forward on the device (refbind), greedy",
                 "tok_s": round(1e3 / ms, 2), "ms_per_tok": round(ms, 4),
                 "new_tokens_timed": new_tokens,
-                "tokens_match_reference": toks == gold["tokens"][:n],
+                "tokens_match_reference": toks == gold["tokens"][:n] and toks_h == toks,
                 "step_hashes_match_reference": hs == gold["step_fnv"][:len(hs)]})
     log(f"refbind generate decode {ms:.3f} ms/tok")
     return out
