@@ -142,7 +142,9 @@ int q48_rope_tables(q48_ctx *ctx, const int64_t **cos_t, const int64_t **sin_t);
  * fp_determinism.c:175-195, exposed so the gate can run on the GPU).
  * func: 0 mul(x,y) 1 div(x,y) [0 where y==0] 2 sqrt 3 sqrt_fast
  * 4 inv_sqrt 5 exp 6 log 7 sincos (out0=cos, out1=sin) 8 sigmoid 9 silu
- * 10 safe_exp 11 exp_dyadic(x, k=y).  out1 may be NULL unless func 7. */
+ * 10 safe_exp 11 exp_dyadic(x, k=y) 12 div(x,y) [0 where y==0] through the
+ * prepared-divisor quotient the softmax rows use.  out1 may be NULL unless
+ * func 7. */
 int q48_fp_eval(q48_ctx *ctx, int func, const int64_t *x, const int64_t *y,
                 int64_t *out0, int64_t *out1, int n);
 

@@ -544,9 +544,9 @@ int q48_rope_tables(q48_ctx *c, const int64_t **cos_t, const int64_t **sin_t)
 int q48_fp_eval(q48_ctx *c, int func, const int64_t *x, const int64_t *y, int64_t *out0,
                 int64_t *out1, int n)
 {
-    if (!c || !x || !out0 || n <= 0 || func < 0 || func > 11)
+    if (!c || !x || !out0 || n <= 0 || func < 0 || func > 12)
         return Q48_EINVAL;
-    if ((func == 0 || func == 1 || func == 11) && !y)
+    if ((func == 0 || func == 1 || func == 11 || func == 12) && !y)
         return Q48_EINVAL;
     if (func == 7 && !out1)
         return Q48_EINVAL;

@@ -256,9 +256,10 @@ __device__ __forceinline__ void attn_v3_head(
     // the exponentials themselves); checked, and the values take the product
     // for non-negative weights (q48_pv_mac) unless one is
     int neg = 0;
+    const q48_divisor dv = q48_divisor_of(sum);
     for (int t = tid; t < S; t += NT) {
         if (sum > 0)
-            sc[t] = q48_div(sc[t], sum);
+            sc[t] = q48_div_by(sc[t], dv);
         neg |= sc[t] < 0;
     }
     neg = __syncthreads_or(neg);

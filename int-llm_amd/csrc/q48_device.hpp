@@ -244,13 +244,16 @@ __device__ __forceinline__ int64_t q48_pv_total(const q48_pv_acc &acc)
 // u^2 = hh 2^64 + 2 lh 2^32 + ll, and w = 2 lh + (ll >> 32) stays below 2^64,
 // so bits 48..111 are (hh << 16) + (w >> 16) mod 2^64: three 32 x 32 -> 64
 // products.
-__device__ __forceinline__ int64_t q48_sqr(int64_t r)
+__device__ __forceinline__ int64_t q48_usqr(uint64_t u)
 {
-    const uint64_t u = r < 0 ? (uint64_t)0 - (uint64_t)r : (uint64_t)r;
     const uint32_t l = (uint32_t)u, h = (uint32_t)(u >> 32);
     const uint64_t ll = (uint64_t)l * l, lh = (uint64_t)l * h, hh = (uint64_t)h * h;
     const uint64_t w = (lh << 1) + (ll >> 32);
     return (int64_t)((hh << 16) + (w >> 16));
+}
+__device__ __forceinline__ int64_t q48_sqr(int64_t r)
+{
+    return q48_usqr(r < 0 ? (uint64_t)0 - (uint64_t)r : (uint64_t)r);
 }
 
 // floor(mag * 2^48 / ub) for 0 < ub and mag < 16 ub (a quotient below
@@ -303,6 +306,78 @@ __device__ __forceinline__ int64_t q48_div(int64_t a, int64_t b)
     if (a < 0)
         num = (q48_i128)(0 - (q48_u128)num);
     return (int64_t)q48_divs_128_64(num, b);
+}
+
+// The nearest integer to 0 <= v < 2^51, minus 1, from the FP64 word of v + 2^52
+// (whose low 52 bits are that integer); as a word, -1 for v below 1/2.
+__device__ __forceinline__ uint64_t q48_round_m1(double v)
+{
+    return (uint64_t)__builtin_bit_cast(int64_t, v + 0x1p52) - 0x4330000000000001ull;
+}
+
+// floor(2^96 / r) = fp_div(ONE, r) for 2^48 <= r < 2^63: the reciprocal in
+// fp_exp of a negative argument and in fp_sigmoid (fp_math.h:516-523 with a
+// = ONE).  y = 1 / r from the hardware reciprocal and two Newton steps has a
+// relative error of a few units of 2^-53 (from any first approximation
+// within 2^-20), so qe = y 2^96 is within 1/16 of 2^96 / r <= 2^48 and q0 =
+// round(qe) - 1 is the quotient or one less.  The remainder 2^96 - q0 r then
+// lies in [0, 2 r), below 2^64, so its low word 0 - q0 r (mod 2^64) is the
+// remainder itself and one compare finishes the quotient.  A remainder that
+// does not settle (an FP64 unit outside those bounds) goes to q48_div.
+__device__ __forceinline__ int64_t q48_recip(int64_t r)
+{
+    const uint64_t u = (uint64_t)r;
+    const double rd = (double)u;
+    double y = __builtin_amdgcn_rcp(rd);
+    y = __builtin_fma(y, __builtin_fma(-rd, y, 1.0), y);
+    y = __builtin_fma(y, __builtin_fma(-rd, y, 1.0), y);
+    const uint64_t q0 = q48_round_m1(y * 0x1p96);
+    const uint64_t rem = (uint64_t)0 - q0 * u;
+    const bool up = rem >= u;
+    if (rem - (up ? u : 0) >= u)
+        return q48_div(Q48_ONE, r);
+    return (int64_t)(q0 + up);
+}
+
+// A divisor prepared for many fp_div(e, d) with the same d (a softmax row's
+// sum, a renormalisation): 2^48 / d in FP64 (two Newton steps, as in
+// q48_recip) when 1 <= d < 2^62, and the largest e the fast quotient takes,
+// min(d, 2^52 - 1) (0 for any other d).
+struct q48_divisor {
+    uint64_t d, lim;
+    double y48;
+};
+__device__ __forceinline__ q48_divisor q48_divisor_of(int64_t d)
+{
+    q48_divisor v = {(uint64_t)d, 0, 0.0};
+    if (d >= 1 && d < ((int64_t)1 << 62)) {
+        const double dd = (double)d;
+        double y = __builtin_amdgcn_rcp(dd);
+        y = __builtin_fma(y, __builtin_fma(-dd, y, 1.0), y);
+        y = __builtin_fma(y, __builtin_fma(-dd, y, 1.0), y);
+        v.y48 = y * 0x1p48;
+        v.lim = d < ((int64_t)1 << 52) ? (uint64_t)d : ((uint64_t)1 << 52) - 1;
+    }
+    return v;
+}
+
+// fp_div(e, d) (fp_math.h:508-524) for a divisor from q48_divisor_of.  For 0 <=
+// e <= lim the quotient e 2^48 / d is at most 2^48, e is exact in FP64, qe =
+// e y48 is within 0.1 of the quotient, q0 = round(qe) - 1 is it or one less,
+// and the remainder e 2^48 - q0 d, in [0, 2 d), is its own low word, as in
+// q48_recip.  (With lim = 0, e = 0 gives q0 = -1, remainder d and quotient 0,
+// which is fp_div(0, d) for every d != 0.)  Any other e goes to q48_div.
+__device__ __forceinline__ int64_t q48_div_by(int64_t e, const q48_divisor &v)
+{
+    if ((uint64_t)e > v.lim)
+        return q48_div(e, (int64_t)v.d);
+    const double ed = __builtin_bit_cast(double, (uint64_t)e | 0x4330000000000000ull) - 0x1p52;
+    const uint64_t q0 = q48_round_m1(ed * v.y48);
+    const uint64_t rem = ((uint64_t)e << 48) - q0 * v.d;
+    const bool up = rem >= v.d;
+    if (rem - (up ? v.d : 0) >= v.d)
+        return q48_div(e, (int64_t)v.d);
+    return (int64_t)(q0 + up);
 }
 
 // fp_from_int, fp_math.h:530-538
@@ -467,32 +542,32 @@ __device__ __forceinline__ int64_t q48_exp(int64_t x)
 }
 
 // fp_exp for |x| <= 10 ONE, the range fp_safe_exp leaves (fp_math.h:739-744):
-// the same squarings, the first 11 on exact doubles.  r0 = ONE + (|x| >> 14)
+// the same squarings, the first 12 on exact doubles.  r0 = ONE + (|x| >> 14)
 // and r_k = floor(r_{k-1}^2 / 2^48) <= e^(10 2^(k - 14)) ONE, so r_0 .. r_11
-// stay below 3.5 ONE < 2^50 and each square is below 2^100: with rs = r 2^-48
-// (exact), f = floor(r rs) and fma(r, rs, -f) = (r^2 - f 2^48) 2^-48 exactly
-// (a multiple of 2^-48 in [-1, 1)), floor(r^2 / 2^48) = f + floor(fma(r, rs,
-// -f)).  Full-rate FP64 instead of three quarter-rate 32 x 32 -> 64 products
-// per square; the last three squares (up to e^10 ONE < 2^63) stay integer.
+// stay below 3.5 ONE < 2^50, each of their squares is below 2^100 and r_12 is
+// below 12.2 ONE < 2^52: with rs = r 2^-48 (exact), f = floor(r rs) and
+// fma(r, rs, -f) = (r^2 - f 2^48) 2^-48 exactly (a multiple of 2^-48 in [-1,
+// 1)), floor(r^2 / 2^48) = f + floor(fma(r, rs, -f)), an integer double.
+// Full-rate FP64 instead of three quarter-rate 32 x 32 -> 64 products per
+// square; the last two squares (up to e^10 ONE < 2^63) stay integer, and the
+// reciprocal of a negative argument is q48_recip (r >= ONE).
 __device__ __forceinline__ int64_t q48_exp_small(int64_t x)
 {
     const uint64_t m = x >= 0 ? (uint64_t)x : (uint64_t)0 - (uint64_t)x;
     double rd = (double)(int64_t)((uint64_t)Q48_ONE + (m >> 14));
 #pragma unroll
-    for (int k = 0; k < 11; ++k) {
+    for (int k = 0; k < 12; ++k) {
         const double rs = rd * 0x1p-48;
         const double f = __builtin_floor(rd * rs);
         rd = f + __builtin_floor(__fma_rn(rd, rs, -f));
     }
-    int64_t r = (int64_t)rd;
-    r = q48_sqr(r);
-    r = q48_sqr(r);
-    r = q48_sqr(r);
+    // rd is an integer below 2^52: the low bits of rd + 2^52's word
+    uint64_t u = (uint64_t)__builtin_bit_cast(int64_t, rd + 0x1p52) - 0x4330000000000000ull;
+    u = (uint64_t)q48_usqr(u);
+    u = (uint64_t)q48_usqr(u);
     if (x > 0)
-        return r;
-    if (r == 0)
-        return 0;
-    return q48_div(Q48_ONE, r);
+        return (int64_t)u;
+    return q48_recip((int64_t)u);
 }
 
 // fp_safe_exp, fp_math.h:739-744
@@ -611,8 +686,9 @@ __device__ __forceinline__ int64_t q48_sigmoid(int64_t x)
         return Q48_ONE;
     if (x < -ten)
         return 0;
+    // ONE + e^-x lies in [ONE, (1 + e^10) ONE], within q48_recip's range
     int64_t en = q48_safe_exp((int64_t)(0 - (uint64_t)x));
-    return q48_div(Q48_ONE, (int64_t)((uint64_t)Q48_ONE + (uint64_t)en));
+    return q48_recip((int64_t)((uint64_t)Q48_ONE + (uint64_t)en));
 }
 
 // fp_silu, fp_math.h:919-921

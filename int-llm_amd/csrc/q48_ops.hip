@@ -180,9 +180,11 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_decode(
         sum = (int64_t)((uint64_t)sum + (uint64_t)e);
     }
     sum = block_sum64<ATT_NT>(sum, red);
-    if (sum > 0)
+    if (sum > 0) {
+        const q48_divisor dv = q48_divisor_of(sum);
         for (int t = tid; t < S; t += ATT_NT)
-            sc[t] = q48_div(sc[t], sum);
+            sc[t] = q48_div_by(sc[t], dv);
+    }
     __syncthreads();
 
     // o[d] = sum_t fp_mul(p_t, v_t[d])  (int64, wrapping)
@@ -328,9 +330,11 @@ __global__ __launch_bounds__(ATT_NT) void k_attn_v2(
         sum = (int64_t)((uint64_t)sum + (uint64_t)e);
     }
     sum = block_sum64<ATT_NT>(sum, red);
-    if (sum > 0)
+    if (sum > 0) {
+        const q48_divisor dv = q48_divisor_of(sum);
         for (int t = tid; t < S; t += ATT_NT)
-            sc[t] = q48_div(sc[t], sum);
+            sc[t] = q48_div_by(sc[t], dv);
+    }
     __syncthreads();
 
     // o[d] = sum_t fp_mul(p_t, v_t[d]): 8 positions per batch, loads first
@@ -642,7 +646,7 @@ __global__ __launch_bounds__(256) void k_attn_s2(int64_t *__restrict__ out,
         vb[u] = vcol[(size_t)tpos(VB + u) * kvd];
     // p_t = fp_div(e_t, sum) when sum > 0, one position per thread
     const int64_t sum = block_sum64<NT>(cs, red, false);
-    pl[tid] = sum > 0 ? q48_div(ev, sum) : ev;
+    pl[tid] = sum > 0 ? q48_div_by(ev, q48_divisor_of(sum)) : ev;
     __syncthreads();
     uint64_t acc = 0;
     auto vmac = [&](const int64_t (&vv)[VB], int i0) {
@@ -1152,7 +1156,7 @@ __global__ __launch_bounds__(ATTG_NT) __attribute__((amdgpu_waves_per_eu(HD == 1
     if (dh == 0 && live) {
         const int64_t sum = loc[hh];
         if (sum > 0)
-            sc[hh][t] = q48_div(sc[hh][t], sum);
+            sc[hh][t] = q48_div_by(sc[hh][t], q48_divisor_of(sum));
         neg = sc[hh][t] < 0;
     }
     neg = __syncthreads_or(neg);
@@ -1369,6 +1373,7 @@ __global__ __launch_bounds__(256) void k_fp_eval(int func, const int64_t *__rest
     case 9: r = q48_silu(a); break;
     case 10: r = q48_safe_exp(a); break;
     case 11: r = q48_exp_dyadic(a, (int)y[i]); break;
+    case 12: r = y[i] != 0 ? q48_div_by(a, q48_divisor_of(y[i])) : 0; break;
     default: break;
     }
     o0[i] = r;

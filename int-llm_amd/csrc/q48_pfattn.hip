@@ -327,6 +327,7 @@ k_pfa(int64_t *__restrict__ out,
     const int S3 = p0 + t0 + r3 + 1;
     const bool rv = r3 < nrow;
     const int64_t den = sums[r3];
+    const q48_divisor dvr = q48_divisor_of(den);
     const int db = lane / JG, jg = lane % JG;
     constexpr int FLUSH = 128 / JPER;   // steps between flushes of the 32-bit Λ sums (< 2^31)
     const uint8_t *vd = VD + (size_t)kh * 8 * HD * Ppad;
@@ -352,7 +353,7 @@ k_pfa(int64_t *__restrict__ out,
 #pragma unroll
             for (int k = 0; k < 4; ++k)
                 if (jb + k < S3)
-                    p[k] = (uint64_t)(den > 0 ? q48_div((int64_t)er[k], den) : (int64_t)er[k]);
+                    p[k] = (uint64_t)(den > 0 ? q48_div_by((int64_t)er[k], dvr) : (int64_t)er[k]);
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k)

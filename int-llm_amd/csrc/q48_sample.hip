@@ -413,9 +413,11 @@ __global__ __launch_bounds__(SMP_T) void k_smp_div(int64_t *__restrict__ base, i
     }
     __syncthreads();
     const int64_t sum = sum_sh;
-    if (sum > 0)
+    if (sum > 0) {
+        const q48_divisor dv = q48_divisor_of(sum);
         for (int i = blockIdx.x * SMP_T + threadIdx.x; i < n; i += gridDim.x * SMP_T)
-            s.p[i] = q48_div(s.p[i], sum);
+            s.p[i] = q48_div_by(s.p[i], dv);
+    }
 }
 
 // First index i (index order) at which the running sum of val(a[j]), j <= i,
@@ -577,7 +579,7 @@ __global__ __launch_bounds__(SMP_B) void k_smp_pick(int64_t *__restrict__ base, 
         if (nucleus) {
             const int64_t sum = (int64_t)blk_sum<SMP_B>((uint64_t)q, redv);
             if (sum > 0 && q > 0)
-                q = q48_div(q, sum);
+                q = q48_div_by(q, q48_divisor_of(sum));
         }
         __syncthreads();
         cv[tid] = q;   // slots past K hold 0
@@ -744,11 +746,13 @@ __global__ __launch_bounds__(SMP_B) void k_smp_pick(int64_t *__restrict__ base, 
         uint64_t part = 0;
         pass_strided(p, n, [&](int, int64_t v) { part += (uint64_t)v; });
         const int64_t sum = (int64_t)blk_sum<SMP_B>(part, redv);
-        if (sum > 0)
+        if (sum > 0) {
+            const q48_divisor dv = q48_divisor_of(sum);
             pass_strided(p, n, [&](int i, int64_t v) {
                 if (v > 0)
-                    p[i] = q48_div(v, sum);
+                    p[i] = q48_div_by(v, dv);
             });
+        }
     }
 
     // the draw: r in [0, ONE) from one rng_next (llama_int.c:2922-2929)

@@ -25,7 +25,7 @@ Q48_ETIMEOUT, Q48_ETOOBIG = -6, -7
 
 # fp_eval function ids (include/intllm_hip.h, q48_fp_eval)
 FP_MUL, FP_DIV, FP_SQRT, FP_SQRT_FAST, FP_INV_SQRT, FP_EXP, FP_LOG, FP_SINCOS, \
-    FP_SIGMOID, FP_SILU, FP_SAFE_EXP, FP_EXP_DYADIC = range(12)
+    FP_SIGMOID, FP_SILU, FP_SAFE_EXP, FP_EXP_DYADIC, FP_DIV_ROW = range(13)
 
 # q48_gemm_ex kernels (include/intllm_hip.h)
 GEMM_AUTO, GEMM_VALU, GEMM_I8 = 0, 1, 2

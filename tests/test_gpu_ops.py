@@ -150,6 +150,10 @@ def test_device_safe_exp_sigmoid_silu_vs_oracle(ctx, oracle):
                                            rng.integers(0, 48, size=8192))]
     for c in (0, ten, -ten, one, -one):
         x += [c + d for d in range(-40, 41)]
+    # within 0.05 ONE of the clamps: the largest squarings (e^|x| ONE near
+    # 2^62.4) and the smallest reciprocals
+    x += [int(v) for v in rng.integers(ten - one // 20, ten + 1, size=4096)]
+    x += [int(v) for v in rng.integers(-ten, -ten + one // 20, size=4096)]
     x += [spec.INT64_MAX, spec.INT64_MIN]
     x = np.array(x, dtype=np.int64)
     say("safe_exp / sigmoid / silu", x.size)
@@ -195,6 +199,54 @@ def test_device_div_quotients_at_integers(ctx, oracle):
     want = np.array([oracle.q48o_fp_div(int(p), int(q)) for p, q in zip(a, b)], dtype=np.int64)
     bad = np.nonzero(d != want)[0]
     assert bad.size == 0, [(int(a[i]), int(b[i]), int(d[i]), int(want[i])) for i in bad[:5]]
+
+
+def test_device_div_prepared_divisor_vs_oracle(ctx, oracle):
+    """The softmax rows' quotient (a reciprocal prepared once per divisor, one
+    FP64 product and one remainder compare per element) equals fp_div: inside
+    its range (0 <= e <= min(d, 2^52 - 1), 1 <= d < 2^62), at the range's
+    edges (e = lim and lim + 1, d = 2^62 - 1 and 2^62, d = 1), near exact
+    quotients, and outside it (negative or larger e, d < 1, d >= 2^62), where
+    the general division answers."""
+    rng = np.random.default_rng(37)
+    one, top = 1 << 48, 1 << 62
+    a, b = [], []
+
+    def lim(d):
+        return min(d, (1 << 52) - 1)
+
+    for _ in range(8192):
+        sh = int(rng.integers(0, 62))
+        d = max(1, int(rng.integers(0, 1 << 62)) >> sh)
+        a.append(int(rng.integers(0, lim(d) + 1)))
+        b.append(d)
+    for _ in range(4096):          # softmax shapes: e <= ONE <= sum
+        a.append(int(rng.integers(0, one + 1)))
+        b.append(int(rng.integers(one, 4097 * one)))
+    for _ in range(2048):          # near exact quotients q = e 2^48 / d
+        d = int(rng.integers(1, top))
+        q = int(rng.integers(0, one + 1))
+        e = (q * d) >> 48
+        for dd in (-1, 0, 1):
+            if 0 <= e + dd <= lim(d):
+                a.append(e + dd)
+                b.append(d)
+    for d in (1, 2, 3, one - 1, one, one + 1, (1 << 52) - 1, 1 << 52, (1 << 52) + 1,
+              top - 1, top, top + 1, spec.INT64_MAX):
+        for e in (0, 1, lim(d) - 1, lim(d), lim(d) + 1, one, -1, -one, spec.INT64_MIN,
+                  spec.INT64_MAX):
+            a.append(e)
+            b.append(d)
+    for _ in range(2048):          # outside the range: negative e or d, e > d
+        a.append(int(rng.integers(spec.INT64_MIN, spec.INT64_MAX)))
+        b.append(int(rng.integers(spec.INT64_MIN, spec.INT64_MAX)) or 5)
+    a = np.array([spec.wrap64(v) for v in a], dtype=np.int64)
+    b = np.array(b, dtype=np.int64)
+    say("div prepared divisor", a.size)
+    got = dev_eval(ctx, intllm.FP_DIV_ROW, a, b)
+    want = np.array([oracle.q48o_fp_div(int(p), int(q)) for p, q in zip(a, b)], dtype=np.int64)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(int(a[i]), int(b[i]), int(got[i]), int(want[i])) for i in bad[:5]]
 
 
 def gemv_dev(ctx, W, x, M, K, w_offset=0):
