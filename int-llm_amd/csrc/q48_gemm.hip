@@ -3,25 +3,35 @@
 // Y[t][n] = (int64)((sum_k (int128)X[t][k] * W[n][k]) >> 48), per output
 // exactly matmul_vec (llama_int.c:1014-1046) applied to each token row.
 //
-// Digits.  Every int64 v is written v = S(v) + C with C = 0x0080808080808080
-// and S(v) = sum_i s_i 256^i, s_i the bytes of v ^ C read as int8 (bytes 0..6
-// are offset by 128, byte 7 is v's own signed top byte).  Then
-//   sum_k W X = sum_{a,b} 256^(a+b) P_ab + C sum_k S(W) + C sum_k S(X) + K C^2,
-//   P_ab = sum_k s_a(X_k) s_b(W_k),
-// an exact integer identity over any k range; sum_k S(v) is the digit sums
-// sum_a 256^a sum_k s_a(v_k), counted with v_dot4_i32_i8 while the tiles are
-// split, so W and X are read once.  Only bits [48,112) are observable,
-// so the pair a = b = 7 (weight 2^112) is dropped and the remaining 63 int8
-// products are grouped by d = a + b into 14 int32 accumulators
-// Q_d = sum_{a+b=d} P_ab; |Q_d| <= 8 * 2^14 * K < 2^31 while K < 16384 per
-// accumulation run (longer K is split across blocks and summed in int128).
+// Digits.  Every int64 v is written with nine signed digits,
+//   v = sum_{i<=7} d_i 256^i + 2^64 d_8,
+// from u = v + C mod 2^64, C = 0x0080808080808080: d_i = byte_i(u) - 128 for
+// i <= 6 (in [-128, 127]), d_7 = byte_7(u) read as int8, and d_8 = 1 when v + C
+// overflowed int64 (v >= 2^63 - C, so u < 0 <= v), else 0.  Zero has all digits
+// zero, and so have the high digits of a small value and the low digits of a
+// value with few significant bits (a bfloat16 weight in Q16.48 has three or
+// four nonzero digits, an activation below 2^55 none above d_6).  Then
+//   sum_k X W = sum_{a,b<=8} 256^(a+b) P_ab,   P_ab = sum_k d_a(X_k) d_b(W_k),
+// an exact integer identity over any k range with no correction terms.  Only
+// bits [48,112) are observable, so the pairs with a + b >= 14 are dropped and
+// the rest are grouped by d = a + b into 14 int32 accumulators Q_d; |Q_d| <=
+// 8 * 2^14 * K < 2^31 while K < 16384 per accumulation run (the plane-8
+// products are at most 2^7 each; longer K is split across blocks and summed in
+// int128).
 //
 // Block: 4 waves, 64 tokens x 64 rows; wave w owns 32 tokens x 32 rows as 14
 // v_mfma_i32_32x32x32_i8 accumulators (224 registers, one wave per SIMD).
-// Per k-step of 32 elements the block splits the int64 tiles into eight byte
-// planes in LDS (double-buffered) and every wave issues 63 MFMAs; the global
-// loads run two steps ahead and the byte split of the next step is
-// interleaved with the MFMAs of the current one.
+// Per k-step of 32 elements the block splits the int64 tiles into nine byte
+// planes in LDS (double-buffered) and records which planes of each tile hold a
+// nonzero digit.  k_gemm_i8 multiplies X planes 0..6 by a window of W planes
+// LO..LO + 3 (28 MFMAs a step, 7 more in a step whose W tile reaches plane
+// LO - 1), LO chosen from the block's first W tile; a block meeting a tile
+// outside that (X digits in planes 7-8, W digits outside LO - 1 .. LO + 3)
+// writes nothing and k_gemm_i8_full redoes it with every pair (63, plus the
+// plane-8 pairs of a tile holding an overflowed value).  Activations below
+// 2^55 and bfloat16-exact weights always fit.  The global loads run two steps
+// ahead and the byte split of the next step is interleaved with the MFMAs of
+// the current one.
 #include "q48_digits.hpp"
 #include "../../include/intllm_hip.h"
 
@@ -31,17 +41,17 @@ constexpr int MT = 64;             // tokens per block
 constexpr int MN = 64;             // rows per block
 constexpr int MK = 32;             // k per step: one MFMA depth
 constexpr int MAXK_RUN = 16320;    // k per accumulation run: |Q_d| < 2^31
-constexpr int FUSE_BELOW_T = 1024; // token counts that count digit sums in the GEMM
 constexpr int NPAIR = MK / 32;     // (row, 8 elements) pieces per thread per operand
-constexpr int CH = MK / 16;        // 16-byte k chunks per row and limb
+constexpr int CH = MK / 16;        // 16-byte k chunks per row and plane
+constexpr int NPL = 9;             // digit planes per operand
 
-// Byte planes of one stage: [limb][32-row slice][k chunk][32 rows][16 bytes].
+// Byte planes of one stage: [plane][32-row slice][k chunk][32 rows][16 bytes].
 // The 64 lanes of an MFMA operand read (row l % 32, chunk 2h + l / 32) touch
 // 1 KiB of consecutive bytes, and the 32 lanes of a half-wave store 256
 // consecutive bytes: no bank conflicts either way.
-constexpr int SLICE = CH * 512;    // one 32-row slice of one limb
-constexpr int PLANE = 2 * SLICE;   // 64 rows of one limb
-constexpr int STAGE = 8 * PLANE;   // one operand: 32 KiB
+constexpr int SLICE = CH * 512;    // one 32-row slice of one plane
+constexpr int PLANE = 2 * SLICE;   // 64 rows of one plane
+constexpr int STAGE = NPL * PLANE; // one operand: 18 KiB
 
 // Piece p (0 .. 64 CH - 1) of a tile: row r, elements [k8, k8 + 8) of the
 // step, and its byte offset in a plane.  Lanes 2i, 2i + 1 take one 16-byte
@@ -56,21 +66,71 @@ __device__ __forceinline__ Piece piece(int p)
     return {r, (2 * c + lo) * 8, (r >> 5) * SLICE + c * 512 + (r & 31) * 16 + 8 * lo};
 }
 
-// Eight consecutive int64 of one row -> eight 8-byte digit words, limb a of
-// element e in byte e of word a, stored at plane a.  sum[a] += ones-weighted
-// sum of the eight limb-a digits (v_dot4_i32_i8; ones = 0x01010101 or 0).
-template <bool FUSE>
-__device__ __forceinline__ void split_store(uint8_t *stage, int off, const uint64_t (&v)[8],
-                                            int (&sum)[8], int ones)
+// Eight consecutive int64 of one row -> nine 8-byte digit words, digit a of
+// element e in byte e of word a, stored at plane a.  Returns the planes that
+// hold a nonzero digit (bit a).
+__device__ __forceinline__ uint32_t split_store(uint8_t *stage, int off, const uint64_t (&v)[8])
 {
+    uint64_t u[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        u[e] = v[e] + kDig;
     uint32_t l0[4], l1[4], h0[4], h1[4];
-    tr4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], l0);
-    tr4((uint32_t)v[4], (uint32_t)v[5], (uint32_t)v[6], (uint32_t)v[7], l1);
-    tr4((uint32_t)(v[0] >> 32), (uint32_t)(v[1] >> 32), (uint32_t)(v[2] >> 32),
-        (uint32_t)(v[3] >> 32), h0);
-    tr4((uint32_t)(v[4] >> 32), (uint32_t)(v[5] >> 32), (uint32_t)(v[6] >> 32),
-        (uint32_t)(v[7] >> 32), h1);
+    tr4((uint32_t)u[0], (uint32_t)u[1], (uint32_t)u[2], (uint32_t)u[3], l0);
+    tr4((uint32_t)u[4], (uint32_t)u[5], (uint32_t)u[6], (uint32_t)u[7], l1);
+    tr4((uint32_t)(u[0] >> 32), (uint32_t)(u[1] >> 32), (uint32_t)(u[2] >> 32),
+        (uint32_t)(u[3] >> 32), h0);
+    tr4((uint32_t)(u[4] >> 32), (uint32_t)(u[5] >> 32), (uint32_t)(u[6] >> 32),
+        (uint32_t)(u[7] >> 32), h1);
+    uint2 d[NPL];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+        d[a] = make_uint2(l0[a] ^ 0x80808080u, l1[a] ^ 0x80808080u);
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+        d[4 + a] = make_uint2(h0[a] ^ 0x80808080u, h1[a] ^ 0x80808080u);
+    d[7] = make_uint2(h0[3], h1[3]);
+    // overflow flags: bit 31 of u's high word set where v's is clear
+    uint32_t f0 = 0, f1 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f0 |= (((uint32_t)(u[e] >> 32) & ~(uint32_t)(v[e] >> 32)) >> 31) << (8 * e);
+        f1 |= (((uint32_t)(u[e + 4] >> 32) & ~(uint32_t)(v[e + 4] >> 32)) >> 31) << (8 * e);
+    }
+    d[8] = make_uint2(f0, f1);
     uint8_t *p = stage + off;
+    uint32_t m = 0;
+#pragma unroll
+    for (int a = 0; a < NPL; ++a) {
+        *reinterpret_cast<uint2 *>(p + a * PLANE) = d[a];
+        m |= ((d[a].x | d[a].y) != 0 ? 1u : 0u) << a;
+    }
+    return m;
+}
+
+// The window pass's split of eight consecutive int64: only planes P0..P1 are
+// stored.  Returns bit 0 when a digit outside P0..P1 is nonzero or a value may
+// have overflowed (v >= 2^63 - C needs v's high word >= 0x7F7F7F7F: tested on
+// that word alone, so a few values below the bound are caught too), and bit 1
+// when plane EXT (-1: none) holds a nonzero digit.
+template <int P0, int P1, int EXT>
+__device__ __forceinline__ uint32_t split_store_win(uint8_t *stage, int off,
+                                                   const uint64_t (&v)[8])
+{
+    uint64_t u[8];
+    bool big = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        u[e] = v[e] + kDig;
+        big |= (int32_t)(uint32_t)(v[e] >> 32) >= 0x7f7f7f7f;
+    }
+    uint32_t l0[4], l1[4], h0[4], h1[4];
+    tr4((uint32_t)u[0], (uint32_t)u[1], (uint32_t)u[2], (uint32_t)u[3], l0);
+    tr4((uint32_t)u[4], (uint32_t)u[5], (uint32_t)u[6], (uint32_t)u[7], l1);
+    tr4((uint32_t)(u[0] >> 32), (uint32_t)(u[1] >> 32), (uint32_t)(u[2] >> 32),
+        (uint32_t)(u[3] >> 32), h0);
+    tr4((uint32_t)(u[4] >> 32), (uint32_t)(u[5] >> 32), (uint32_t)(u[6] >> 32),
+        (uint32_t)(u[7] >> 32), h1);
     uint2 d[8];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -79,17 +139,22 @@ __device__ __forceinline__ void split_store(uint8_t *stage, int off, const uint6
     for (int a = 0; a < 3; ++a)
         d[4 + a] = make_uint2(h0[a] ^ 0x80808080u, h1[a] ^ 0x80808080u);
     d[7] = make_uint2(h0[3], h1[3]);
+    uint8_t *p = stage + off;
+    uint32_t out = 0;
 #pragma unroll
     for (int a = 0; a < 8; ++a) {
-        *reinterpret_cast<uint2 *>(p + a * PLANE) = d[a];
-        if (FUSE) {
-            sum[a] = __builtin_amdgcn_sdot4((int)d[a].x, ones, sum[a], false);
-            sum[a] = __builtin_amdgcn_sdot4((int)d[a].y, ones, sum[a], false);
-        }
+        if (a >= P0 && a <= P1)
+            *reinterpret_cast<uint2 *>(p + a * PLANE) = d[a];
+        else
+            out |= d[a].x | d[a].y;
     }
+    uint32_t r = (out != 0 || big) ? 1u : 0u;
+    if (EXT >= 0)
+        r |= (d[EXT < 0 ? 0 : EXT].x | d[EXT < 0 ? 0 : EXT].y) != 0 ? 2u : 0u;
+    return r;
 }
 
-// Eight elements [k, k + 8) of a row; positions at or past kend read as C
+// Eight elements [k, k + 8) of a row; positions at or past kend read as 0
 // (all digits zero, so they add nothing to any Q_d).
 template <bool VEC, bool TAIL>
 __device__ __forceinline__ void load8(uint64_t (&v)[8], const int64_t *row, int k, int kend)
@@ -106,30 +171,102 @@ __device__ __forceinline__ void load8(uint64_t (&v)[8], const int64_t *row, int 
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             v[e] = (!TAIL || k + e < kend) ? (uint64_t)row[TAIL ? min(k + e, kend - 1) : k + e]
-                                           : kDig;
+                                           : 0;
     }
 }
 
-// One step: for each 32-deep half, the 8 + 8 operand limbs and 63 MFMAs.
-__device__ __forceinline__ void mfma_step(v16i (&acc)[14], const uint8_t *xs,
-                                          const uint8_t *ws, int lane)
+// OR of a 32-bit value over the wave (DPP within rows of 16, then the rows)
+__device__ __forceinline__ uint32_t wave_or(uint32_t v)
 {
+    v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, Q48_DPP_XOR1, 0xf, 0xf, false);
+    v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, Q48_DPP_XOR2, 0xf, 0xf, false);
+    v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, Q48_DPP_HALF_MIRROR, 0xf, 0xf, false);
+    v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, Q48_DPP_MIRROR, 0xf, 0xf, false);
+    return (uint32_t)(__builtin_amdgcn_readlane((int)v, 0) | __builtin_amdgcn_readlane((int)v, 16) |
+                      __builtin_amdgcn_readlane((int)v, 32) | __builtin_amdgcn_readlane((int)v, 48));
+}
+
+// Operand offset of lane l in a 32-row slice of a plane (one 32-deep half)
+__device__ __forceinline__ int opnd_off(int lane) { return (lane >> 5) * 512 + (lane & 31) * 16; }
+
+// The 28 MFMAs of a step whose X digits lie in planes 0..6 and W digits in
+// planes LO..LO + 3.
+template <int LO>
+__device__ __forceinline__ void mfma_window(v16i (&acc)[14], const uint8_t *xs, const uint8_t *ws,
+                                            int lane)
+{
+    static_assert(LO >= 0 && LO + 3 <= 7, "window within planes 0..7");
+    const int off = opnd_off(lane);
+    v4i A[7], B[4];
 #pragma unroll
-    for (int h = 0; h < MK / 32; ++h) {
-        const int off = (2 * h + (lane >> 5)) * 512 + (lane & 31) * 16;
-        v4i A[8], B[8];
+    for (int a = 0; a < 7; ++a)
+        A[a] = *reinterpret_cast<const v4i *>(xs + a * PLANE + off);
 #pragma unroll
-        for (int a = 0; a < 8; ++a) {
-            A[a] = *reinterpret_cast<const v4i *>(xs + a * PLANE + off);
-            B[a] = *reinterpret_cast<const v4i *>(ws + a * PLANE + off);
+    for (int j = 0; j < 4; ++j)
+        B[j] = *reinterpret_cast<const v4i *>(ws + (LO + j) * PLANE + off);
+#pragma unroll
+    for (int a = 0; a < 7; ++a)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[a + LO + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[a], B[j], acc[a + LO + j],
+                                                                    0, 0, 0);
+}
+
+// X planes 0..6 against one more W plane B (B <= 7).
+template <int B>
+__device__ __forceinline__ void mfma_plane_w(v16i (&acc)[14], const uint8_t *xs,
+                                             const uint8_t *ws, int lane)
+{
+    const int off = opnd_off(lane);
+    const v4i Bv = *reinterpret_cast<const v4i *>(ws + B * PLANE + off);
+#pragma unroll
+    for (int a = 0; a < 7; ++a)
+        if (a + B <= 13) {
+            const v4i A = *reinterpret_cast<const v4i *>(xs + a * PLANE + off);
+            acc[a + B] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bv, acc[a + B], 0, 0, 0);
         }
+}
+
+// The 63 MFMAs of planes 0..7 x 0..7 (a + b <= 13).
+__device__ __forceinline__ void mfma_all(v16i (&acc)[14], const uint8_t *xs, const uint8_t *ws,
+                                         int lane)
+{
+    const int off = opnd_off(lane);
+    v4i A[8], B[8];
 #pragma unroll
-        for (int a = 0; a < 8; ++a)
+    for (int a = 0; a < 8; ++a) {
+        A[a] = *reinterpret_cast<const v4i *>(xs + a * PLANE + off);
+        B[a] = *reinterpret_cast<const v4i *>(ws + a * PLANE + off);
+    }
 #pragma unroll
-            for (int b = 0; b < 8; ++b)
-                if (a + b <= 13)
-                    acc[a + b] =
-                        __builtin_amdgcn_mfma_i32_32x32x32_i8(A[a], B[b], acc[a + b], 0, 0, 0);
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+            if (a + b <= 13)
+                acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[a], B[b], acc[a + b], 0, 0, 0);
+}
+
+// The plane-8 pairs: X planes 0..5 with W plane 8 (wide: W overflowed) and X
+// plane 8 with W planes 0..5.
+__device__ __forceinline__ void mfma_plane8(v16i (&acc)[14], const uint8_t *xs,
+                                            const uint8_t *ws, int lane, bool w8, bool x8)
+{
+    const int off = opnd_off(lane);
+    if (w8) {
+        const v4i B8 = *reinterpret_cast<const v4i *>(ws + 8 * PLANE + off);
+#pragma unroll
+        for (int a = 0; a < 6; ++a) {
+            const v4i A = *reinterpret_cast<const v4i *>(xs + a * PLANE + off);
+            acc[a + 8] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B8, acc[a + 8], 0, 0, 0);
+        }
+    }
+    if (x8) {
+        const v4i A8 = *reinterpret_cast<const v4i *>(xs + 8 * PLANE + off);
+#pragma unroll
+        for (int b = 0; b < 6; ++b) {
+            const v4i B = *reinterpret_cast<const v4i *>(ws + b * PLANE + off);
+            acc[b + 8] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A8, B, acc[b + 8], 0, 0, 0);
+        }
     }
 }
 
@@ -148,56 +285,65 @@ __device__ __forceinline__ void tile_of(int b, int nn, int nt, int &n_tile, int 
     t_tile = in / gs;
 }
 
-// grid (ceil(N/64) * ceil(T/64), 1, S): split z covers k-steps [z*spb, (z+1)*spb).
-// FUSE: every block adds the digit corrections of its own k range (the digit
-// sums of its rows, counted while splitting them, and its length times C^2).
-// Otherwise cw[n] = C sum_k W - K C^2 and cx[t] = C sum_k X come from
-// k_digit_corr and are added once: here when S == 1, else by the reduction.
-// S == 1: Y gets the shifted result;
-// S > 1: P[z][t][n] gets the block's int128 partial sum (two uint64, lo first).
-template <bool VEC, bool FUSE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
-k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__restrict__ W,
-          const int64_t *__restrict__ X, const uint64_t *__restrict__ cw,
-          const uint64_t *__restrict__ cx, int T, int N, int K, int spb)
-{
-    __shared__ __align__(16) uint8_t lds[2][2][STAGE];   // [stage][X, W]
-    __shared__ int dsum[2][64][8];                        // [X, W][row][limb] digit sums
-    __shared__ q48_u128 corr[2][64];                      // [X, W][row] corrections
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    int n_tile, t_tile;
-    tile_of(blockIdx.x, (N + MN - 1) / MN, (T + MT - 1) / MT, n_tile, t_tile);
-    const int n0 = n_tile * MN, t0 = t_tile * MT;
-    const int kbeg = blockIdx.z * spb * MK;
-    const int kend = max(kbeg, min(K, kbeg + spb * MK));
-    const int nfull = (kend - kbeg) / MK;
-    const bool tail = (kend - kbeg) % MK != 0;
+// The block's tiles, loaders and accumulators, shared by the kernel's paths.
+struct GemmTile {
+    int64_t *Y;
+    uint64_t *P;
+    int T, N, n0, t0, kbeg, kend, nfull, z, S;
+    bool tail;
+};
 
-    // loader role: pieces tid and tid + 256 of both tiles
-    Piece pc[NPAIR];
-    const int64_t *xrow[NPAIR], *wrow[NPAIR];
+// Block b's tile and k range (split z of S, spb steps each), and the rows it
+// loads: piece tid of both tiles.
+__device__ __forceinline__ GemmTile gemm_tile(int b, int z, int S, int64_t *Y, uint64_t *P,
+                                              const int64_t *W, const int64_t *X, int T, int N,
+                                              int K, int spb, Piece (&pc)[NPAIR],
+                                              const int64_t *(&xrow)[NPAIR],
+                                              const int64_t *(&wrow)[NPAIR])
+{
+    int n_tile, t_tile;
+    tile_of(b, (N + MN - 1) / MN, (T + MT - 1) / MT, n_tile, t_tile);
+    GemmTile g;
+    g.Y = Y;
+    g.P = P;
+    g.T = T;
+    g.N = N;
+    g.n0 = n_tile * MN;
+    g.t0 = t_tile * MT;
+    g.z = z;
+    g.S = S;
+    g.kbeg = z * spb * MK;
+    g.kend = max(g.kbeg, min(K, g.kbeg + spb * MK));
+    g.nfull = (g.kend - g.kbeg) / MK;
+    g.tail = (g.kend - g.kbeg) % MK != 0;
 #pragma unroll
     for (int j = 0; j < NPAIR; ++j) {
-        pc[j] = piece(tid + 256 * j);
-        xrow[j] = X + (size_t)min(t0 + pc[j].r, T - 1) * K + pc[j].k8;
-        wrow[j] = W + (size_t)min(n0 + pc[j].r, N - 1) * K + pc[j].k8;
+        pc[j] = piece((int)threadIdx.x + 256 * j);
+        xrow[j] = X + (size_t)min(g.t0 + pc[j].r, T - 1) * K + pc[j].k8;
+        wrow[j] = W + (size_t)min(g.n0 + pc[j].r, N - 1) * K + pc[j].k8;
     }
+    return g;
+}
 
+// One pass of the block's k range.  LO >= 0: X planes 0..6 against W planes
+// LO..LO + 3, plus W plane LO - 1 in the steps whose tile holds it; a step
+// with digits elsewhere returns false before anything is written (the caller
+// then runs LO = -1).  LO = -1: every pair, never fails.  On success the
+// block's outputs are written.
+template <int LO, bool VEC>
+__device__ __forceinline__ bool gemm_pass(const GemmTile &g, uint8_t (&lds)[2][2][STAGE],
+                                          uint32_t (&pm)[2][4], const int64_t *const (&xrow)[NPAIR],
+                                          const int64_t *const (&wrow)[NPAIR],
+                                          const Piece (&pc)[NPAIR])
+{
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wt = w >> 1, wn = w & 1;   // wave's token slice, row slice
+    const int kbeg = g.kbeg, kend = g.kend, nfull = g.nfull;
     v16i acc[14];
 #pragma unroll
     for (int d = 0; d < 14; ++d)
         acc[d] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    for (int i = tid; i < 2 * 64 * 8; i += 256)
-        (&dsum[0][0][0])[i] = 0;
-    int sx[NPAIR][8], sw[NPAIR][8];
-#pragma unroll
-    for (int j = 0; j < NPAIR; ++j)
-#pragma unroll
-        for (int a = 0; a < 8; ++a)
-            sx[j][a] = sw[j][a] = 0;
-    constexpr int ONES = 0x01010101;
 
-    const int wt = w >> 1, wn = w & 1;   // wave's token slice, row slice
     typedef uint64_t Regs[NPAIR][8];
     auto load = [&](Regs &gx, Regs &gw, int k) {
 #pragma unroll
@@ -206,11 +352,74 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
             load8<VEC, false>(gw[j], wrow[j], k, kend);
         }
     };
-    auto store = [&](int st, const Regs &gx, const Regs &gw, int ones) {
+    // split a step's tiles into stage st and publish the wave's plane masks
+    // W planes a window pass stores and takes: LO - 1 .. LO + 3
+    constexpr int WP0 = LO > 0 ? LO - 1 : 0, WP1 = LO + 3, WEXT = LO > 0 ? LO - 1 : -1;
+    // split a step's tiles into stage st and publish the wave's plane masks:
+    // every plane's (X in bits 0..8, W in 9..17) for the full pass; for a
+    // window pass bit 0 = a digit outside the window, bit 1 = W plane LO - 1
+    auto store = [&](int st, const Regs &gx, const Regs &gw) {
+        uint32_t m;
+        if constexpr (LO >= 0) {
+            uint32_t r = 0;
 #pragma unroll
-        for (int j = 0; j < NPAIR; ++j) {
-            split_store<FUSE>(lds[st][0], pc[j].off, gx[j], sx[j], ones);
-            split_store<FUSE>(lds[st][1], pc[j].off, gw[j], sw[j], ones);
+            for (int j = 0; j < NPAIR; ++j)
+                r |= split_store_win<0, 6, -1>(lds[st][0], pc[j].off, gx[j]) |
+                     split_store_win<WP0, WP1, WEXT>(lds[st][1], pc[j].off, gw[j]);
+            m = (__builtin_amdgcn_ballot_w64((r & 1u) != 0) != 0 ? 1u : 0u) |
+                (__builtin_amdgcn_ballot_w64((r & 2u) != 0) != 0 ? 2u : 0u);
+        } else {
+            uint32_t mx = 0, mw = 0;
+#pragma unroll
+            for (int j = 0; j < NPAIR; ++j) {
+                mx |= split_store(lds[st][0], pc[j].off, gx[j]);
+                mw |= split_store(lds[st][1], pc[j].off, gw[j]);
+            }
+            m = wave_or(mx | (mw << 9));
+        }
+        if (lane == 0)
+            pm[st][w] = m;
+    };
+    // the stage's masks (uniform over the block)
+    auto planes = [&](int st) {
+        const uint32_t m = pm[st][0] | pm[st][1] | pm[st][2] | pm[st][3];
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)m);
+    };
+    bool ok = true;
+    // MFMAs of stage st with the split of the next step interleaved (its data
+    // arrived a step ago); the last step splits a clamped re-read, never used
+    auto multiply = [&](int st, bool split_next, const Regs &cx_, const Regs &cw_) {
+        const uint8_t *xs = &lds[st][0][0] + wt * SLICE, *ws = &lds[st][1][0] + wn * SLICE;
+        const uint32_t m = planes(st);
+        if constexpr (LO >= 0) {
+            if (m & 1u) {
+                ok = false;
+                return;
+            }
+            mfma_window<LO < 0 ? 0 : LO>(acc, xs, ws, lane);
+            if (split_next)
+                store(st ^ 1, cx_, cw_);
+            __builtin_amdgcn_sched_group_barrier(0x100, 11, 0);
+#pragma unroll
+            for (int i = 0; i < 28; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+            }
+            if (LO > 0 && (m & 2u))
+                mfma_plane_w<LO < 1 ? 0 : LO - 1>(acc, xs, ws, lane);
+        } else {
+            const uint32_t mx = m & 0x1ffu, mw = m >> 9;
+            mfma_all(acc, xs, ws, lane);
+            if (split_next)
+                store(st ^ 1, cx_, cw_);
+            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+#pragma unroll
+            for (int i = 0; i < 63; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
+            if ((mw | mx) & 0x100u)
+                mfma_plane8(acc, xs, ws, lane, (mw & 0x100u) != 0, (mx & 0x100u) != 0);
         }
     };
     // Steps go two ahead: step s multiplies stage s & 1, splits step s + 1
@@ -218,157 +427,163 @@ k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int64_t *__re
     // Register sets alternate: step s loads into set s & 1.
     Regs gx0, gw0, gx1, gw1;
     const int last = max(nfull - 1, 0);
+    __syncthreads();   // the stages and masks of an earlier pass are consumed
     if (nfull > 0) {
         load(gx0, gw0, kbeg);
         load(gx1, gw1, kbeg + min(1, last) * MK);
-        store(0, gx0, gw0, ONES);
+        store(0, gx0, gw0);
     }
     __syncthreads();
     auto step = [&](int s, Regs &lx, Regs &lw, const Regs &cx_, const Regs &cw_) {
         // step s + 2's tiles (clamped to the last step: in bounds, unused)
         load(lx, lw, kbeg + min(s + 2, last) * MK);
         __builtin_amdgcn_sched_barrier(0);
-        const uint8_t *st = &lds[s & 1][0][0];
-        mfma_step(acc, st + wt * SLICE, st + STAGE + wn * SLICE, lane);
-        // the last step splits a clamped re-read: stored, never used, not summed
-        store((s + 1) & 1, cx_, cw_, s + 1 < nfull ? ONES : 0);
-        // operand reads first, then the MFMAs with the digit split of the
-        // next step interleaved (its data arrived a step ago)
-#pragma unroll
-        for (int h = 0; h < MK / 32; ++h) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-#pragma unroll
-            for (int i = 0; i < 63; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 2 / (MK / 32), 0);
-            }
-        }
+        multiply(s & 1, true, cx_, cw_);
         __syncthreads();
     };
-    // pairs with no branch inside, so the loads stay where they are issued
+    // pairs with no branch inside the loop body's loads; a failed step is
+    // seen by the whole block (the masks are uniform), which leaves together
     int s = 0;
-    for (; s + 1 < nfull; s += 2) {
+    for (; ok && s + 1 < nfull; s += 2) {
         step(s, gx0, gw0, gx1, gw1);
-        step(s + 1, gx1, gw1, gx0, gw0);
+        if (ok)
+            step(s + 1, gx1, gw1, gx0, gw0);
     }
-    if (s < nfull)
+    if (ok && s < nfull)
         step(s, gx0, gw0, gx1, gw1);
-    if (tail) {
+    if (ok && g.tail) {
         const int kt = kbeg + nfull * MK;
 #pragma unroll
         for (int j = 0; j < NPAIR; ++j) {
             load8<VEC, true>(gx0[j], xrow[j], kt, kend - pc[j].k8);
             load8<VEC, true>(gw0[j], wrow[j], kt, kend - pc[j].k8);
         }
-        store(nfull & 1, gx0, gw0, ONES);
+        store(nfull & 1, gx0, gw0);
         __syncthreads();
-        const uint8_t *st = &lds[nfull & 1][0][0];
-        mfma_step(acc, st + wt * SLICE, st + STAGE + wn * SLICE, lane);
+        multiply(nfull & 1, false, gx0, gw0);
     }
-
-    // Digit corrections of this k range: per row, C * sum_k S(v) =
-    // C * sum_a 256^a (digit sum of limb a); W rows also carry len * C^2.
-    if (FUSE) {
-#pragma unroll
-        for (int j = 0; j < NPAIR; ++j)
-#pragma unroll
-            for (int a = 0; a < 8; ++a) {
-                atomicAdd(&dsum[0][pc[j].r][a], sx[j][a]);
-                atomicAdd(&dsum[1][pc[j].r][a], sw[j][a]);
-            }
-    }
-    __syncthreads();
-    if (FUSE && tid < 128) {
-        const int op = tid >> 6, row = tid & 63;
-        q48_u128 sum = 0;
-#pragma unroll
-        for (int a = 7; a >= 0; --a)
-            sum = (sum << 8) + (q48_u128)(q48_i128)dsum[op][row][a];
-        q48_u128 v = sum * kDig;
-        if (op == 1)
-            v += (q48_u128)kDig * kDig * (q48_u128)(uint64_t)(kend - kbeg);
-        corr[op][row] = v;
-    }
-    __syncthreads();
+    if (!ok)
+        return false;
 
     // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32
-    const int nl = 32 * wn + (lane & 31), n = n0 + nl;
-    if (n >= N)
-        return;
-    q48_u128 cwn = 0;
-    if (FUSE)
-        cwn = corr[1][nl];
-    else if (gridDim.z == 1)
-        cwn = ((q48_u128)cw[2 * n + 1] << 64) | cw[2 * n];
+    const int nl = 32 * wn + (lane & 31), n = g.n0 + nl;
+    if (n >= g.N)
+        return true;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const int tl = 32 * wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3), t = t0 + tl;
-        if (t >= T)
+        const int tl = 32 * wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3), t = g.t0 + tl;
+        if (t >= g.T)
             continue;
         q48_u128 tot = 0;
 #pragma unroll
         for (int d = 13; d >= 0; --d)
             tot = (tot << 8) + (q48_u128)(q48_i128)acc[d][i];
-        if (FUSE)
-            tot += cwn + corr[0][tl];
-        else if (gridDim.z == 1)
-            tot += cwn + (((q48_u128)cx[2 * t + 1] << 64) | cx[2 * t]);
-        if (gridDim.z == 1) {
-            Y[(size_t)t * N + n] = (int64_t)((q48_i128)tot >> 48);
+        if (g.S == 1) {
+            g.Y[(size_t)t * g.N + n] = (int64_t)((q48_i128)tot >> 48);
         } else {
-            uint64_t *p = P + 2 * (((size_t)blockIdx.z * T + t) * N + n);
+            uint64_t *p = g.P + 2 * (((size_t)g.z * g.T + t) * g.N + n);
             *reinterpret_cast<ulonglong2 *>(p) = make_ulonglong2((uint64_t)tot,
                                                                  (uint64_t)(tot >> 64));
         }
     }
+    return true;
 }
 
-// Y[t][n] = (sum_z P[z][t][n] (+ cw[n] + cx[t] when given)) >> 48
+// grid (ceil(N/64) * ceil(T/64), 1, S): split z covers k-steps [z*spb, (z+1)*spb).
+// S == 1: Y gets the shifted result;
+// S > 1: P[z][t][n] gets the block's int128 partial sum (two uint64, lo first).
+// The window of W planes comes from the block's first W tile (its top plane
+// h gives LO = h - 3, clamped to 0..4: small weights reach lower planes, the
+// largest magnitudes set the top).  A block whose tiles leave the window
+// writes nothing and sets redo[block] (else clears it) for k_gemm_i8_full.
+template <bool VEC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+k_gemm_i8(int64_t *__restrict__ Y, uint64_t *__restrict__ P, int *__restrict__ redo,
+          const int64_t *__restrict__ W, const int64_t *__restrict__ X, int T, int N, int K,
+          int spb)
+{
+    __shared__ __align__(16) uint8_t lds[2][2][STAGE];   // [stage][X, W]
+    __shared__ uint32_t pm[2][4];                         // [stage][wave]: planes, X | W << 9
+    const int tid = threadIdx.x;
+    Piece pc[NPAIR];
+    const int64_t *xrow[NPAIR], *wrow[NPAIR];
+    const GemmTile g = gemm_tile(blockIdx.x, blockIdx.z, gridDim.z, Y, P, W, X, T, N, K, spb,
+                                 pc, xrow, wrow);
+
+    // the first W tile's planes (every digit of the block's first step)
+    uint32_t mw = 0;
+    if (g.kend > g.kbeg) {
+#pragma unroll
+        for (int j = 0; j < NPAIR; ++j) {
+            uint64_t v[8];
+            if (g.nfull > 0)
+                load8<VEC, false>(v, wrow[j], g.kbeg, g.kend);
+            else
+                load8<VEC, true>(v, wrow[j], g.kbeg, g.kend - pc[j].k8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint64_t u = v[e] + kDig, dz = u ^ kDig;   // digits 0..6: bytes of dz
+#pragma unroll
+                for (int a = 0; a < 7; ++a)
+                    mw |= ((dz >> (8 * a)) & 0xffu) != 0 ? 1u << a : 0u;
+                mw |= (u >> 56) != 0 ? 1u << 7 : 0u;
+            }
+        }
+    }
+    mw = wave_or(mw);
+    if ((tid & 63) == 0)
+        pm[0][tid >> 6] = mw;
+    __syncthreads();
+    mw = (uint32_t)__builtin_amdgcn_readfirstlane((int)(pm[0][0] | pm[0][1] | pm[0][2] | pm[0][3]));
+    const int h = mw ? 31 - __builtin_clz(mw) : 3;
+    const int lo = min(max(h - 3, 0), 4);
+    bool done;
+    switch (lo) {
+    case 0: done = gemm_pass<0, VEC>(g, lds, pm, xrow, wrow, pc); break;
+    case 1: done = gemm_pass<1, VEC>(g, lds, pm, xrow, wrow, pc); break;
+    case 2: done = gemm_pass<2, VEC>(g, lds, pm, xrow, wrow, pc); break;
+    case 3: done = gemm_pass<3, VEC>(g, lds, pm, xrow, wrow, pc); break;
+    default: done = gemm_pass<4, VEC>(g, lds, pm, xrow, wrow, pc); break;
+    }
+    if (tid == 0)
+        redo[blockIdx.z * gridDim.x + blockIdx.x] = done ? 0 : 1;
+}
+
+// Every pair for the blocks k_gemm_i8 left (redo set), nb blocks of S splits:
+// block b of this grid takes blocks b, b + gridDim.x, ... of that grid.
+template <bool VEC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+k_gemm_i8_full(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int *__restrict__ redo,
+               const int64_t *__restrict__ W, const int64_t *__restrict__ X, int T, int N,
+               int K, int spb, int nb, int S)
+{
+    __shared__ __align__(16) uint8_t lds[2][2][STAGE];
+    __shared__ uint32_t pm[2][4];
+    for (int i = blockIdx.x; i < nb * S; i += gridDim.x) {
+        if (!redo[i])
+            continue;   // uniform over the block
+        Piece pc[NPAIR];
+        const int64_t *xrow[NPAIR], *wrow[NPAIR];
+        const GemmTile g = gemm_tile(i % nb, i / nb, S, Y, P, W, X, T, N, K, spb, pc, xrow, wrow);
+        gemm_pass<-1, VEC>(g, lds, pm, xrow, wrow, pc);
+    }
+}
+
+// Y[t][n] = (sum_z P[z][t][n]) >> 48
 __global__ __launch_bounds__(256) void k_gemm_i8_reduce(int64_t *__restrict__ Y,
-                                                       const uint64_t *__restrict__ P,
-                                                       const uint64_t *__restrict__ cw,
-                                                       const uint64_t *__restrict__ cx,
-                                                       int T, int N, int S)
+                                                       const uint64_t *__restrict__ P, int T,
+                                                       int N, int S)
 {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (size_t)T * N)
         return;
     q48_u128 tot = 0;
-    if (cw) {
-        const int t = (int)(i / N), n = (int)(i % N);
-        tot = (((q48_u128)cw[2 * n + 1] << 64) | cw[2 * n]) +
-              (((q48_u128)cx[2 * t + 1] << 64) | cx[2 * t]);
-    }
     for (int z = 0; z < S; ++z) {
         const ulonglong2 u =
             *reinterpret_cast<const ulonglong2 *>(P + 2 * ((size_t)z * T * N + i));
         tot += ((q48_u128)u.y << 64) | u.x;
     }
     Y[i] = (int64_t)((q48_i128)tot >> 48);
-}
-
-// out[row] = C * sum_k A[row][k] (exact int128, mod 2^128), minus K C^2 when
-// sub_kc2: the digit corrections of the identity above.  One wave per row.
-__global__ __launch_bounds__(256) void k_digit_corr(uint64_t *__restrict__ out,
-                                                   const int64_t *__restrict__ A, int rows,
-                                                   int K, int sub_kc2)
-{
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows)
-        return;
-    const int64_t *p = A + (size_t)row * K;
-    q48_i128 s = 0;
-    for (int k = lane; k < K; k += 64)
-        s += p[k];
-    s = (q48_i128)q48_wave_sum128((q48_u128)s);
-    if (lane == 0) {
-        q48_u128 v = (q48_u128)s * kDig;
-        if (sub_kc2)
-            v -= (q48_u128)kDig * kDig * (q48_u128)(uint64_t)K;
-        out[2 * row] = (uint64_t)v;
-        out[2 * row + 1] = (uint64_t)(v >> 64);
-    }
 }
 
 } // namespace
@@ -402,50 +617,33 @@ int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *
     const int S = q48_gemm_i8_splits(T, N, K, c->cu_count);
     const int steps = (K + MK - 1) / MK;
     const int spb = (steps + S - 1) / S;
-    // short token counts count the digit sums inside the GEMM (W is read
-    // once); long ones amortise a separate pass over W and X, which keeps
-    // 32 v_dot4 per step out of the MFMA loop
-    const bool fuse = T < FUSE_BELOW_T;
-    const size_t corr = fuse ? 0 : 16 * ((size_t)N + (size_t)T);
+    const int nb = ((N + MN - 1) / MN) * ((T + MT - 1) / MT);
+    // workspace: the blocks' redo flags, then (S > 1) the int128 partials
+    const size_t flags = ((size_t)nb * S * sizeof(int) + 255) & ~(size_t)255;
     const size_t part = S > 1 ? 16 * (size_t)S * T * N : 0;
-    uint64_t *cw = nullptr, *cx = nullptr, *P = nullptr;
-    if (corr + part) {
-        int rc = q48_ws_reserve(c, corr + part);
-        if (rc)
-            return rc;
-        uint64_t *ws = (uint64_t *)c->ws;
-        if (!fuse) {
-            cw = ws;
-            cx = cw + 2 * (size_t)N;
-            ws = cx + 2 * (size_t)T;
-        }
-        if (S > 1)
-            P = ws;
-        if (!fuse) {
-            hipLaunchKernelGGL(k_digit_corr, dim3((N + 3) / 4), dim3(256), 0, c->stream, cw, W,
-                               N, K, 1);
-            hipLaunchKernelGGL(k_digit_corr, dim3((T + 3) / 4), dim3(256), 0, c->stream, cx, X,
-                               T, K, 0);
-        }
-    }
-    const dim3 grid(((N + MN - 1) / MN) * ((T + MT - 1) / MT), 1, S);
+    int rc = q48_ws_reserve(c, flags + part);
+    if (rc)
+        return rc;
+    int *redo = (int *)c->ws;
+    uint64_t *P = S > 1 ? (uint64_t *)((char *)c->ws + flags) : nullptr;
+    const dim3 grid(nb, 1, S);
+    const int fgrid = min(nb * S, c->cu_count);
     const bool vec = K % 2 == 0 && (((uintptr_t)W | (uintptr_t)X) & 15) == 0;
-#define GEMM_I8_LAUNCH(V, F)                                                                 \
-    hipLaunchKernelGGL((k_gemm_i8<V, F>), grid, dim3(256), 0, c->stream, Y, P, W, X, cw, cx, T, \
-                       N, K, spb)
-    if (vec && fuse)
-        GEMM_I8_LAUNCH(true, true);
-    else if (vec)
-        GEMM_I8_LAUNCH(true, false);
-    else if (fuse)
-        GEMM_I8_LAUNCH(false, true);
-    else
-        GEMM_I8_LAUNCH(false, false);
-#undef GEMM_I8_LAUNCH
+    if (vec) {
+        hipLaunchKernelGGL((k_gemm_i8<true>), grid, dim3(256), 0, c->stream, Y, P, redo, W, X, T,
+                           N, K, spb);
+        hipLaunchKernelGGL((k_gemm_i8_full<true>), dim3(fgrid), dim3(256), 0, c->stream, Y, P,
+                           redo, W, X, T, N, K, spb, nb, S);
+    } else {
+        hipLaunchKernelGGL((k_gemm_i8<false>), grid, dim3(256), 0, c->stream, Y, P, redo, W, X,
+                           T, N, K, spb);
+        hipLaunchKernelGGL((k_gemm_i8_full<false>), dim3(fgrid), dim3(256), 0, c->stream, Y, P,
+                           redo, W, X, T, N, K, spb, nb, S);
+    }
     if (S > 1) {
         const size_t tn = (size_t)T * N;
         hipLaunchKernelGGL(k_gemm_i8_reduce, dim3((unsigned)((tn + 255) / 256)), dim3(256), 0,
-                           c->stream, Y, P, cw, cx, T, N, S);
+                           c->stream, Y, P, T, N, S);
     }
     return (int)hipGetLastError();
 }
