@@ -392,10 +392,9 @@ __device__ __forceinline__ bool gemm_pass(const GemmTile &g, uint8_t (&lds)[2][2
         const uint8_t *xs = &lds[st][0][0] + wt * SLICE, *ws = &lds[st][1][0] + wn * SLICE;
         const uint32_t m = planes(st);
         if constexpr (LO >= 0) {
-            if (m & 1u) {
-                ok = false;
-                return;
-            }
+            // a step outside the window still runs (its products are
+            // discarded with the pass), so the loop body has no exit
+            ok &= (m & 1u) == 0;
             mfma_window<LO < 0 ? 0 : LO>(acc, xs, ws, lane);
             if (split_next)
                 store(st ^ 1, cx_, cw_);
@@ -425,32 +424,50 @@ __device__ __forceinline__ bool gemm_pass(const GemmTile &g, uint8_t (&lds)[2][2
     // Steps go two ahead: step s multiplies stage s & 1, splits step s + 1
     // (loaded during step s - 1) into the other stage and loads step s + 2.
     // Register sets alternate: step s loads into set s & 1.
-    Regs gx0, gw0, gx1, gw1;
+    // The window pass loads three steps ahead (register sets rotating by
+    // step), so a step's tiles have two steps to arrive; the full pass, at
+    // the register limit, two.
+    constexpr int AHEAD = LO >= 0 ? 3 : 2;
+    Regs gx0, gw0, gx1, gw1, gx2, gw2;
     const int last = max(nfull - 1, 0);
     __syncthreads();   // the stages and masks of an earlier pass are consumed
     if (nfull > 0) {
         load(gx0, gw0, kbeg);
         load(gx1, gw1, kbeg + min(1, last) * MK);
+        if (AHEAD == 3)
+            load(gx2, gw2, kbeg + min(2, last) * MK);
         store(0, gx0, gw0);
     }
     __syncthreads();
     auto step = [&](int s, Regs &lx, Regs &lw, const Regs &cx_, const Regs &cw_) {
-        // step s + 2's tiles (clamped to the last step: in bounds, unused)
-        load(lx, lw, kbeg + min(s + 2, last) * MK);
+        // step s + AHEAD's tiles (clamped to the last step: in bounds, unused)
+        load(lx, lw, kbeg + min(s + AHEAD, last) * MK);
         __builtin_amdgcn_sched_barrier(0);
         multiply(s & 1, true, cx_, cw_);
         __syncthreads();
     };
-    // pairs with no branch inside the loop body's loads; a failed step is
+    // groups with no branch inside the loop body's loads; a failed step is
     // seen by the whole block (the masks are uniform), which leaves together
     int s = 0;
-    for (; ok && s + 1 < nfull; s += 2) {
-        step(s, gx0, gw0, gx1, gw1);
-        if (ok)
-            step(s + 1, gx1, gw1, gx0, gw0);
+    if constexpr (AHEAD == 3) {
+        for (; ok && s + 2 < nfull; s += 3) {
+            step(s, gx0, gw0, gx1, gw1);
+            step(s + 1, gx1, gw1, gx2, gw2);
+            step(s + 2, gx2, gw2, gx0, gw0);
+        }
+        if (ok && s < nfull)
+            step(s, gx0, gw0, gx1, gw1);
+        if (ok && s + 1 < nfull)
+            step(s + 1, gx1, gw1, gx2, gw2);
+    } else {
+        for (; ok && s + 1 < nfull; s += 2) {
+            step(s, gx0, gw0, gx1, gw1);
+            if (ok)
+                step(s + 1, gx1, gw1, gx0, gw0);
+        }
+        if (ok && s < nfull)
+            step(s, gx0, gw0, gx1, gw1);
     }
-    if (ok && s < nfull)
-        step(s, gx0, gw0, gx1, gw1);
     if (ok && g.tail) {
         const int kt = kbeg + nfull * MK;
 #pragma unroll
