@@ -307,8 +307,9 @@ def test_gemm_random_vs_oracle(ctx, oracle, T, N, K, kernel):
     """Full-range int64 operands.  The cases cover partial tiles, a k tail
     (K not a multiple of 32), odd K (8-byte loads), K split across blocks
     (64x64x8192: one tile, many splits), K past one int32 accumulation run of
-    the int8 kernel (20000), and T >= 1024, where the int8 kernel takes its
-    digit corrections from a separate pass (alone and with K splits)."""
+    the int8 kernel (20000), and T >= 1024 (alone and with K splits).  Full-range
+    operands leave the int8 kernel's digit window in the first step, so these
+    run its every-pair pass."""
     rng = np.random.default_rng(T * 31 + N * 7 + K)
     W = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=N * K, dtype=np.int64)
     X = rng.integers(spec.INT64_MIN, spec.INT64_MAX, size=T * K, dtype=np.int64)
@@ -318,6 +319,63 @@ def test_gemm_random_vs_oracle(ctx, oracle, T, N, K, kernel):
     say("gemm", T, N, K, "kernel", kernel)
     ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K, kernel)
     assert np.array_equal(dY.download(), want)
+    for b in (dW, dX, dY):
+        b.free()
+
+
+def _bf16ish(rng, n, scale):
+    """Values with 8 significant bits around `scale` (a bfloat16 weight in
+    Q16.48), both signs, and a few zeros."""
+    m = rng.integers(128, 256, size=n).astype(np.int64)
+    e = rng.integers(-6, 1, size=n)
+    v = np.array([int(a) << max(0, int(scale) + int(b) - 7) for a, b in zip(m, e)], dtype=np.int64)
+    v *= rng.choice([-1, 1], size=n)
+    v[rng.random(n) < 0.01] = 0
+    return v
+
+
+@pytest.mark.parametrize("case", ["plain", "ext", "late_w", "late_x", "big_w", "ovf_w",
+                                  "lo0", "lo4", "zero_w", "split"])
+def test_gemm_digit_windows(ctx, oracle, case):
+    """The int8 GEMM's digit-plane window (X digits 0..6 against four W
+    planes chosen from the block's first W tile, plus the plane below in the
+    steps that reach it; blocks leaving it redone with every pair) against the
+    oracle: weights with 8 significant bits (bfloat16-like) and activations
+    below 2^55, a W plane below the window in one step ("ext"), a step late
+    in K whose W or X digits leave the window ("late_w", "late_x"), W values
+    at the high-word bound that is treated as a possible overflow ("big_w")
+    and values that do overflow v + C ("ovf_w"), windows at both ends of the
+    plane range ("lo0", "lo4"), an all-zero W tile, and K split across blocks
+    with some splits redone ("split")."""
+    rng = np.random.default_rng(sum(map(ord, case)))
+    T, N, K = (64, 64, 8192) if case == "split" else (96, 130, 1000)
+    scale = {"lo0": 27, "lo4": 58}.get(case, 42)
+    W = _bf16ish(rng, N * K, scale)
+    X = rng.integers(-(1 << 52), 1 << 52, size=T * K, dtype=np.int64)
+    if case == "ext":
+        W[5 * K + 100] = 3 << 10            # digit 1, below a window of planes 2..5
+    elif case == "late_w":
+        W[7 * K + 900] = 1 << 60            # plane 7 in the 29th step
+    elif case == "late_x":
+        X[3 * K + 950] = -(1 << 58)
+    elif case == "big_w":
+        W[2 * K + 40] = 0x7F7F7F7F00000000  # high word at the bound, no overflow
+    elif case == "ovf_w":
+        W[K + 17] = spec.INT64_MAX
+        W[9 * K + 500] = 0x7F7F7F7F7F7F7F80  # 2^63 - C: the first value that overflows
+        X[11 * K + 500] = 0x7F7F7F7F7F7F7F90
+    elif case == "zero_w":
+        W[:64 * K] = 0
+    elif case == "split":
+        W[30 * K + 7000] = -(1 << 62)        # one k range of one row tile leaves the window
+    want = np.empty(T * N, dtype=np.int64)
+    oracle.q48o_gemm(want.ctypes.data, W.ctypes.data, X.ctypes.data, T, N, K)
+    dW, dX, dY = ctx.to_device(W), ctx.to_device(X), ctx.buffer(T * N)
+    say("gemm window", case, T, N, K)
+    ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K, intllm.GEMM_I8)
+    got = dY.download()
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, (case, bad[:5])
     for b in (dW, dX, dY):
         b.free()
 
