@@ -576,13 +576,28 @@ k_gemm_i8_full(int64_t *__restrict__ Y, uint64_t *__restrict__ P, const int *__r
 {
     __shared__ __align__(16) uint8_t lds[2][2][STAGE];
     __shared__ uint32_t pm[2][4];
-    for (int i = blockIdx.x; i < nb * S; i += gridDim.x) {
-        if (!redo[i])
-            continue;   // uniform over the block
-        Piece pc[NPAIR];
-        const int64_t *xrow[NPAIR], *wrow[NPAIR];
-        const GemmTile g = gemm_tile(i % nb, i / nb, S, Y, P, W, X, T, N, K, spb, pc, xrow, wrow);
-        gemm_pass<-1, VEC>(g, lds, pm, xrow, wrow, pc);
+    __shared__ int list[256], cnt;
+    // the block's candidates i = blockIdx.x + c gridDim.x, 256 flags read at
+    // once (one memory round trip when nothing is to be redone)
+    const int tid = threadIdx.x, per = (nb * S - (int)blockIdx.x + gridDim.x - 1) / gridDim.x;
+    for (int c0 = 0; c0 < per; c0 += 256) {
+        if (tid == 0)
+            cnt = 0;
+        __syncthreads();
+        const int i = (int)blockIdx.x + (c0 + tid) * (int)gridDim.x;
+        if (c0 + tid < per && redo[i])
+            list[atomicAdd(&cnt, 1)] = i;
+        __syncthreads();
+        const int n = cnt;
+        for (int l = 0; l < n; ++l) {
+            const int b = list[l];
+            Piece pc[NPAIR];
+            const int64_t *xrow[NPAIR], *wrow[NPAIR];
+            const GemmTile g =
+                gemm_tile(b % nb, b / nb, S, Y, P, W, X, T, N, K, spb, pc, xrow, wrow);
+            gemm_pass<-1, VEC>(g, lds, pm, xrow, wrow, pc);
+        }
+        __syncthreads();   // list and cnt reused
     }
 }
 
