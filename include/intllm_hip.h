@@ -368,6 +368,11 @@ int q48_argmax_step(q48_ctx *ctx, const int64_t *v, int n, int *d_tokens, int ca
  * state's number of tokens chosen so far; enqueue it before the step's
  * q48_argmax_step or q48_sample_step. */
 int q48_record_step(q48_ctx *ctx, const int64_t *v, int n, int64_t *rec, int cap);
+/* q48_record_step (into rec, rec_cap) followed by q48_argmax_step, as one
+ * launch: the same record and the same token.  No reference counterpart
+ * (as q48_record_step). */
+int q48_argmax_record_step(q48_ctx *ctx, const int64_t *v, int n, int *d_tokens, int cap,
+                           int64_t *rec, int rec_cap);
 
 
 /* ---- batched prefill ------------------------------------------------------ */

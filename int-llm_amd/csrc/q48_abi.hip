@@ -144,6 +144,7 @@ int q48_ctx_create(q48_ctx **out, int device)
     if (hipMalloc(&c->consts, sizeof(q48_consts)) != hipSuccess ||
         hipMalloc(&c->d_scalar, 64 * sizeof(int)) != hipSuccess ||
         hipMalloc(&c->d_step, 4 * sizeof(int)) != hipSuccess ||
+        hipMalloc(&c->amax_part, q48_amax_part_bytes()) != hipSuccess ||
         hipMalloc(&c->rms_count, 512 * sizeof(int)) != hipSuccess ||
         hipMalloc(&c->attx_sync, q48_attn_sync_bytes()) != hipSuccess) {
         q48_ctx_destroy(c);
@@ -158,6 +159,8 @@ int q48_ctx_create(q48_ctx **out, int device)
         rc = launch_rc(q48_launch_step_set(c, 0, 0));
     if (rc == Q48_OK)
         rc = launch_rc(q48_launch_zero(c, c->rms_count, 512 * sizeof(int)));
+    if (rc == Q48_OK)
+        rc = launch_rc(q48_launch_zero(c, c->amax_part, q48_amax_part_bytes()));
     if (rc == Q48_OK)
         rc = launch_rc(q48_launch_zero(c, c->d_scalar, 64 * sizeof(int)));
     if (rc == Q48_OK)
@@ -182,6 +185,7 @@ int q48_ctx_destroy(q48_ctx *c)
     (void)hipFree(c->ws);
     (void)hipFree(c->d_scalar);
     (void)hipFree(c->d_step);
+    (void)hipFree(c->amax_part);
     (void)hipFree(c->rms_count);
     (void)hipFree(c->rms_part);
     (void)hipFree(c->smp);
@@ -1046,7 +1050,15 @@ int q48_argmax_step(q48_ctx *c, const int64_t *v, int n, int *d_tokens, int cap)
 {
     if (!c || !v || n <= 0 || cap < 0 || (cap > 0 && !d_tokens))
         return Q48_EINVAL;
-    return launch_rc(q48_launch_step_argmax(c, d_tokens, cap, v, n));
+    return launch_rc(q48_launch_step_argmax(c, d_tokens, cap, v, n, nullptr, 0));
+}
+
+int q48_argmax_record_step(q48_ctx *c, const int64_t *v, int n, int *d_tokens, int cap,
+                           int64_t *rec, int rec_cap)
+{
+    if (!c || !v || n <= 0 || cap < 0 || (cap > 0 && !d_tokens) || !rec || rec_cap <= 0)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_step_argmax(c, d_tokens, cap, v, n, rec, rec_cap));
 }
 
 int q48_record_step(q48_ctx *c, const int64_t *v, int n, int64_t *rec, int cap)

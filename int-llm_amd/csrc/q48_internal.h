@@ -21,6 +21,8 @@ struct q48_ctx {
     size_t ws_bytes;
     int *d_scalar;               // device: small int outputs (argmax)
     int *d_step;                 // device: decode-step state {token, pos, count}
+    uint64_t *amax_part;         // device: q48_argmax_step's per-block (max, index) partials,
+                                 // then its ticket (back to 0 after use); zeroed at creation
     int step_mode;               // ops read token / pos from d_step
     void *tmp;                   // device temporaries of the unfused fallbacks
     size_t tmp_bytes;
@@ -171,7 +173,9 @@ size_t q48_attn_sync_bytes();
 int q48_scratch_init(q48_ctx *c);
 size_t q48_scratch_bytes();
 int q48_launch_step_set(q48_ctx *c, int token, int pos);
-int q48_launch_step_argmax(q48_ctx *c, int *tokens, int cap, const int64_t *v, int n);
+int q48_launch_step_argmax(q48_ctx *c, int *tokens, int cap, const int64_t *v, int n,
+                           int64_t *rec, int rec_cap);
+size_t q48_amax_part_bytes();
 int q48_launch_step_record(q48_ctx *c, int64_t *rec, int cap, const int64_t *v, int n);
 int q48_launch_silu_mul_pairs(q48_ctx *c, int64_t *out, const int64_t *t, int n);
 int q48_launch_silu_mul(q48_ctx *c, int64_t *out, const int64_t *g,

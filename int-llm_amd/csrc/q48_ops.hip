@@ -1203,6 +1203,95 @@ __global__ void k_step_set(int *__restrict__ st, int token, int pos)
     }
 }
 
+// argmax of v[0..n) into the state on AMAX_BLOCKS blocks of 256: each block
+// scans a chunk (and with rec copies it to rec[count][..] while count <
+// rec_cap, count read before any block's ticket), its (maximum, first index)
+// goes out with agent-coherent stores ahead of a ticket, and the last block
+// combines the partials (the largest value, the lowest index among equal
+// ones: the reference's first maximum), updates the state and resets the
+// ticket.  The same token as k_step_argmax; no block waits on another.
+constexpr int AMAX_BLOCKS = 32;
+__global__ __launch_bounds__(256) void k_step_argmax_mb(int *__restrict__ st,
+                                                       int *__restrict__ tokens, int cap,
+                                                       const int64_t *__restrict__ v, int n,
+                                                       int64_t *__restrict__ rec, int rec_cap,
+                                                       uint64_t *__restrict__ part)
+{
+    __shared__ int64_t bv[4];
+    __shared__ int bi[4];
+    __shared__ int last_sh;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int k = st[2];
+    int64_t *dst = rec && k >= 0 && k < rec_cap ? rec + (size_t)k * n : nullptr;
+    const int chunk = (n + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int i0 = (int)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+    int64_t best = INT64_MIN;
+    int idx = n;
+    for (int i = i0 + tid; i < i1; i += 256) {
+        const int64_t x = v[i];
+        if (dst)
+            dst[i] = x;
+        if (x > best) {   // ascending i: the first maximum of this thread
+            best = x;
+            idx = i;
+        }
+    }
+    auto wave_best = [&]() {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const int64_t ov = __shfl_xor(best, off, 64);
+            const int oi = __shfl_xor(idx, off, 64);
+            if (ov > best || (ov == best && oi < idx)) {
+                best = ov;
+                idx = oi;
+            }
+        }
+    };
+    wave_best();
+    if (lane == 0) {
+        bv[tid >> 6] = best;
+        bi[tid >> 6] = idx;
+    }
+    __syncthreads();
+    uint64_t *ticket = part + 2 * AMAX_BLOCKS;
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
+                best = bv[w];
+                idx = bi[w];
+            }
+        __hip_atomic_store(&part[2 * blockIdx.x], (uint64_t)best, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&part[2 * blockIdx.x + 1], (uint64_t)(uint32_t)idx, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        const uint64_t t = __hip_atomic_fetch_add(ticket, (uint64_t)1, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        last_sh = t == (uint64_t)gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last_sh || tid >= 64)
+        return;
+    best = INT64_MIN;
+    idx = n;
+    if (tid < (int)gridDim.x) {
+        best = (int64_t)__hip_atomic_load(&part[2 * tid], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        idx = (int)__hip_atomic_load(&part[2 * tid + 1], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+    }
+    wave_best();
+    if (tid == 0) {
+        const int tok = idx < n ? idx : 0;
+        st[0] = tok;
+        st[1] = st[1] + 1;
+        if (k < cap)
+            tokens[k] = tok;
+        st[2] = k + 1;
+        __hip_atomic_store(ticket, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 __global__ __launch_bounds__(1024) void k_step_argmax(int *__restrict__ st,
                                                      int *__restrict__ tokens, int cap,
                                                      const int64_t *__restrict__ v, int n)
@@ -1654,8 +1743,23 @@ int q48_launch_step_set(q48_ctx *c, int token, int pos)
     return (int)hipGetLastError();
 }
 
-int q48_launch_step_argmax(q48_ctx *c, int *tokens, int cap, const int64_t *v, int n)
+size_t q48_amax_part_bytes() { return (2 * AMAX_BLOCKS + 2) * sizeof(uint64_t); }
+
+// n below AMAX_BLOCKS * 256 takes the one-block kernel (the record, when
+// asked, as its own launch before it)
+int q48_launch_step_argmax(q48_ctx *c, int *tokens, int cap, const int64_t *v, int n,
+                           int64_t *rec, int rec_cap)
 {
+    if (n >= AMAX_BLOCKS * 256) {
+        hipLaunchKernelGGL(k_step_argmax_mb, dim3(AMAX_BLOCKS), dim3(256), 0, c->stream,
+                           c->d_step, tokens, cap, v, n, rec, rec_cap, c->amax_part);
+        return (int)hipGetLastError();
+    }
+    if (rec) {
+        const int rc = q48_launch_step_record(c, rec, rec_cap, v, n);
+        if (rc)
+            return rc;
+    }
     hipLaunchKernelGGL(k_step_argmax, dim3(1), dim3(1024), 0, c->stream, c->d_step, tokens,
                        cap, v, n);
     return (int)hipGetLastError();

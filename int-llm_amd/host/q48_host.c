@@ -393,6 +393,21 @@ static int select_token_step(q48h_model *m)
     return q48_argmax_step(m->ctx, m->logits, m->c.vocab, m->d_tokens, m->c.max_seq);
 }
 
+/* The step's logits recorded (when the model records) and its token chosen,
+ * on the device; greedy steps do both in one launch. */
+static int record_and_select_step(q48h_model *m)
+{
+    if (m->record && m->temperature < Q48_ONE / 100)
+        return q48_argmax_record_step(m->ctx, m->logits, m->c.vocab, m->d_tokens, m->c.max_seq,
+                                      m->rec, m->rec_cap);
+    if (m->record) {
+        int rc = q48_record_step(m->ctx, m->logits, m->c.vocab, m->rec, m->rec_cap);
+        if (rc)
+            return rc;
+    }
+    return select_token_step(m);
+}
+
 void q48h_model_set_fused(q48h_model *m, int fused)
 {
     if (fused < 0 || fused > 3)
@@ -1159,10 +1174,8 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
     int rc = q48_step_set(x, token, pos);
     if (rc == Q48_OK) {
         rc = enqueue_forward(m, token, pos);
-        if (rc == Q48_OK && m->record)
-            rc = q48_record_step(x, m->logits, m->c.vocab, m->rec, m->rec_cap);
         if (rc == Q48_OK)
-            rc = select_token_step(m);
+            rc = record_and_select_step(m);
         if (rc == Q48_OK)
             rc = q48_sync(x);
     }
@@ -1208,10 +1221,8 @@ static int first_step_and_capture(q48h_model *m, int token, int pos)
         rc = q48_graph_capture(x);
         if (rc == Q48_OK) {
             int rc1 = enqueue_forward(m, token, pos);
-            if (rc1 == Q48_OK && m->record)
-                rc1 = q48_record_step(x, m->logits, m->c.vocab, m->rec, m->rec_cap);
             if (rc1 == Q48_OK)
-                rc1 = select_token_step(m);
+                rc1 = record_and_select_step(m);
             q48_graph *g = NULL;
             rc = q48_graph_instantiate(x, &g);
             if (rc == Q48_OK && rc1) {

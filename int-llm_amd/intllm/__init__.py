@@ -94,6 +94,7 @@ ABI_SIGNATURES = {
     "q48_step_get": [_P, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)],
     "q48_argmax_step": [_P, _P, _I, _P, _I],
     "q48_record_step": [_P, _P, _I, _P, _I],
+    "q48_argmax_record_step": [_P, _P, _I, _P, _I, _P, _I],
     "q48_graph_begin": [_P],
     "q48_graph_end": [_P],
     "q48_graph_launch": [_P, _I],

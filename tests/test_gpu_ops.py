@@ -534,6 +534,59 @@ def test_add_embed_argmax(ctx):
         dvv.free()
 
 
+@pytest.mark.parametrize("n", [1, 1000, 8191, 8192, 9001, 32000])
+def test_argmax_step_and_record(ctx, n):
+    """q48_argmax_step and q48_argmax_record_step (the decode step's token
+    choice, llama_int.c:2888-2893: the first maximum) against numpy over
+    several steps in a row, with ties across the blocks' chunks, INT64_MIN
+    and INT64_MAX entries, and the state (token, pos + 1, count + 1), the
+    tokens array and the recorded rows checked after every step; the record
+    stops at its capacity and the tokens at theirs."""
+    lib = intllm.hip_lib()
+    rng = np.random.default_rng(n)
+    steps, rec_cap, tok_cap = 5, 3, 4
+    rows = []
+    for s in range(steps):
+        v = rng.integers(-(1 << 40), 1 << 40, size=n, dtype=np.int64)
+        if s == 1:
+            v[:] = spec.INT64_MIN                       # all equal: index 0
+        if s == 2 and n > 10:
+            v[n // 3] = v[n - 1] = v[2 * n // 3] = spec.INT64_MAX   # first of three
+        if s == 3:
+            v[rng.integers(0, n, size=min(n, 7))] = v.max()      # repeated maximum
+        rows.append(v)
+    dv = ctx.buffer(n)
+    tokens = ctx.buffer(tok_cap // 2)   # int32 tokens in int64 words
+    rec = ctx.buffer(rec_cap * n)
+    rec.upload(np.zeros(rec_cap * n, dtype=np.int64))
+    for fused in (False, True):
+        assert lib.q48_step_mode(ctx.h, 1) == 0
+        assert lib.q48_step_set(ctx.h, 11, 40) == 0
+        tokens.upload(np.full(tok_cap // 2, -1, dtype=np.int64))
+        want_tok = []
+        for s, v in enumerate(rows):
+            dv.upload(v)
+            if fused:
+                rc = lib.q48_argmax_record_step(ctx.h, dv.ptr, n, tokens.ptr, tok_cap, rec.ptr,
+                                                rec_cap)
+            else:
+                rc = lib.q48_argmax_step(ctx.h, dv.ptr, n, tokens.ptr, tok_cap)
+            assert rc == 0
+            want_tok.append(int(np.argmax(v)))
+            tok, pos, cnt = C.c_int(), C.c_int(), C.c_int()
+            assert lib.q48_step_get(ctx.h, C.byref(tok), C.byref(pos), C.byref(cnt)) == 0
+            assert (tok.value, pos.value, cnt.value) == (want_tok[-1], 41 + s, s + 1), (fused, s)
+        got = tokens.download().view(np.int32)[:tok_cap]
+        assert list(got) == want_tok[:tok_cap]
+        if fused:
+            r = rec.download().reshape(rec_cap, n)
+            for s in range(rec_cap):
+                assert np.array_equal(r[s], rows[s])
+        assert lib.q48_step_mode(ctx.h, 0) == 0
+    for b in (dv, tokens, rec):
+        b.free()
+
+
 def test_abi_rejects_bad_arguments(ctx):
     lib = intllm.hip_lib()
     assert lib.q48_gemv(ctx.h, None, None, None, 4, 4) == intllm.Q48_EINVAL
