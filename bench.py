@@ -127,8 +127,10 @@ def traffic_bytes():
 
 def gemm_prefill(ctx, spec, intllm, reps: int):
     """Config 4: q48_gemm at T in {128, 512, 2048} tokens on the config-2
-    shapes, with both kernels (int8 digits on the matrix cores, 32-bit limbs
-    on the vector ALUs).  Each output is hashed against the golden vector of
+    shapes, with each kernel: int8 digits on the matrix cores ("i8": the one
+    q48_gemm picks by shape; "i8_fused": digit split inside the k loop;
+    "i8_planes": digit planes split once per call, read by DMA) and 32-bit
+    limbs on the vector ALUs ("valu").  Each output is hashed against the golden vector of
     the reference's per-token matmul_vec; times are whole q48_gemm calls
     (the redo pass for blocks outside the digit window and the split-K
     reduction included) between two HIP events on the library's stream."""
@@ -144,7 +146,10 @@ def gemm_prefill(ctx, spec, intllm, reps: int):
             key = f"{T}x{N}x{K}"
             macs = T * N * K
             rec = {}
-            for name, kern, n in (("i8", intllm.GEMM_I8, reps), ("valu", intllm.GEMM_VALU, 1)):
+            for name, kern, n in (("i8", intllm.GEMM_I8, reps),
+                                  ("i8_fused", intllm.GEMM_I8_FUSED, reps),
+                                  ("i8_planes", intllm.GEMM_I8_PLANES, reps),
+                                  ("valu", intllm.GEMM_VALU, 1)):
                 ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K, kern)
                 rec[f"{name}_bit_exact"] = intllm.fnv(dY.download()) == gold[key]["fnv"]
                 ctx.timer_start()

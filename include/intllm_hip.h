@@ -77,14 +77,18 @@ int q48_gemm(q48_ctx *ctx, int64_t *Y, const int64_t *W, const int64_t *X,
 
 /* q48_gemm with the kernel named: Q48_GEMM_VALU multiplies 32-bit limbs on
  * the vector ALUs; Q48_GEMM_I8 splits both operands into int8 digits and
- * multiplies them on the matrix cores (v_mfma_i32_32x32x32_i8); Q48_GEMM_AUTO
- * is q48_gemm's choice (the decode GEMV for T = 1, else Q48_GEMM_I8).  All
- * give the same bits.  No reference
- * counterpart: it exists so that callers and benchmarks can compare the two
- * kernels on the same inputs. */
-#define Q48_GEMM_AUTO 0
-#define Q48_GEMM_VALU 1
-#define Q48_GEMM_I8   2
+ * multiplies them on the matrix cores (v_mfma_i32_32x32x32_i8), with the
+ * split either inside the k loop (Q48_GEMM_I8_FUSED) or done once per call
+ * into digit planes that the k loop reads by DMA (Q48_GEMM_I8_PLANES);
+ * Q48_GEMM_I8 picks one of the two by shape, and Q48_GEMM_AUTO is q48_gemm's
+ * choice (the decode GEMV for T = 1, else Q48_GEMM_I8).  All give the same
+ * bits.  No reference counterpart: it exists so that callers and benchmarks
+ * can compare the kernels on the same inputs. */
+#define Q48_GEMM_AUTO      0
+#define Q48_GEMM_VALU      1
+#define Q48_GEMM_I8        2
+#define Q48_GEMM_I8_FUSED  3
+#define Q48_GEMM_I8_PLANES 4
 int q48_gemm_ex(q48_ctx *ctx, int64_t *Y, const int64_t *W, const int64_t *X,
                 int T, int N, int K, int kernel);
 

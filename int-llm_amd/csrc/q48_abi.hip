@@ -403,17 +403,18 @@ int q48_gemm_ex(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int 
                 int K, int kernel)
 {
     if (!c || !Y || !W || !X || T <= 0 || N <= 0 || K <= 0 || T > 65535 * 64 ||
-        N > kMaxDim || K > kMaxDim || kernel < Q48_GEMM_AUTO || kernel > Q48_GEMM_I8)
+        N > kMaxDim || K > kMaxDim || kernel < Q48_GEMM_AUTO || kernel > Q48_GEMM_I8_PLANES)
         return Q48_EINVAL;
     if ((((uintptr_t)W | (uintptr_t)X | (uintptr_t)Y) & 7) != 0)
         return Q48_EINVAL;
     int rc;
     if (kernel == Q48_GEMM_AUTO && T == 1)
         rc = q48_launch_gemv(c, Y, W, X, N, K);   // one token: the decode GEMV
-    else if ((kernel == Q48_GEMM_AUTO ? q48_gemm_auto_kernel(T, N, K) : kernel) == Q48_GEMM_I8)
-        rc = q48_launch_gemm_i8(c, Y, W, X, T, N, K);
-    else
+    else if (kernel == Q48_GEMM_VALU ||
+             (kernel == Q48_GEMM_AUTO && q48_gemm_auto_kernel(T, N, K) == Q48_GEMM_VALU))
         rc = q48_launch_gemm(c, Y, W, X, T, N, K);
+    else
+        rc = q48_launch_gemm_i8(c, Y, W, X, T, N, K, kernel);
     if (rc == Q48_ENOMEM)
         return rc;
     return launch_rc(rc);

@@ -618,6 +618,266 @@ __global__ __launch_bounds__(256) void k_gemm_i8_reduce(int64_t *__restrict__ Y,
     Y[i] = (int64_t)((q48_i128)tot >> 48);
 }
 
+// ---------------------------------------------------------------------------
+// Planes path: operands split once into digit planes in HBM, then moved
+// into LDS by DMA (global_load_lds), so the k loop runs no digit split.
+// ---------------------------------------------------------------------------
+
+// Digit planes of a row-major int64 matrix (R rows, K columns) in the LDS
+// stage order of the window kernels: per row tile rt (64 rows) and k-step s
+// (32 columns), block rt * nsteps + s holds planes 0..7 of the nine-digit
+// form, 2 KB each ([32-row slice][16-column chunk][32 rows][16 bytes]; rows
+// past R and columns past K are zero), and mask[rt * nsteps + s] has bit a
+// when plane a holds a nonzero digit and bit 8 when a value may have
+// overflowed v + C (high word >= 0x7F7F7F7F; plane 8 itself is not stored).
+__global__ __launch_bounds__(256) void k_planes(uint8_t *__restrict__ dst,
+                                               uint32_t *__restrict__ mask,
+                                               const int64_t *__restrict__ src, int R, int K,
+                                               int nsteps)
+{
+    __shared__ uint32_t red[4];
+    const int tid = threadIdx.x;
+    const int rt = (int)blockIdx.x / nsteps, st = (int)blockIdx.x % nsteps;
+    const Piece pc = piece(tid);
+    const int row = rt * MN + pc.r, k0 = st * MK + pc.k8;
+    uint64_t v[8];
+    const int64_t *rp = src + (size_t)min(row, R - 1) * K + k0;
+    if (row < R && k0 + 8 <= K && (((uintptr_t)rp) & 15) == 0) {
+        const ulonglong2 *q = reinterpret_cast<const ulonglong2 *>(rp);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const ulonglong2 u = q[e];
+            v[2 * e] = u.x;
+            v[2 * e + 1] = u.y;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            v[e] = row < R && k0 + e < K ? (uint64_t)rp[e] : 0;
+    }
+    uint64_t u[8];
+    bool big = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        u[e] = v[e] + kDig;
+        big |= (int32_t)(uint32_t)(v[e] >> 32) >= 0x7f7f7f7f;
+    }
+    uint32_t l0[4], l1[4], h0[4], h1[4];
+    tr4((uint32_t)u[0], (uint32_t)u[1], (uint32_t)u[2], (uint32_t)u[3], l0);
+    tr4((uint32_t)u[4], (uint32_t)u[5], (uint32_t)u[6], (uint32_t)u[7], l1);
+    tr4((uint32_t)(u[0] >> 32), (uint32_t)(u[1] >> 32), (uint32_t)(u[2] >> 32),
+        (uint32_t)(u[3] >> 32), h0);
+    tr4((uint32_t)(u[4] >> 32), (uint32_t)(u[5] >> 32), (uint32_t)(u[6] >> 32),
+        (uint32_t)(u[7] >> 32), h1);
+    uint2 d[8];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+        d[a] = make_uint2(l0[a] ^ 0x80808080u, l1[a] ^ 0x80808080u);
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+        d[4 + a] = make_uint2(h0[a] ^ 0x80808080u, h1[a] ^ 0x80808080u);
+    d[7] = make_uint2(h0[3], h1[3]);
+    uint8_t *p = dst + (size_t)blockIdx.x * 8 * PLANE + pc.off;
+    uint32_t m = big ? 0x100u : 0u;
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        *reinterpret_cast<uint2 *>(p + a * PLANE) = d[a];
+        m |= (d[a].x | d[a].y) != 0 ? 1u << a : 0u;
+    }
+    m = wave_or(m);
+    if ((tid & 63) == 0)
+        red[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0)
+        mask[blockIdx.x] = red[0] | red[1] | red[2] | red[3];
+}
+
+// One LDS stage of the planes path: X planes 0..6, then W planes WP0 .. WP0 + 4.
+constexpr int PX_BYTES = 7 * PLANE, PSTAGE = 12 * PLANE;
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// The k loop of one window (LO): per step the block's 24 KB of planes come
+// by DMA two steps ahead into a ring of three stages (each wave moves six
+// 1 KB chunks: 64 lanes x 16 bytes), and the step runs only MFMAs.  The
+// stages are three LDS objects named statically in each step, so the reads
+// of one stage need no wait for the DMA into another.
+typedef const __attribute__((address_space(4))) uint32_t *ConstMask;
+
+// Workgroup barrier without the fence of __syncthreads (whose release waits
+// for every DMA still in flight); the caller's s_waitcnt before it decides
+// which DMA the barrier publishes.  The empty asm keeps LDS accesses on
+// their side of it.
+__device__ __forceinline__ void stage_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int LO>
+__device__ __forceinline__ void planes_pass(uint8_t (&s0)[PSTAGE], uint8_t (&s1)[PSTAGE],
+                                            uint8_t (&s2)[PSTAGE], ConstMask wm,
+                                            const uint8_t *xsrc, const uint8_t *wsrc, int ns,
+                                            v16i (&acc)[14])
+{
+    constexpr int WP0 = LO > 0 ? LO - 1 : 0;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wt = w >> 1, wn = w & 1;
+    const uint8_t *ws_src = wsrc + WP0 * PLANE;
+    auto dma = [&](int s, uint8_t(&dst)[PSTAGE]) {
+#pragma unroll
+        for (int j = 0; j < 6; ++j) {
+            const int c = w + 4 * j;   // chunk 0..23: X 0..13, W 14..23
+            const uint8_t *g = c < 14 ? xsrc + (size_t)s * 8 * PLANE + c * 1024
+                                      : ws_src + (size_t)s * 8 * PLANE + (c - 14) * 1024;
+            __builtin_amdgcn_global_load_lds(g + lane * 16, dst + c * 1024, 16, 0, 0);
+        }
+    };
+    // step i multiplies stage cur and loads step i + 2 into stage nxt (read
+    // by step i - 1, which every wave has left at the barrier); more: there
+    // is a step i + 2
+    auto step = [&](int i, uint8_t(&cur)[PSTAGE], uint8_t(&nxt)[PSTAGE], bool more) {
+        if (more)
+            dma(i + 2, nxt);
+        const uint8_t *xs = cur + wt * SLICE;
+        const uint8_t *ws = cur + PX_BYTES - WP0 * PLANE + wn * SLICE;
+        mfma_window<LO>(acc, xs, ws, lane);
+        if (LO > 0 && ((wm[i] >> WP0) & 1u))   // a scalar load: no wait on the DMA
+            mfma_plane_w<WP0>(acc, xs, ws, lane);
+        // this wave's DMA into the next stage has landed; the barrier makes
+        // every wave's visible
+        if (more)
+            wait_vm<6>();
+        else
+            wait_vm<0>();
+        stage_barrier();
+    };
+    // The main loop runs groups of three steps that all load ahead (no
+    // branch around a DMA, so the compiler's own waits stay at vmcnt(6));
+    // the last two to four steps run with the tests.
+    int i = 0;
+    if (ns >= 5) {
+        dma(0, s0);
+        dma(1, s1);
+        wait_vm<6>();
+        stage_barrier();
+        do {
+            step(i, s0, s2, true);
+            step(i + 1, s1, s0, true);
+            step(i + 2, s2, s1, true);
+            i += 3;
+        } while (i + 4 < ns);
+    } else {
+        if (ns > 0)
+            dma(0, s0);
+        if (ns > 1) {
+            dma(1, s1);
+            wait_vm<6>();
+        } else {
+            wait_vm<0>();
+        }
+        stage_barrier();
+    }
+    if (i < ns)
+        step(i, s0, s2, i + 2 < ns);
+    if (i + 1 < ns)
+        step(i + 1, s1, s0, i + 3 < ns);
+    if (i + 2 < ns)
+        step(i + 2, s2, s1, i + 4 < ns);
+    if (i + 3 < ns)
+        step(i + 3, s0, s2, false);
+}
+
+// grid (ceil(N/64) * ceil(T/64), 1, S) over operands split by k_planes
+// (nsteps k-steps): split z covers steps [z spb, (z + 1) spb).  The block
+// ORs its tiles' masks over its steps; the window is LO = top W plane - 3
+// (clamped to 0..4); a block whose X digits reach plane 7 (or may overflow)
+// or whose W digits leave LO - 1 .. LO + 3 writes nothing and sets
+// redo[block] (else clears it) for k_gemm_i8_full.  S == 1: Y gets the
+// shifted result; S > 1: P[z][t][n] the int128 partial.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+k_gemm_i8p(int64_t *__restrict__ Y, uint64_t *__restrict__ P, int *__restrict__ redo,
+           const uint8_t *__restrict__ Xp, const uint32_t *__restrict__ Xm,
+           const uint8_t *__restrict__ Wp, const uint32_t *__restrict__ Wm, int T, int N,
+           int nsteps, int spb)
+{
+    __shared__ __align__(16) uint8_t st0[PSTAGE];
+    __shared__ __align__(16) uint8_t st1[PSTAGE];
+    __shared__ __align__(16) uint8_t st2[PSTAGE];
+    __shared__ uint32_t red[2][4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int n_tile, t_tile;
+    tile_of(blockIdx.x, (N + MN - 1) / MN, (T + MT - 1) / MT, n_tile, t_tile);
+    const int s0 = (int)blockIdx.z * spb, ns = max(0, min(nsteps, s0 + spb) - s0);
+    uint32_t mx = 0, mw = 0;
+    for (int i = tid; i < ns; i += 256) {
+        mx |= Xm[(size_t)t_tile * nsteps + s0 + i];
+        mw |= Wm[(size_t)n_tile * nsteps + s0 + i];
+    }
+    mx = wave_or(mx);
+    mw = wave_or(mw);
+    if (lane == 0) {
+        red[0][w] = mx;
+        red[1][w] = mw;
+    }
+    __syncthreads();
+    mx = (uint32_t)__builtin_amdgcn_readfirstlane((int)(red[0][0] | red[0][1] | red[0][2] | red[0][3]));
+    mw = (uint32_t)__builtin_amdgcn_readfirstlane((int)(red[1][0] | red[1][1] | red[1][2] | red[1][3]));
+    const int top = (mw & 0xffu) ? 31 - __builtin_clz(mw & 0xffu) : 3;
+    const int LO = min(max(top - 3, 0), 4);
+    const uint32_t win = ((0x1fu << LO) >> 1) & 0xffu;
+    const bool fit = (mx & ~0x7fu) == 0 && (mw & ~win) == 0;
+    if (tid == 0)
+        redo[blockIdx.z * gridDim.x + blockIdx.x] = fit ? 0 : 1;
+    if (!fit)
+        return;   // uniform over the block
+
+    v16i acc[14];
+#pragma unroll
+    for (int d = 0; d < 14; ++d)
+        acc[d] = (v16i){0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const uint8_t *xsrc = Xp + ((size_t)t_tile * nsteps + s0) * 8 * PLANE;
+    const uint8_t *wsrc = Wp + ((size_t)n_tile * nsteps + s0) * 8 * PLANE;
+    const ConstMask wm = (ConstMask)(Wm + (size_t)n_tile * nsteps + s0);
+    switch (LO) {
+    case 0: planes_pass<0>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
+    case 1: planes_pass<1>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
+    case 2: planes_pass<2>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
+    case 3: planes_pass<3>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
+    default: planes_pass<4>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
+    }
+
+    // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32
+    const int wt = w >> 1, wn = w & 1;
+    const int n = n_tile * MN + 32 * wn + (lane & 31);
+    if (n >= N)
+        return;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int t = t_tile * MT + 32 * wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (t >= T)
+            continue;
+        q48_u128 tot = 0;
+#pragma unroll
+        for (int d = 13; d >= 0; --d)
+            tot = (tot << 8) + (q48_u128)(q48_i128)acc[d][i];
+        if (gridDim.z == 1) {
+            Y[(size_t)t * N + n] = (int64_t)((q48_i128)tot >> 48);
+        } else {
+            uint64_t *p = P + 2 * (((size_t)blockIdx.z * T + t) * N + n);
+            *reinterpret_cast<ulonglong2 *>(p) = make_ulonglong2((uint64_t)tot,
+                                                                 (uint64_t)(tot >> 64));
+        }
+    }
+}
+
 } // namespace
 
 int q48_gemm_auto_kernel(int T, int N, int K)
@@ -644,34 +904,57 @@ int q48_gemm_i8_splits(int T, int N, int K, int cu_count)
 }
 
 int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int T,
-                       int N, int K)
+                       int N, int K, int kernel)
 {
     const int S = q48_gemm_i8_splits(T, N, K, c->cu_count);
     const int steps = (K + MK - 1) / MK;
     const int spb = (steps + S - 1) / S;
-    const int nb = ((N + MN - 1) / MN) * ((T + MT - 1) / MT);
-    // workspace: the blocks' redo flags, then (S > 1) the int128 partials
-    const size_t flags = ((size_t)nb * S * sizeof(int) + 255) & ~(size_t)255;
+    const int nt = (T + MT - 1) / MT, nn = (N + MN - 1) / MN, nb = nn * nt;
+    // the planes path pays one split of X and W per call: it wins once
+    // tiles are reused enough (measured: T >= 512 with N >= 2048 faster by
+    // 7-39%, N = 256 slower by 5-22%, T = 128 even)
+    const bool planes = kernel == Q48_GEMM_I8_PLANES ||
+                        (kernel != Q48_GEMM_I8_FUSED && T >= 256 && N >= 1024);
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    // workspace: the blocks' redo flags, (S > 1) the int128 partials, then
+    // (planes path) X and W digit planes and their masks
+    const size_t flags = al((size_t)nb * S * sizeof(int));
     const size_t part = S > 1 ? 16 * (size_t)S * T * N : 0;
-    int rc = q48_ws_reserve(c, flags + part);
+    const size_t xpl = planes ? (size_t)nt * steps * 8 * PLANE : 0;
+    const size_t wpl = planes ? (size_t)nn * steps * 8 * PLANE : 0;
+    const size_t xms = planes ? al((size_t)nt * steps * 4) : 0;
+    const size_t wms = planes ? al((size_t)nn * steps * 4) : 0;
+    int rc = q48_ws_reserve(c, flags + part + xpl + wpl + xms + wms);
     if (rc)
         return rc;
-    int *redo = (int *)c->ws;
-    uint64_t *P = S > 1 ? (uint64_t *)((char *)c->ws + flags) : nullptr;
+    char *ws = (char *)c->ws;
+    int *redo = (int *)ws;
+    uint64_t *P = S > 1 ? (uint64_t *)(ws + flags) : nullptr;
     const dim3 grid(nb, 1, S);
     const int fgrid = min(nb * S, c->cu_count);
     const bool vec = K % 2 == 0 && (((uintptr_t)W | (uintptr_t)X) & 15) == 0;
-    if (vec) {
+    if (planes) {
+        uint8_t *Xp = (uint8_t *)(ws + flags + part), *Wp = Xp + xpl;
+        uint32_t *Xm = (uint32_t *)(Wp + wpl), *Wm = (uint32_t *)((char *)Xm + xms);
+        hipLaunchKernelGGL(k_planes, dim3(nt * steps), dim3(256), 0, c->stream, Xp, Xm, X, T, K,
+                           steps);
+        hipLaunchKernelGGL(k_planes, dim3(nn * steps), dim3(256), 0, c->stream, Wp, Wm, W, N, K,
+                           steps);
+        hipLaunchKernelGGL(k_gemm_i8p, grid, dim3(256), 0, c->stream, Y, P, redo, Xp, Xm, Wp, Wm,
+                           T, N, steps, spb);
+    } else if (vec) {
         hipLaunchKernelGGL((k_gemm_i8<true>), grid, dim3(256), 0, c->stream, Y, P, redo, W, X, T,
                            N, K, spb);
-        hipLaunchKernelGGL((k_gemm_i8_full<true>), dim3(fgrid), dim3(256), 0, c->stream, Y, P,
-                           redo, W, X, T, N, K, spb, nb, S);
     } else {
         hipLaunchKernelGGL((k_gemm_i8<false>), grid, dim3(256), 0, c->stream, Y, P, redo, W, X,
                            T, N, K, spb);
+    }
+    if (vec)
+        hipLaunchKernelGGL((k_gemm_i8_full<true>), dim3(fgrid), dim3(256), 0, c->stream, Y, P,
+                           redo, W, X, T, N, K, spb, nb, S);
+    else
         hipLaunchKernelGGL((k_gemm_i8_full<false>), dim3(fgrid), dim3(256), 0, c->stream, Y, P,
                            redo, W, X, T, N, K, spb, nb, S);
-    }
     if (S > 1) {
         const size_t tn = (size_t)T * N;
         hipLaunchKernelGGL(k_gemm_i8_reduce, dim3((unsigned)((tn + 255) / 256)), dim3(256), 0,

@@ -132,9 +132,11 @@ int q48_launch_stats_r(q48_ctx *c, int64_t *r_out, const int64_t *stats, int dim
 int q48_rms_reserve(q48_ctx *c, int blocks);
 int q48_launch_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X,
                     int T, int N, int K);
-// int8-digit GEMM on the matrix cores (q48_gemm.hip); same bits as q48_launch_gemm
+// int8-digit GEMM on the matrix cores (q48_gemm.hip); same bits as
+// q48_launch_gemm.  kernel: Q48_GEMM_I8_FUSED or Q48_GEMM_I8_PLANES, anything
+// else picks one of them by shape.
 int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X,
-                       int T, int N, int K);
+                       int T, int N, int K, int kernel);
 // K splits the int8 GEMM uses for this shape on cu_count compute units
 int q48_gemm_i8_splits(int T, int N, int K, int cu_count);
 // Q48_GEMM_VALU or Q48_GEMM_I8: the kernel q48_gemm runs for this shape

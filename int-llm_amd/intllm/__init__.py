@@ -28,7 +28,7 @@ FP_MUL, FP_DIV, FP_SQRT, FP_SQRT_FAST, FP_INV_SQRT, FP_EXP, FP_LOG, FP_SINCOS, \
     FP_SIGMOID, FP_SILU, FP_SAFE_EXP, FP_EXP_DYADIC, FP_DIV_ROW = range(13)
 
 # q48_gemm_ex kernels (include/intllm_hip.h)
-GEMM_AUTO, GEMM_VALU, GEMM_I8 = 0, 1, 2
+GEMM_AUTO, GEMM_VALU, GEMM_I8, GEMM_I8_FUSED, GEMM_I8_PLANES = 0, 1, 2, 3, 4
 
 # ABI entry points and their argument types (include/intllm_hip.h)
 _P, _I, _SZ = C.c_void_p, C.c_int, C.c_size_t
@@ -301,7 +301,8 @@ class Context:
         return check("q48_set_gemv_persistent", hip_lib().q48_set_gemv_persistent(self.h, int(on)))
 
     def gemm(self, Y, W, X, T, N, K, kernel=None):
-        """kernel: None (q48_gemm's choice), GEMM_VALU or GEMM_I8."""
+        """kernel: None (q48_gemm's choice), GEMM_VALU, GEMM_I8 (the int8
+        kernel chosen by shape), GEMM_I8_FUSED or GEMM_I8_PLANES."""
         if kernel is None:
             return check("q48_gemm", hip_lib().q48_gemm(self.h, Y, W, X, T, N, K))
         return check("q48_gemm_ex", hip_lib().q48_gemm_ex(self.h, Y, W, X, T, N, K, kernel))

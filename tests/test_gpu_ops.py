@@ -295,7 +295,8 @@ def test_gemv_random_vs_oracle(ctx, M, K):
         assert np.array_equal(gemv_dev(ctx, W, x, M, K, off), want), (M, K, off)
 
 
-GEMM_KERNELS = [pytest.param(intllm.GEMM_VALU, id="valu"), pytest.param(intllm.GEMM_I8, id="i8")]
+GEMM_KERNELS = [pytest.param(intllm.GEMM_VALU, id="valu"), pytest.param(intllm.GEMM_I8, id="i8"),
+                pytest.param(intllm.GEMM_I8_PLANES, id="i8planes")]
 
 
 @pytest.mark.parametrize("kernel", GEMM_KERNELS)
@@ -334,9 +335,11 @@ def _bf16ish(rng, n, scale):
     return v
 
 
+@pytest.mark.parametrize("tokens,kernel", [pytest.param(96, intllm.GEMM_I8_FUSED, id="fused"),
+                                           pytest.param(300, intllm.GEMM_I8_PLANES, id="planes")])
 @pytest.mark.parametrize("case", ["plain", "ext", "late_w", "late_x", "big_w", "ovf_w",
                                   "lo0", "lo4", "zero_w", "split"])
-def test_gemm_digit_windows(ctx, oracle, case):
+def test_gemm_digit_windows(ctx, oracle, case, tokens, kernel):
     """The int8 GEMM's digit-plane window (X digits 0..6 against four W
     planes chosen from the block's first W tile, plus the plane below in the
     steps that reach it; blocks leaving it redone with every pair) against the
@@ -346,9 +349,11 @@ def test_gemm_digit_windows(ctx, oracle, case):
     at the high-word bound that is treated as a possible overflow ("big_w")
     and values that do overflow v + C ("ovf_w"), windows at both ends of the
     plane range ("lo0", "lo4"), an all-zero W tile, and K split across blocks
-    with some splits redone ("split")."""
+    with some splits redone ("split").  Both int8 kernels run each case: the
+    one that splits tiles into digits inside its k loop (96 tokens) and the
+    one fed digit planes split beforehand (300: a ragged last token tile)."""
     rng = np.random.default_rng(sum(map(ord, case)))
-    T, N, K = (64, 64, 8192) if case == "split" else (96, 130, 1000)
+    T, N, K = (tokens - 32, 64, 8192) if case == "split" else (tokens, 130, 1000)
     scale = {"lo0": 27, "lo4": 58}.get(case, 42)
     W = _bf16ish(rng, N * K, scale)
     X = rng.integers(-(1 << 52), 1 << 52, size=T * K, dtype=np.int64)
@@ -372,7 +377,7 @@ def test_gemm_digit_windows(ctx, oracle, case):
     oracle.q48o_gemm(want.ctypes.data, W.ctypes.data, X.ctypes.data, T, N, K)
     dW, dX, dY = ctx.to_device(W), ctx.to_device(X), ctx.buffer(T * N)
     say("gemm window", case, T, N, K)
-    ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K, intllm.GEMM_I8)
+    ctx.gemm(dY.ptr, dW.ptr, dX.ptr, T, N, K, kernel)
     got = dY.download()
     bad = np.nonzero(got != want)[0]
     assert bad.size == 0, (case, bad[:5])
