@@ -703,11 +703,6 @@ __device__ __forceinline__ void wait_vm()
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// The k loop of one window (LO): per step the block's 24 KB of planes come
-// by DMA two steps ahead into a ring of three stages (each wave moves six
-// 1 KB chunks: 64 lanes x 16 bytes), and the step runs only MFMAs.  The
-// stages are three LDS objects named statically in each step, so the reads
-// of one stage need no wait for the DMA into another.
 typedef const __attribute__((address_space(4))) uint32_t *ConstMask;
 
 // Workgroup barrier without the fence of __syncthreads (whose release waits
@@ -721,15 +716,26 @@ __device__ __forceinline__ void stage_barrier()
     asm volatile("" ::: "memory");
 }
 
+// The k loop of one window (LO) over a ring of four LDS stages.  Step i:
+//   wait for step i + 1's DMA (this wave's), barrier (every wave's);
+//   DMA step i + 3 into the stage step i - 1 used (each wave moves six 1 KB
+//   chunks: 64 lanes x 16 bytes);
+//   read step i + 1's operands into the spare register set, while the MFMAs
+//   of step i run on the set read during step i - 1.
+// The stages are four LDS objects named statically in each step (the loop
+// is unrolled by four), so the compiler's own waits for the reads of one
+// stage do not count the DMA into another.
 template <int LO>
 __device__ __forceinline__ void planes_pass(uint8_t (&s0)[PSTAGE], uint8_t (&s1)[PSTAGE],
-                                            uint8_t (&s2)[PSTAGE], ConstMask wm,
-                                            const uint8_t *xsrc, const uint8_t *wsrc, int ns,
-                                            v16i (&acc)[14])
+                                            uint8_t (&s2)[PSTAGE], uint8_t (&s3)[PSTAGE],
+                                            ConstMask wm, const uint8_t *xsrc,
+                                            const uint8_t *wsrc, int ns, v16i (&acc)[14])
 {
-    constexpr int WP0 = LO > 0 ? LO - 1 : 0;
+    constexpr int WP0 = LO > 0 ? LO - 1 : 0;   // first W plane in the stage
+    constexpr int NB = LO > 0 ? 5 : 4;         // W planes the MFMAs read
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wt = w >> 1, wn = w & 1;
+    const int off = opnd_off(lane);
     const uint8_t *ws_src = wsrc + WP0 * PLANE;
     auto dma = [&](int s, uint8_t(&dst)[PSTAGE]) {
 #pragma unroll
@@ -740,59 +746,119 @@ __device__ __forceinline__ void planes_pass(uint8_t (&s0)[PSTAGE], uint8_t (&s1)
             __builtin_amdgcn_global_load_lds(g + lane * 16, dst + c * 1024, 16, 0, 0);
         }
     };
-    // step i multiplies stage cur and loads step i + 2 into stage nxt (read
-    // by step i - 1, which every wave has left at the barrier); more: there
-    // is a step i + 2
-    auto step = [&](int i, uint8_t(&cur)[PSTAGE], uint8_t(&nxt)[PSTAGE], bool more) {
-        if (more)
-            dma(i + 2, nxt);
-        const uint8_t *xs = cur + wt * SLICE;
-        const uint8_t *ws = cur + PX_BYTES - WP0 * PLANE + wn * SLICE;
-        mfma_window<LO>(acc, xs, ws, lane);
-        if (LO > 0 && ((wm[i] >> WP0) & 1u))   // a scalar load: no wait on the DMA
-            mfma_plane_w<WP0>(acc, xs, ws, lane);
-        // this wave's DMA into the next stage has landed; the barrier makes
-        // every wave's visible
-        if (more)
+    v4i A0[7], B0[NB], A1[7], B1[NB];
+    auto rd = [&](const uint8_t(&src)[PSTAGE], v4i (&A)[7], v4i (&B)[NB]) {
+#pragma unroll
+        for (int a = 0; a < 7; ++a)
+            A[a] = *reinterpret_cast<const v4i *>(src + wt * SLICE + a * PLANE + off);
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            B[j] = *reinterpret_cast<const v4i *>(src + PX_BYTES + j * PLANE + wn * SLICE + off);
+    };
+    // the step's MFMAs; ext: its W tile reaches plane LO - 1.  The reads of
+    // the next step's operands (issued just before) go out one per MFMA
+    // from the start, so they finish under the MFMAs.
+    auto mult = [&](bool ext, const v4i (&A)[7], const v4i (&B)[NB]) {
+#pragma unroll
+        for (int a = 0; a < 7; ++a)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[a + LO + j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[a], B[LO - WP0 + j],
+                                                                        acc[a + LO + j], 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 7 + NB; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 28 - 7 - NB, 0);
+        if (LO > 0 && ext) {
+#pragma unroll
+            for (int a = 0; a < 7; ++a)
+                acc[a + WP0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[a], B[0], acc[a + WP0], 0,
+                                                                     0, 0);
+        }
+    };
+    auto ext_of = [&](int i) {
+        uint32_t e = LO > 0 ? wm[i] : 0;
+        asm volatile("" : "+s"(e));
+        return ((e >> WP0) & 1u) != 0;
+    };
+    // wait until at most n of this wave's chunk DMAs are in flight
+    auto wait_n = [&](int n) {
+        if (n >= 12)
+            wait_vm<12>();
+        else if (n >= 6)
             wait_vm<6>();
         else
             wait_vm<0>();
-        stage_barrier();
     };
-    // The main loop runs groups of three steps that all load ahead (no
-    // branch around a DMA, so the compiler's own waits stay at vmcnt(6));
-    // the last two to four steps run with the tests.
-    int i = 0;
-    if (ns >= 5) {
+    // prologue: steps 0..2 in flight, step 0 landed and read
+    if (ns > 0)
         dma(0, s0);
+    if (ns > 1)
         dma(1, s1);
+    if (ns > 2)
+        dma(2, s2);
+    wait_n(6 * (min(ns, 3) - 1));
+    stage_barrier();
+    if (ns > 0)
+        rd(s0, A0, B0);
+    // steady state: every step has a step i + 3 to load.  The group's four
+    // step masks come in one scalar load at its top, held there by the
+    // empty asm (the wave waits for its operand reads at that point anyway;
+    // a wait in mid-step would also wait for the reads just issued).
+    int i = 0;
+    for (; i + 6 < ns; i += 4) {
+        uint32_t e0 = 0, e1 = 0, e2 = 0, e3 = 0;
+        if (LO > 0) {
+            e0 = wm[i];
+            e1 = wm[i + 1];
+            e2 = wm[i + 2];
+            e3 = wm[i + 3];
+            asm volatile("" : "+s"(e0), "+s"(e1), "+s"(e2), "+s"(e3));
+        }
         wait_vm<6>();
         stage_barrier();
-        do {
-            step(i, s0, s2, true);
-            step(i + 1, s1, s0, true);
-            step(i + 2, s2, s1, true);
-            i += 3;
-        } while (i + 4 < ns);
-    } else {
-        if (ns > 0)
-            dma(0, s0);
-        if (ns > 1) {
-            dma(1, s1);
-            wait_vm<6>();
-        } else {
-            wait_vm<0>();
-        }
+        dma(i + 3, s3);
+        rd(s1, A1, B1);
+        mult((e0 >> WP0) & 1u, A0, B0);
+        wait_vm<6>();
         stage_barrier();
+        dma(i + 4, s0);
+        rd(s2, A0, B0);
+        mult((e1 >> WP0) & 1u, A1, B1);
+        wait_vm<6>();
+        stage_barrier();
+        dma(i + 5, s1);
+        rd(s3, A1, B1);
+        mult((e2 >> WP0) & 1u, A0, B0);
+        wait_vm<6>();
+        stage_barrier();
+        dma(i + 6, s2);
+        rd(s0, A0, B0);
+        mult((e3 >> WP0) & 1u, A1, B1);
     }
-    if (i < ns)
-        step(i, s0, s2, i + 2 < ns);
-    if (i + 1 < ns)
-        step(i + 1, s1, s0, i + 3 < ns);
-    if (i + 2 < ns)
-        step(i + 2, s2, s1, i + 4 < ns);
-    if (i + 3 < ns)
-        step(i + 3, s0, s2, false);
+    // the last zero to six steps (i is a multiple of four: stages continue
+    // the ring)
+    auto tail = [&](int k, uint8_t(&nxt_st)[PSTAGE], uint8_t(&ld_st)[PSTAGE], v4i(&Ac)[7],
+                    v4i(&Bc)[NB], v4i(&An)[7], v4i(&Bn)[NB]) {
+        if (k >= ns)
+            return;
+        wait_n(k + 1 < ns ? 6 * (min(ns - 1, k + 2) - (k + 1)) : 0);
+        stage_barrier();
+        if (k + 3 < ns)
+            dma(k + 3, ld_st);
+        const bool ext = ext_of(k);
+        if (k + 1 < ns)
+            rd(nxt_st, An, Bn);
+        mult(ext, Ac, Bc);
+    };
+    tail(i, s1, s3, A0, B0, A1, B1);
+    tail(i + 1, s2, s0, A1, B1, A0, B0);
+    tail(i + 2, s3, s1, A0, B0, A1, B1);
+    tail(i + 3, s0, s2, A1, B1, A0, B0);
+    tail(i + 4, s1, s3, A0, B0, A1, B1);
+    tail(i + 5, s2, s0, A1, B1, A0, B0);
 }
 
 // grid (ceil(N/64) * ceil(T/64), 1, S) over operands split by k_planes
@@ -811,6 +877,7 @@ k_gemm_i8p(int64_t *__restrict__ Y, uint64_t *__restrict__ P, int *__restrict__ 
     __shared__ __align__(16) uint8_t st0[PSTAGE];
     __shared__ __align__(16) uint8_t st1[PSTAGE];
     __shared__ __align__(16) uint8_t st2[PSTAGE];
+    __shared__ __align__(16) uint8_t st3[PSTAGE];
     __shared__ uint32_t red[2][4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     int n_tile, t_tile;
@@ -847,11 +914,11 @@ k_gemm_i8p(int64_t *__restrict__ Y, uint64_t *__restrict__ P, int *__restrict__ 
     const uint8_t *wsrc = Wp + ((size_t)n_tile * nsteps + s0) * 8 * PLANE;
     const ConstMask wm = (ConstMask)(Wm + (size_t)n_tile * nsteps + s0);
     switch (LO) {
-    case 0: planes_pass<0>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
-    case 1: planes_pass<1>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
-    case 2: planes_pass<2>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
-    case 3: planes_pass<3>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
-    default: planes_pass<4>(st0, st1, st2, wm, xsrc, wsrc, ns, acc); break;
+    case 0: planes_pass<0>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
+    case 1: planes_pass<1>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
+    case 2: planes_pass<2>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
+    case 3: planes_pass<3>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
+    default: planes_pass<4>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
     }
 
     // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32
