@@ -92,6 +92,21 @@ int q48_gemm(q48_ctx *ctx, int64_t *Y, const int64_t *W, const int64_t *X,
 int q48_gemm_ex(q48_ctx *ctx, int64_t *Y, const int64_t *W, const int64_t *X,
                 int T, int N, int K, int kernel);
 
+/* A weight matrix's digit planes, prepared once for every later q48_gemm on
+ * it (the int8 kernel otherwise splits W into planes in each call that
+ * takes the planes path).  q48_gemm_planes_bytes gives the size of the
+ * buffer (device memory the caller owns, 16-byte aligned; about 8 bytes per
+ * weight); q48_gemm_prepare fills it from W [N][K]; q48_gemm_prepared is
+ * q48_gemm over W with those planes (W itself is still read where a block's
+ * digits leave the int8 kernel's window, and for T = 1).  Same bits as
+ * q48_gemm.  The planes describe W as it was when prepared: prepare again
+ * after W changes.  No reference counterpart (the reference has no batched
+ * prefill): it exists for callers that run many prefills over one model. */
+int q48_gemm_planes_bytes(int N, int K, size_t *bytes);
+int q48_gemm_prepare(q48_ctx *ctx, void *Wp, const int64_t *W, int N, int K);
+int q48_gemm_prepared(q48_ctx *ctx, int64_t *Y, const int64_t *W, const void *Wp,
+                      const int64_t *X, int T, int N, int K);
+
 /* out = rmsnorm(x) * w.  Replaces rmsnorm (llama_int.c:1048-1058). */
 int q48_rmsnorm(q48_ctx *ctx, int64_t *out, const int64_t *x,
                 const int64_t *w, int dim);

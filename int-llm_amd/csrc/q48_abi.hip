@@ -414,7 +414,7 @@ int q48_gemm_ex(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int 
              (kernel == Q48_GEMM_AUTO && q48_gemm_auto_kernel(T, N, K) == Q48_GEMM_VALU))
         rc = q48_launch_gemm(c, Y, W, X, T, N, K);
     else
-        rc = q48_launch_gemm_i8(c, Y, W, X, T, N, K, kernel);
+        rc = q48_launch_gemm_i8(c, Y, W, X, T, N, K, kernel, nullptr);
     if (rc == Q48_ENOMEM)
         return rc;
     return launch_rc(rc);
@@ -423,6 +423,38 @@ int q48_gemm_ex(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int 
 int q48_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int T, int N, int K)
 {
     return q48_gemm_ex(c, Y, W, X, T, N, K, Q48_GEMM_AUTO);
+}
+
+int q48_gemm_planes_bytes(int N, int K, size_t *bytes)
+{
+    if (!bytes || N <= 0 || K <= 0 || N > kMaxDim || K > kMaxDim)
+        return Q48_EINVAL;
+    *bytes = q48_gemm_planes_size(N, K);
+    return Q48_OK;
+}
+
+int q48_gemm_prepare(q48_ctx *c, void *Wp, const int64_t *W, int N, int K)
+{
+    if (!c || !Wp || !W || N <= 0 || K <= 0 || N > kMaxDim || K > kMaxDim)
+        return Q48_EINVAL;
+    if ((((uintptr_t)W) & 7) != 0 || (((uintptr_t)Wp) & 15) != 0)
+        return Q48_EINVAL;
+    return launch_rc(q48_launch_gemm_prepare(c, Wp, W, N, K));
+}
+
+int q48_gemm_prepared(q48_ctx *c, int64_t *Y, const int64_t *W, const void *Wp,
+                      const int64_t *X, int T, int N, int K)
+{
+    if (!c || !Y || !W || !Wp || !X || T <= 0 || N <= 0 || K <= 0 || T > 65535 * 64 ||
+        N > kMaxDim || K > kMaxDim)
+        return Q48_EINVAL;
+    if ((((uintptr_t)W | (uintptr_t)X | (uintptr_t)Y) & 7) != 0 || (((uintptr_t)Wp) & 15) != 0)
+        return Q48_EINVAL;
+    int rc = T == 1 ? q48_launch_gemv(c, Y, W, X, N, K)
+                    : q48_launch_gemm_i8(c, Y, W, X, T, N, K, Q48_GEMM_I8, Wp);
+    if (rc == Q48_ENOMEM)
+        return rc;
+    return launch_rc(rc);
 }
 
 int q48_rmsnorm(q48_ctx *c, int64_t *out, const int64_t *x, const int64_t *w, int dim)

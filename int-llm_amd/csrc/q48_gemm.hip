@@ -970,27 +970,49 @@ int q48_gemm_i8_splits(int T, int N, int K, int cu_count)
     return s > min_s ? s : min_s;
 }
 
+size_t q48_gemm_planes_size(int N, int K)
+{
+    const size_t tiles = (size_t)((N + MN - 1) / MN) * ((K + MK - 1) / MK);
+    return tiles * 8 * PLANE + ((tiles * 4 + 255) & ~(size_t)255);
+}
+
+int q48_launch_gemm_prepare(q48_ctx *c, void *Wp, const int64_t *W, int N, int K)
+{
+    const int steps = (K + MK - 1) / MK, nn = (N + MN - 1) / MN;
+    if ((size_t)nn * steps > 0x7fffffff)
+        return Q48_EINVAL;
+    uint8_t *p = (uint8_t *)Wp;
+    uint32_t *m = (uint32_t *)(p + (size_t)nn * steps * 8 * PLANE);
+    hipLaunchKernelGGL(k_planes, dim3(nn * steps), dim3(256), 0, c->stream, p, m, W, N, K,
+                       steps);
+    return (int)hipGetLastError();
+}
+
 int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int T,
-                       int N, int K, int kernel)
+                       int N, int K, int kernel, const void *Wpre)
 {
     const int S = q48_gemm_i8_splits(T, N, K, c->cu_count);
     const int steps = (K + MK - 1) / MK;
     const int spb = (steps + S - 1) / S;
     const int nt = (T + MT - 1) / MT, nn = (N + MN - 1) / MN, nb = nn * nt;
-    // the planes path pays one split of X and W per call: it wins once
-    // tiles are reused enough (measured: T >= 512 with N >= 2048 faster by
-    // 7-39%, N = 256 slower by 5-22%, T = 128 even)
-    const bool planes = kernel == Q48_GEMM_I8_PLANES ||
-                        (kernel != Q48_GEMM_I8_FUSED && T >= 256 && N >= 1024);
+    // the planes path pays one split of X (and of W unless prepared) per
+    // call: it wins once tiles are reused enough (measured: T >= 512 with
+    // N >= 2048 faster by 7-39%, N = 256 slower by 5-22%, T = 128 even when
+    // W is split in the call, faster by about a quarter when it is not)
+    const bool fits = (size_t)max(nt, nn) * steps <= 0x7fffffff;
+    const bool planes =
+        fits && (kernel == Q48_GEMM_I8_PLANES ||
+                 (kernel != Q48_GEMM_I8_FUSED && T >= (Wpre ? 128 : 256) && N >= 1024));
+    const bool wsplit = planes && !Wpre;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     // workspace: the blocks' redo flags, (S > 1) the int128 partials, then
     // (planes path) X and W digit planes and their masks
     const size_t flags = al((size_t)nb * S * sizeof(int));
     const size_t part = S > 1 ? 16 * (size_t)S * T * N : 0;
     const size_t xpl = planes ? (size_t)nt * steps * 8 * PLANE : 0;
-    const size_t wpl = planes ? (size_t)nn * steps * 8 * PLANE : 0;
+    const size_t wpl = wsplit ? (size_t)nn * steps * 8 * PLANE : 0;
     const size_t xms = planes ? al((size_t)nt * steps * 4) : 0;
-    const size_t wms = planes ? al((size_t)nn * steps * 4) : 0;
+    const size_t wms = wsplit ? al((size_t)nn * steps * 4) : 0;
     int rc = q48_ws_reserve(c, flags + part + xpl + wpl + xms + wms);
     if (rc)
         return rc;
@@ -1005,8 +1027,14 @@ int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *
         uint32_t *Xm = (uint32_t *)(Wp + wpl), *Wm = (uint32_t *)((char *)Xm + xms);
         hipLaunchKernelGGL(k_planes, dim3(nt * steps), dim3(256), 0, c->stream, Xp, Xm, X, T, K,
                            steps);
-        hipLaunchKernelGGL(k_planes, dim3(nn * steps), dim3(256), 0, c->stream, Wp, Wm, W, N, K,
-                           steps);
+        if (Wpre) {
+            // planes from q48_launch_gemm_prepare: masks after the planes
+            Wp = (uint8_t *)Wpre;
+            Wm = (uint32_t *)(Wp + (size_t)nn * steps * 8 * PLANE);
+        } else {
+            hipLaunchKernelGGL(k_planes, dim3(nn * steps), dim3(256), 0, c->stream, Wp, Wm, W, N,
+                               K, steps);
+        }
         hipLaunchKernelGGL(k_gemm_i8p, grid, dim3(256), 0, c->stream, Y, P, redo, Xp, Xm, Wp, Wm,
                            T, N, steps, spb);
     } else if (vec) {

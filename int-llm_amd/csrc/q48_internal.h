@@ -134,9 +134,13 @@ int q48_launch_gemm(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X,
                     int T, int N, int K);
 // int8-digit GEMM on the matrix cores (q48_gemm.hip); same bits as
 // q48_launch_gemm.  kernel: Q48_GEMM_I8_FUSED or Q48_GEMM_I8_PLANES, anything
-// else picks one of them by shape.
+// else picks one of them by shape.  Wpre: W's planes from
+// q48_launch_gemm_prepare (or NULL: the planes path splits W in the call).
 int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X,
-                       int T, int N, int K, int kernel);
+                       int T, int N, int K, int kernel, const void *Wpre);
+// bytes of W's digit planes and masks for q48_launch_gemm_prepare
+size_t q48_gemm_planes_size(int N, int K);
+int q48_launch_gemm_prepare(q48_ctx *c, void *Wp, const int64_t *W, int N, int K);
 // K splits the int8 GEMM uses for this shape on cu_count compute units
 int q48_gemm_i8_splits(int T, int N, int K, int cu_count);
 // Q48_GEMM_VALU or Q48_GEMM_I8: the kernel q48_gemm runs for this shape

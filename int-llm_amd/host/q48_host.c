@@ -66,6 +66,10 @@ struct q48h_model {
     int batched_prefill;        /* generate's prompt through q48h_prefill (default) */
     int64_t *pf;                /* device: batched-prefill rows (grown on demand) */
     size_t pf_words;
+    void *wp;                   /* device: digit planes of every layer's four projection
+                                   matrices (q48_gemm_prepare), for the batched prefill */
+    int wp_on;                  /* the prefill may prepare and use them (default) */
+    int wp_ok;                  /* wp holds the planes of the current weights */
     int64_t *rec;               /* device: logits of recorded decode steps [rec_cap][vocab] */
     int rec_cap;
     int record;                 /* the decode step records its logits into rec */
@@ -236,6 +240,7 @@ static int model_alloc(q48h_model **out, q48_ctx *ctx, const q48h_config *cfg, i
     m->prefetch = 1;
     m->rope_gemv = 1;
     m->batched_prefill = 1;
+    m->wp_on = 1;
     if ((rc = q48_malloc(ctx, (void **)&m->w, weight_elems(m) * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->kc, kvn * 8)) ||
         (rc = q48_malloc(ctx, (void **)&m->vc, kvn * 8)) ||
@@ -298,6 +303,80 @@ static void drop_bf16(q48h_model *m)
     m->bf16 = 0;
 }
 
+/* Byte offsets of a layer's prepared q|k|v, o, gate|up and down planes
+ * within the layer's stride of m->wp; returns the stride (0 on error). */
+static size_t planes_layout(const q48h_model *m, size_t off[4])
+{
+    const q48h_config *c = &m->c;
+    const int dim = c->dim, kvd = c->n_kv_heads * c->head_dim, ffn = c->ffn;
+    const int shape[4][2] = {{dim + 2 * kvd, dim}, {dim, dim}, {2 * ffn, dim}, {dim, ffn}};
+    size_t s = 0;
+    for (int i = 0; i < 4; ++i) {
+        size_t b = 0;
+        if (q48_gemm_planes_bytes(shape[i][0], shape[i][1], &b) != Q48_OK)
+            return 0;
+        off[i] = s;
+        s += (b + 255) & ~(size_t)255;
+    }
+    return s;
+}
+
+/* The prefill's prepared planes, made once per set of weights.  Without
+ * device memory for them the prefill goes on splitting W in each call. */
+static int prepare_planes(q48h_model *m)
+{
+    if (!m->wp_on || m->wp_ok)
+        return Q48_OK;
+    const q48h_config *c = &m->c;
+    const int dim = c->dim, kvd = c->n_kv_heads * c->head_dim, ffn = c->ffn;
+    size_t off[4];
+    const size_t stride = planes_layout(m, off);
+    if (!stride)
+        return Q48_EINVAL;
+    if (!m->wp) {
+        int rc = q48_malloc(m->ctx, &m->wp, stride * (size_t)c->n_layers);
+        if (rc == Q48_ENOMEM) {
+            m->wp = NULL;
+            m->wp_on = 0;
+            return Q48_OK;
+        }
+        if (rc)
+            return rc;
+    }
+    for (int l = 0; l < c->n_layers; ++l) {
+        const int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
+        char *p = (char *)m->wp + (size_t)l * stride;
+        int rc;
+        if ((rc = q48_gemm_prepare(m->ctx, p + off[0], b + m->lo_qkv, dim + 2 * kvd, dim)) ||
+            (rc = q48_gemm_prepare(m->ctx, p + off[1], b + m->lo_wo, dim, dim)) ||
+            (rc = q48_gemm_prepare(m->ctx, p + off[2], b + m->lo_gu, 2 * ffn, dim)) ||
+            (rc = q48_gemm_prepare(m->ctx, p + off[3], b + m->lo_wd, dim, ffn)))
+            return rc;
+    }
+    m->wp_ok = 1;
+    return Q48_OK;
+}
+
+void q48h_model_set_gemm_planes(q48h_model *m, int on)
+{
+    if (!m)
+        return;
+    m->wp_on = on != 0;
+    if (!m->wp_on && m->wp) {
+        (void)q48_sync(m->ctx);   /* earlier prefill kernels may still read them */
+        q48_free(m->ctx, m->wp);
+        m->wp = NULL;
+        m->wp_ok = 0;
+    }
+}
+
+/* A GEMM of the prefill: through W's prepared planes when there are some. */
+static int prefill_gemm(q48_ctx *x, int64_t *Y, const int64_t *W, const void *Wp,
+                        const int64_t *X, int T, int N, int K)
+{
+    return Wp ? q48_gemm_prepared(x, Y, W, Wp, X, T, N, K) : q48_gemm(x, Y, W, X, T, N, K);
+}
+
 int q48h_model_set_bf16(q48h_model *m, int on)
 {
     if (!m)
@@ -351,6 +430,7 @@ void q48h_model_free(q48h_model *m)
     q48_free(m->ctx, m->d_tokens);
     q48_free(m->ctx, m->d_rng);
     q48_free(m->ctx, m->pf);
+    q48_free(m->ctx, m->wp);
     q48_free(m->ctx, m->rec);
     free(m);
 }
@@ -498,6 +578,7 @@ int q48h_upload(q48h_model *m, const char *name, const int64_t *host, int64_t n)
     if (tensor_slot(m, name, &dst, &want) || n != want)
         return Q48_EINVAL;
     drop_bf16(m);   /* the bfloat16 copy would be stale */
+    m->wp_ok = 0;   /* and so would the prefill's planes */
     return q48_memcpy_h2d(m->ctx, dst, host, (size_t)n * 8);
 }
 
@@ -1015,22 +1096,32 @@ int q48h_prefill(q48h_model *m, const int *tokens, int T, int p0, int64_t *logit
     int64_t *GU = D + (size_t)T * dim, *HF = GU + (size_t)T * 2 * ffn;
     int64_t *LG = HF + (size_t)T * ffn;
     int *ids = (int *)(LG + nlog);
+    /* prepared weight planes pay off from 128 tokens (q48_gemm_prepared) */
+    size_t poff[4] = {0, 0, 0, 0}, pstride = 0;
+    if (T >= 128) {
+        TRY(prepare_planes(m));
+        if (m->wp_ok)
+            pstride = planes_layout(m, poff);
+    }
     TRY(q48_memcpy_h2d(x, ids, tokens, (size_t)T * sizeof(int)));
     TRY(q48_embed_rows(x, H, m->w + m->off_embed, ids, T, dim));
     for (int l = 0; l < c->n_layers; ++l) {
         const int64_t *b = m->w + m->off_layers + (size_t)l * m->layer_elems;
+        const char *wp = pstride ? (const char *)m->wp + (size_t)l * pstride : NULL;
+#define WP(i) (wp ? wp + poff[i] : NULL)
         TRY(q48_rmsnorm_rows(x, XN, H, b + m->lo_an, T, dim));
-        TRY(q48_gemm(x, QKV, b + m->lo_qkv, XN, T, nq, dim));
+        TRY(prefill_gemm(x, QKV, b + m->lo_qkv, WP(0), XN, T, nq, dim));
         TRY(q48_rope_store_rows(x, QKV, m->kc, m->vc, l, p0, T, c->n_heads, c->n_kv_heads, hd,
                                 c->max_seq));
         TRY(q48_attn_prefill(x, ATT, QKV, m->kc, m->vc, l, p0, T, c->n_heads, c->n_kv_heads, hd,
                              c->max_seq));
-        TRY(q48_gemm(x, D, b + m->lo_wo, ATT, T, dim, dim));
+        TRY(prefill_gemm(x, D, b + m->lo_wo, WP(1), ATT, T, dim, dim));
         TRY(q48_add(x, H, D, T * dim));
         TRY(q48_rmsnorm_rows(x, XN, H, b + m->lo_fn, T, dim));
-        TRY(q48_gemm(x, GU, b + m->lo_gu, XN, T, 2 * ffn, dim));
+        TRY(prefill_gemm(x, GU, b + m->lo_gu, WP(2), XN, T, 2 * ffn, dim));
         TRY(q48_silu_mul_rows(x, HF, GU, T, ffn));
-        TRY(q48_gemm(x, D, b + m->lo_wd, HF, T, dim, ffn));
+        TRY(prefill_gemm(x, D, b + m->lo_wd, WP(3), HF, T, dim, ffn));
+#undef WP
         TRY(q48_add(x, H, D, T * dim));
     }
     TRY(q48_rmsnorm_rows(x, XN, H, m->w + m->off_norm, T, dim));

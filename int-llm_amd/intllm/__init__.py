@@ -45,6 +45,9 @@ ABI_SIGNATURES = {
     "q48_gemv": [_P, _P, _P, _P, _I, _I],
     "q48_gemm": [_P, _P, _P, _P, _I, _I, _I],
     "q48_gemm_ex": [_P, _P, _P, _P, _I, _I, _I, _I],
+    "q48_gemm_planes_bytes": [_I, _I, C.POINTER(C.c_size_t)],
+    "q48_gemm_prepare": [_P, _P, _P, _I, _I],
+    "q48_gemm_prepared": [_P, _P, _P, _P, _P, _I, _I, _I],
     "q48_bf16_pack": [_P, _P, _P, _SZ, C.POINTER(C.c_int)],
     "q48_gemv_bf16": [_P, _P, _P, _P, _I, _I],
     "q48_norm_gemv_stats_bf16": [_P, _P, _P, _P, _P, _P, _I, _I],
@@ -307,6 +310,22 @@ class Context:
             return check("q48_gemm", hip_lib().q48_gemm(self.h, Y, W, X, T, N, K))
         return check("q48_gemm_ex", hip_lib().q48_gemm_ex(self.h, Y, W, X, T, N, K, kernel))
 
+    @staticmethod
+    def gemm_planes_bytes(N, K) -> int:
+        """Bytes of a prepared weight's digit planes (q48_gemm_prepare)."""
+        out = C.c_size_t(0)
+        check("q48_gemm_planes_bytes", hip_lib().q48_gemm_planes_bytes(N, K, C.byref(out)))
+        return out.value
+
+    def gemm_prepare(self, Wp, W, N, K):
+        """W [N][K]'s digit planes into the device buffer Wp."""
+        return check("q48_gemm_prepare", hip_lib().q48_gemm_prepare(self.h, Wp, W, N, K))
+
+    def gemm_prepared(self, Y, W, Wp, X, T, N, K):
+        """q48_gemm over W with its planes Wp from gemm_prepare."""
+        return check("q48_gemm_prepared",
+                     hip_lib().q48_gemm_prepared(self.h, Y, W, Wp, X, T, N, K))
+
     def rmsnorm(self, out, x, w, dim):
         return check("q48_rmsnorm", hip_lib().q48_rmsnorm(self.h, out, x, w, dim))
 
@@ -498,6 +517,7 @@ HOST_SIGNATURES = {
     "q48h_model_set_bf16": ([_P, _I], C.c_int),
     "q48h_model_set_sampling": ([_P, C.c_int64, _I, C.c_int64, C.c_uint64], C.c_int),
     "q48h_model_set_batched_prefill": ([_P, _I], None),
+    "q48h_model_set_gemm_planes": ([_P, _I], None),
     "q48h_prefill": ([_P, C.POINTER(C.c_int), _I, _I, _P, C.POINTER(C.c_int)], C.c_int),
 
     "q48h_gemv_sweep": ([_P, _I, C.POINTER(C.c_int), C.POINTER(C.c_double)], C.c_int),
@@ -600,6 +620,11 @@ class HostModel:
     def set_batched_prefill(self, on: bool):
         """generate's prompt in one batched pass (default) or per token."""
         host_lib().q48h_model_set_batched_prefill(self.h, int(bool(on)))
+
+    def set_gemm_planes(self, on: bool):
+        """The batched prefill through prepared weight planes (default) or
+        splitting W in each GEMM (and freeing the planes)."""
+        host_lib().q48h_model_set_gemm_planes(self.h, int(bool(on)))
 
     def kv_reset(self):
         check("q48h_kv_reset", host_lib().q48h_kv_reset(self.h))

@@ -385,6 +385,50 @@ def test_gemm_digit_windows(ctx, oracle, case, tokens, kernel):
         b.free()
 
 
+def test_gemm_prepared_planes(ctx, oracle):
+    """q48_gemm_prepared: W's digit planes prepared once (q48_gemm_prepare),
+    then GEMMs of 1, 64, 128 and 300 tokens (the GEMV, the in-loop split,
+    and the planes path with W's planes read from the prepared buffer) over
+    bfloat16-like weights with one row tile leaving the digit window (its
+    blocks redone from W itself), against the oracle; then the buffer
+    re-prepared from other weights.  Misaligned buffers are refused."""
+    N, K = 1030, 1000
+    rng = np.random.default_rng(99)
+    W = _bf16ish(rng, N * K, 42)
+    W[40 * K + 333] = 1 << 61
+    need = intllm.Context.gemm_planes_bytes(N, K)
+    assert need >= N * K * 8
+    dW, dP = ctx.to_device(W), ctx.buffer(need // 8 + 2)
+    ctx.gemm_prepare(dP.ptr, dW.ptr, N, K)
+    for T in (1, 64, 128, 300):
+        X = rng.integers(-(1 << 52), 1 << 52, size=T * K, dtype=np.int64)
+        want = np.empty(T * N, dtype=np.int64)
+        oracle.q48o_gemm(want.ctypes.data, W.ctypes.data, X.ctypes.data, T, N, K)
+        dX, dY = ctx.to_device(X), ctx.buffer(T * N)
+        say("gemm prepared", T, N, K)
+        ctx.gemm_prepared(dY.ptr, dW.ptr, dP.ptr, dX.ptr, T, N, K)
+        assert np.array_equal(dY.download(), want), T
+        dX.free()
+        dY.free()
+    W2 = _bf16ish(rng, N * K, 35)
+    dW2 = ctx.to_device(W2)
+    ctx.gemm_prepare(dP.ptr, dW2.ptr, N, K)
+    T = 256
+    X = rng.integers(-(1 << 52), 1 << 52, size=T * K, dtype=np.int64)
+    want = np.empty(T * N, dtype=np.int64)
+    oracle.q48o_gemm(want.ctypes.data, W2.ctypes.data, X.ctypes.data, T, N, K)
+    dX, dY = ctx.to_device(X), ctx.buffer(T * N)
+    say("gemm prepared again", T, N, K)
+    ctx.gemm_prepared(dY.ptr, dW2.ptr, dP.ptr, dX.ptr, T, N, K)
+    assert np.array_equal(dY.download(), want)
+    with pytest.raises(intllm.Q48Error):
+        ctx.gemm_prepare(dP.ptr + 8, dW2.ptr, N, K)
+    with pytest.raises(intllm.Q48Error):
+        ctx.gemm_prepared(dY.ptr, dW2.ptr, dP.ptr + 8, dX.ptr, T, N, K)
+    for b in (dW, dW2, dP, dX, dY):
+        b.free()
+
+
 @pytest.mark.parametrize("kernel", GEMM_KERNELS)
 def test_gemm_extreme_digits(ctx, oracle, kernel):
     """INT64_MIN has every int8 digit at -128 (the largest digit products);

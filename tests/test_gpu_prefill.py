@@ -157,7 +157,9 @@ def test_tinyllama_prefill_equals_reference_and_sequential(ctx):
     """Config 3: the 32-token golden prompt in one pass against the
     reference's hashes and first token, then 480 more random tokens in one
     pass at p0 = 32 against the per-token forward (hashes of every row and
-    the KV cache)."""
+    the KV cache).  The 480-token pass runs its projections through the
+    weights' prepared digit planes (the default) and again splitting W in
+    each GEMM."""
     g = golden("tinyllama_generate.json")
     cfg = g["config"]
     m = intllm.HostModel(ctx, intllm.Config(*cfg))
@@ -174,6 +176,13 @@ def test_tinyllama_prefill_equals_reference_and_sequential(ctx):
         _, lg = m.prefill(more, P, cfg[6], choose=False)
         got = [intllm.fnv(r) for r in lg]
         kb = kv_rows(ctx, m, cfg, P + 480)
+        m.kv_reset()
+        m.set_gemm_planes(False)
+        say("tinyllama prefill T 32 + 480, W split per GEMM")
+        m.prefill(g["prompt"], 0, cfg[6], choose=False)
+        _, lg = m.prefill(more, P, cfg[6], choose=False)
+        assert [intllm.fnv(r) for r in lg] == got
+        m.set_gemm_planes(True)
         m.kv_reset()
         say("tinyllama sequential forward 512")
         want = []
