@@ -70,6 +70,7 @@ int q48_ws_reserve(q48_ctx *c, size_t bytes)
     size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
     if (hipMalloc(&c->ws, sz) != hipSuccess) {
         c->ws = nullptr;
+        (void)hipGetLastError();   // not left for the next launch's error check
         return Q48_ENOMEM;
     }
     c->ws_bytes = sz;
@@ -90,8 +91,11 @@ int q48_rms_reserve(q48_ctx *c, int blocks)
         c->rms_blocks = 0;
     }
     int n = blocks < 1024 ? 1024 : blocks;
-    if (hipMalloc(&c->rms_part, (size_t)n * 2 * sizeof(uint64_t)) != hipSuccess)
+    if (hipMalloc(&c->rms_part, (size_t)n * 2 * sizeof(uint64_t)) != hipSuccess) {
+        c->rms_part = nullptr;
+        (void)hipGetLastError();
         return Q48_ENOMEM;
+    }
     c->rms_blocks = n;
     return Q48_OK;
 }
@@ -218,6 +222,7 @@ int q48_malloc(q48_ctx *c, void **dptr, size_t bytes)
         return Q48_EINVAL;
     if (hipMalloc(dptr, bytes) != hipSuccess) {
         *dptr = nullptr;
+        (void)hipGetLastError();   // not left for the next launch's error check
         return Q48_ENOMEM;
     }
     return Q48_OK;
@@ -488,6 +493,7 @@ int q48_rope_init(q48_ctx *c, int head_dim, int max_seq, int theta)
         hipMalloc(&c->rope_sin, n + sizeof(int64_t)) != hipSuccess) {
         (void)hipFree(c->rope_cos);
         c->rope_cos = c->rope_sin = nullptr;
+        (void)hipGetLastError();
         return Q48_ENOMEM;
     }
     c->rope_head_dim = head_dim;
