@@ -285,6 +285,34 @@ __device__ __forceinline__ void tile_of(int b, int nn, int nt, int &n_tile, int 
     t_tile = in / gs;
 }
 
+// Register i of the 14 digit-sum accumulators as the 128-bit sum
+// S = sum_d acc[d][i] 256^d (mod 2^128, words lo and hi), where only digit
+// sums D0..D1 can be nonzero.  Groups of four digit sums are exact int64
+// (|g| < 2^31 (1 + 2^8 + 2^16 + 2^24) < 2^56), then
+// S = g0 + 2^32 g1 + 2^64 g2 + 2^96 g3 in two words with one carry.
+template <int D0, int D1>
+__device__ __forceinline__ void acc_sum128(const v16i (&acc)[14], int i, uint64_t &lo,
+                                           uint64_t &hi)
+{
+    int64_t g[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint64_t v = 0;
+#pragma unroll
+        for (int e = 3; e >= 0; --e) {
+            const int d = 4 * j + e;
+            v <<= 8;
+            if (d >= D0 && d <= D1 && d < 14)
+                v += (uint64_t)(int64_t)acc[d][i];
+        }
+        g[j] = (int64_t)v;
+    }
+    lo = (uint64_t)g[0] + ((uint64_t)g[1] << 32);
+    const uint64_t carry = lo < (uint64_t)g[0] ? 1u : 0u;
+    hi = (uint64_t)(g[0] >> 63) + (uint64_t)(g[1] >> 32) + carry + (uint64_t)g[2] +
+         ((uint64_t)g[3] << 32);
+}
+
 // The block's tiles, loaders and accumulators, shared by the kernel's paths.
 struct GemmTile {
     int64_t *Y;
@@ -482,7 +510,9 @@ __device__ __forceinline__ bool gemm_pass(const GemmTile &g, uint8_t (&lds)[2][2
     if (!ok)
         return false;
 
-    // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32
+    // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32;
+    // the window pass touches digit sums LO - 1 .. LO + 9 only
+    constexpr int D0 = LO > 0 ? LO - 1 : 0, D1 = LO < 0 ? 13 : LO + 9;
     const int nl = 32 * wn + (lane & 31), n = g.n0 + nl;
     if (n >= g.N)
         return true;
@@ -491,16 +521,13 @@ __device__ __forceinline__ bool gemm_pass(const GemmTile &g, uint8_t (&lds)[2][2
         const int tl = 32 * wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3), t = g.t0 + tl;
         if (t >= g.T)
             continue;
-        q48_u128 tot = 0;
-#pragma unroll
-        for (int d = 13; d >= 0; --d)
-            tot = (tot << 8) + (q48_u128)(q48_i128)acc[d][i];
+        uint64_t lo, hi;
+        acc_sum128<D0, D1>(acc, i, lo, hi);
         if (g.S == 1) {
-            g.Y[(size_t)t * g.N + n] = (int64_t)((q48_i128)tot >> 48);
+            g.Y[(size_t)t * g.N + n] = (int64_t)((hi << 16) | (lo >> 48));
         } else {
             uint64_t *p = g.P + 2 * (((size_t)g.z * g.T + t) * g.N + n);
-            *reinterpret_cast<ulonglong2 *>(p) = make_ulonglong2((uint64_t)tot,
-                                                                 (uint64_t)(tot >> 64));
+            *reinterpret_cast<ulonglong2 *>(p) = make_ulonglong2(lo, hi);
         }
     }
     return true;
@@ -913,35 +940,50 @@ k_gemm_i8p(int64_t *__restrict__ Y, uint64_t *__restrict__ P, int *__restrict__ 
     const uint8_t *xsrc = Xp + ((size_t)t_tile * nsteps + s0) * 8 * PLANE;
     const uint8_t *wsrc = Wp + ((size_t)n_tile * nsteps + s0) * 8 * PLANE;
     const ConstMask wm = (ConstMask)(Wm + (size_t)n_tile * nsteps + s0);
-    switch (LO) {
-    case 0: planes_pass<0>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
-    case 1: planes_pass<1>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
-    case 2: planes_pass<2>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
-    case 3: planes_pass<3>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
-    default: planes_pass<4>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc); break;
-    }
-
-    // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32
+    // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32;
+    // window LO touches digit sums LO - 1 .. LO + 9 only
     const int wt = w >> 1, wn = w & 1;
     const int n = n_tile * MN + 32 * wn + (lane & 31);
-    if (n >= N)
-        return;
+    auto store = [&](auto d0, auto d1) {
+        if (n >= N)
+            return;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int t = t_tile * MT + 32 * wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (t >= T)
-            continue;
-        q48_u128 tot = 0;
-#pragma unroll
-        for (int d = 13; d >= 0; --d)
-            tot = (tot << 8) + (q48_u128)(q48_i128)acc[d][i];
-        if (gridDim.z == 1) {
-            Y[(size_t)t * N + n] = (int64_t)((q48_i128)tot >> 48);
-        } else {
-            uint64_t *p = P + 2 * (((size_t)blockIdx.z * T + t) * N + n);
-            *reinterpret_cast<ulonglong2 *>(p) = make_ulonglong2((uint64_t)tot,
-                                                                 (uint64_t)(tot >> 64));
+        for (int i = 0; i < 16; ++i) {
+            const int t = t_tile * MT + 32 * wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+            if (t >= T)
+                continue;
+            uint64_t lo, hi;
+            acc_sum128<decltype(d0)::value, decltype(d1)::value>(acc, i, lo, hi);
+            if (gridDim.z == 1) {
+                Y[(size_t)t * N + n] = (int64_t)((hi << 16) | (lo >> 48));
+            } else {
+                uint64_t *p = P + 2 * (((size_t)blockIdx.z * T + t) * N + n);
+                *reinterpret_cast<ulonglong2 *>(p) = make_ulonglong2(lo, hi);
+            }
         }
+    };
+    using std::integral_constant;
+    switch (LO) {
+    case 0:
+        planes_pass<0>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        store(integral_constant<int, 0>{}, integral_constant<int, 9>{});
+        break;
+    case 1:
+        planes_pass<1>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        store(integral_constant<int, 0>{}, integral_constant<int, 10>{});
+        break;
+    case 2:
+        planes_pass<2>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        store(integral_constant<int, 1>{}, integral_constant<int, 11>{});
+        break;
+    case 3:
+        planes_pass<3>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        store(integral_constant<int, 2>{}, integral_constant<int, 12>{});
+        break;
+    default:
+        planes_pass<4>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        store(integral_constant<int, 3>{}, integral_constant<int, 13>{});
+        break;
     }
 }
 

@@ -11,7 +11,9 @@ on, and its digit-plane window, checked by brute force with Python integers
 3. the window: for X digits in planes 0..6 and W digits in planes
    LO - 1 .. LO + 3, the pairs (a <= 6, b in the window) alone give the same
    bits, and the conservative overflow test of the window split (the high
-   word >= 0x7F7F7F7F) catches every value that overflows.
+   word >= 0x7F7F7F7F) catches every value that overflows;
+4. the epilogue: the 128-bit sum of 256^d Q_d from four exact int64 group
+   sums and one carry.
 
 A plausible slip (d_7 offset like the others, a missing plane-8 term, the
 plane-8 flag from the wrong sign test, a window one plane short) fails one of
@@ -145,3 +147,51 @@ def test_overflow_test_is_conservative():
         assert (v >> 32) >= 0x7F7F7F7F
     for v in [rng.randrange(-(1 << 63), lo) for _ in range(5000)]:
         assert digits9(v)[8] == 0
+
+
+def sum128_grouped(acc, carry=True, arith=True):
+    """The kernels' epilogue (acc_sum128): four exact int64 group sums of
+    four digit sums each, then S = g0 + 2^32 g1 + 2^64 g2 + 2^96 g3 as two
+    64-bit words with one carry, every operation wrapped to 64 bits."""
+    def s64(x):
+        x &= M64
+        return x - (1 << 64) if x >> 63 else x
+    g = []
+    for j in range(4):
+        v = 0
+        for e in range(3, -1, -1):
+            d = 4 * j + e
+            v = (v << 8) & M64
+            if d < 14:
+                v = (v + (acc[d] & M64)) & M64
+        g.append(s64(v))
+    lo = ((g[0] & M64) + ((g[1] << 32) & M64)) & M64
+    c = 1 if carry and lo < (g[0] & M64) else 0
+    g1hi = (g[1] >> 32) & M64 if arith else ((g[1] & M64) >> 32)
+    hi = (((g[0] >> 63) & M64) + g1hi + c + (g[2] & M64) + ((g[3] << 32) & M64)) & M64
+    return lo, hi
+
+
+def test_epilogue_grouped_sum_is_the_128_bit_sum():
+    """S mod 2^128 and the output word bits 48..111 from the grouped form
+    equal the direct sum of 256^d acc_d for int32 digit sums, extremes
+    included; dropping the carry or shifting g1 logically fails."""
+    rng = random.Random(13)
+    lim = (1 << 31) - 1
+    cases = [[lim] * 14, [-(1 << 31)] * 14, [0] * 14, [-1] * 14,
+             [lim if d % 2 else -(1 << 31) for d in range(14)]]
+    cases += [[rng.randint(-(1 << 31), lim) for _ in range(14)] for _ in range(3000)]
+    cases += [[rng.choice([0, 1, -1, lim, -(1 << 31)]) for _ in range(14)] for _ in range(1000)]
+    M128 = (1 << 128) - 1
+    bad_carry = bad_arith = 0
+    for acc in cases:
+        want = sum(a << (8 * d) for d, a in enumerate(acc)) & M128
+        lo, hi = sum128_grouped(acc)
+        assert (hi << 64 | lo) == want, acc
+        out = ((hi << 16) | (lo >> 48)) & M64
+        assert out == (want >> 48) & M64
+        l2, h2 = sum128_grouped(acc, carry=False)
+        bad_carry += (h2 << 64 | l2) != want
+        l3, h3 = sum128_grouped(acc, arith=False)
+        bad_arith += (h3 << 64 | l3) != want
+    assert bad_carry > 100 and bad_arith > 100
