@@ -1036,6 +1036,9 @@ int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *
     const int S = q48_gemm_i8_splits(T, N, K, c->cu_count);
     const int steps = (K + MK - 1) / MK;
     const int spb = (steps + S - 1) / S;
+    // blocks (and their redo flags) are numbered in int
+    if ((size_t)((N + MN - 1) / MN) * ((T + MT - 1) / MT) * S > 0x7fffffff)
+        return Q48_EINVAL;
     const int nt = (T + MT - 1) / MT, nn = (N + MN - 1) / MN, nb = nn * nt;
     // the planes path pays one split of X (and of W unless prepared) per
     // call: it wins once tiles are reused enough (measured: T >= 512 with
