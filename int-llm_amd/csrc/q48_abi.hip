@@ -420,8 +420,8 @@ int q48_gemm_ex(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *X, int 
         rc = q48_launch_gemm(c, Y, W, X, T, N, K);
     else
         rc = q48_launch_gemm_i8(c, Y, W, X, T, N, K, kernel, nullptr);
-    if (rc == Q48_ENOMEM)
-        return rc;
+    if (rc < 0)
+        return rc;   // a Q48_E* code from the launcher (ENOMEM, EINVAL)
     return launch_rc(rc);
 }
 
@@ -444,7 +444,8 @@ int q48_gemm_prepare(q48_ctx *c, void *Wp, const int64_t *W, int N, int K)
         return Q48_EINVAL;
     if ((((uintptr_t)W) & 7) != 0 || (((uintptr_t)Wp) & 15) != 0)
         return Q48_EINVAL;
-    return launch_rc(q48_launch_gemm_prepare(c, Wp, W, N, K));
+    const int rc = q48_launch_gemm_prepare(c, Wp, W, N, K);
+    return rc < 0 ? rc : launch_rc(rc);
 }
 
 int q48_gemm_prepared(q48_ctx *c, int64_t *Y, const int64_t *W, const void *Wp,
@@ -457,8 +458,8 @@ int q48_gemm_prepared(q48_ctx *c, int64_t *Y, const int64_t *W, const void *Wp,
         return Q48_EINVAL;
     int rc = T == 1 ? q48_launch_gemv(c, Y, W, X, N, K)
                     : q48_launch_gemm_i8(c, Y, W, X, T, N, K, Q48_GEMM_I8, Wp);
-    if (rc == Q48_ENOMEM)
-        return rc;
+    if (rc < 0)
+        return rc;   // a Q48_E* code from the launcher (ENOMEM, EINVAL)
     return launch_rc(rc);
 }
 
@@ -531,8 +532,8 @@ int q48_attn_decode(q48_ctx *c, int64_t *out, const int64_t *q, int64_t *kcache,
                                       n_heads, n_kv, head_dim, max_seq, 0, nullptr, 0)
                  : q48_launch_attn(c, out, q, kcache, vcache, k_new, v_new, layer, dp, pos,
                                    n_heads, n_kv, head_dim, max_seq);
-    if (rc == Q48_ENOMEM)
-        return rc;
+    if (rc < 0)
+        return rc;   // a Q48_E* code from the launcher (ENOMEM, EINVAL)
     return launch_rc(rc);
 }
 
@@ -805,8 +806,8 @@ int q48_attn_decode_rope_prefetch(q48_ctx *c, int64_t *out, const int64_t *q, in
     int rc = q48_launch_attn_v2(c, out, q, kcache, vcache, k_new, v_new, layer, dp, pos, n_heads,
                                 n_kv, head_dim, max_seq, 1, prefetch,
                                 prefetch ? prefetch_bytes : 0);
-    if (rc == Q48_ENOMEM)
-        return rc;
+    if (rc < 0)
+        return rc;   // a Q48_E* code from the launcher (ENOMEM, EINVAL)
     return launch_rc(rc);
 }
 
