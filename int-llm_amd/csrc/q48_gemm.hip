@@ -756,7 +756,8 @@ template <int LO>
 __device__ __forceinline__ void planes_pass(uint8_t (&s0)[PSTAGE], uint8_t (&s1)[PSTAGE],
                                             uint8_t (&s2)[PSTAGE], uint8_t (&s3)[PSTAGE],
                                             ConstMask wm, const uint8_t *xsrc,
-                                            const uint8_t *wsrc, int ns, v16i (&acc)[14])
+                                            const uint8_t *wsrc, int ns, bool rev,
+                                            v16i (&acc)[14])
 {
     constexpr int WP0 = LO > 0 ? LO - 1 : 0;   // first W plane in the stage
     constexpr int NB = LO > 0 ? 5 : 4;         // W planes the MFMAs read
@@ -764,7 +765,9 @@ __device__ __forceinline__ void planes_pass(uint8_t (&s0)[PSTAGE], uint8_t (&s1)
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), wt = w >> 1, wn = w & 1;
     const int off = opnd_off(lane);
     const uint8_t *ws_src = wsrc + WP0 * PLANE;
+    // step s of the loop is k-step rev ? ns - 1 - s : s of the block's range
     auto dma = [&](int s, uint8_t(&dst)[PSTAGE]) {
+        s = rev ? ns - 1 - s : s;
 #pragma unroll
         for (int j = 0; j < 6; ++j) {
             const int c = w + 4 * j;   // chunk 0..23: X 0..13, W 14..23
@@ -806,7 +809,7 @@ __device__ __forceinline__ void planes_pass(uint8_t (&s0)[PSTAGE], uint8_t (&s1)
         }
     };
     auto ext_of = [&](int i) {
-        uint32_t e = LO > 0 ? wm[i] : 0;
+        uint32_t e = LO > 0 ? wm[rev ? ns - 1 - i : i] : 0;
         asm volatile("" : "+s"(e));
         return ((e >> WP0) & 1u) != 0;
     };
@@ -838,10 +841,12 @@ __device__ __forceinline__ void planes_pass(uint8_t (&s0)[PSTAGE], uint8_t (&s1)
     for (; i + 6 < ns; i += 4) {
         uint32_t e0 = 0, e1 = 0, e2 = 0, e3 = 0;
         if (LO > 0) {
-            e0 = wm[i];
-            e1 = wm[i + 1];
-            e2 = wm[i + 2];
-            e3 = wm[i + 3];
+            const ConstMask g = wm + (rev ? ns - 4 - i : i);   // steps i .. i + 3
+            const uint32_t g0 = g[0], g1 = g[1], g2 = g[2], g3 = g[3];
+            e0 = rev ? g3 : g0;
+            e1 = rev ? g2 : g1;
+            e2 = rev ? g1 : g2;
+            e3 = rev ? g0 : g3;
             asm volatile("" : "+s"(e0), "+s"(e1), "+s"(e2), "+s"(e3));
         }
         wait_vm<6>();
@@ -899,7 +904,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 k_gemm_i8p(int64_t *__restrict__ Y, uint64_t *__restrict__ P, int *__restrict__ redo,
            const uint8_t *__restrict__ Xp, const uint32_t *__restrict__ Xm,
            const uint8_t *__restrict__ Wp, const uint32_t *__restrict__ Wm, int T, int N,
-           int nsteps, int spb)
+           int nsteps, int spb, int cpx)
 {
     __shared__ __align__(16) uint8_t st0[PSTAGE];
     __shared__ __align__(16) uint8_t st1[PSTAGE];
@@ -940,6 +945,12 @@ k_gemm_i8p(int64_t *__restrict__ Y, uint64_t *__restrict__ P, int *__restrict__ 
     const uint8_t *xsrc = Xp + ((size_t)t_tile * nsteps + s0) * 8 * PLANE;
     const uint8_t *wsrc = Wp + ((size_t)n_tile * nsteps + s0) * 8 * PLANE;
     const ConstMask wm = (ConstMask)(Wm + (size_t)n_tile * nsteps + s0);
+    // Blocks run in rounds of one per compute unit; each XCD's round holds 8
+    // row tiles x 4 token tiles (tile_of), and the next round's blocks take
+    // the same row tiles with the next token tiles.  Odd rounds walk k
+    // downwards, so they start on the W planes the round before ended on,
+    // which are still in L2.
+    const bool rev = ((((int)blockIdx.x >> 3) / cpx) & 1) != 0;
     // lane l, register i: token 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32;
     // window LO touches digit sums LO - 1 .. LO + 9 only
     const int wt = w >> 1, wn = w & 1;
@@ -965,23 +976,23 @@ k_gemm_i8p(int64_t *__restrict__ Y, uint64_t *__restrict__ P, int *__restrict__ 
     using std::integral_constant;
     switch (LO) {
     case 0:
-        planes_pass<0>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        planes_pass<0>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, rev, acc);
         store(integral_constant<int, 0>{}, integral_constant<int, 9>{});
         break;
     case 1:
-        planes_pass<1>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        planes_pass<1>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, rev, acc);
         store(integral_constant<int, 0>{}, integral_constant<int, 10>{});
         break;
     case 2:
-        planes_pass<2>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        planes_pass<2>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, rev, acc);
         store(integral_constant<int, 1>{}, integral_constant<int, 11>{});
         break;
     case 3:
-        planes_pass<3>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        planes_pass<3>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, rev, acc);
         store(integral_constant<int, 2>{}, integral_constant<int, 12>{});
         break;
     default:
-        planes_pass<4>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, acc);
+        planes_pass<4>(st0, st1, st2, st3, wm, xsrc, wsrc, ns, rev, acc);
         store(integral_constant<int, 3>{}, integral_constant<int, 13>{});
         break;
     }
@@ -1081,7 +1092,7 @@ int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *
                                K, steps);
         }
         hipLaunchKernelGGL(k_gemm_i8p, grid, dim3(256), 0, c->stream, Y, P, redo, Xp, Xm, Wp, Wm,
-                           T, N, steps, spb);
+                           T, N, steps, spb, max(1, c->cu_count / 8));
     } else if (vec) {
         hipLaunchKernelGGL((k_gemm_i8<true>), grid, dim3(256), 0, c->stream, Y, P, redo, W, X, T,
                            N, K, spb);
