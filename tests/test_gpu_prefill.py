@@ -118,6 +118,42 @@ def test_tiny_long_prefill_equals_sequential(ctx, chunks):
         m.free()
 
 
+def test_prefill_planes_follow_weight_uploads(ctx):
+    """The prefill's prepared weight planes (made at the first prefill of 128
+    tokens or more; the tiny config's gate|up, 1376 rows, takes the planes
+    kernel) are made again after q48h_upload: a 200-token prefill after one
+    layer's gate and up weights change equals the per-token forward on the
+    new weights, and one with the planes turned off equals it too."""
+    cfg = list(spec.TINY)
+    n = 200
+    toks = [int(t) for t in np.random.default_rng(21).integers(0, cfg[6], size=n)]
+    m = intllm.HostModel(ctx, intllm.Config(*cfg))
+    try:
+        m.synth(9, threads())
+        say("tiny prefill 200 (prepares the planes)")
+        m.prefill(toks, 0, cfg[6], choose=False)
+        rng = np.random.default_rng(22)
+        for nm in ("model.layers.1.mlp.gate_proj.weight", "model.layers.1.mlp.up_proj.weight"):
+            w = (rng.integers(-(1 << 40), 1 << 40, size=cfg[5] * cfg[0], dtype=np.int64)
+                 >> 24) << 24
+            m.upload(nm, w)
+        m.kv_reset()
+        say("tiny prefill 200 after the upload")
+        _, got = m.prefill(toks, 0, cfg[6], choose=False)
+        m.kv_reset()
+        m.set_gemm_planes(False)
+        _, off = m.prefill(toks, 0, cfg[6], choose=False)
+        m.set_gemm_planes(True)
+        m.kv_reset()
+        say("tiny sequential forward 200")
+        want = sequential(m, toks, 0, cfg[6])
+        bad = [i for i in range(n) if not np.array_equal(got[i], want[i])]
+        assert not bad, (len(bad), bad[:5])
+        assert np.array_equal(off, want)
+    finally:
+        m.free()
+
+
 def test_generate_batched_and_per_token_prefill_agree(ctx):
     """generate() with the batched prompt (default) and with per-token
     forward calls: both the reference's tokens and step hashes."""
