@@ -1096,9 +1096,9 @@ int q48h_prefill(q48h_model *m, const int *tokens, int T, int p0, int64_t *logit
     int64_t *GU = D + (size_t)T * dim, *HF = GU + (size_t)T * 2 * ffn;
     int64_t *LG = HF + (size_t)T * ffn;
     int *ids = (int *)(LG + nlog);
-    /* prepared weight planes pay off from 128 tokens (q48_gemm_prepared) */
+    /* prepared weight planes pay off from 16 tokens (q48_gemm_prepared) */
     size_t poff[4] = {0, 0, 0, 0}, pstride = 0;
-    if (T >= 128) {
+    if (T >= 16) {
         TRY(prepare_planes(m));
         if (m->wp_ok)
             pstride = planes_layout(m, poff);
