@@ -1058,7 +1058,7 @@ int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *
     const bool fits = (size_t)max(nt, nn) * steps <= 0x7fffffff;
     const bool planes =
         fits && (kernel == Q48_GEMM_I8_PLANES ||
-                 (kernel != Q48_GEMM_I8_FUSED && T >= (Wpre ? 16 : 256) && N >= 1024));
+                 (kernel != Q48_GEMM_I8_FUSED && T >= (Wpre ? 2 : 256) && N >= 1024));
     const bool wsplit = planes && !Wpre;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     // workspace: the blocks' redo flags, (S > 1) the int128 partials, then

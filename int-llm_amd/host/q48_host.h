@@ -110,7 +110,8 @@ int q48h_generate(q48h_model *m, const int *prompt, int prompt_len, int max_new,
  * projections, filling the KV cache exactly as T forward calls do.
  * logits_all (host, may be NULL) receives the T logits rows; next (may be
  * NULL) the token chosen from the last row (argmax or sample_token).  Past
- * position 4096, or for T = 1, the tokens go one forward call at a time. */
+ * position 4096, or for T < 3 (where forward calls are as fast), the tokens
+ * go one forward call at a time. */
 int q48h_prefill(q48h_model *m, const int *tokens, int T, int p0, int64_t *logits_all,
                  int *next);
 /* q48h_generate's prompt through q48h_prefill (1, the default) or one
