@@ -1054,7 +1054,8 @@ int q48_launch_gemm_i8(q48_ctx *c, int64_t *Y, const int64_t *W, const int64_t *
     // the planes path pays one split of X (and of W unless prepared) per
     // call: it wins once tiles are reused enough (measured: T >= 512 with
     // N >= 2048 faster by 7-39%, N = 256 slower by 5-22%, T = 128 even when
-    // W is split in the call, faster by about a quarter when it is not)
+    // W is split in the call); with W prepared it wins from 2 tokens, where
+    // the GEMM streams W and the planes hold 5 of its 8 bytes per element
     const bool fits = (size_t)max(nt, nn) * steps <= 0x7fffffff;
     const bool planes =
         fits && (kernel == Q48_GEMM_I8_PLANES ||

@@ -117,10 +117,10 @@ int q48h_prefill(q48h_model *m, const int *tokens, int T, int p0, int64_t *logit
 /* q48h_generate's prompt through q48h_prefill (1, the default) or one
  * forward call per token (0); the bits are the same. */
 void q48h_model_set_batched_prefill(q48h_model *m, int on);
-/* The batched prefill of 128 tokens or more multiplies through digit planes
- * of each layer's projection matrices, prepared once per set of weights
- * (q48_gemm_prepare; about 8 bytes per weight of device memory, made at the
- * first such prefill and again after q48h_upload).  1 (the default) or 0:
+/* The batched prefill multiplies through digit planes of each layer's
+ * projection matrices, prepared once per set of weights (q48_gemm_prepare;
+ * about 8 bytes per weight of device memory, made at the first batched
+ * prefill and again after q48h_upload).  1 (the default) or 0:
  * split W in each call, and free the planes.  The bits are the same. */
 void q48h_model_set_gemm_planes(q48h_model *m, int on);
 
