@@ -397,7 +397,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the Q16.48 decode path is "
-              "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "single-GPU)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
