@@ -387,8 +387,8 @@ def test_gemm_digit_windows(ctx, oracle, case, tokens, kernel):
 
 def test_gemm_prepared_planes(ctx, oracle):
     """q48_gemm_prepared: W's digit planes prepared once (q48_gemm_prepare),
-    then GEMMs of 1, 64, 128 and 300 tokens (the GEMV, the in-loop split,
-    and the planes path with W's planes read from the prepared buffer) over
+    then GEMMs of 1, 3, 17, 64, 128 and 300 tokens (the GEMV for one token,
+    else the planes path with W's planes read from the prepared buffer) over
     bfloat16-like weights with one row tile leaving the digit window (its
     blocks redone from W itself), against the oracle; then the buffer
     re-prepared from other weights.  Misaligned buffers are refused."""
@@ -400,7 +400,7 @@ def test_gemm_prepared_planes(ctx, oracle):
     assert need >= N * K * 8
     dW, dP = ctx.to_device(W), ctx.buffer(need // 8 + 2)
     ctx.gemm_prepare(dP.ptr, dW.ptr, N, K)
-    for T in (1, 64, 128, 300):
+    for T in (1, 3, 17, 64, 128, 300):
         X = rng.integers(-(1 << 52), 1 << 52, size=T * K, dtype=np.int64)
         want = np.empty(T * N, dtype=np.int64)
         oracle.q48o_gemm(want.ctypes.data, W.ctypes.data, X.ctypes.data, T, N, K)
